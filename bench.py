@@ -1,0 +1,353 @@
+#!/usr/bin/env python3
+"""MoE-layer benchmark on one MI355X.
+
+Default workload: BASELINE.json configs[1], a GPT-OSS-20B-shaped MoE decode
+layer (hidden = intermediate = 2880, 32 experts, top-4 on logits then softmax,
+clamped SwiGLU, mlx affine 4-bit gs64 with bf16 scales/biases, biased bf16
+router) on one token. 24 independent layers' weights stay resident in HBM
+(10.7 GB, beyond the 256 MB Infinity Cache) and successive steps rotate
+through them. One step = one layer call on one token; the timed region
+replays a HIP graph of the 24-layer rotation.
+
+Prints one JSON line:
+  value       MoE-layer tokens/s (1 token per step / time per step)
+  roofline    the dominant kernel (routed gate/up grouped GEMV), HBM bound:
+              algorithmic bytes per launch / its average duration, timed with
+              hipEvents on the launch stream
+  cpu_baseline the C oracle (oracle/) on layer 0, one token at a time
+Other configs: --config qwen3 (configs[2], --batch B), prefill,
+mixed.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+CONFIGS = {
+    # name: hidden, experts, top_k, inter, gate/up bits, down bits, sb dtype, activation,
+    #       gating, router bias, tokens, shared inter
+    "gptoss": dict(H=2880, E=32, k=4, I=2880, bits_gu=4, bits_d=4, sb="bf16", act="gptoss",
+                   gating="topk_softmax", router_bias=True, T=1, SI=0,
+                   workload="gptoss20b_moe_decode_b1"),
+    "qwen3": dict(H=2048, E=128, k=8, I=768, bits_gu=4, bits_d=4, sb="f16", act="swiglu",
+                  gating="softmax_topk", router_bias=False, T=1, SI=0,
+                  workload="qwen3moe_decode"),
+    "prefill": dict(H=2048, E=128, k=8, I=768, bits_gu=4, bits_d=4, sb="f16", act="swiglu",
+                    gating="softmax_topk", router_bias="zipf", T=4096, SI=0,
+                    workload="qwen3moe_prefill_4096_zipf1.1"),
+    "mixed": dict(H=2048, E=256, k=8, I=512, bits_gu=3, bits_d=6, sb="bf16", act="swiglu",
+                  gating="softmax_topk", router_bias=False, T=2048, SI=512,
+                  workload="mixed_3b6b_shared_prefill_2048"),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------ hip events --
+class HipEvents:
+    """hipEvent handles straight from libamdhip64 (recorded by libmoehip)."""
+
+    def __init__(self):
+        self.hip = C.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [C.c_void_p]
+
+    def create(self):
+        e = C.c_void_p()
+        assert self.hip.hipEventCreate(C.byref(e)) == 0
+        return e
+
+    def elapsed_ms(self, a, b):
+        ms = C.c_float()
+        assert self.hip.hipEventSynchronize(b) == 0
+        assert self.hip.hipEventElapsedTime(C.byref(ms), a, b) == 0
+        return ms.value
+
+    def destroy(self, e):
+        self.hip.hipEventDestroy(e)
+
+
+# ------------------------------------------------------------- the layer --
+def make_layer(cfg, seed, torch, fl, lib):
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    H, E, I = cfg["H"], cfg["E"], cfg["I"]
+    sb = {"bf16": torch.bfloat16, "f16": torch.float16}[cfg["sb"]]
+
+    def proj(E_, N, K, bits):
+        words = K * bits // 32
+        w = torch.randint(0, 256, (E_, N, words * 4), dtype=torch.uint8, device=dev, generator=g)
+        s = torch.empty(E_, N, K // 64, dtype=sb, device=dev).uniform_(0.005, 0.02, generator=g)
+        b = torch.empty(E_, N, K // 64, dtype=sb, device=dev).uniform_(-0.1, 0.1, generator=g)
+        return fl.StackedExperts(w.view(torch.int32), s, b, bits, 64)
+
+    rw = (torch.randn(E, H, device=dev, generator=g) / math.sqrt(H)).to(torch.bfloat16)
+    rb = None
+    if cfg["router_bias"] is True:
+        rb = (torch.randn(E, device=dev, generator=g) * 0.1).to(torch.bfloat16)
+    elif cfg["router_bias"] == "zipf":
+        rb = zipf_bias(E, cfg.get("beta", 1.0), seed, torch).to(dev)
+    gating = fl.MoEGatingMode.topKThenSoftmax if cfg["gating"] == "topk_softmax" else \
+        fl.MoEGatingMode.softmaxThenTopK
+    router = fl.MoERouter(E, cfg["k"], gating, True)
+    shared = None
+    sgw = None
+    if cfg["SI"]:
+        shared = (proj(1, cfg["SI"], H, cfg["bits_gu"]), proj(1, cfg["SI"], H, cfg["bits_gu"]),
+                  proj(1, H, cfg["SI"], cfg["bits_d"]))
+        sgw = (torch.randn(1, H, device=dev, generator=g) / math.sqrt(H)).to(torch.bfloat16)
+    act = lib.MOE_ACT_GPTOSS if cfg["act"] == "gptoss" else lib.MOE_ACT_SWIGLU
+    return fl.MoELayer(router_weight=rw, router=router,
+                       gate=proj(E, I, H, cfg["bits_gu"]), up=proj(E, I, H, cfg["bits_gu"]),
+                       down=proj(E, H, I, cfg["bits_d"]), hidden=H, act_dtype=torch.bfloat16,
+                       router_bias=rb, activation=act, alpha=1.702, limit=7.0, shared=shared,
+                       shared_gate_weight=sgw)
+
+
+def zipf_bias(E, beta, seed, torch):
+    import numpy as np
+    rng = np.random.default_rng(seed + 7)
+    ranks = rng.permutation(E) + 1
+    p = ranks.astype(np.float64) ** -1.1
+    p /= p.sum()
+    return torch.from_numpy((beta * np.log(p)).astype(np.float32)).to(torch.bfloat16)
+
+
+def proj_bytes(p, experts):
+    """Compulsory HBM bytes of `experts` experts of one stacked projection."""
+    n, k = p.n, p.k
+    sb = p.scales.element_size()
+    return experts * (n * k * p.bits // 8 + 2 * n * (k // p.group_size) * sb)
+
+
+# ------------------------------------------------------------ CPU oracle --
+def cpu_baseline(layer, cfg, torch, budget_s=12.0):
+    """Times the C oracle (oracle/) on layer 0, one token per call."""
+    import numpy as np
+    import oracle as orc
+
+    def host(t):
+        if t is None:
+            return None
+        t = t.detach().cpu()
+        if t.dtype == torch.bfloat16:
+            return t.view(torch.int16).numpy().view(np.uint16)
+        if t.dtype == torch.int32:
+            return t.numpy().view(np.uint32)
+        return t.numpy()
+
+    sbdt = orc.BF16 if layer.gate.scales.dtype == torch.bfloat16 else orc.F16
+
+    def qp(p):
+        return orc.QProj(host(p.weight), host(p.scales), host(p.biases), p.bits, p.group_size,
+                         orc.BF16 if p.scales.dtype == torch.bfloat16 else orc.F16)
+
+    keep = dict(rw=host(layer.router_weight), rb=host(layer.router_bias), gate=qp(layer.gate),
+                up=qp(layer.up), down=qp(layer.down))
+    L = orc.OrLayer()
+    L.hidden, L.n_experts, L.top_k = cfg["H"], cfg["E"], cfg["k"]
+    L.intermediate, L.act_dt = cfg["I"], orc.BF16
+    L.router_weight, L.router_dt = keep["rw"].ctypes.data, orc.BF16
+    L.router_bias = None if keep["rb"] is None else keep["rb"].ctypes.data
+    L.gating = orc.TOPK_THEN_SOFTMAX if cfg["gating"] == "topk_softmax" else orc.SOFTMAX_THEN_TOPK
+    L.norm_topk = 1
+    L.gate, L.up, L.down = keep["gate"].c(), keep["up"].c(), keep["down"].c()
+    L.activation = orc.ACT_GPTOSS if cfg["act"] == "gptoss" else orc.ACT_SWIGLU
+    L.alpha, L.limit = 1.702, 7.0
+    rng = np.random.default_rng(1)
+    lib = orc.lib()
+    T = 1 if cfg["T"] == 1 else 4
+    x = orc.from_f32(rng.normal(0, 1, (64, T, cfg["H"])).astype(np.float32), orc.BF16)
+    y = np.zeros((T, cfg["H"]), np.uint16)
+    t0 = time.perf_counter()
+    n = 0
+    while n < 64:
+        lib.or_moe_layer(C.byref(L), x[n].ctypes.data_as(C.c_void_p), T, y.ctypes.data_as(C.c_void_p),
+                         None, None, None, None)
+        n += 1
+        if time.perf_counter() - t0 > budget_s and n >= 3:
+            break
+    dt = time.perf_counter() - t0
+    _ = sbdt
+    return dict(value=n * T / dt, unit="tokens/s", cores=1, kind="port",
+                sample=f"{n} oracle layer calls of {T} token(s) on layer 0 (single thread, "
+                       f"{dt:.1f} s)")
+
+
+# ------------------------------------------------------------------ main --
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2400)
+    ap.add_argument("--warmup", type=int, default=240)
+    ap.add_argument("--config", default="gptoss", choices=sorted(CONFIGS))
+    ap.add_argument("--batch", type=int, default=None, help="tokens per step (overrides config)")
+    ap.add_argument("--layers", type=int, default=24, help="resident layers rotated per step")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus > 1 or world > 1:
+        print("bench.py: this build measures one GPU only (single-GPU MoE layer; no multi-GPU "
+              "path is built). Run with --gpus 1.", flush=True)
+        sys.exit(2)
+
+    import torch
+    from ffai_amd import _lib as lib
+    from ffai_amd import layer as fl
+
+    cfg = dict(CONFIGS[args.config])
+    if args.batch:
+        cfg["T"] = args.batch
+    T = cfg["T"]
+    torch.manual_seed(0)
+    L = args.layers if T <= 64 else min(args.layers, 4)
+    log(f"building {L} resident layers of {args.config} ...")
+    layers = [make_layer(cfg, seed=100 + l, torch=torch, fl=fl, lib=lib) for l in range(L)]
+    xs = [torch.randn(T, cfg["H"], device="cuda").to(torch.bfloat16) for _ in range(L)]
+    ys = [torch.empty_like(x) for x in xs]
+    for l in range(L):
+        layers[l].workspace(T)
+    torch.cuda.synchronize()
+
+    steps = max(L, (args.steps // L) * L)
+    warm = max(L, (args.warmup // L) * L)
+
+    # eager warm-up
+    for i in range(warm):
+        layers[i % L].forward(xs[i % L], out=ys[i % L])
+    torch.cuda.synchronize()
+
+    # HIP graph of one rotation through the resident layers
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for l in range(L):
+            layers[l].forward(xs[l], out=ys[l])
+    graph.replay()
+    torch.cuda.synchronize()
+
+    # timed region: `steps` layer calls
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps // L):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    ms_total = e0.elapsed_time(e1)
+    ms_per_step = ms_total / steps
+    value = T * 1000.0 / ms_per_step
+    log(f"{steps} steps: {ms_total:.3f} ms (events), {wall * 1e3:.3f} ms (wall); "
+        f"{ms_per_step * 1e3:.2f} us/step")
+
+    # kernel-level timing of the routed expert kernels (eager, GPU kept busy
+    # ahead of the host so events bracket only device work)
+    ev = HipEvents()
+    reps = max(1, min(20, 480 // L))
+    marks = [[[ev.create() for _ in range(3)] for _ in range(L)] for _ in range(reps)]
+    trace = []
+    for r in range(reps):
+        for l in range(L):
+            t = lib.LayerTrace()
+            for i in range(3):
+                t.events[i] = marks[r][l][i].value
+            trace.append(t)
+    # keep the GPU busy while the host queues the measured calls
+    busy = torch.ones(128 * 1024 * 1024, dtype=torch.float32, device="cuda")
+    for _ in range(200):
+        busy.mul_(1.0)
+    j = 0
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for r in range(reps):
+        for l in range(L):
+            lay = layers[l]
+            lib.check(lib.load().moe_layer_forward(
+                C.byref(lay.desc), C.c_void_p(xs[l].data_ptr()), T, C.c_void_p(ys[l].data_ptr()),
+                C.c_void_p(lay._ws.data_ptr()), lay._ws.numel(), C.byref(trace[j]), stream))
+            j += 1
+    torch.cuda.synchronize()
+    gu = [ev.elapsed_ms(marks[r][l][0], marks[r][l][1]) for r in range(reps) for l in range(L)]
+    dn = [ev.elapsed_ms(marks[r][l][1], marks[r][l][2]) for r in range(reps) for l in range(L)]
+    for row in marks:
+        for m in row:
+            for e in m:
+                ev.destroy(e)
+    gu_us = 1e3 * sum(gu) / len(gu)
+    dn_us = 1e3 * sum(dn) / len(dn)
+
+    # algorithmic bytes: distinct experts actually routed (decode) or FLOPs (prefill)
+    lay0 = layers[0]
+    _, tr = lay0.forward(xs[0], trace=True)
+    torch.cuda.synchronize()
+    U = int(torch.unique(tr["topk_idx"]).numel())
+    gu_bytes = proj_bytes(lay0.gate, U) + proj_bytes(lay0.up, U) + \
+        T * cfg["H"] * 2 + T * cfg["k"] * cfg["I"] * 2
+    dn_bytes = proj_bytes(lay0.down, U) + T * cfg["k"] * cfg["I"] * 2 + T * cfg["H"] * 2
+    M = T * cfg["k"]
+    gu_flops = 2.0 * M * 2 * cfg["H"] * cfg["I"]
+    if T <= 64:
+        roof = dict(bound="hbm", achieved=round(gu_bytes / (gu_us * 1e-6) / 1e9, 1),
+                    peak=HBM_PEAK_GBS, unit="GB/s")
+    else:
+        roof = dict(bound="mfma", achieved=round(gu_flops / (gu_us * 1e-6) / 1e12, 2),
+                    peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s")
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["traffic"] = None
+    roof["kernel"] = "routed gate/up grouped dequant GEMV (gemv_single_kernel / gemv_grouped_kernel)"
+    roof["avg_us"] = round(gu_us, 3)
+    roof["algorithmic_bytes"] = gu_bytes
+    log(f"gate/up kernel {gu_us:.2f} us ({gu_bytes / 1e6:.2f} MB, "
+        f"{gu_bytes / (gu_us * 1e-6) / 1e9:.0f} GB/s); down+combine {dn_us:.2f} us "
+        f"({dn_bytes / 1e6:.2f} MB, {dn_bytes / (dn_us * 1e-6) / 1e9:.0f} GB/s); U={U}")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle ...")
+        cpu = cpu_baseline(layers[0], cfg, torch)
+
+    out = {
+        "metric": "MoE-layer tokens/s",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random packed codes, U-distributed scales/biases, N(0,1) activations)",
+        "config": {"workload": cfg["workload"], "hidden": cfg["H"], "experts": cfg["E"],
+                   "top_k": cfg["k"], "intermediate": cfg["I"], "tokens_per_step": T,
+                   "bits": [cfg["bits_gu"], cfg["bits_d"]], "group_size": 64,
+                   "resident_layers": L, "parallelism": "single-gpu"},
+        "roofline": roof,
+        "expert_stream": {"gate_up_us": round(gu_us, 3), "down_combine_us": round(dn_us, 3),
+                          "bytes": gu_bytes + dn_bytes, "distinct_experts": U,
+                          "GBps": round((gu_bytes + dn_bytes) / ((gu_us + dn_us) * 1e-6) / 1e9, 1)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

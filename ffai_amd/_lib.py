@@ -1,0 +1,122 @@
+"""ctypes binding of libmoehip.so (include/moe_hip.h).
+
+This is the Python view of the C ABI that a Swift (or any FFI) caller binds;
+tests and bench.py drive the library through it with device buffers owned by
+PyTorch. There is no fallback: if the library is missing, loading fails with
+an error naming the build step.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmoehip.so")
+
+MOE_OK, MOE_ERR_INVALID, MOE_ERR_UNSUPPORTED, MOE_ERR_WORKSPACE, MOE_ERR_HIP = range(5)
+MOE_F32, MOE_F16, MOE_BF16 = 0, 1, 2
+MOE_SOFTMAX_THEN_TOPK, MOE_TOPK_THEN_SOFTMAX = 0, 1
+MOE_ACT_SWIGLU, MOE_ACT_GPTOSS = 0, 1
+
+EXPORTS = [
+    "moe_last_error_string", "moe_version", "moe_validate_qproj", "moe_validate_layer",
+    "moe_derive_bits", "moe_router_logits", "moe_router_topk", "moe_dispatch_workspace_bytes",
+    "moe_dispatch_plan", "moe_dequantize_affine", "moe_expert_matmul_workspace_bytes",
+    "moe_expert_matmul", "moe_activation_apply", "moe_unpermute", "moe_layer_workspace_bytes",
+    "moe_layer_forward", "moe_layer_create", "moe_layer_destroy", "moe_layer_decode",
+    "moe_layer_decode_many",
+]
+
+
+class MoeError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"moe status {status}: {msg}")
+        self.status = status
+
+
+class QProj(C.Structure):
+    _fields_ = [
+        ("weight", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p),
+        ("out_bias", C.c_void_p),
+        ("bits", C.c_int32), ("group_size", C.c_int32), ("sb_dtype", C.c_int32),
+        ("n", C.c_int32), ("k", C.c_int32), ("n_experts", C.c_int32),
+    ]
+
+
+class LayerDesc(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_int32), ("n_experts", C.c_int32), ("top_k", C.c_int32),
+        ("intermediate", C.c_int32), ("act_dtype", C.c_int32),
+        ("router_weight", C.c_void_p), ("router_dtype", C.c_int32), ("router_bias", C.c_void_p),
+        ("gating", C.c_int32), ("norm_topk_prob", C.c_int32), ("expert_bias", C.c_void_p),
+        ("gate", QProj), ("up", QProj), ("down", QProj),
+        ("activation", C.c_int32), ("act_alpha", C.c_float), ("act_limit", C.c_float),
+        ("has_shared", C.c_int32),
+        ("shared_gate", QProj), ("shared_up", QProj), ("shared_down", QProj),
+        ("shared_gate_weight", C.c_void_p),
+    ]
+
+
+class LayerTrace(C.Structure):
+    _fields_ = [
+        ("logits", C.c_void_p), ("topk_idx", C.c_void_p), ("topk_weight", C.c_void_p),
+        ("perm", C.c_void_p), ("offsets", C.c_void_p), ("events", C.c_void_p * 3),
+    ]
+
+
+_lib = None
+
+
+def load():
+    """Load libmoehip.so (built by ffai_amd.build.build())."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`")
+    lib = C.CDLL(LIB_PATH)
+    vp, i32, sz, st = C.c_void_p, C.c_int32, C.c_size_t, C.c_void_p
+    lib.moe_last_error_string.restype = C.c_char_p
+    lib.moe_version.restype = C.c_char_p
+    lib.moe_validate_qproj.argtypes = [C.POINTER(QProj)]
+    lib.moe_validate_layer.argtypes = [C.POINTER(LayerDesc)]
+    lib.moe_derive_bits.argtypes = [C.c_int64, C.c_int64, i32, C.POINTER(i32)]
+    lib.moe_router_logits.argtypes = [vp, i32, i32, i32, vp, i32, vp, i32, vp, st]
+    lib.moe_router_topk.argtypes = [vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, st]
+    lib.moe_dispatch_workspace_bytes.argtypes = [i32, i32, i32]
+    lib.moe_dispatch_workspace_bytes.restype = sz
+    lib.moe_dispatch_plan.argtypes = [vp, i32, i32, i32, vp, vp, vp, vp, vp, sz, st]
+    lib.moe_dequantize_affine.argtypes = [vp, vp, vp, i32, i32, i32, C.c_int64, vp, i32, st]
+    lib.moe_expert_matmul_workspace_bytes.argtypes = [i32, i32]
+    lib.moe_expert_matmul_workspace_bytes.restype = sz
+    lib.moe_expert_matmul.argtypes = [C.POINTER(QProj), vp, i32, vp, i32, i32, vp, vp, vp, sz, st]
+    lib.moe_activation_apply.argtypes = [vp, vp, vp, C.c_int64, i32, i32, C.c_float, C.c_float, st]
+    lib.moe_unpermute.argtypes = [vp, vp, vp, i32, i32, i32, vp, i32, st]
+    lib.moe_layer_workspace_bytes.argtypes = [C.POINTER(LayerDesc), i32]
+    lib.moe_layer_workspace_bytes.restype = sz
+    lib.moe_layer_forward.argtypes = [C.POINTER(LayerDesc), vp, i32, vp, vp, sz,
+                                      C.POINTER(LayerTrace), st]
+    lib.moe_layer_create.argtypes = [C.POINTER(LayerDesc), C.POINTER(vp)]
+    lib.moe_layer_destroy.argtypes = [vp]
+    lib.moe_layer_destroy.restype = None
+    lib.moe_layer_decode.argtypes = [vp, vp, vp, st]
+    lib.moe_layer_decode_many.argtypes = [vp, vp, i32, vp, st]
+    for name in ["moe_validate_qproj", "moe_validate_layer", "moe_derive_bits", "moe_router_logits",
+                 "moe_router_topk", "moe_dispatch_plan", "moe_dequantize_affine",
+                 "moe_expert_matmul", "moe_activation_apply", "moe_unpermute",
+                 "moe_layer_forward", "moe_layer_create", "moe_layer_decode",
+                 "moe_layer_decode_many"]:
+        getattr(lib, name).restype = C.c_int
+    _lib = lib
+    return lib
+
+
+def check(status: int):
+    if status != MOE_OK:
+        raise MoeError(status, load().moe_last_error_string().decode())
+    return status
+
+
+def last_error() -> str:
+    return load().moe_last_error_string().decode()

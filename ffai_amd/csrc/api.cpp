@@ -1,0 +1,743 @@
+// api.cpp — the C ABI of libmoehip.so (include/moe_hip.h) and the host-side
+// MoELayer that mirrors FFAI's Swift block (Sources/FFAI/Models/MoELayer.swift).
+//
+// Everything here is host code: argument validation (the reference's Swift
+// preconditions and validators), workspace layout, launch geometry, and the
+// stream-ordered sequence of kernels for one layer call. No call on the hot
+// path allocates, synchronises or copies to the host.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "../../include/moe_hip.h"
+#include "moe_internal.hpp"
+
+namespace moe {
+hipError_t launch_gemv_b2(int, int, bool, int, const GemvArgs&, int, hipStream_t);
+hipError_t launch_gemv_b3(int, int, bool, int, const GemvArgs&, int, hipStream_t);
+hipError_t launch_gemv_b4(int, int, bool, int, const GemvArgs&, int, hipStream_t);
+hipError_t launch_gemv_b5(int, int, bool, int, const GemvArgs&, int, hipStream_t);
+hipError_t launch_gemv_b6(int, int, bool, int, const GemvArgs&, int, hipStream_t);
+hipError_t launch_gemv_b8(int, int, bool, int, const GemvArgs&, int, hipStream_t);
+hipError_t launch_down_combine_b2(int, int, const DownCombineArgs&, int, hipStream_t);
+hipError_t launch_down_combine_b3(int, int, const DownCombineArgs&, int, hipStream_t);
+hipError_t launch_down_combine_b4(int, int, const DownCombineArgs&, int, hipStream_t);
+hipError_t launch_down_combine_b5(int, int, const DownCombineArgs&, int, hipStream_t);
+hipError_t launch_down_combine_b6(int, int, const DownCombineArgs&, int, hipStream_t);
+hipError_t launch_down_combine_b8(int, int, const DownCombineArgs&, int, hipStream_t);
+
+hipError_t launch_gemv(int bits, int xdt, int sbdt, bool gateup, int tokmax, const GemvArgs& a,
+                       int grid, hipStream_t st) {
+  switch (bits) {
+    case 2: return launch_gemv_b2(xdt, sbdt, gateup, tokmax, a, grid, st);
+    case 3: return launch_gemv_b3(xdt, sbdt, gateup, tokmax, a, grid, st);
+    case 4: return launch_gemv_b4(xdt, sbdt, gateup, tokmax, a, grid, st);
+    case 5: return launch_gemv_b5(xdt, sbdt, gateup, tokmax, a, grid, st);
+    case 6: return launch_gemv_b6(xdt, sbdt, gateup, tokmax, a, grid, st);
+    case 8: return launch_gemv_b8(xdt, sbdt, gateup, tokmax, a, grid, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_down_combine(int bits, int xdt, int sbdt, const DownCombineArgs& a, int grid,
+                               hipStream_t st) {
+  switch (bits) {
+    case 2: return launch_down_combine_b2(xdt, sbdt, a, grid, st);
+    case 3: return launch_down_combine_b3(xdt, sbdt, a, grid, st);
+    case 4: return launch_down_combine_b4(xdt, sbdt, a, grid, st);
+    case 5: return launch_down_combine_b5(xdt, sbdt, a, grid, st);
+    case 6: return launch_down_combine_b6(xdt, sbdt, a, grid, st);
+    case 8: return launch_down_combine_b8(xdt, sbdt, a, grid, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+size_t gemv_smem_bytes(int xdt, int K, int tok_chunk) {
+  const size_t xs = (xdt == DT_F32) ? 4 : 2;
+  return (size_t)tok_chunk * ((size_t)K * xs + (size_t)(K / 32) * 4);
+}
+
+size_t down_combine_smem_bytes(int, int, int) { return 0; }
+}  // namespace moe
+
+using namespace moe;
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+namespace {
+
+thread_local std::string g_err;
+
+moe_status fail(moe_status s, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return s;
+}
+
+moe_status ok() {
+  g_err.clear();
+  return MOE_OK;
+}
+
+moe_status hip_check(hipError_t e, const char* what) {
+  if (e == hipSuccess) return MOE_OK;
+  return fail(MOE_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define MOE_TRY(expr)                    \
+  do {                                   \
+    moe_status _s = (expr);              \
+    if (_s != MOE_OK) return _s;         \
+  } while (0)
+
+#define MOE_HIP(expr, what) MOE_TRY(hip_check((expr), (what)))
+
+bool dt_ok(int dt) { return dt == MOE_F32 || dt == MOE_F16 || dt == MOE_BF16; }
+size_t dt_size(int dt) { return dt == MOE_F32 ? 4u : 2u; }
+bool bits_ok(int b) { return b == 2 || b == 3 || b == 4 || b == 5 || b == 6 || b == 8; }
+
+// activation dtype x scale dtype pairs built into the kernels
+bool pair_ok(int xdt, int sbdt) {
+  if (xdt == MOE_F32) return sbdt == MOE_F32;
+  return sbdt == MOE_F16 || sbdt == MOE_BF16;
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+moe_status validate_qproj_named(const moe_qproj* p, const char* name) {
+  if (!p) return fail(MOE_ERR_INVALID, "%s: descriptor is NULL", name);
+  if (!p->weight || !p->scales || !p->biases)
+    return fail(MOE_ERR_INVALID, "%s: weight/scales/biases must be non-NULL", name);
+  if (!bits_ok(p->bits))
+    return fail(MOE_ERR_INVALID, "%s: bits=%d unsupported — must be 2 / 3 / 4 / 5 / 6 / 8", name,
+                p->bits);
+  if (p->group_size <= 0) return fail(MOE_ERR_INVALID, "%s: group_size must be positive", name);
+  if (p->n <= 0 || p->k <= 0 || p->n_experts <= 0)
+    return fail(MOE_ERR_INVALID, "%s: n=%d k=%d n_experts=%d must be positive", name, p->n, p->k,
+                p->n_experts);
+  if (p->k % p->group_size)
+    return fail(MOE_ERR_INVALID, "%s: k=%d must be a multiple of group_size=%d", name, p->k,
+                p->group_size);
+  if (((long)p->k * p->bits) % 32)
+    return fail(MOE_ERR_INVALID, "%s: k*bits must be a multiple of 32 (u32 bit-stream alignment)",
+                name);
+  if (!dt_ok(p->sb_dtype)) return fail(MOE_ERR_INVALID, "%s: bad scale dtype %d", name, p->sb_dtype);
+  // reference-valid shapes this build does not implement
+  if (p->group_size != 32 && p->group_size != 64 && p->group_size != 128)
+    return fail(MOE_ERR_UNSUPPORTED, "%s: group_size=%d not built (32, 64, 128 are)", name,
+                p->group_size);
+  if (p->k % 32) return fail(MOE_ERR_UNSUPPORTED, "%s: k=%d must be a multiple of 32", name, p->k);
+  if ((uintptr_t)p->weight % 16)
+    return fail(MOE_ERR_INVALID, "%s: weight pointer must be 16-byte aligned", name);
+  if ((uintptr_t)p->scales % dt_size(p->sb_dtype) || (uintptr_t)p->biases % dt_size(p->sb_dtype))
+    return fail(MOE_ERR_INVALID, "%s: scales/biases pointers misaligned", name);
+  return MOE_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// diagnostics + validation
+// ---------------------------------------------------------------------------
+extern "C" const char* moe_last_error_string(void) { return g_err.c_str(); }
+extern "C" const char* moe_version(void) { return "moehip 0.1 gfx950"; }
+
+extern "C" moe_status moe_validate_qproj(const moe_qproj* p) {
+  MOE_TRY(validate_qproj_named(p, "qproj"));
+  return ok();
+}
+
+extern "C" moe_status moe_derive_bits(int64_t packed_cols, int64_t scale_cols, int32_t group_size,
+                                      int32_t* bits_out) {
+  const int64_t in_features = scale_cols * (int64_t)group_size;
+  if (in_features <= 0)
+    return fail(MOE_ERR_INVALID, "deriveAffineQuantBits: non-positive in-features");
+  if ((32 * packed_cols) % in_features)
+    return fail(MOE_ERR_INVALID,
+                "deriveAffineQuantBits: %lld packed columns are inconsistent with %lld in-features",
+                (long long)packed_cols, (long long)in_features);
+  if (bits_out) *bits_out = (int32_t)((32 * packed_cols) / in_features);
+  return ok();
+}
+
+namespace {
+
+constexpr int kMaxExperts = 512;
+
+moe_status validate_layer_impl(const moe_layer_desc* d) {
+  if (!d) return fail(MOE_ERR_INVALID, "MoELayer: descriptor is NULL");
+  if (d->n_experts <= 0) return fail(MOE_ERR_INVALID, "MoERouter: nExperts must be positive");
+  if (d->top_k <= 0 || d->top_k > d->n_experts)
+    return fail(MOE_ERR_INVALID, "MoERouter: topK (%d) must be in 1...nExperts (%d)", d->top_k,
+                d->n_experts);
+  if (d->hidden <= 0 || d->intermediate <= 0)
+    return fail(MOE_ERR_INVALID, "MoELayer: hidden and intermediate must be positive");
+  if (!dt_ok(d->act_dtype) || !dt_ok(d->router_dtype))
+    return fail(MOE_ERR_INVALID, "MoELayer: bad dtype");
+  if (!d->router_weight) return fail(MOE_ERR_INVALID, "MoELayer: router weight is NULL");
+  if (d->gating != MOE_SOFTMAX_THEN_TOPK && d->gating != MOE_TOPK_THEN_SOFTMAX)
+    return fail(MOE_ERR_INVALID, "MoERouter: bad gating mode %d", d->gating);
+  if (d->activation != MOE_ACT_SWIGLU && d->activation != MOE_ACT_GPTOSS)
+    return fail(MOE_ERR_INVALID, "MoELayer: bad activation %d", d->activation);
+  MOE_TRY(validate_qproj_named(&d->gate, "gate_proj"));
+  MOE_TRY(validate_qproj_named(&d->up, "up_proj"));
+  MOE_TRY(validate_qproj_named(&d->down, "down_proj"));
+  const moe_qproj* g = &d->gate;
+  const moe_qproj* u = &d->up;
+  const moe_qproj* dn = &d->down;
+  if (g->n_experts != d->n_experts || u->n_experts != d->n_experts || dn->n_experts != d->n_experts)
+    return fail(MOE_ERR_INVALID, "MoELayer: gate/up/down expert counts must equal nExperts (%d)",
+                d->n_experts);
+  if (g->n != d->intermediate || u->n != d->intermediate || g->k != d->hidden || u->k != d->hidden)
+    return fail(MOE_ERR_INVALID, "MoELayer: gate/up must be [intermediate=%d, hidden=%d]",
+                d->intermediate, d->hidden);
+  if (dn->n != d->hidden || dn->k != d->intermediate)
+    return fail(MOE_ERR_INVALID, "MoELayer: down must be [hidden=%d, intermediate=%d]", d->hidden,
+                d->intermediate);
+  if (g->bits != u->bits || g->group_size != u->group_size || g->sb_dtype != u->sb_dtype)
+    return fail(MOE_ERR_UNSUPPORTED, "MoELayer: gate and up must share bits/group size/scale dtype");
+  if (!pair_ok(d->act_dtype, g->sb_dtype) || !pair_ok(d->act_dtype, dn->sb_dtype))
+    return fail(MOE_ERR_UNSUPPORTED,
+                "MoELayer: activation dtype %d with scale dtype %d/%d is not built", d->act_dtype,
+                g->sb_dtype, dn->sb_dtype);
+  if (d->n_experts > kMaxExperts)
+    return fail(MOE_ERR_UNSUPPORTED, "MoELayer: nExperts=%d above %d", d->n_experts, kMaxExperts);
+  if (d->has_shared) {
+    MOE_TRY(validate_qproj_named(&d->shared_gate, "shared_expert.gate_proj"));
+    MOE_TRY(validate_qproj_named(&d->shared_up, "shared_expert.up_proj"));
+    MOE_TRY(validate_qproj_named(&d->shared_down, "shared_expert.down_proj"));
+    const moe_qproj* sg = &d->shared_gate;
+    const moe_qproj* su = &d->shared_up;
+    const moe_qproj* sd = &d->shared_down;
+    if (sg->n_experts != 1 || su->n_experts != 1 || sd->n_experts != 1)
+      return fail(MOE_ERR_INVALID, "MoELayer: shared expert projections hold exactly one expert");
+    if (sg->k != d->hidden || su->k != d->hidden || su->n != sg->n || sd->k != sg->n ||
+        sd->n != d->hidden)
+      return fail(MOE_ERR_INVALID, "MoELayer: shared expert shapes do not chain hidden->I->hidden");
+    if (sg->bits != su->bits || sg->group_size != su->group_size || sg->sb_dtype != su->sb_dtype)
+      return fail(MOE_ERR_UNSUPPORTED, "MoELayer: shared gate/up must share bits/group/dtype");
+    if (!pair_ok(d->act_dtype, sg->sb_dtype) || !pair_ok(d->act_dtype, sd->sb_dtype))
+      return fail(MOE_ERR_UNSUPPORTED, "MoELayer: shared expert scale dtype not built");
+  }
+  return MOE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// launch geometry
+// ---------------------------------------------------------------------------
+
+// log2 of the lanes per output row: the best lane utilisation of the K/32
+// units with at most umax units per lane; ties go to fewer lanes (more rows
+// in flight per wave, fewer shuffle steps).
+int pick_lg(int CU, int umax) {
+  int best = 6;
+  double best_eff = -1.0;
+  for (int lg = 0; lg <= 6; lg++) {
+    const int L = 1 << lg;
+    const int upl = (CU + L - 1) / L;
+    if (upl > umax) continue;
+    const double eff = (double)CU / (double)(L * upl);
+    if (eff > best_eff + 1e-9) {
+      best_eff = eff;
+      best = lg;
+    }
+  }
+  return best;
+}
+
+constexpr int kTargetBlocks = 1024;
+
+struct GemvGeom {
+  int lg, row_blocks, rows_per_block, grid, tokmax, tok_chunk;
+};
+
+GemvGeom gemv_geom(int N, int K, int slots, bool single, int M, int xdt) {
+  GemvGeom g{};
+  const int CU = K / 32;
+  g.tokmax = single ? 1 : 8;
+  g.lg = pick_lg(CU, single ? 4 : 8);
+  const int SG = 64 >> g.lg;
+  g.tok_chunk = 1;
+  if (!single) {
+    const size_t per_tok = gemv_smem_bytes(xdt, K, 1);
+    int cap = (int)std::min<size_t>(8, 65536 / per_tok);
+    g.tok_chunk = std::max(1, std::min(cap, M));
+  }
+  const int rows_per_iter = 4 * SG;
+  const int max_rb = std::max(1, (N + rows_per_iter - 1) / rows_per_iter);
+  int rb = std::max(1, (kTargetBlocks + slots - 1) / slots);
+  rb = std::min(rb, max_rb);
+  g.rows_per_block = (N + rb - 1) / rb;
+  g.row_blocks = (N + g.rows_per_block - 1) / g.rows_per_block;
+  g.grid = slots * g.row_blocks;
+  return g;
+}
+
+// Down+combine lanes: positions per sub-group <= 2, units per lane <= 4.
+int pick_lg_combine(int CU, int k) {
+  int best = -1;
+  double best_eff = -1.0;
+  for (int lg = 0; lg <= 6; lg++) {
+    const int L = 1 << lg, SG = 64 >> lg;
+    const int upl = (CU + L - 1) / L;
+    const int pr = (k + SG - 1) / SG;
+    if (upl > 4 || pr > 2) continue;
+    const double eff = (double)CU / (double)(L * upl) * (double)k / (double)(SG * pr);
+    if (eff > best_eff + 1e-9) {
+      best_eff = eff;
+      best = lg;
+    }
+  }
+  return best;
+}
+
+// ---------------------------------------------------------------------------
+// workspace
+// ---------------------------------------------------------------------------
+
+struct Workspace {
+  size_t logits, idx, w, counts, offsets, used, perm, inv, act, Y, plan_scratch;
+  size_t s_off, s_used, s_act, s_out, s_logit;
+  size_t total;
+};
+
+Workspace layout(const moe_layer_desc* d, int T) {
+  Workspace w{};
+  const size_t A = 256, ds = dt_size(d->act_dtype);
+  const size_t E = (size_t)d->n_experts, k = (size_t)d->top_k, M = (size_t)T * k;
+  const size_t H = (size_t)d->hidden, I = (size_t)d->intermediate;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = o;
+    o = align_up(o + std::max<size_t>(bytes, 1), A);
+    return at;
+  };
+  w.logits = take((size_t)T * E * ds);
+  w.idx = take(M * 4);
+  w.w = take(M * 4);
+  w.counts = take(E * 4);
+  w.offsets = take((E + 1) * 4);
+  w.used = take((E + 1) * 4);
+  w.perm = take(M * 4);
+  w.inv = take(M * 4);
+  w.act = take(M * I * ds);
+  w.Y = take(M * H * ds);
+  w.plan_scratch = take(dispatch_scratch_bytes(T, (int)k, (int)E));
+  if (d->has_shared) {
+    const size_t SI = (size_t)d->shared_gate.n;
+    w.s_off = take(2 * 4);
+    w.s_used = take(2 * 4);
+    w.s_act = take((size_t)T * SI * ds);
+    w.s_out = take((size_t)T * H * ds);
+    w.s_logit = take((size_t)T * ds);
+  }
+  w.total = o;
+  return w;
+}
+
+template <typename P> P* at(void* base, size_t off) {
+  return reinterpret_cast<P*>(reinterpret_cast<char*>(base) + off);
+}
+
+GemvProj to_proj(const moe_qproj& q) { return GemvProj{q.weight, q.scales, q.biases, q.out_bias}; }
+
+// out[p] = W[e(p)] . a[row(p)] over a plan; optionally a gate/up pair with
+// the activation fused.
+moe_status run_gemv(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
+                    const uint32_t* perm, int topk, const uint32_t* offsets, const uint32_t* used,
+                    int slots, int M, bool single, void* out, int act, float alpha, float limit,
+                    hipStream_t st) {
+  GemvGeom g = gemv_geom(p0.n, p0.k, slots, single, M, xdt);
+  GemvArgs a{};
+  a.p0 = to_proj(p0);
+  if (p1) a.p1 = to_proj(*p1);
+  a.x = x;
+  a.perm = perm;
+  a.topk = topk;
+  a.offsets = offsets;
+  a.used = used;
+  a.out = out;
+  a.N = p0.n;
+  a.K = p0.k;
+  a.gs = p0.group_size;
+  a.row_blocks = g.row_blocks;
+  a.rows_per_block = g.rows_per_block;
+  a.lg = g.lg;
+  a.tok_chunk = g.tok_chunk;
+  a.act = act;
+  a.alpha = alpha;
+  a.limit = limit;
+  MOE_HIP(launch_gemv(p0.bits, xdt, p0.sb_dtype, p1 != nullptr, g.tokmax, a, g.grid, st),
+          "grouped GEMV launch");
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" moe_status moe_validate_layer(const moe_layer_desc* d) {
+  MOE_TRY(validate_layer_impl(d));
+  return ok();
+}
+
+// ---------------------------------------------------------------------------
+// kernels
+// ---------------------------------------------------------------------------
+
+extern "C" moe_status moe_router_logits(const void* x, int32_t x_dtype, int32_t T, int32_t hidden,
+                                        const void* weight, int32_t w_dtype, const void* bias,
+                                        int32_t n_experts, void* logits, hipStream_t stream) {
+  if (!x || !weight || !logits) return fail(MOE_ERR_INVALID, "router_logits: NULL pointer");
+  if (T <= 0 || hidden <= 0 || n_experts <= 0)
+    return fail(MOE_ERR_INVALID, "router_logits: T, hidden and n_experts must be positive");
+  if (!dt_ok(x_dtype) || !dt_ok(w_dtype)) return fail(MOE_ERR_INVALID, "router_logits: bad dtype");
+  if (hidden % 8) return fail(MOE_ERR_UNSUPPORTED, "router_logits: hidden must be a multiple of 8");
+  MOE_HIP(launch_router_logits(x, x_dtype, T, hidden, weight, w_dtype, bias, n_experts, logits,
+                               stream),
+          "router logits launch");
+  return ok();
+}
+
+extern "C" moe_status moe_router_topk(const void* logits, int32_t dtype, int32_t T,
+                                      int32_t n_experts, int32_t k, int32_t gating,
+                                      int32_t norm_topk_prob, const float* expert_bias,
+                                      uint32_t* topk_idx, float* topk_weight, hipStream_t stream) {
+  if (!logits || !topk_idx || !topk_weight) return fail(MOE_ERR_INVALID, "router_topk: NULL pointer");
+  if (T <= 0) return fail(MOE_ERR_INVALID, "Ops.moeRouterTopKMany: t must be positive");
+  if (n_experts <= 0) return fail(MOE_ERR_INVALID, "MoERouter: nExperts must be positive");
+  if (k <= 0 || k > n_experts)
+    return fail(MOE_ERR_INVALID, "MoERouter: topK (%d) must be in 1...nExperts (%d)", k, n_experts);
+  if (gating != MOE_SOFTMAX_THEN_TOPK && gating != MOE_TOPK_THEN_SOFTMAX)
+    return fail(MOE_ERR_INVALID, "router_topk: bad gating mode");
+  if (!dt_ok(dtype)) return fail(MOE_ERR_INVALID, "router_topk: bad dtype");
+  if (n_experts > kMaxExperts)
+    return fail(MOE_ERR_UNSUPPORTED, "router_topk: nExperts=%d above %d", n_experts, kMaxExperts);
+  MOE_HIP(launch_router_topk(logits, dtype, T, n_experts, k, gating, norm_topk_prob, expert_bias,
+                             topk_idx, topk_weight, stream),
+          "router top-k launch");
+  return ok();
+}
+
+extern "C" size_t moe_dispatch_workspace_bytes(int32_t T, int32_t k, int32_t n_experts) {
+  if (T <= 0 || k <= 0 || n_experts <= 0) return 0;
+  return align_up((size_t)(n_experts + 1) * 4, 256) + dispatch_scratch_bytes(T, k, n_experts);
+}
+
+extern "C" moe_status moe_dispatch_plan(const uint32_t* topk_idx, int32_t T, int32_t k,
+                                        int32_t n_experts, uint32_t* counts, uint32_t* offsets,
+                                        uint32_t* perm, uint32_t* inv_perm, void* workspace,
+                                        size_t workspace_bytes, hipStream_t stream) {
+  if (!topk_idx || !counts || !offsets || !perm || !inv_perm)
+    return fail(MOE_ERR_INVALID, "dispatch_plan: NULL pointer");
+  if (T <= 0 || k <= 0 || n_experts <= 0)
+    return fail(MOE_ERR_INVALID, "dispatch_plan: T, k and n_experts must be positive");
+  if ((long)T * k > 0x7fffffffL) return fail(MOE_ERR_INVALID, "dispatch_plan: T*k too large");
+  if (n_experts > 1024) return fail(MOE_ERR_UNSUPPORTED, "dispatch_plan: n_experts above 1024");
+  const size_t need = moe_dispatch_workspace_bytes(T, k, n_experts);
+  if (!workspace || workspace_bytes < need)
+    return fail(MOE_ERR_WORKSPACE, "dispatch_plan: workspace of %zu bytes needed", need);
+  uint32_t* used = reinterpret_cast<uint32_t*>(workspace);
+  void* scratch = reinterpret_cast<char*>(workspace) + align_up((size_t)(n_experts + 1) * 4, 256);
+  MOE_HIP(launch_dispatch_plan(topk_idx, T, k, n_experts, counts, offsets, perm, inv_perm, used,
+                               scratch, workspace_bytes - align_up((size_t)(n_experts + 1) * 4, 256),
+                               stream),
+          "dispatch plan launch");
+  return ok();
+}
+
+extern "C" moe_status moe_dequantize_affine(const uint32_t* weight, const void* scales,
+                                            const void* biases, int32_t sb_dtype, int32_t bits,
+                                            int32_t group_size, int64_t numel, void* out,
+                                            int32_t out_dtype, hipStream_t stream) {
+  if (!weight || !scales || !biases || !out) return fail(MOE_ERR_INVALID, "dequantize: NULL pointer");
+  if (numel <= 0) return fail(MOE_ERR_INVALID, "numel must be positive (got %lld)", (long long)numel);
+  if (group_size <= 0)
+    return fail(MOE_ERR_INVALID, "groupSize must be positive (got %d)", group_size);
+  if (numel % group_size)
+    return fail(MOE_ERR_INVALID, "numel=%lld must be a multiple of groupSize=%d", (long long)numel,
+                group_size);
+  if (bits == 2 || bits == 4 || bits == 8) {
+    if (group_size % (32 / bits))
+      return fail(MOE_ERR_INVALID, "groupSize=%d must be a multiple of pack_factor=%d for bits=%d",
+                  group_size, 32 / bits, bits);
+  } else if (bits == 3 || bits == 5 || bits == 6) {
+    if ((group_size * bits) % 32)
+      return fail(MOE_ERR_INVALID,
+                  "groupSize=%d x bits=%d must be a multiple of 32 (u32 bit-stream alignment)",
+                  group_size, bits);
+  } else {
+    return fail(MOE_ERR_INVALID, "bits=%d unsupported — must be 2 / 3 / 4 / 5 / 6 / 8", bits);
+  }
+  if ((numel * bits) % 32)
+    return fail(MOE_ERR_INVALID, "numel=%lld x bits=%d must be a multiple of 32", (long long)numel,
+                bits);
+  if (!dt_ok(sb_dtype) || !dt_ok(out_dtype)) return fail(MOE_ERR_INVALID, "dequantize: bad dtype");
+  MOE_HIP(launch_dequantize(weight, scales, biases, sb_dtype, bits, group_size, numel, out,
+                            out_dtype, stream),
+          "dequantize launch");
+  return ok();
+}
+
+extern "C" size_t moe_expert_matmul_workspace_bytes(int32_t n_experts, int32_t M) {
+  if (n_experts <= 0 || M <= 0) return 0;
+  return align_up((size_t)(n_experts + 1) * 4, 256);
+}
+
+extern "C" moe_status moe_expert_matmul(const moe_qproj* p, const void* a, int32_t a_dtype,
+                                        const uint32_t* perm, int32_t top_k, int32_t M,
+                                        const uint32_t* offsets, void* out, void* workspace,
+                                        size_t workspace_bytes, hipStream_t stream) {
+  MOE_TRY(validate_qproj_named(p, "expert_matmul"));
+  if (!a || !offsets || !out) return fail(MOE_ERR_INVALID, "expert_matmul: NULL pointer");
+  if (M <= 0) return fail(MOE_ERR_INVALID, "expert_matmul: M must be positive");
+  if (perm && top_k <= 0) return fail(MOE_ERR_INVALID, "expert_matmul: top_k must be positive");
+  if (!dt_ok(a_dtype) || !pair_ok(a_dtype, p->sb_dtype))
+    return fail(MOE_ERR_UNSUPPORTED, "expert_matmul: activation/scale dtype pair not built");
+  if (p->n_experts > 1024) return fail(MOE_ERR_UNSUPPORTED, "expert_matmul: n_experts above 1024");
+  const size_t need = moe_expert_matmul_workspace_bytes(p->n_experts, M);
+  if (!workspace || workspace_bytes < need)
+    return fail(MOE_ERR_WORKSPACE, "expert_matmul: workspace of %zu bytes needed", need);
+  uint32_t* used = reinterpret_cast<uint32_t*>(workspace);
+  MOE_HIP(launch_used_from_offsets(offsets, p->n_experts, used, stream), "used list launch");
+  const int slots = std::min(p->n_experts, M);
+  MOE_TRY(run_gemv(*p, nullptr, a, a_dtype, perm, top_k, offsets, used, slots, M, false, out, 0,
+                   0.f, 0.f, stream));
+  return ok();
+}
+
+extern "C" moe_status moe_activation_apply(const void* gate, const void* up, void* out, int64_t n,
+                                           int32_t dtype, int32_t activation, float alpha,
+                                           float limit, hipStream_t stream) {
+  if (!gate || !up || !out) return fail(MOE_ERR_INVALID, "activation: NULL pointer");
+  if (n <= 0) return fail(MOE_ERR_INVALID, "activation: n must be positive");
+  if (!dt_ok(dtype)) return fail(MOE_ERR_INVALID, "activation: bad dtype");
+  if (activation != MOE_ACT_SWIGLU && activation != MOE_ACT_GPTOSS)
+    return fail(MOE_ERR_INVALID, "activation: bad kind");
+  MOE_HIP(launch_activation(gate, up, out, n, dtype, activation, alpha, limit, stream),
+          "activation launch");
+  return ok();
+}
+
+extern "C" moe_status moe_unpermute(const void* Y, const uint32_t* inv_perm,
+                                    const float* topk_weight, int32_t T, int32_t hidden, int32_t k,
+                                    void* out, int32_t dtype, hipStream_t stream) {
+  if (!Y || !inv_perm || !topk_weight || !out) return fail(MOE_ERR_INVALID, "unpermute: NULL pointer");
+  if (T <= 0 || hidden <= 0 || k <= 0)
+    return fail(MOE_ERR_INVALID, "unpermute: T, hidden and k must be positive");
+  if (hidden % 8) return fail(MOE_ERR_UNSUPPORTED, "unpermute: hidden must be a multiple of 8");
+  if (!dt_ok(dtype)) return fail(MOE_ERR_INVALID, "unpermute: bad dtype");
+  MOE_HIP(launch_unpermute(Y, inv_perm, topk_weight, T, hidden, k, out, dtype, nullptr, nullptr, 0,
+                           stream),
+          "unpermute launch");
+  return ok();
+}
+
+// ---------------------------------------------------------------------------
+// whole layer
+// ---------------------------------------------------------------------------
+
+extern "C" size_t moe_layer_workspace_bytes(const moe_layer_desc* d, int32_t max_tokens) {
+  if (!d || max_tokens <= 0 || validate_layer_impl(d) != MOE_OK) return 0;
+  return layout(d, max_tokens).total;
+}
+
+namespace {
+
+moe_status copy_trace(const moe_layer_desc* d, int T, void* ws, const Workspace& w,
+                      const moe_layer_trace* tr, hipStream_t st) {
+  if (!tr) return MOE_OK;
+  const size_t M = (size_t)T * d->top_k, E = (size_t)d->n_experts;
+  auto cp = [&](void* dst, size_t off, size_t bytes) -> moe_status {
+    if (!dst) return MOE_OK;
+    return hip_check(hipMemcpyAsync(dst, at<char>(ws, off), bytes, hipMemcpyDeviceToDevice, st),
+                     "trace copy");
+  };
+  MOE_TRY(cp(tr->logits, w.logits, (size_t)T * E * dt_size(d->act_dtype)));
+  MOE_TRY(cp(tr->topk_idx, w.idx, M * 4));
+  MOE_TRY(cp(tr->topk_weight, w.w, M * 4));
+  MOE_TRY(cp(tr->perm, w.perm, M * 4));
+  MOE_TRY(cp(tr->offsets, w.offsets, (E + 1) * 4));
+  return MOE_OK;
+}
+
+moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y, void* ws,
+                         size_t ws_bytes, const moe_layer_trace* tr, hipStream_t st) {
+  MOE_TRY(validate_layer_impl(d));
+  if (!x || !y) return fail(MOE_ERR_INVALID, "MoELayer: input/output is NULL");
+  if (T <= 0) return fail(MOE_ERR_INVALID, "MoELayer.decodeMany: T must be positive");
+  const Workspace w = layout(d, T);
+  if (!ws || ws_bytes < w.total)
+    return fail(MOE_ERR_WORKSPACE, "MoELayer: workspace of %zu bytes needed for T=%d", w.total, T);
+  const int E = d->n_experts, k = d->top_k, H = d->hidden, I = d->intermediate;
+  const int M = T * k, xdt = d->act_dtype;
+
+  // 1. router projection + selection (MoELayer.swift:540-573 / 689-750)
+  MOE_HIP(launch_router_logits(x, xdt, T, H, d->router_weight, d->router_dtype, d->router_bias, E,
+                               at<void>(ws, w.logits), st),
+          "router logits launch");
+  MOE_HIP(launch_router_topk(at<void>(ws, w.logits), xdt, T, E, k, d->gating, d->norm_topk_prob,
+                             d->expert_bias, at<uint32_t>(ws, w.idx), at<float>(ws, w.w), st),
+          "router top-k launch");
+  // 2. dispatch plan (MoELayer.swift:752-792)
+  MOE_HIP(launch_dispatch_plan(at<uint32_t>(ws, w.idx), T, k, E, at<uint32_t>(ws, w.counts),
+                               at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.perm),
+                               at<uint32_t>(ws, w.inv), at<uint32_t>(ws, w.used),
+                               at<void>(ws, w.plan_scratch), dispatch_scratch_bytes(T, k, E), st),
+          "dispatch plan launch");
+  const bool single = (T == 1);
+  const int slots = std::min(E, M);
+  auto mark = [&](int i) -> moe_status {
+    if (!tr || !tr->events[i]) return MOE_OK;
+    return hip_check(hipEventRecord(reinterpret_cast<hipEvent_t>(tr->events[i]), st),
+                     "trace event");
+  };
+  // 3. gate/up + activation (MoELayer.swift:883-893)
+  MOE_TRY(mark(0));
+  MOE_TRY(run_gemv(d->gate, &d->up, x, xdt, at<uint32_t>(ws, w.perm), k,
+                   at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, single,
+                   at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st));
+  MOE_TRY(mark(1));
+
+  // shared expert first so the combine can fold it in (Qwen3xText.swift:1047-1104)
+  int smode = 0;
+  if (d->has_shared) {
+    smode = d->shared_gate_weight ? 2 : 1;
+    MOE_HIP(launch_identity_plan(at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), T, st),
+            "identity plan launch");
+    MOE_TRY(run_gemv(d->shared_gate, &d->shared_up, x, xdt, nullptr, 1, at<uint32_t>(ws, w.s_off),
+                     at<uint32_t>(ws, w.s_used), 1, T, single, at<void>(ws, w.s_act),
+                     MOE_ACT_SWIGLU, 0.f, 0.f, st));
+    MOE_TRY(run_gemv(d->shared_down, nullptr, at<void>(ws, w.s_act), xdt, nullptr, 1,
+                     at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), 1, T, single,
+                     at<void>(ws, w.s_out), 0, 0.f, 0.f, st));
+    if (d->shared_gate_weight)
+      MOE_HIP(launch_router_logits(x, xdt, T, H, d->shared_gate_weight, d->router_dtype, nullptr, 1,
+                                   at<void>(ws, w.s_logit), st),
+              "shared gate launch");
+  }
+
+  // 4. down projection + weighted combine (MoELayer.swift:899-939)
+  const int lgc = pick_lg_combine(I / 32, k);
+  if (single && lgc >= 0) {
+    DownCombineArgs a{};
+    a.p = to_proj(d->down);
+    a.act = at<void>(ws, w.act);
+    a.perm = at<uint32_t>(ws, w.perm);
+    a.idx = at<uint32_t>(ws, w.idx);
+    a.w = at<float>(ws, w.w);
+    a.out = y;
+    a.k = k;
+    a.N = H;
+    a.K = I;
+    a.gs = d->down.group_size;
+    a.lg = lgc;
+    const int rpb = std::max(4, (H + 511) / 512);
+    a.rows_per_block = rpb;
+    const int grid = (H + rpb - 1) / rpb;
+    MOE_HIP(launch_down_combine(d->down.bits, xdt, d->down.sb_dtype, a, grid, st),
+            "down+combine launch");
+    MOE_TRY(mark(2));
+    if (smode)
+      MOE_HIP(launch_add_shared(y, at<void>(ws, w.s_out), at<void>(ws, w.s_logit), smode, T, H, xdt,
+                                st),
+              "shared add launch");
+  } else {
+    MOE_TRY(run_gemv(d->down, nullptr, at<void>(ws, w.act), xdt, nullptr, 1,
+                     at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, single,
+                     at<void>(ws, w.Y), 0, 0.f, 0.f, st));
+    MOE_HIP(launch_unpermute(at<void>(ws, w.Y), at<uint32_t>(ws, w.inv), at<float>(ws, w.w), T, H,
+                             k, y, xdt, smode ? at<void>(ws, w.s_out) : nullptr,
+                             smode ? at<void>(ws, w.s_logit) : nullptr, smode, st),
+            "unpermute launch");
+    MOE_TRY(mark(2));
+  }
+  MOE_TRY(copy_trace(d, T, ws, w, tr, st));
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" moe_status moe_layer_forward(const moe_layer_desc* d, const void* x, int32_t T, void* y,
+                                        void* workspace, size_t workspace_bytes,
+                                        const moe_layer_trace* trace, hipStream_t stream) {
+  MOE_TRY(layer_forward(d, x, T, y, workspace, workspace_bytes, trace, stream));
+  return ok();
+}
+
+// ---------------------------------------------------------------------------
+// MoELayer handle
+// ---------------------------------------------------------------------------
+
+// Host-side mirror of the reference's MoELayer instance: it holds the layer
+// description and lazily sized scratch (MoELayer.swift:408-429). Calls are
+// stream-ordered and the instance is not reentrant (MoELayer.swift:311-318).
+struct moe_layer {
+  moe_layer_desc desc;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  int ws_tokens = 0;
+
+  moe_status reserve(int T) {
+    if (T <= ws_tokens) return MOE_OK;
+    const size_t need = moe_layer_workspace_bytes(&desc, T);
+    if (ws) {
+      // A previous call may still be reading the old scratch on its stream.
+      MOE_HIP(hipDeviceSynchronize(), "MoELayer scratch resize");
+      MOE_HIP(hipFree(ws), "MoELayer scratch free");
+      ws = nullptr;
+    }
+    MOE_HIP(hipMalloc(&ws, need), "MoELayer scratch allocation");
+    ws_bytes = need;
+    ws_tokens = T;
+    return MOE_OK;
+  }
+
+  moe_status decode_many(const void* h, int T, void* out, hipStream_t st) {
+    if (T <= 0) return fail(MOE_ERR_INVALID, "MoELayer.decodeMany: T must be positive");
+    MOE_TRY(reserve(T));
+    return layer_forward(&desc, h, T, out, ws, ws_bytes, nullptr, st);
+  }
+};
+
+extern "C" moe_status moe_layer_create(const moe_layer_desc* d, moe_layer_t* out) {
+  if (!out) return fail(MOE_ERR_INVALID, "moe_layer_create: out is NULL");
+  *out = nullptr;
+  MOE_TRY(validate_layer_impl(d));
+  moe_layer* L = new (std::nothrow) moe_layer();
+  if (!L) return fail(MOE_ERR_INVALID, "moe_layer_create: out of host memory");
+  L->desc = *d;
+  *out = L;
+  return ok();
+}
+
+extern "C" void moe_layer_destroy(moe_layer_t layer) {
+  if (!layer) return;
+  if (layer->ws) {
+    (void)hipDeviceSynchronize();
+    (void)hipFree(layer->ws);
+  }
+  delete layer;
+}
+
+extern "C" moe_status moe_layer_decode(moe_layer_t layer, const void* h, void* out,
+                                       hipStream_t stream) {
+  if (!layer) return fail(MOE_ERR_INVALID, "MoELayer.decode: layer is NULL");
+  MOE_TRY(layer->decode_many(h, 1, out, stream));
+  return ok();
+}
+
+extern "C" moe_status moe_layer_decode_many(moe_layer_t layer, const void* h, int32_t T, void* out,
+                                            hipStream_t stream) {
+  if (!layer) return fail(MOE_ERR_INVALID, "MoELayer.decodeMany: layer is NULL");
+  MOE_TRY(layer->decode_many(h, T, out, stream));
+  return ok();
+}

@@ -1,0 +1,198 @@
+// combine.hip — weighted combine back to token order, shared-expert add,
+// elementwise activation and standalone affine dequantisation for gfx950.
+//
+//   unpermute      Ops.moeUnpermute (Sources/FFAI/Ops/Ops.swift:5030-5110) with
+//                  the combine weights rounded to the activation dtype first
+//                  (Sources/FFAI/Models/MoELayer.swift:921-935)
+//   shared add     MoELayer.swift:620-624 (unconditional add) and
+//                  Ops.sigmoidScalarFMA (Ops.swift:6256-6317; Qwen3xText.swift:
+//                  1054-1103): y = round(routed + sigmoid(g) * shared)
+//   activation     Ops.swiglu (Ops.swift:6411-6460) / GPT-OSS clamped swish
+//   dequantize     QuantizedOps.dequantizeAffine (QuantizedOps.swift:62-221)
+#include "moe_common.hpp"
+#include "moe_internal.hpp"
+
+namespace moe {
+
+template <typename T> struct Vec8 {
+  static __device__ __forceinline__ void load(const T* p, float (&v)[8]) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      v[2 * j] = to_f<T>(__builtin_bit_cast(T, (uint16_t)(w[j] & 0xFFFFu)));
+      v[2 * j + 1] = to_f<T>(__builtin_bit_cast(T, (uint16_t)(w[j] >> 16)));
+    }
+  }
+  static __device__ __forceinline__ void store(T* p, const float (&v)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint16_t lo = __builtin_bit_cast(uint16_t, from_f<T>(v[2 * j]));
+      const uint16_t hi = __builtin_bit_cast(uint16_t, from_f<T>(v[2 * j + 1]));
+      w[j] = (uint32_t)lo | ((uint32_t)hi << 16);
+    }
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+template <> struct Vec8<float> {
+  static __device__ __forceinline__ void load(const float* p, float (&v)[8]) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  static __device__ __forceinline__ void store(float* p, const float (&v)[8]) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+};
+
+// shared_mode: 0 none, 1 unconditional add, 2 sigmoid-gated add.
+template <typename XT>
+__device__ __forceinline__ float shared_gate(int mode, const XT* logit, int t) {
+  if (mode == 2) return 1.0f / (1.0f + __expf(-to_f<XT>(logit[t])));
+  return 1.0f;
+}
+
+// One block per token; threads stride over hidden 8 values at a time.
+template <typename XT>
+__global__ __launch_bounds__(256) void unpermute_kernel(const XT* __restrict__ Y,
+                                                        const uint32_t* __restrict__ inv,
+                                                        const float* __restrict__ w, int T, int H,
+                                                        int k, XT* __restrict__ out,
+                                                        const XT* __restrict__ sout,
+                                                        const XT* __restrict__ slogit, int smode) {
+  const int t = blockIdx.x;
+  const uint32_t M = (uint32_t)T * (uint32_t)k;
+  const float g = smode ? shared_gate<XT>(smode, slogit, t) : 0.f;
+  for (int h = threadIdx.x * 8; h < H; h += blockDim.x * 8) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < k; s++) {
+      const uint32_t p = inv[(size_t)t * k + s];
+      if (p >= M) continue;
+      const float ws = round_to<XT>(w[(size_t)t * k + s]);
+      float y[8];
+      Vec8<XT>::load(Y + (size_t)p * H + h, y);
+#pragma unroll
+      for (int j = 0; j < 8; j++) acc[j] = acc[j] + ws * y[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[j] = round_to<XT>(acc[j]);
+    if (smode) {
+      float sv[8];
+      Vec8<XT>::load(sout + (size_t)t * H + h, sv);
+#pragma unroll
+      for (int j = 0; j < 8; j++) acc[j] = acc[j] + g * sv[j];
+    }
+    Vec8<XT>::store(out + (size_t)t * H + h, acc);
+  }
+}
+
+template <typename XT>
+__global__ __launch_bounds__(256) void add_shared_kernel(XT* __restrict__ y,
+                                                         const XT* __restrict__ sout,
+                                                         const XT* __restrict__ slogit, int smode,
+                                                         int H) {
+  const int t = blockIdx.x;
+  const float g = shared_gate<XT>(smode, slogit, t);
+  for (int h = threadIdx.x * 8; h < H; h += blockDim.x * 8) {
+    float a[8], b[8];
+    Vec8<XT>::load(y + (size_t)t * H + h, a);
+    Vec8<XT>::load(sout + (size_t)t * H + h, b);
+#pragma unroll
+    for (int j = 0; j < 8; j++) a[j] = a[j] + g * b[j];
+    Vec8<XT>::store(y + (size_t)t * H + h, a);
+  }
+}
+
+template <typename XT>
+__global__ __launch_bounds__(256) void activation_kernel(const XT* __restrict__ g,
+                                                         const XT* __restrict__ u,
+                                                         XT* __restrict__ out, int64_t n, int act,
+                                                         float alpha, float limit) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = from_f<XT>(apply_act(to_f<XT>(g[i]), to_f<XT>(u[i]), act, alpha, limit));
+}
+
+template <typename ST, typename OT>
+__global__ __launch_bounds__(256) void dequantize_kernel(const uint32_t* __restrict__ w,
+                                                         const ST* __restrict__ s,
+                                                         const ST* __restrict__ b, int bits,
+                                                         int gs, int64_t numel,
+                                                         OT* __restrict__ out) {
+#pragma clang fp contract(off)
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < numel;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const uint64_t bit = (uint64_t)i * (uint64_t)bits;
+    const uint64_t word = bit >> 5;
+    const uint32_t sh = (uint32_t)(bit & 31u);
+    uint64_t win = w[word];
+    if (sh + (uint32_t)bits > 32u) win |= (uint64_t)w[word + 1] << 32;
+    const float q = (float)((uint32_t)(win >> sh) & ((1u << bits) - 1u));
+    const int64_t g = i / gs;
+    const float sq = to_f<ST>(s[g]) * q;
+    out[i] = from_f<OT>(sq + to_f<ST>(b[g]));
+  }
+}
+
+#define MOE_BY_DT(dt, MACRO)          \
+  if ((dt) == DT_BF16) { MACRO(bf16_t) } \
+  if ((dt) == DT_F16) { MACRO(f16_t) }   \
+  if ((dt) == DT_F32) { MACRO(float) }
+
+hipError_t launch_unpermute(const void* Y, const uint32_t* inv, const float* w, int T, int H,
+                            int k, void* out, int dt, const void* shared_out,
+                            const void* shared_logit, int shared_mode, hipStream_t st) {
+#define MOE_UP(XT)                                                                            \
+  hipLaunchKernelGGL((unpermute_kernel<XT>), dim3(T), dim3(256), 0, st, (const XT*)Y, inv, w, \
+                     T, H, k, (XT*)out, (const XT*)shared_out, (const XT*)shared_logit,       \
+                     shared_mode);                                                            \
+  return hipGetLastError();
+  MOE_BY_DT(dt, MOE_UP)
+#undef MOE_UP
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_add_shared(void* y, const void* shared_out, const void* shared_logit,
+                             int shared_mode, int T, int H, int dt, hipStream_t st) {
+#define MOE_AS(XT)                                                                        \
+  hipLaunchKernelGGL((add_shared_kernel<XT>), dim3(T), dim3(256), 0, st, (XT*)y,          \
+                     (const XT*)shared_out, (const XT*)shared_logit, shared_mode, H);      \
+  return hipGetLastError();
+  MOE_BY_DT(dt, MOE_AS)
+#undef MOE_AS
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_activation(const void* g, const void* u, void* out, int64_t n, int dt, int act,
+                             float alpha, float limit, hipStream_t st) {
+  const int64_t blocks64 = (n + 255) / 256;
+  const int grid = (int)(blocks64 < 65536 ? blocks64 : 65536);
+#define MOE_ACT(XT)                                                                          \
+  hipLaunchKernelGGL((activation_kernel<XT>), dim3(grid), dim3(256), 0, st, (const XT*)g,   \
+                     (const XT*)u, (XT*)out, n, act, alpha, limit);                         \
+  return hipGetLastError();
+  MOE_BY_DT(dt, MOE_ACT)
+#undef MOE_ACT
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_dequantize(const uint32_t* w, const void* s, const void* b, int sbdt, int bits,
+                             int gs, int64_t numel, void* out, int odt, hipStream_t st) {
+  const int64_t blocks64 = (numel + 255) / 256;
+  const int grid = (int)(blocks64 < 65536 ? blocks64 : 65536);
+#define MOE_DQ2(ST, OT)                                                                     \
+  hipLaunchKernelGGL((dequantize_kernel<ST, OT>), dim3(grid), dim3(256), 0, st, w,         \
+                     (const ST*)s, (const ST*)b, bits, gs, numel, (OT*)out);               \
+  return hipGetLastError();
+#define MOE_DQ(ST)                              \
+  if (odt == DT_BF16) { MOE_DQ2(ST, bf16_t) }   \
+  if (odt == DT_F16) { MOE_DQ2(ST, f16_t) }     \
+  if (odt == DT_F32) { MOE_DQ2(ST, float) }
+  MOE_BY_DT(sbdt, MOE_DQ)
+#undef MOE_DQ
+#undef MOE_DQ2
+  return hipErrorInvalidValue;
+}
+
+}  // namespace moe

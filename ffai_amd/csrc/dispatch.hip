@@ -1,0 +1,259 @@
+// dispatch.hip — deterministic token->expert dispatch plan for gfx950.
+//
+// Replaces the host plan of MoELayer.decodeMany (Sources/FFAI/Models/
+// MoELayer.swift:752-792: token-major (expert, token, slot) tuples, a stable
+// sort by expert, inv_perm) and the host CSR offsets of the m1 path
+// (:1035-1058), with no host round trip:
+//   1. histogram of expert ids (LDS atomics: counts are order independent),
+//   2. exclusive scan -> CSR offsets, plus the ascending list of used experts,
+//   3. stable permute: entries are ranked inside each wave with ballots over
+//      the expert-id bits, waves are ordered inside a tile, tiles in order, so
+//      position = offsets[e] + (#earlier entries with expert e). The result is
+//      the stable order (expert asc, token asc, slot asc) bit for bit.
+//
+// Small plans run in one workgroup. Large plans (prefill) split the entries
+// into chunks: a per-chunk histogram pass, a scan pass, and a scatter pass
+// that starts every chunk at its own per-expert base.
+#include "moe_common.hpp"
+#include "moe_internal.hpp"
+
+namespace moe {
+
+constexpr int kPlanThreads = 256;
+constexpr int kPlanMaxE = 1024;
+constexpr int kChunk = 2048;             // entries per chunk in the multi-block plan
+constexpr int kSingleBlockMax = 4096;    // M at or below which one workgroup plans
+
+// Exclusive scan of cnt[0..E) over 256 threads (4 experts per thread).
+// Writes offsets[0..E], counts, the used list, and base[e] = offsets[e].
+__device__ void scan_experts(const uint32_t* cnt, int E, uint32_t* counts, uint32_t* offsets,
+                             uint32_t* used, uint32_t* base) {
+  __shared__ uint32_t wsum[kPlanThreads / 64], wused[kPlanThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t c[4], f[4], tot = 0, ftot = 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int e = tid * 4 + j;
+    c[j] = e < E ? cnt[e] : 0u;
+    f[j] = c[j] > 0 ? 1u : 0u;
+    tot += c[j];
+    ftot += f[j];
+  }
+  // inclusive wave scan of (tot, ftot)
+  uint32_t s = tot, fs = ftot;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = __shfl_up(s, off, 64), fo = __shfl_up(fs, off, 64);
+    if (lane >= off) {
+      s += o;
+      fs += fo;
+    }
+  }
+  if (lane == 63) {
+    wsum[wave] = s;
+    wused[wave] = fs;
+  }
+  __syncthreads();
+  uint32_t wb = 0, fb = 0;
+  for (int w = 0; w < wave; w++) {
+    wb += wsum[w];
+    fb += wused[w];
+  }
+  uint32_t run = wb + s - tot, frun = fb + fs - ftot;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int e = tid * 4 + j;
+    if (e < E) {
+      counts[e] = c[j];
+      offsets[e] = run;
+      base[e] = run;
+      if (f[j]) used[1 + frun] = (uint32_t)e;
+    }
+    run += c[j];
+    frun += f[j];
+  }
+  if (tid == kPlanThreads - 1) {
+    offsets[E] = run;
+    used[0] = frun;
+  }
+  __syncthreads();
+}
+
+// Rank of this lane's entry among earlier lanes of the wave with the same
+// expert, and the number of such lanes in the wave (valid lanes only).
+__device__ __forceinline__ void wave_peers(uint32_t e, bool valid, int nbits, uint32_t* rank,
+                                           uint32_t* count, bool* last) {
+  const int lane = threadIdx.x & 63;
+  uint64_t peers = __ballot(valid);
+  for (int b = 0; b < nbits; b++) {
+    const bool bit = (e >> b) & 1u;
+    const uint64_t bal = __ballot(valid && bit);
+    peers &= bit ? bal : ~bal;
+  }
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  *rank = (uint32_t)__popcll(peers & below);
+  *count = (uint32_t)__popcll(peers);
+  *last = (peers >> lane) == 1ull;
+}
+
+// Ranks the entries [begin, end) in order and scatters them starting from
+// cursor[e]; cursor ends advanced by the number of entries of each expert.
+__device__ void stable_scatter(const uint32_t* __restrict__ idx, int begin, int end, int E,
+                               int nbits, uint32_t* cursor, uint32_t* __restrict__ perm,
+                               uint32_t* __restrict__ inv) {
+  const int tid = threadIdx.x, wave = tid >> 6;
+  for (int base = begin; base < end; base += kPlanThreads) {
+    const int m = base + tid;
+    uint32_t e = m < end ? idx[m] : 0xffffffffu;
+    const bool valid = m < end && e < (uint32_t)E;
+    uint32_t rank, count;
+    bool last;
+    wave_peers(e, valid, nbits, &rank, &count, &last);
+    for (int w = 0; w < kPlanThreads / 64; w++) {
+      if (wave == w && valid) {
+        const uint32_t pos = cursor[e] + rank;
+        perm[pos] = (uint32_t)m;
+        inv[m] = pos;
+        if (last) cursor[e] += count;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__device__ __forceinline__ int id_bits(int E) {
+  int nb = 0;
+  while ((1 << nb) < E) nb++;
+  return nb;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void plan_single_kernel(
+    const uint32_t* __restrict__ idx, int M, int E, uint32_t* counts, uint32_t* offsets,
+    uint32_t* perm, uint32_t* inv, uint32_t* used) {
+  __shared__ uint32_t cnt[kPlanMaxE], cursor[kPlanMaxE];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += kPlanThreads) cnt[e] = 0;
+  __syncthreads();
+  for (int m = tid; m < M; m += kPlanThreads) {
+    const uint32_t e = idx[m];
+    if (e < (uint32_t)E) atomicAdd(&cnt[e], 1u);
+  }
+  __syncthreads();
+  scan_experts(cnt, E, counts, offsets, used, cursor);
+  stable_scatter(idx, 0, M, E, id_bits(E), cursor, perm, inv);
+}
+
+// Multi-block pass 1: per-chunk histograms, hist[c * E + e].
+__global__ __launch_bounds__(kPlanThreads) void plan_hist_kernel(const uint32_t* __restrict__ idx,
+                                                                 int M, int E,
+                                                                 uint32_t* __restrict__ hist) {
+  __shared__ uint32_t cnt[kPlanMaxE];
+  const int tid = threadIdx.x, c = blockIdx.x;
+  for (int e = tid; e < E; e += kPlanThreads) cnt[e] = 0;
+  __syncthreads();
+  const int begin = c * kChunk, end = min(M, begin + kChunk);
+  for (int m = begin + tid; m < end; m += kPlanThreads) {
+    const uint32_t e = idx[m];
+    if (e < (uint32_t)E) atomicAdd(&cnt[e], 1u);
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kPlanThreads) hist[(size_t)c * E + e] = cnt[e];
+}
+
+// Multi-block pass 2 (one block): totals, scan, and each chunk's starting
+// position per expert, written back over hist.
+__global__ __launch_bounds__(kPlanThreads) void plan_scan_kernel(int nchunks, int E,
+                                                                 uint32_t* __restrict__ hist,
+                                                                 uint32_t* counts, uint32_t* offsets,
+                                                                 uint32_t* used) {
+  __shared__ uint32_t cnt[kPlanMaxE], base[kPlanMaxE];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += kPlanThreads) {
+    uint32_t s = 0;
+    for (int c = 0; c < nchunks; c++) s += hist[(size_t)c * E + e];
+    cnt[e] = s;
+  }
+  __syncthreads();
+  scan_experts(cnt, E, counts, offsets, used, base);
+  for (int e = tid; e < E; e += kPlanThreads) {
+    uint32_t run = base[e];
+    for (int c = 0; c < nchunks; c++) {
+      const uint32_t h = hist[(size_t)c * E + e];
+      hist[(size_t)c * E + e] = run;
+      run += h;
+    }
+  }
+}
+
+// Multi-block pass 3: stable scatter of each chunk from its own bases.
+__global__ __launch_bounds__(kPlanThreads) void plan_scatter_kernel(
+    const uint32_t* __restrict__ idx, int M, int E, const uint32_t* __restrict__ hist,
+    uint32_t* perm, uint32_t* inv) {
+  __shared__ uint32_t cursor[kPlanMaxE];
+  const int tid = threadIdx.x, c = blockIdx.x;
+  for (int e = tid; e < E; e += kPlanThreads) cursor[e] = hist[(size_t)c * E + e];
+  __syncthreads();
+  const int begin = c * kChunk, end = min(M, begin + kChunk);
+  stable_scatter(idx, begin, end, E, id_bits(E), cursor, perm, inv);
+}
+
+__global__ void identity_plan_kernel(uint32_t* offsets, uint32_t* used, int M) {
+  if (threadIdx.x == 0) {
+    offsets[0] = 0;
+    offsets[1] = (uint32_t)M;
+    used[0] = 1;
+    used[1] = 0;
+  }
+}
+
+__global__ __launch_bounds__(kPlanThreads) void used_from_offsets_kernel(const uint32_t* offsets,
+                                                                         int E, uint32_t* used) {
+  __shared__ uint32_t cnt[kPlanMaxE], dummy_off[kPlanMaxE + 1], dummy_cnt[kPlanMaxE],
+      dummy_base[kPlanMaxE];
+  for (int e = threadIdx.x; e < E; e += kPlanThreads) cnt[e] = offsets[e + 1] - offsets[e];
+  __syncthreads();
+  scan_experts(cnt, E, dummy_cnt, dummy_off, used, dummy_base);
+}
+
+size_t dispatch_scratch_bytes(int T, int k, int E) {
+  const long M = (long)T * k;
+  if (M <= kSingleBlockMax) return 0;
+  const long nchunks = (M + kChunk - 1) / kChunk;
+  return (size_t)(nchunks * E * 4);
+}
+
+hipError_t launch_dispatch_plan(const uint32_t* idx, int T, int k, int E, uint32_t* counts,
+                                uint32_t* offsets, uint32_t* perm, uint32_t* inv_perm,
+                                uint32_t* used, void* scratch, size_t scratch_bytes,
+                                hipStream_t st) {
+  const int M = T * k;
+  if (E > kPlanMaxE) return hipErrorInvalidValue;
+  if (M <= kSingleBlockMax) {
+    hipLaunchKernelGGL(plan_single_kernel, dim3(1), dim3(kPlanThreads), 0, st, idx, M, E, counts,
+                       offsets, perm, inv_perm, used);
+    return hipGetLastError();
+  }
+  const int nchunks = (M + kChunk - 1) / kChunk;
+  if (scratch == nullptr || scratch_bytes < (size_t)nchunks * E * 4) return hipErrorInvalidValue;
+  uint32_t* hist = reinterpret_cast<uint32_t*>(scratch);
+  hipLaunchKernelGGL(plan_hist_kernel, dim3(nchunks), dim3(kPlanThreads), 0, st, idx, M, E, hist);
+  hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(kPlanThreads), 0, st, nchunks, E, hist,
+                     counts, offsets, used);
+  hipLaunchKernelGGL(plan_scatter_kernel, dim3(nchunks), dim3(kPlanThreads), 0, st, idx, M, E,
+                     hist, perm, inv_perm);
+  return hipGetLastError();
+}
+
+hipError_t launch_identity_plan(uint32_t* offsets, uint32_t* used, int M, hipStream_t st) {
+  hipLaunchKernelGGL(identity_plan_kernel, dim3(1), dim3(64), 0, st, offsets, used, M);
+  return hipGetLastError();
+}
+
+hipError_t launch_used_from_offsets(const uint32_t* offsets, int E, uint32_t* used,
+                                    hipStream_t st) {
+  if (E > kPlanMaxE) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(used_from_offsets_kernel, dim3(1), dim3(kPlanThreads), 0, st, offsets, E,
+                     used);
+  return hipGetLastError();
+}
+
+}  // namespace moe

@@ -1,0 +1,242 @@
+// moe_common.hpp — device helpers shared by the gfx950 MoE kernels.
+//
+// Element types are the storage types of FFAI's DType (f32 / f16 / bf16,
+// Sources/FFAI/DType.swift:20-39). Every kernel accumulates in fp32 and rounds
+// to the storage type (round-to-nearest-even) where the reference stores a
+// tensor in the activation dtype.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moe {
+
+constexpr int kWave = 64;
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- convert --
+template <typename T> __device__ __forceinline__ float to_f(T v) { return (float)v; }
+template <> __device__ __forceinline__ float to_f<bf16_t>(bf16_t v) {
+  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, v) << 16);
+}
+template <typename T> __device__ __forceinline__ T from_f(float v) { return (T)v; }
+
+template <typename T> __device__ __forceinline__ float round_to(float v) { return to_f<T>(from_f<T>(v)); }
+
+// --------------------------------------------------------- wave reductions --
+__device__ __forceinline__ float wave_sum_width(float v, int width) {
+  for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// ------------------------------------------------------ deterministic exp --
+// Cody-Waite reduction by ln2 plus Moshier's degree-5 polynomial (Cephes
+// expf), written as explicit fused/unfused fp32 operations so that the CPU
+// restatement of the router evaluates the identical bits.
+__device__ __forceinline__ float det_expf(float x) {
+#pragma clang fp contract(off)
+  if (x > 88.0f) return __builtin_huge_valf();
+  if (x < -87.0f) return 0.0f;
+  float n = __builtin_rintf(x * 1.44269504088896341f);
+  float r = __builtin_fmaf(n, -0.693359375f, x);
+  r = __builtin_fmaf(n, 2.12194440e-4f, r);
+  float p = 1.9875691500e-4f;
+  p = __builtin_fmaf(p, r, 1.3981999507e-3f);
+  p = __builtin_fmaf(p, r, 8.3334519073e-3f);
+  p = __builtin_fmaf(p, r, 4.1665795894e-2f);
+  p = __builtin_fmaf(p, r, 1.6666665459e-1f);
+  p = __builtin_fmaf(p, r, 5.0000001201e-1f);
+  float r2 = r * r;
+  float y = __builtin_fmaf(p, r2, r) + 1.0f;
+  return __builtin_ldexpf(y, (int)n);
+}
+
+// ------------------------------------------------------------ activations --
+enum { ACT_SWIGLU = 0, ACT_GPTOSS = 1 };
+
+__device__ __forceinline__ float apply_act(float g, float u, int act, float alpha, float limit) {
+  if (act == ACT_GPTOSS) {
+    g = fminf(g, limit);
+    u = fminf(fmaxf(u, -limit), limit);
+    float glu = g / (1.0f + __expf(-alpha * g));
+    return glu * (u + 1.0f);
+  }
+  return g / (1.0f + __expf(-g)) * u;
+}
+
+// ------------------------------------------------------ affine bit stream --
+// A "unit" is 32 consecutive values of one weight row: BITS u32 words of the
+// little-endian bit stream (value i at bit offset i*BITS). Units never
+// straddle a scale group because group sizes are multiples of 32.
+//
+// unpack_pairs<BITS> turns a unit into 16 code pairs, each u32 holding two
+// codes in its low bits of the 16-bit halves: pair j = (q_a, q_b) with the
+// sub-block pairing (i, i + P/2) inside blocks of P values, P = 16 for 2-bit,
+// 8 for 3/4-bit and 4 for 5/6/8-bit. Activations are stored in the same
+// pair order (pair_pos) so a dot2 multiplies matching values.
+template <int BITS> struct Pairing;
+template <> struct Pairing<2> { static constexpr int P = 16; };
+template <> struct Pairing<3> { static constexpr int P = 8; };
+template <> struct Pairing<4> { static constexpr int P = 8; };
+template <> struct Pairing<5> { static constexpr int P = 4; };
+template <> struct Pairing<6> { static constexpr int P = 4; };
+template <> struct Pairing<8> { static constexpr int P = 4; };
+
+// Position of value v (0..31 within a unit) in the pair-ordered layout.
+template <int BITS> __host__ __device__ __forceinline__ int pair_pos(int v) {
+  constexpr int P = Pairing<BITS>::P, H = P / 2;
+  int blk = v / P, i = v % P;
+  return blk * P + (i < H ? 2 * i : 2 * (i - H) + 1);
+}
+
+__device__ __forceinline__ uint32_t funnel(uint32_t hi, uint32_t lo, int sh) {
+  return sh == 0 ? lo : (uint32_t)((((uint64_t)hi << 32) | lo) >> sh);
+}
+
+template <int BITS>
+__device__ __forceinline__ void unpack_pairs(const uint32_t (&w)[BITS], uint32_t (&cp)[16]) {
+  if constexpr (BITS == 2) {
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int i = 0; i < 8; i++) cp[j * 8 + i] = (w[j] >> (2 * i)) & 0x00030003u;
+  } else if constexpr (BITS == 4) {
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) cp[j * 4 + i] = (w[j] >> (4 * i)) & 0x000F000Fu;
+  } else if constexpr (BITS == 8) {
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+      for (int i = 0; i < 2; i++) cp[j * 2 + i] = (w[j] >> (8 * i)) & 0x00FF00FFu;
+  } else if constexpr (BITS == 3) {
+    // 4 sub-blocks of 24 bits (8 values); spread the upper 12 bits to bit 16
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int bit = 24 * j, lo = bit >> 5, sh = bit & 31;
+      uint32_t s = (sh + 24 <= 32) ? (w[lo] >> sh) : funnel(w[lo + 1], w[lo], sh);
+      s &= 0xFFFFFFu;
+      uint32_t t = (s & 0xFFFu) | ((s & 0xFFF000u) << 4);
+#pragma unroll
+      for (int i = 0; i < 4; i++) cp[j * 4 + i] = (t >> (3 * i)) & 0x00070007u;
+    }
+  } else if constexpr (BITS == 6) {
+    // 8 sub-blocks of 24 bits (4 values)
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int bit = 24 * j, lo = bit >> 5, sh = bit & 31;
+      uint32_t s = (sh + 24 <= 32) ? (w[lo] >> sh) : funnel(w[lo + 1], w[lo], sh);
+      s &= 0xFFFFFFu;
+      uint32_t t = (s & 0xFFFu) | ((s & 0xFFF000u) << 4);
+#pragma unroll
+      for (int i = 0; i < 2; i++) cp[j * 2 + i] = (t >> (6 * i)) & 0x003F003Fu;
+    }
+  } else if constexpr (BITS == 5) {
+    // 8 sub-blocks of 20 bits (4 values); spread the upper 10 bits to bit 16
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int bit = 20 * j, lo = bit >> 5, sh = bit & 31;
+      uint32_t s = (sh + 20 <= 32) ? (w[lo] >> sh) : funnel(w[lo + 1], w[lo], sh);
+      s &= 0xFFFFFu;
+      uint32_t t = (s & 0x3FFu) | ((s & 0xFFC00u) << 6);
+#pragma unroll
+      for (int i = 0; i < 2; i++) cp[j * 2 + i] = (t >> (5 * i)) & 0x001F001Fu;
+    }
+  }
+}
+
+// Loads one unit (BITS consecutive u32) with the widest loads its alignment
+// allows (rows start 16-byte aligned: k is a multiple of 32).
+template <int BITS>
+__device__ __forceinline__ void load_unit(const uint32_t* __restrict__ p, uint32_t (&w)[BITS]) {
+  if constexpr (BITS == 2) {
+    uint2 v = *reinterpret_cast<const uint2*>(p);
+    w[0] = v.x; w[1] = v.y;
+  } else if constexpr (BITS == 3) {
+    w[0] = p[0]; w[1] = p[1]; w[2] = p[2];
+  } else if constexpr (BITS == 4) {
+    uint4 v = *reinterpret_cast<const uint4*>(p);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else if constexpr (BITS == 5) {
+    // 20-byte units are only 4-byte aligned
+    w[0] = p[0]; w[1] = p[1]; w[2] = p[2]; w[3] = p[3]; w[4] = p[4];
+  } else if constexpr (BITS == 6) {
+    uint2 a = *reinterpret_cast<const uint2*>(p);
+    uint2 b = *reinterpret_cast<const uint2*>(p + 2);
+    uint2 c = *reinterpret_cast<const uint2*>(p + 4);
+    w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y; w[4] = c.x; w[5] = c.y;
+  } else {
+    uint4 a = *reinterpret_cast<const uint4*>(p);
+    uint4 b = *reinterpret_cast<const uint4*>(p + 4);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+  }
+}
+
+// --------------------------------------------------------- unit dot product --
+// D = sum over the unit of (MAGIC + q) * x for 16-bit activations: codes are
+// or-ed into the mantissa of MAGIC = 128.0 (bf16, exact for codes < 128) or
+// 1024.0 (f16, exact for codes < 1024), and v_dot2 multiplies two pairs at a
+// time with fp32 accumulation. 8-bit codes with bf16 activations, and f32
+// activations, use exact integer->fp32 conversion instead (MAGIC = 0). The
+// caller removes MAGIC * sum(x) through the bias term.
+template <int BITS, typename XT> struct Magic {
+  static constexpr bool dot2 = !__is_same(XT, float) && !(BITS == 8 && __is_same(XT, bf16_t));
+  static constexpr uint32_t bits = !dot2 ? 0u : (__is_same(XT, bf16_t) ? 0x43004300u : 0x64006400u);
+  static constexpr float value = !dot2 ? 0.0f : (__is_same(XT, bf16_t) ? 128.0f : 1024.0f);
+};
+
+// x16: the unit's 32 activations in pair order, as 16 u32 (16-bit types).
+template <int BITS, typename XT>
+__device__ __forceinline__ float unit_dot16(const uint32_t (&cp)[16], const uint32_t (&x16)[16]) {
+  float d0 = 0.f, d1 = 0.f;
+  if constexpr (Magic<BITS, XT>::dot2) {
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      uint32_t a0 = cp[i] | Magic<BITS, XT>::bits, a1 = cp[i + 1] | Magic<BITS, XT>::bits;
+      if constexpr (__is_same(XT, bf16_t)) {
+        d0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a0),
+                                             __builtin_bit_cast(bf16x2_t, x16[i]), d0, false);
+        d1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a1),
+                                             __builtin_bit_cast(bf16x2_t, x16[i + 1]), d1, false);
+      } else {
+        d0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a0),
+                                    __builtin_bit_cast(f16x2_t, x16[i]), d0, false);
+        d1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a1),
+                                    __builtin_bit_cast(f16x2_t, x16[i + 1]), d1, false);
+      }
+    }
+  } else {
+    // bf16 activations with 8-bit codes
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      float xa = __uint_as_float(x16[i] << 16), xb = __uint_as_float(x16[i] & 0xFFFF0000u);
+      d0 = __builtin_fmaf((float)(cp[i] & 0xFFFFu), xa, d0);
+      d1 = __builtin_fmaf((float)(cp[i] >> 16), xb, d1);
+    }
+  }
+  return d0 + d1;
+}
+
+// f32 activations: x32 in pair order.
+__device__ __forceinline__ float unit_dot32(const uint32_t (&cp)[16], const float (&x32)[32]) {
+  float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    d0 = __builtin_fmaf((float)(cp[i] & 0xFFFFu), x32[2 * i], d0);
+    d1 = __builtin_fmaf((float)(cp[i] >> 16), x32[2 * i + 1], d1);
+  }
+  return d0 + d1;
+}
+
+// Scale/bias element loads (scale dtype independent of activations).
+template <typename ST> __device__ __forceinline__ float ld_sb(const void* p, size_t i) {
+  return to_f<ST>(reinterpret_cast<const ST*>(p)[i]);
+}
+
+}  // namespace moe

@@ -1,0 +1,108 @@
+// moe_internal.hpp — argument blocks and launchers shared between the C-ABI
+// layer (api.cpp) and the kernel translation units. Host code only sees
+// plain pointers; every launcher returns hipSuccess or the launch error.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace moe {
+
+enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
+
+// ------------------------------------------------------------------ GEMV --
+// Expert-grouped dequant GEMV over a dispatch plan. Block b handles expert
+// slot b / row_blocks (the slot-th used expert) and rows
+// [rb*rows_per_block, ...) of its N output rows for every sorted position of
+// that expert.
+struct GemvProj {
+  const uint32_t* w;     // [E, N, K*bits/32]
+  const void* s;         // [E, N, K/gs] sb dtype
+  const void* b;         // [E, N, K/gs] sb dtype
+  const void* ob;        // nullable [E, N] activation dtype
+};
+
+struct GemvArgs {
+  GemvProj p0, p1;           // p0 = gate (or the single projection), p1 = up
+  const void* x;             // activation rows, [rows, K]
+  const uint32_t* perm;      // nullable: row(p) = perm[p] / topk, else row(p) = p
+  int topk;
+  const uint32_t* offsets;   // [E+1] CSR over sorted positions
+  const uint32_t* used;      // [1+E]: used[0] = U, used[1..U] = expert ids
+  void* out;                 // [M, N]
+  int N, K, gs;
+  int row_blocks, rows_per_block;
+  int lg;                    // log2(lanes per row)
+  int tok_chunk;             // activation rows staged per pass (<= TOKMAX)
+  int act;                   // activation (gate/up pair only)
+  float alpha, limit;
+};
+
+// Fused down projection + weighted combine for one token (T = 1): every
+// sorted position is a distinct expert.
+struct DownCombineArgs {
+  GemvProj p;                // down projection
+  const void* act;           // [k, K] activations in sorted order
+  const uint32_t* perm;      // [k]
+  const uint32_t* idx;       // [k] expert of each token-major slot
+  const float* w;            // [k] combine weight of each slot
+  void* out;                 // [N]
+  int k, N, K, gs;
+  int rows_per_block;
+  int lg;
+};
+
+hipError_t launch_gemv(int bits, int xdt, int sbdt, bool gateup, int tokmax, const GemvArgs& a,
+                       int grid, hipStream_t st);
+hipError_t launch_down_combine(int bits, int xdt, int sbdt, const DownCombineArgs& a, int grid,
+                               hipStream_t st);
+size_t gemv_smem_bytes(int xdt, int K, int tok_chunk);
+size_t down_combine_smem_bytes(int xdt, int K, int k);
+
+// ---------------------------------------------------------------- router --
+hipError_t launch_router_logits(const void* x, int xdt, int T, int H, const void* W, int wdt,
+                                const void* bias, int E, void* logits, hipStream_t st);
+hipError_t launch_router_topk(const void* logits, int dt, int T, int E, int k, int gating,
+                              int norm, const float* ebias, uint32_t* idx, float* w,
+                              hipStream_t st);
+
+// ------------------------------------------------------------- dispatch --
+// Writes counts, offsets, perm, inv_perm and the used-expert list.
+hipError_t launch_dispatch_plan(const uint32_t* idx, int T, int k, int E, uint32_t* counts,
+                                uint32_t* offsets, uint32_t* perm, uint32_t* inv_perm,
+                                uint32_t* used, void* scratch, size_t scratch_bytes,
+                                hipStream_t st);
+size_t dispatch_scratch_bytes(int T, int k, int E);
+// Fills offsets {0, M}, used {1, 0} for a single-expert identity plan.
+hipError_t launch_identity_plan(uint32_t* offsets, uint32_t* used, int M, hipStream_t st);
+// Builds the used list from CSR offsets only (caller-supplied plans).
+hipError_t launch_used_from_offsets(const uint32_t* offsets, int E, uint32_t* used,
+                                    hipStream_t st);
+
+// -------------------------------------------------------------- combine --
+hipError_t launch_unpermute(const void* Y, const uint32_t* inv, const float* w, int T, int H,
+                            int k, void* out, int dt, const void* shared_out,
+                            const void* shared_logit, int shared_mode, hipStream_t st);
+hipError_t launch_add_shared(void* y, const void* shared_out, const void* shared_logit,
+                             int shared_mode, int T, int H, int dt, hipStream_t st);
+hipError_t launch_activation(const void* g, const void* u, void* out, int64_t n, int dt,
+                             int act, float alpha, float limit, hipStream_t st);
+hipError_t launch_dequantize(const uint32_t* w, const void* s, const void* b, int sbdt, int bits,
+                             int gs, int64_t numel, void* out, int odt, hipStream_t st);
+
+// ----------------------------------------------------------------- GEMM --
+struct GemmArgs {
+  GemvProj p0, p1;
+  const void* x;
+  const uint32_t* perm;
+  int topk;
+  const uint32_t* offsets;
+  const uint32_t* tiles;     // work list: [1 + max_tiles] (count, packed expert/m-tile)
+  void* out;
+  int N, K, gs, M;
+  int act;
+  float alpha, limit;
+};
+
+}  // namespace moe

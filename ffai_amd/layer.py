@@ -1,0 +1,173 @@
+"""MoE layer over PyTorch device buffers, driven through the C ABI.
+
+Mirrors the Swift block API of FFAI (Sources/FFAI/Models/MoELayer.swift:
+MoEGatingMode :71, MoERouter :97-124, MoELayer.init :440-498, decode :530,
+decodeMany :677) on top of libmoehip.so. PyTorch only provides device memory
+and the stream; every computation is a libmoehip.so kernel.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import LayerDesc, LayerTrace, QProj, check
+
+_DT = {torch.float32: _lib.MOE_F32, torch.float16: _lib.MOE_F16, torch.bfloat16: _lib.MOE_BF16}
+
+
+def moe_dtype(t: torch.dtype) -> int:
+    return _DT[t]
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+class MoEGatingMode:
+    """MoELayer.swift:71-78."""
+    softmaxThenTopK = _lib.MOE_SOFTMAX_THEN_TOPK
+    topKThenSoftmax = _lib.MOE_TOPK_THEN_SOFTMAX
+
+
+@dataclass
+class MoERouter:
+    """MoERouter (MoELayer.swift:97-124): the gating configuration."""
+    nExperts: int
+    topK: int
+    gatingMode: int = MoEGatingMode.softmaxThenTopK
+    normTopKProb: bool = True
+    expertBias: Optional[torch.Tensor] = None  # [nExperts] float32 on device
+
+    def __post_init__(self):
+        if self.nExperts <= 0:
+            raise ValueError("MoERouter: nExperts must be positive")
+        if not (0 < self.topK <= self.nExperts):
+            raise ValueError(f"MoERouter: topK ({self.topK}) must be in 1...nExperts ({self.nExperts})")
+        if self.expertBias is not None and self.expertBias.numel() != self.nExperts:
+            raise ValueError("MoERouter: expertBias must have nExperts entries")
+
+
+@dataclass
+class StackedExperts:
+    """One stacked mlx-affine projection: weight [E, N, K*bits/32] (int32
+    storage of u32 words), scales/biases [E, N, K/gs], optional per-expert
+    output bias [E, N] in the activation dtype."""
+    weight: torch.Tensor
+    scales: torch.Tensor
+    biases: torch.Tensor
+    bits: int
+    group_size: int
+    out_bias: Optional[torch.Tensor] = None
+
+    @property
+    def n_experts(self) -> int:
+        return self.weight.shape[0]
+
+    @property
+    def n(self) -> int:
+        return self.weight.shape[1]
+
+    @property
+    def k(self) -> int:
+        return self.scales.shape[-1] * self.group_size
+
+    def struct(self) -> QProj:
+        return QProj(self.weight.data_ptr(), self.scales.data_ptr(), self.biases.data_ptr(),
+                     None if self.out_bias is None else self.out_bias.data_ptr(),
+                     self.bits, self.group_size, moe_dtype(self.scales.dtype),
+                     self.n, self.k, self.n_experts)
+
+
+class MoELayer:
+    """MoE feed-forward layer (router -> dispatch -> grouped expert products
+    -> combine [+ shared expert]) on one GPU."""
+
+    def __init__(self, *, router_weight: torch.Tensor, router: MoERouter,
+                 gate: StackedExperts, up: StackedExperts, down: StackedExperts,
+                 hidden: int, act_dtype: torch.dtype,
+                 router_bias: Optional[torch.Tensor] = None,
+                 activation: int = _lib.MOE_ACT_SWIGLU, alpha: float = 1.702, limit: float = 7.0,
+                 shared: Optional[tuple] = None, shared_gate_weight: Optional[torch.Tensor] = None):
+        self.router_weight, self.router, self.router_bias = router_weight, router, router_bias
+        self.gate, self.up, self.down = gate, up, down
+        self.hidden, self.act_dtype = hidden, act_dtype
+        self.activation, self.alpha, self.limit = activation, alpha, limit
+        self.shared, self.shared_gate_weight = shared, shared_gate_weight
+        self._desc = self._build_desc()
+        check(_lib.load().moe_validate_layer(C.byref(self._desc)))
+        self._ws = None
+
+    def _build_desc(self) -> LayerDesc:
+        d = LayerDesc()
+        d.hidden, d.n_experts, d.top_k = self.hidden, self.router.nExperts, self.router.topK
+        d.intermediate = self.gate.n
+        d.act_dtype = moe_dtype(self.act_dtype)
+        d.router_weight = self.router_weight.data_ptr()
+        d.router_dtype = moe_dtype(self.router_weight.dtype)
+        d.router_bias = None if self.router_bias is None else self.router_bias.data_ptr()
+        d.gating, d.norm_topk_prob = self.router.gatingMode, int(bool(self.router.normTopKProb))
+        d.expert_bias = None if self.router.expertBias is None else self.router.expertBias.data_ptr()
+        d.gate, d.up, d.down = self.gate.struct(), self.up.struct(), self.down.struct()
+        d.activation, d.act_alpha, d.act_limit = self.activation, self.alpha, self.limit
+        if self.shared is not None:
+            d.has_shared = 1
+            d.shared_gate, d.shared_up, d.shared_down = (p.struct() for p in self.shared)
+            d.shared_gate_weight = (None if self.shared_gate_weight is None
+                                    else self.shared_gate_weight.data_ptr())
+        return d
+
+    @property
+    def desc(self) -> LayerDesc:
+        return self._desc
+
+    def workspace_bytes(self, T: int) -> int:
+        return _lib.load().moe_layer_workspace_bytes(C.byref(self._desc), T)
+
+    def workspace(self, T: int) -> torch.Tensor:
+        need = self.workspace_bytes(T)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.router_weight.device)
+        return self._ws
+
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, trace: bool = False,
+                stream=None):
+        """decodeMany: x [T, hidden] -> [T, hidden]. With trace=True also
+        returns the routing (logits, topk_idx, topk_weight, perm, offsets)."""
+        T = x.shape[0]
+        if out is None:
+            out = torch.empty_like(x)
+        ws = self.workspace(T)
+        tr = None
+        tensors = None
+        if trace:
+            dev = x.device
+            E, k = self.router.nExperts, self.router.topK
+            tensors = dict(
+                logits=torch.empty(T, E, dtype=self.act_dtype, device=dev),
+                topk_idx=torch.empty(T, k, dtype=torch.int32, device=dev),
+                topk_weight=torch.empty(T, k, dtype=torch.float32, device=dev),
+                perm=torch.empty(T * k, dtype=torch.int32, device=dev),
+                offsets=torch.empty(E + 1, dtype=torch.int32, device=dev))
+            tr = LayerTrace(*(tensors[n].data_ptr() for n in
+                              ("logits", "topk_idx", "topk_weight", "perm", "offsets")))
+        check(_lib.load().moe_layer_forward(C.byref(self._desc), _ptr(x), T, _ptr(out),
+                                            _ptr(ws), ws.numel(),
+                                            C.byref(tr) if tr is not None else None,
+                                            _stream(stream)))
+        return (out, tensors) if trace else out
+
+    # Swift-API names
+    def decode(self, h: torch.Tensor, stream=None) -> torch.Tensor:
+        return self.forward(h.reshape(1, -1), stream=stream).reshape(-1)
+
+    def decodeMany(self, hFlat: torch.Tensor, t: int, stream=None) -> torch.Tensor:
+        return self.forward(hFlat.reshape(t, self.hidden), stream=stream).reshape(-1)

@@ -1,0 +1,628 @@
+/*
+ * moe_oracle.c — CPU restatement of FFAI's MoE feed-forward layer.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP path and the timed CPU
+ * baseline. The product never loads it; only tests/, smoke() and bench.py's
+ * cpu_baseline leg do.
+ *
+ * The reference (thewafflehaus/FFAI) is Swift + Metal and cannot be built
+ * here, so this file restates its semantics in plain C. Build flags keep the
+ * arithmetic literal: -ffp-contract=off, no fast-math.
+ *
+ * What pins each part (tests/test_oracle_golden.py):
+ *   conversions     IEEE special values + exhaustive f16/bf16 round trips
+ *   or_expf         |or_expf(x) - exp(x)| <= 2 ulp over a dense sweep
+ *   bit stream      the reference's own byte-level packers
+ *                   (Tests/FFAITests/Ops/QuantizedOpsTests.swift:33-121),
+ *                   dequant KAT (QuantizedOpsAffineTests.swift:124-159),
+ *                   deriveAffineQuantBits cases (LayersTests.swift:79-98)
+ *   router          KATs MoELayerTests.swift:36-110, QuantizedOpsTests.swift:
+ *                   999-1028, brute-force full stable sort
+ *   dispatch plan   brute-force sort + invariants
+ *   grouped GEMM    numpy float64 matmul of the dequantised dense matrix on
+ *                   the reference's generators (MoEBgemmBm64MppTests.swift:
+ *                   159-271, QuantizedOpsTests.swift:126-438)
+ *   activations     KATs OpsSpecialPathTests.swift:314-354; GPT-OSS closed
+ *                   form at hand-picked points (clamp branches)
+ *   combine         KAT OpsSpecialPathTests.swift:1080-1122
+ *   whole layer     KATs MoELayerTests.swift:147-265 (scalar experts)
+ */
+#include "moe_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* conversions                                                              */
+/* ------------------------------------------------------------------------ */
+
+float or_bf16_to_f32(uint16_t h) {
+    uint32_t x = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+/* Round-to-nearest-even, the bias trick of Tensor.swift:146-150 and
+ * MoELayer.swift:927-931. NaN stays NaN. */
+uint16_t or_f32_to_bf16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x0040u);
+    uint32_t r = x + 0x7fffu + ((x >> 16) & 1u);
+    return (uint16_t)(r >> 16);
+}
+
+float or_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu, x;
+    if (e == 0) {
+        float v = (float)m * 5.9604644775390625e-8f; /* m * 2^-24, exact */
+        return sign ? -v : v;
+    }
+    if (e == 31) x = sign | 0x7f800000u | (m << 13);
+    else x = sign | ((e + 112u) << 23) | (m << 13);
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+uint16_t or_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u));
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 -> inf */
+    if (ax < 0x38800000u) {                                    /* below 2^-14 */
+        float a;
+        memcpy(&a, &ax, 4);
+        uint32_t m = (uint32_t)nearbyintf(a * 16777216.0f); /* units of 2^-24, RNE */
+        return (uint16_t)(sign | m);
+    }
+    uint32_t e = (ax >> 23) - 112u;
+    uint32_t mant = ax & 0x7fffffu;
+    uint32_t h = (e << 10) | (mant >> 13);
+    uint32_t rem = mant & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
+float or_round_dt(float v, int dt) {
+    if (dt == OR_BF16) return or_bf16_to_f32(or_f32_to_bf16(v));
+    if (dt == OR_F16) return or_f16_to_f32(or_f32_to_f16(v));
+    return v;
+}
+
+void or_load(const void* src, int dt, size_t n, float* dst) {
+    if (dt == OR_F32) {
+        memcpy(dst, src, n * 4);
+    } else if (dt == OR_F16) {
+        const uint16_t* s = (const uint16_t*)src;
+        for (size_t i = 0; i < n; i++) dst[i] = or_f16_to_f32(s[i]);
+    } else {
+        const uint16_t* s = (const uint16_t*)src;
+        for (size_t i = 0; i < n; i++) dst[i] = or_bf16_to_f32(s[i]);
+    }
+}
+
+void or_store(const float* src, int dt, size_t n, void* dst) {
+    if (dt == OR_F32) {
+        memcpy(dst, src, n * 4);
+    } else if (dt == OR_F16) {
+        uint16_t* d = (uint16_t*)dst;
+        for (size_t i = 0; i < n; i++) d[i] = or_f32_to_f16(src[i]);
+    } else {
+        uint16_t* d = (uint16_t*)dst;
+        for (size_t i = 0; i < n; i++) d[i] = or_f32_to_bf16(src[i]);
+    }
+}
+
+static float load1(const void* p, int dt, size_t i) {
+    if (dt == OR_F32) return ((const float*)p)[i];
+    if (dt == OR_F16) return or_f16_to_f32(((const uint16_t*)p)[i]);
+    return or_bf16_to_f32(((const uint16_t*)p)[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* deterministic exp                                                        */
+/* ------------------------------------------------------------------------ */
+
+/* Cody-Waite reduction by ln2 and Moshier's degree-5 minimax polynomial
+ * (Cephes expf). Every step is an explicit fused or unfused single-precision
+ * operation, so the GPU router (which evaluates the same sequence) returns
+ * the identical bits. The reference calls Foundation.exp
+ * (MoELayer.swift:213); the two agree to within 2 ulp. */
+float or_expf(float x) {
+    if (x > 88.0f) return INFINITY;
+    if (x < -87.0f) return 0.0f;
+    float n = rintf(x * 1.44269504088896341f);
+    float r = fmaf(n, -0.693359375f, x);
+    r = fmaf(n, 2.12194440e-4f, r);
+    float p = 1.9875691500e-4f;
+    p = fmaf(p, r, 1.3981999507e-3f);
+    p = fmaf(p, r, 8.3334519073e-3f);
+    p = fmaf(p, r, 4.1665795894e-2f);
+    p = fmaf(p, r, 1.6666665459e-1f);
+    p = fmaf(p, r, 5.0000001201e-1f);
+    float r2 = r * r;
+    float y = fmaf(p, r2, r) + 1.0f;
+    return ldexpf(y, (int)n);
+}
+
+/* ------------------------------------------------------------------------ */
+/* affine bit stream                                                        */
+/* ------------------------------------------------------------------------ */
+
+static int bits_ok(int bits) {
+    return bits == 2 || bits == 3 || bits == 4 || bits == 5 || bits == 6 || bits == 8;
+}
+
+/* Value i of a row lives at bit offset i*bits of the little-endian u32
+ * stream (Layers.swift:134-143; QuantizedOpsTests.swift:33-121 packers);
+ * 3/5/6-bit values straddle byte and word boundaries. */
+static inline uint32_t get_code(const uint32_t* w, int bits, size_t i) {
+    size_t bit = i * (size_t)bits;
+    size_t word = bit >> 5;
+    unsigned sh = (unsigned)(bit & 31u);
+    uint64_t win = w[word];
+    if (sh + (unsigned)bits > 32u) win |= (uint64_t)w[word + 1] << 32;
+    return (uint32_t)(win >> sh) & ((1u << bits) - 1u);
+}
+
+int or_unpack_codes(const uint32_t* w, int bits, size_t n, uint8_t* codes) {
+    if (!bits_ok(bits) || (n * (size_t)bits) % 32u) return -1;
+    for (size_t i = 0; i < n; i++) codes[i] = (uint8_t)get_code(w, bits, i);
+    return 0;
+}
+
+int or_pack_codes(const uint8_t* codes, int bits, size_t n, uint32_t* w) {
+    if (!bits_ok(bits) || (n * (size_t)bits) % 32u) return -1;
+    memset(w, 0, n * (size_t)bits / 8);
+    for (size_t i = 0; i < n; i++) {
+        uint64_t v = (uint64_t)(codes[i] & ((1u << bits) - 1u));
+        size_t bit = i * (size_t)bits;
+        size_t word = bit >> 5;
+        unsigned sh = (unsigned)(bit & 31u);
+        w[word] |= (uint32_t)(v << sh);
+        if (sh + (unsigned)bits > 32u) w[word + 1] |= (uint32_t)(v >> (32u - sh));
+    }
+    return 0;
+}
+
+/* QuantizedOpsValidation.packedUInt32Count (QuantizedOpsValidation.swift:52-57) */
+long or_packed_u32_count(long numel, int bits) {
+    if (!bits_ok(bits)) return -1;
+    long bitcount = numel * bits;
+    if (bitcount % 32) return -1;
+    return bitcount / 32;
+}
+
+/* deriveAffineQuantBits (Layers.swift:348-363): bits = 32*packed/(scale*gs).
+ * Returns -1 where the Swift code traps. */
+int or_derive_bits(long packed_cols, long scale_cols, long group_size) {
+    long in_features = scale_cols * group_size;
+    if (in_features <= 0) return -1;
+    if ((32 * packed_cols) % in_features) return -1;
+    return (int)((32 * packed_cols) / in_features);
+}
+
+/* QuantizedOps.dequantizeAffine (QuantizedOps.swift:62-221) with the
+ * validator of QuantizedOpsValidation.swift:64-110: w = scale*q + bias. */
+int or_dequantize_affine(const uint32_t* w, const void* scales, const void* biases,
+                         int sb_dt, int bits, int group_size, size_t numel, float* out) {
+    if (!bits_ok(bits) || group_size <= 0 || numel % (size_t)group_size) return -1;
+    if (bits == 2 || bits == 4 || bits == 8) {
+        if (group_size % (32 / bits)) return -1;
+    } else if ((group_size * bits) % 32) {
+        return -1;
+    }
+    for (size_t i = 0; i < numel; i++) {
+        size_t g = i / (size_t)group_size;
+        float s = load1(scales, sb_dt, g), b = load1(biases, sb_dt, g);
+        float q = (float)get_code(w, bits, i);
+        float sq = s * q;
+        out[i] = sq + b;
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* router                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Router projection (Layers.swift:201, GPTOSSText.swift:361-365):
+ * logits = round_dt(W x), then with a bias round_dt(logits + b), both in the
+ * activation dtype. Dot products accumulate in double. */
+void or_router_logits(const void* x, int x_dt, int T, int H,
+                      const void* W, int w_dt, const void* bias, int E,
+                      float* logits) {
+    float* xr = (float*)malloc(sizeof(float) * (size_t)H);
+    float* wr = (float*)malloc(sizeof(float) * (size_t)H * (size_t)E);
+    or_load(W, w_dt, (size_t)H * (size_t)E, wr);
+    for (int t = 0; t < T; t++) {
+        or_load((const char*)x + (size_t)t * H * (x_dt == OR_F32 ? 4 : 2), x_dt, (size_t)H, xr);
+        for (int e = 0; e < E; e++) {
+            double acc = 0.0;
+            const float* w = wr + (size_t)e * H;
+            for (int h = 0; h < H; h++) acc += (double)w[h] * (double)xr[h];
+            float l = or_round_dt((float)acc, x_dt);
+            if (bias) l = or_round_dt(l + load1(bias, x_dt, (size_t)e), x_dt);
+            logits[(size_t)t * E + e] = l;
+        }
+    }
+    free(xr);
+    free(wr);
+}
+
+/* Numerically-stable softmax with the uniform fallback
+ * (MoELayer.swift:210-219); the sum runs in index order. */
+void or_softmax(const float* x, int n, float* out) {
+    if (n <= 0) return;
+    float m = x[0];
+    for (int i = 1; i < n; i++) m = x[i] > m ? x[i] : m;
+    float s = 0.0f;
+    for (int i = 0; i < n; i++) {
+        out[i] = or_expf(x[i] - m);
+        s += out[i];
+    }
+    if (!(s > 0.0f)) {
+        for (int i = 0; i < n; i++) out[i] = 1.0f / (float)n;
+        return;
+    }
+    for (int i = 0; i < n; i++) out[i] = out[i] / s;
+}
+
+/* Heap top-k of MoELayer.swift:223-296: a k-sized min-heap ordered by
+ * (value asc, index desc), drained and sorted by (value desc, index asc). */
+typedef struct { float v; int i; } vi_t;
+
+static int vi_less(vi_t a, vi_t b) { /* a is the easier evict */
+    if (a.v != b.v) return a.v < b.v;
+    return a.i > b.i;
+}
+
+static int vi_cmp_desc(const void* pa, const void* pb) {
+    vi_t a = *(const vi_t*)pa, b = *(const vi_t*)pb;
+    if (a.v != b.v) return a.v > b.v ? -1 : 1;
+    return a.i < b.i ? -1 : (a.i > b.i);
+}
+
+int or_topk_indices(const float* v, int n, int k, int* out) {
+    if (k <= 0 || k > n) return -1;
+    vi_t* heap = (vi_t*)malloc(sizeof(vi_t) * (size_t)k);
+    int cnt = 0;
+    for (int i = 0; i < n; i++) {
+        vi_t e = {v[i], i};
+        if (cnt < k) {
+            int j = cnt++;
+            heap[j] = e;
+            while (j > 0) {
+                int p = (j - 1) >> 1;
+                if (vi_less(heap[j], heap[p])) {
+                    vi_t t = heap[j]; heap[j] = heap[p]; heap[p] = t;
+                    j = p;
+                } else {
+                    break;
+                }
+            }
+        } else if (vi_less(heap[0], e)) {
+            heap[0] = e;
+            int j = 0;
+            for (;;) {
+                int l = 2 * j + 1, r = 2 * j + 2, s = j;
+                if (l < cnt && vi_less(heap[l], heap[s])) s = l;
+                if (r < cnt && vi_less(heap[r], heap[s])) s = r;
+                if (s == j) break;
+                vi_t t = heap[j]; heap[j] = heap[s]; heap[s] = t;
+                j = s;
+            }
+        }
+    }
+    qsort(heap, (size_t)cnt, sizeof(vi_t), vi_cmp_desc);
+    for (int j = 0; j < k; j++) out[j] = heap[j].i;
+    free(heap);
+    return 0;
+}
+
+/* MoERouter.route (MoELayer.swift:140-205). GPT-OSS's router
+ * (GPTOSSText.swift:1349-1361: full stable sort, top-k, softmax over the k)
+ * is the topKThenSoftmax branch. */
+int or_route(const float* logits, int T, int E, int k, int gating, int norm_topk,
+             const float* expert_bias, uint32_t* idx, float* weights) {
+    if (E <= 0 || k <= 0 || k > E) return -1;
+    int* sel = (int*)malloc(sizeof(int) * (size_t)k);
+    float* probs = (float*)malloc(sizeof(float) * (size_t)E);
+    float* pick = (float*)malloc(sizeof(float) * (size_t)k);
+    for (int t = 0; t < T; t++) {
+        const float* l = logits + (size_t)t * E;
+        uint32_t* oi = idx + (size_t)t * k;
+        float* ow = weights + (size_t)t * k;
+        if (gating == OR_TOPK_THEN_SOFTMAX ||
+            (gating == OR_SOFTMAX_THEN_TOPK && norm_topk && !expert_bias)) {
+            or_topk_indices(l, E, k, sel);
+            for (int j = 0; j < k; j++) pick[j] = l[sel[j]];
+            or_softmax(pick, k, ow);
+        } else {
+            or_softmax(l, E, probs);
+            if (expert_bias)
+                for (int e = 0; e < E; e++) probs[e] = probs[e] + expert_bias[e];
+            or_topk_indices(probs, E, k, sel);
+            for (int j = 0; j < k; j++) ow[j] = probs[sel[j]];
+            if (norm_topk) {
+                float s = 0.0f;
+                for (int j = 0; j < k; j++) s += ow[j];
+                if (s > 0.0f)
+                    for (int j = 0; j < k; j++) ow[j] = ow[j] / s;
+            }
+        }
+        for (int j = 0; j < k; j++) oi[j] = (uint32_t)sel[j];
+    }
+    free(sel);
+    free(probs);
+    free(pick);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* dispatch plan                                                            */
+/* ------------------------------------------------------------------------ */
+
+typedef struct { uint32_t e, src; } plan_t;
+
+/* Stable merge sort by expert id. */
+static void plan_sort(plan_t* a, plan_t* tmp, size_t n) {
+    if (n < 2) return;
+    size_t h = n / 2;
+    plan_sort(a, tmp, h);
+    plan_sort(a + h, tmp, n - h);
+    size_t i = 0, j = h, o = 0;
+    while (i < h && j < n) tmp[o++] = (a[j].e < a[i].e) ? a[j++] : a[i++];
+    while (i < h) tmp[o++] = a[i++];
+    while (j < n) tmp[o++] = a[j++];
+    memcpy(a, tmp, n * sizeof(plan_t));
+}
+
+/* MoELayer.decodeMany's plan (MoELayer.swift:752-792): the T*k entries are
+ * listed token-major, then stably sorted by expert. perm[p] is the
+ * token-major entry (t*k + s) at sorted position p; inv_perm is its inverse;
+ * offsets is the CSR row start of each expert. */
+int or_dispatch_plan(const uint32_t* idx, int T, int k, int E,
+                     uint32_t* counts, uint32_t* offsets,
+                     uint32_t* perm, uint32_t* inv_perm) {
+    size_t M = (size_t)T * (size_t)k;
+    for (size_t m = 0; m < M; m++)
+        if (idx[m] >= (uint32_t)E) return -1;
+    plan_t* a = (plan_t*)malloc(sizeof(plan_t) * (M ? M : 1));
+    plan_t* tmp = (plan_t*)malloc(sizeof(plan_t) * (M ? M : 1));
+    for (size_t m = 0; m < M; m++) {
+        a[m].e = idx[m];
+        a[m].src = (uint32_t)m;
+    }
+    plan_sort(a, tmp, M);
+    for (int e = 0; e < E; e++) counts[e] = 0;
+    for (size_t p = 0; p < M; p++) {
+        perm[p] = a[p].src;
+        inv_perm[a[p].src] = (uint32_t)p;
+        counts[a[p].e]++;
+    }
+    offsets[0] = 0;
+    for (int e = 0; e < E; e++) offsets[e + 1] = offsets[e] + counts[e];
+    free(a);
+    free(tmp);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* grouped dequant GEMM                                                     */
+/* ------------------------------------------------------------------------ */
+
+/* Restates the CPU m1 oracle of MoEBgemmBm64MppTests.swift:82-114
+ * generalised to every bit width: w = s*q + b in fp32, dot products in
+ * double. Rows are processed expert by expert so each dequantised weight row
+ * is built once. */
+int or_qgemm_rows(const or_qproj* p, const float* a, int M,
+                  const uint32_t* row_expert, float* out) {
+    int N = p->n, K = p->k, gs = p->group_size, bits = p->bits;
+    if (!bits_ok(bits) || gs <= 0 || K % gs || (K * bits) % 32 || M < 0) return -1;
+    size_t row_words = (size_t)K * bits / 32;
+    int groups = K / gs;
+    int E = 0;
+    for (int m = 0; m < M; m++)
+        if ((int)row_expert[m] + 1 > E) E = (int)row_expert[m] + 1;
+    int* cnt = (int*)calloc((size_t)E + 1, sizeof(int));
+    int* start = (int*)calloc((size_t)E + 1, sizeof(int));
+    int* rows = (int*)malloc(sizeof(int) * ((size_t)M + 1));
+    for (int m = 0; m < M; m++) cnt[row_expert[m]]++;
+    for (int e = 0; e < E; e++) start[e + 1] = start[e] + cnt[e];
+    for (int e = 0; e < E; e++) cnt[e] = 0;
+    for (int m = 0; m < M; m++) rows[start[row_expert[m]] + cnt[row_expert[m]]++] = m;
+    float* wrow = (float*)malloc(sizeof(float) * (size_t)K);
+    for (int e = 0; e < E; e++) {
+        if (start[e + 1] == start[e]) continue;
+        for (int n = 0; n < N; n++) {
+            size_t r = (size_t)e * N + n;
+            const uint32_t* wr = p->weight + r * row_words;
+            for (int g = 0; g < groups; g++) {
+                float s = load1(p->scales, p->sb_dt, r * groups + g);
+                float b = load1(p->biases, p->sb_dt, r * groups + g);
+                for (int j = 0; j < gs; j++) {
+                    float q = (float)get_code(wr, bits, (size_t)g * gs + j);
+                    float sq = s * q;
+                    wrow[g * gs + j] = sq + b;
+                }
+            }
+            for (int i = start[e]; i < start[e + 1]; i++) {
+                int m = rows[i];
+                const float* x = a + (size_t)m * K;
+                double acc0 = 0.0, acc1 = 0.0, acc2 = 0.0, acc3 = 0.0;
+                int kk = 0;
+                for (; kk + 4 <= K; kk += 4) {
+                    acc0 += (double)wrow[kk] * (double)x[kk];
+                    acc1 += (double)wrow[kk + 1] * (double)x[kk + 1];
+                    acc2 += (double)wrow[kk + 2] * (double)x[kk + 2];
+                    acc3 += (double)wrow[kk + 3] * (double)x[kk + 3];
+                }
+                for (; kk < K; kk++) acc0 += (double)wrow[kk] * (double)x[kk];
+                out[(size_t)m * N + n] = (float)((acc0 + acc1) + (acc2 + acc3));
+            }
+        }
+    }
+    free(cnt);
+    free(start);
+    free(rows);
+    free(wrow);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* activations and combine                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* SwiGLU silu(g)*u in fp32 (Ops.swift:6400-6411); GPT-OSS clamped
+ * alpha-swish with the upper-only gate clamp (GPTOSSText.swift:1415-1431). */
+float or_act(float g, float u, int act, float alpha, float limit) {
+    if (act == OR_ACT_GPTOSS) {
+        if (g > limit) g = limit;
+        if (u > limit) u = limit;
+        if (u < -limit) u = -limit;
+        float ag = alpha * g;
+        float glu = g / (1.0f + expf(-ag));
+        return glu * (u + 1.0f);
+    }
+    float silu = g / (1.0f + expf(-g));
+    return silu * u;
+}
+
+/* mt_moe_unpermute (Ops.swift:5030-5110) with the combine weights rounded to
+ * the activation dtype first (MoELayer.swift:921-935); fp32 accumulation in
+ * slot order, one rounding at the store. */
+void or_unpermute(const float* Y, const uint32_t* inv_perm, const float* w,
+                  int T, int H, int k, int dt, float* out) {
+    for (int t = 0; t < T; t++) {
+        for (int h = 0; h < H; h++) {
+            float acc = 0.0f;
+            for (int s = 0; s < k; s++) {
+                float ws = or_round_dt(w[(size_t)t * k + s], dt);
+                float prod = ws * Y[(size_t)inv_perm[(size_t)t * k + s] * H + h];
+                acc = acc + prod;
+            }
+            out[(size_t)t * H + h] = or_round_dt(acc, dt);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* whole layer                                                              */
+/* ------------------------------------------------------------------------ */
+
+/* Rounds a [M, N] projection output to dt and applies the optional
+ * per-expert projection bias (GPTOSSText.swift:1403-1410,1439-1441:
+ * round(round(Wx) + b)). */
+static void finish_proj(const or_qproj* p, float* v, int M, const uint32_t* row_expert, int dt) {
+    int N = p->n;
+    for (int m = 0; m < M; m++) {
+        for (int n = 0; n < N; n++) {
+            float r = or_round_dt(v[(size_t)m * N + n], dt);
+            if (p->out_bias) {
+                float b = load1(p->out_bias, dt, (size_t)row_expert[m] * N + n);
+                r = or_round_dt(r + b, dt);
+            }
+            v[(size_t)m * N + n] = r;
+        }
+    }
+}
+
+int or_moe_layer(const or_layer* L, const void* x, int T, void* y,
+                 const float* given_logits,
+                 float* logits_out, uint32_t* idx_out, float* w_out) {
+    int H = L->hidden, E = L->n_experts, k = L->top_k, I = L->intermediate, dt = L->act_dt;
+    if (T <= 0 || H <= 0 || E <= 0 || k <= 0 || k > E || I <= 0) return -1;
+    size_t M = (size_t)T * k;
+    float* xf = (float*)malloc(sizeof(float) * (size_t)T * H);
+    or_load(x, dt, (size_t)T * H, xf);
+
+    /* 1. router projection */
+    float* logits = (float*)malloc(sizeof(float) * (size_t)T * E);
+    if (given_logits) memcpy(logits, given_logits, sizeof(float) * (size_t)T * E);
+    else or_router_logits(x, dt, T, H, L->router_weight, L->router_dt, L->router_bias, E, logits);
+
+    /* 2. routing */
+    uint32_t* idx = (uint32_t*)malloc(sizeof(uint32_t) * M);
+    float* w = (float*)malloc(sizeof(float) * M);
+    or_route(logits, T, E, k, L->gating, L->norm_topk, L->expert_bias, idx, w);
+
+    /* 3. plan */
+    uint32_t* counts = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)E);
+    uint32_t* offsets = (uint32_t*)malloc(sizeof(uint32_t) * ((size_t)E + 1));
+    uint32_t* perm = (uint32_t*)malloc(sizeof(uint32_t) * M);
+    uint32_t* inv = (uint32_t*)malloc(sizeof(uint32_t) * M);
+    or_dispatch_plan(idx, T, k, E, counts, offsets, perm, inv);
+
+    /* 4. gather + gate/up + activation (MoELayer.swift:843-893) */
+    uint32_t* rexp = (uint32_t*)malloc(sizeof(uint32_t) * M);
+    float* a = (float*)malloc(sizeof(float) * M * H);
+    for (size_t p = 0; p < M; p++) {
+        rexp[p] = idx[perm[p]];
+        memcpy(a + p * H, xf + (size_t)(perm[p] / k) * H, sizeof(float) * (size_t)H);
+    }
+    float* g = (float*)malloc(sizeof(float) * M * I);
+    float* u = (float*)malloc(sizeof(float) * M * I);
+    or_qgemm_rows(&L->gate, a, (int)M, rexp, g);
+    or_qgemm_rows(&L->up, a, (int)M, rexp, u);
+    finish_proj(&L->gate, g, (int)M, rexp, dt);
+    finish_proj(&L->up, u, (int)M, rexp, dt);
+    for (size_t i = 0; i < M * (size_t)I; i++)
+        g[i] = or_round_dt(or_act(g[i], u[i], L->activation, L->alpha, L->limit), dt);
+
+    /* 5. down projection (MoELayer.swift:899-902) */
+    float* Y = (float*)malloc(sizeof(float) * M * H);
+    or_qgemm_rows(&L->down, g, (int)M, rexp, Y);
+    finish_proj(&L->down, Y, (int)M, rexp, dt);
+
+    /* 6. weighted combine (MoELayer.swift:936-939) */
+    float* out = (float*)malloc(sizeof(float) * (size_t)T * H);
+    or_unpermute(Y, inv, w, T, H, k, dt, out);
+
+    /* 7. shared expert: Granite-style unconditional add (MoELayer.swift:
+     * 620-624) or Qwen3.5's sigmoid gate (Qwen3xText.swift:1047-1104). */
+    if (L->has_shared) {
+        int SI = L->shared_gate.n;
+        uint32_t* zero = (uint32_t*)calloc((size_t)T, sizeof(uint32_t));
+        float* sg = (float*)malloc(sizeof(float) * (size_t)T * SI);
+        float* su = (float*)malloc(sizeof(float) * (size_t)T * SI);
+        float* so = (float*)malloc(sizeof(float) * (size_t)T * H);
+        or_qgemm_rows(&L->shared_gate, xf, T, zero, sg);
+        or_qgemm_rows(&L->shared_up, xf, T, zero, su);
+        finish_proj(&L->shared_gate, sg, T, zero, dt);
+        finish_proj(&L->shared_up, su, T, zero, dt);
+        for (size_t i = 0; i < (size_t)T * SI; i++)
+            sg[i] = or_round_dt(or_act(sg[i], su[i], OR_ACT_SWIGLU, 0.f, 0.f), dt);
+        or_qgemm_rows(&L->shared_down, sg, T, zero, so);
+        finish_proj(&L->shared_down, so, T, zero, dt);
+        float* gl = NULL;
+        if (L->shared_gate_weight) {
+            gl = (float*)malloc(sizeof(float) * (size_t)T);
+            or_router_logits(x, dt, T, H, L->shared_gate_weight, L->router_dt, NULL, 1, gl);
+        }
+        for (int t = 0; t < T; t++) {
+            float gate = 1.0f;
+            if (gl) gate = 1.0f / (1.0f + expf(-gl[t]));
+            for (int h = 0; h < H; h++) {
+                size_t i = (size_t)t * H + h;
+                float prod = gate * so[i];
+                out[i] = or_round_dt(out[i] + prod, dt);
+            }
+        }
+        free(zero); free(sg); free(su); free(so); free(gl);
+    }
+    or_store(out, dt, (size_t)T * H, y);
+
+    if (logits_out) memcpy(logits_out, logits, sizeof(float) * (size_t)T * E);
+    if (idx_out) memcpy(idx_out, idx, sizeof(uint32_t) * M);
+    if (w_out) memcpy(w_out, w, sizeof(float) * M);
+    free(xf); free(logits); free(idx); free(w); free(counts); free(offsets);
+    free(perm); free(inv); free(rexp); free(a); free(g); free(u); free(Y); free(out);
+    return 0;
+}

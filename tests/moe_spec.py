@@ -1,0 +1,213 @@
+"""Synthetic MoE layers for the parity tests and the
+glue that hands the same numpy arrays to the CPU oracle and to libmoehip.so.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Optional
+
+import numpy as np
+
+import oracle as orc
+
+F32, F16, BF16 = orc.F32, orc.F16, orc.BF16
+
+
+def store(a, dt):
+    """float32 values -> storage array of dt (RNE)."""
+    return orc.from_f32(np.asarray(a, dtype=np.float32), dt)
+
+
+def load(a, dt):
+    return orc.to_f32(a, dt)
+
+
+def gen_qproj(rng, E, N, K, bits, gs, sb_dt, s_range=(0.005, 0.02), b_range=(-0.1, 0.1),
+              out_bias_dt=None):
+    """Uniform codes (random u32 words are uniform codes at every width),
+    scales ~U(s_range), biases ~U(b_range) stored in sb_dt."""
+    words = K * bits // 32
+    w = rng.integers(0, 2**32, size=(E, N, words), dtype=np.uint64).astype(np.uint32)
+    s = store(rng.uniform(*s_range, size=(E, N, K // gs)), sb_dt)
+    b = store(rng.uniform(*b_range, size=(E, N, K // gs)), sb_dt)
+    ob = None
+    if out_bias_dt is not None:
+        ob = store(rng.normal(0, 0.1, size=(E, N)), out_bias_dt)
+    return orc.QProj(w, s, b, bits, gs, sb_dt, out_bias=ob)
+
+
+@dataclass
+class LayerSpec:
+    hidden: int
+    n_experts: int
+    top_k: int
+    intermediate: int
+    act_dt: int
+    router_weight: np.ndarray
+    router_dt: int
+    gate: orc.QProj
+    up: orc.QProj
+    down: orc.QProj
+    gating: int = orc.SOFTMAX_THEN_TOPK
+    norm_topk: bool = True
+    router_bias: Optional[np.ndarray] = None
+    expert_bias: Optional[np.ndarray] = None
+    activation: int = orc.ACT_SWIGLU
+    alpha: float = 1.702
+    limit: float = 7.0
+    shared: Optional[tuple] = None
+    shared_gate_weight: Optional[np.ndarray] = None
+    name: str = ""
+    meta: dict = field(default_factory=dict)
+
+    # ---- CPU oracle view -------------------------------------------------
+    def oracle_struct(self) -> orc.OrLayer:
+        L = orc.OrLayer()
+        L.hidden, L.n_experts, L.top_k = self.hidden, self.n_experts, self.top_k
+        L.intermediate, L.act_dt = self.intermediate, self.act_dt
+        L.router_weight = self.router_weight.ctypes.data
+        L.router_dt = self.router_dt
+        L.router_bias = None if self.router_bias is None else self.router_bias.ctypes.data
+        L.gating, L.norm_topk = self.gating, int(self.norm_topk)
+        L.expert_bias = None if self.expert_bias is None else self.expert_bias.ctypes.data
+        L.gate, L.up, L.down = self.gate.c(), self.up.c(), self.down.c()
+        L.activation, L.alpha, L.limit = self.activation, self.alpha, self.limit
+        if self.shared is not None:
+            L.has_shared = 1
+            L.shared_gate, L.shared_up, L.shared_down = (p.c() for p in self.shared)
+            L.shared_gate_weight = (None if self.shared_gate_weight is None
+                                    else self.shared_gate_weight.ctypes.data)
+        self._keep = L
+        return L
+
+    # ---- device view (GPU tests) ----------------------------------------
+    def device(self):
+        import torch
+        from ffai_amd import layer as fl
+
+        def T(a):
+            if a is None:
+                return None
+            if a.dtype == np.uint16:
+                return torch.from_numpy(a.view(np.int16)).cuda().view(torch.bfloat16)
+            if a.dtype == np.uint32:
+                return torch.from_numpy(a.view(np.int32)).cuda()
+            return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+        def P(q):
+            return fl.StackedExperts(T(q.weight), T(q.scales), T(q.biases), q.bits, q.gs,
+                                     out_bias=T(q.out_bias))
+
+        act = {F32: torch.float32, F16: torch.float16, BF16: torch.bfloat16}[self.act_dt]
+        router = fl.MoERouter(self.n_experts, self.top_k, self.gating, self.norm_topk,
+                              None if self.expert_bias is None else T(self.expert_bias))
+        shared = None if self.shared is None else tuple(P(q) for q in self.shared)
+        return fl.MoELayer(router_weight=T(self.router_weight), router=router, gate=P(self.gate),
+                           up=P(self.up), down=P(self.down), hidden=self.hidden, act_dtype=act,
+                           router_bias=T(self.router_bias), activation=self.activation,
+                           alpha=self.alpha, limit=self.limit, shared=shared,
+                           shared_gate_weight=T(self.shared_gate_weight))
+
+    def x(self, T, seed=0):
+        rng = np.random.default_rng(seed + 1000)
+        return store(rng.normal(0, 1, size=(T, self.hidden)), self.act_dt)
+
+
+def to_torch(a):
+    import torch
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda().view(torch.bfloat16)
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def to_numpy_f32(t):
+    import torch
+    return t.detach().float().cpu().numpy() if t.dtype != torch.float32 else t.detach().cpu().numpy()
+
+
+# ---------------------------------------------------------------- configs --
+
+def cfg_tiny(seed=0, act_dt=F16):
+    """hidden=256, 8 experts, top-2, I=512, 4-bit gs64, f16."""
+    rng = np.random.default_rng(seed)
+    H, E, k, I = 256, 8, 2, 512
+    return LayerSpec(H, E, k, I, act_dt,
+                     router_weight=store(rng.normal(0, 0.02, size=(E, H)), F16), router_dt=F16,
+                     gate=gen_qproj(rng, E, I, H, 4, 64, F16), up=gen_qproj(rng, E, I, H, 4, 64, F16),
+                     down=gen_qproj(rng, E, H, I, 4, 64, F16), name="tiny")
+
+
+def cfg_gptoss(seed=0, n_experts=32, hidden=2880, inter=2880, expert_bias=False):
+    """GPT-OSS-20B-shaped decode layer (4-bit gs64, bf16)."""
+    rng = np.random.default_rng(seed)
+    H, E, k, I = hidden, n_experts, 4, inter
+    ob = BF16 if expert_bias else None
+    return LayerSpec(H, E, k, I, BF16,
+                     router_weight=store(rng.normal(0, 1 / np.sqrt(H), size=(E, H)), BF16),
+                     router_dt=BF16, router_bias=store(rng.normal(0, 0.1, size=E), BF16),
+                     gating=orc.TOPK_THEN_SOFTMAX,
+                     gate=gen_qproj(rng, E, I, H, 4, 64, BF16, out_bias_dt=ob),
+                     up=gen_qproj(rng, E, I, H, 4, 64, BF16, out_bias_dt=ob),
+                     down=gen_qproj(rng, E, H, I, 4, 64, BF16, out_bias_dt=ob),
+                     activation=orc.ACT_GPTOSS, alpha=1.702, limit=7.0, name="gptoss")
+
+
+def cfg_qwen3(seed=0, n_experts=128, hidden=2048, inter=768, router_bias=None):
+    """configs[2]/[3]: Qwen3-MoE shape, 4-bit gs64, fp16 scales, bf16 acts."""
+    rng = np.random.default_rng(seed)
+    H, E, k, I = hidden, n_experts, 8, inter
+    return LayerSpec(H, E, k, I, BF16,
+                     router_weight=store(rng.normal(0, 1 / np.sqrt(H), size=(E, H)), BF16),
+                     router_dt=BF16,
+                     router_bias=None if router_bias is None else store(router_bias, BF16),
+                     gate=gen_qproj(rng, E, I, H, 4, 64, F16), up=gen_qproj(rng, E, I, H, 4, 64, F16),
+                     down=gen_qproj(rng, E, H, I, 4, 64, F16), name="qwen3")
+
+
+def zipf_router_bias(E, s=1.1, beta=1.0, seed=0):
+    """beta * log p_e with p Zipf(s) over a random permutation of ranks."""
+    rng = np.random.default_rng(seed + 7)
+    ranks = rng.permutation(E) + 1
+    p = ranks.astype(np.float64) ** (-s)
+    p /= p.sum()
+    return (beta * np.log(p)).astype(np.float32)
+
+
+def cfg_mixed(seed=0, n_experts=256, hidden=2048, inter=512, shared_inter=512):
+    """3-bit gate/up, 6-bit down, bf16 scales, shared expert with
+    a sigmoid gate."""
+    rng = np.random.default_rng(seed)
+    H, E, k, I = hidden, n_experts, 8, inter
+    shared = (gen_qproj(rng, 1, shared_inter, H, 3, 64, BF16),
+              gen_qproj(rng, 1, shared_inter, H, 3, 64, BF16),
+              gen_qproj(rng, 1, H, shared_inter, 6, 64, BF16))
+    return LayerSpec(H, E, k, I, BF16,
+                     router_weight=store(rng.normal(0, 1 / np.sqrt(H), size=(E, H)), BF16),
+                     router_dt=BF16,
+                     gate=gen_qproj(rng, E, I, H, 3, 64, BF16), up=gen_qproj(rng, E, I, H, 3, 64, BF16),
+                     down=gen_qproj(rng, E, H, I, 6, 64, BF16), shared=shared,
+                     shared_gate_weight=store(rng.normal(0, 1 / np.sqrt(H), size=(1, H)), BF16),
+                     name="mixed")
+
+
+# ------------------------------------------------------------- tolerance --
+
+def check_close(got, ref, dt, label=""):
+    """The layer's float bar: fp16/bf16 outputs within 2e-2 absolute
+    (relative to |ref| once |ref| > 1) and 1e-3 mean relative error against
+    the fp32-accumulated oracle; f32 outputs within 1e-3 (MoELayerTests.swift
+    :224 uses 1e-3)."""
+    got = np.asarray(got, dtype=np.float64).ravel()
+    ref = np.asarray(ref, dtype=np.float64).ravel()
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    assert np.all(np.isfinite(got)), f"{label}: non-finite output"
+    d = np.abs(got - ref)
+    scale = np.maximum(1.0, np.abs(ref))
+    max_scaled = float((d / scale).max()) if d.size else 0.0
+    mean_rel = float(d.mean() / max(np.abs(ref).mean(), 1e-30)) if d.size else 0.0
+    tol = 1e-3 if dt == F32 else 2e-2
+    assert max_scaled <= tol, f"{label}: max |d|/max(1,|ref|) = {max_scaled:.3e} > {tol}"
+    if dt != F32:
+        assert mean_rel <= 1e-3, f"{label}: mean relative error {mean_rel:.3e} > 1e-3"
+    return max_scaled, mean_rel

@@ -1,0 +1,291 @@
+"""GPU parity tests: libmoehip.so through its C ABI against the CPU oracle.
+
+Integer outputs (expert ids, dispatch permutations, unpacked codes) must be
+bit-exact; float outputs meet moe_spec.check_close (2e-2 max-abs scaled by
+max(1,|ref|), 1e-3 mean relative, bf16/f16; 1e-3 for f32).
+Routing is compared at the router input: the oracle routes from the logits
+the GPU produced, so ids and weights must match exactly, and the GPU logits
+themselves must be within one storage ulp of the oracle's."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from moe_spec import (BF16, F16, F32, cfg_gptoss, cfg_mixed, cfg_qwen3, cfg_tiny, check_close, load,
+                      store, to_numpy_f32, to_torch, zipf_router_bias)
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+from ffai_amd import _lib  # noqa: E402
+from ffai_amd._lib import check  # noqa: E402
+
+
+def _stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _p(t):
+    return C.c_void_p(t.data_ptr())
+
+
+def _u32(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    _lib.load()
+    yield
+    torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------ bit stream --
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+def test_dequantize_codes_bit_exact(bits):
+    rng = np.random.default_rng(bits)
+    n = 64 * 97
+    words = rng.integers(0, 2**32, n * bits // 32, dtype=np.uint64).astype(np.uint32)
+    ones = np.ones(n // 64, np.float32)
+    zeros = np.zeros(n // 64, np.float32)
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    check(_lib.load().moe_dequantize_affine(_p(to_torch(words.view(np.int32))), _p(to_torch(ones)),
+                                            _p(to_torch(zeros)), F32, bits, 64, n, _p(out), F32,
+                                            _stream()))
+    torch.cuda.synchronize()
+    codes = orc.unpack_codes(words, bits, n)
+    assert np.array_equal(out.cpu().numpy(), codes.astype(np.float32))
+    # bf16 scales/biases, bf16 output: the oracle's dequant rounded once
+    s = store(rng.uniform(0.005, 0.02, n // 64), BF16)
+    b = store(rng.uniform(-0.1, 0.1, n // 64), BF16)
+    out2 = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    check(_lib.load().moe_dequantize_affine(_p(to_torch(words.view(np.int32))), _p(to_torch(s)),
+                                            _p(to_torch(b)), BF16, bits, 64, n, _p(out2), BF16,
+                                            _stream()))
+    torch.cuda.synchronize()
+    ref = orc.round_dt(orc.dequantize_affine(words, s, b, BF16, bits, 64, n), BF16)
+    got = out2.float().cpu().numpy()
+    assert np.array_equal(got, ref)
+
+
+# ----------------------------------------------------------------- router --
+
+@pytest.mark.parametrize("E,k", [(8, 2), (32, 4), (128, 8), (256, 8), (512, 16)])
+@pytest.mark.parametrize("mode", ["renorm", "topk_softmax", "no_renorm", "bias"])
+def test_router_topk_bit_exact(E, k, mode):
+    rng = np.random.default_rng(E + k)
+    T = 96
+    logits = np.concatenate([rng.integers(-3, 4, size=(T // 2, E)).astype(np.float32),
+                             rng.normal(0, 1, size=(T // 2, E)).astype(np.float32)])
+    lb = store(logits, BF16)
+    lf = load(lb, BF16)
+    gating, norm, eb = {"renorm": (0, True, None), "topk_softmax": (1, True, None),
+                        "no_renorm": (0, False, None),
+                        "bias": (0, True, rng.normal(0, 0.01, E).astype(np.float32))}[mode]
+    idx = torch.empty(T, k, dtype=torch.int32, device="cuda")
+    w = torch.empty(T, k, dtype=torch.float32, device="cuda")
+    ebt = None if eb is None else to_torch(eb)
+    check(_lib.load().moe_router_topk(_p(to_torch(lb)), BF16, T, E, k, gating, int(norm),
+                                      None if ebt is None else _p(ebt), _p(idx), _p(w), _stream()))
+    torch.cuda.synchronize()
+    ref_idx, ref_w = orc.route(lf, k, gating, norm, eb)
+    assert np.array_equal(_u32(idx), ref_idx)
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), ref_w.view(np.uint32))
+
+
+@pytest.mark.parametrize("dt,wdt,E,H", [(BF16, BF16, 128, 2048), (F16, F16, 8, 256), (BF16, BF16, 32, 2880),
+                                         (F32, F32, 4, 64)])
+def test_router_logits_within_one_ulp(dt, wdt, E, H):
+    rng = np.random.default_rng(H)
+    T = 19
+    x = store(rng.normal(0, 1, (T, H)), dt)
+    W = store(rng.normal(0, 1 / np.sqrt(H), (E, H)), wdt)
+    bias = store(rng.normal(0, 0.1, E), dt)
+    out = torch.empty(T, E, dtype={BF16: torch.bfloat16, F16: torch.float16, F32: torch.float32}[dt],
+                      device="cuda")
+    check(_lib.load().moe_router_logits(_p(to_torch(x)), dt, T, H, _p(to_torch(W)), wdt,
+                                        _p(to_torch(bias)), E, _p(out), _stream()))
+    torch.cuda.synchronize()
+    ref = orc.router_logits(x, dt, W, wdt, bias)
+    got = to_numpy_f32(out)
+    ulp = np.abs(ref) * (2.0 ** -7 if dt == BF16 else 2.0 ** -10 if dt == F16 else 2.0 ** -22) + 1e-6
+    # the bias add rounds a second time: two storage ulps at most
+    assert np.all(np.abs(got - ref) <= 2.02 * ulp)
+
+
+# ------------------------------------------------------------------- plan --
+
+@pytest.mark.parametrize("T,k,E", [(1, 8, 128), (1, 4, 32), (16, 2, 8), (64, 8, 128), (512, 8, 128),
+                                   (4096, 8, 128), (2048, 8, 256), (777, 3, 1000)])
+def test_dispatch_plan_bit_exact(T, k, E):
+    rng = np.random.default_rng(T * 7 + E)
+    if T >= 2048:  # skewed load as in the Zipf prefill config
+        p = (np.arange(E) + 1.0) ** -1.1
+        idx = rng.choice(E, size=(T, k), p=p / p.sum()).astype(np.uint32)
+    else:
+        idx = rng.integers(0, E, (T, k)).astype(np.uint32)
+    M = T * k
+    lib = _lib.load()
+    counts = torch.empty(E, dtype=torch.int32, device="cuda")
+    offsets = torch.empty(E + 1, dtype=torch.int32, device="cuda")
+    perm = torch.empty(M, dtype=torch.int32, device="cuda")
+    inv = torch.empty(M, dtype=torch.int32, device="cuda")
+    wsb = lib.moe_dispatch_workspace_bytes(T, k, E)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
+    check(lib.moe_dispatch_plan(_p(to_torch(idx.view(np.int32))), T, k, E, _p(counts), _p(offsets),
+                                _p(perm), _p(inv), _p(ws), wsb, _stream()))
+    torch.cuda.synchronize()
+    rc, ro, rp, ri = orc.dispatch_plan(idx, E)
+    assert np.array_equal(_u32(counts), rc)
+    assert np.array_equal(_u32(offsets), ro)
+    assert np.array_equal(_u32(perm), rp)
+    assert np.array_equal(_u32(inv), ri)
+
+
+# ------------------------------------------------------- grouped products --
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("dt,sb", [(BF16, BF16), (BF16, F16), (F16, F16), (F32, F32)])
+def test_expert_matmul_all_widths(bits, dt, sb):
+    rng = np.random.default_rng(bits * 10 + dt)
+    E, N, K, M = 6, 96, 320, 23
+    from moe_spec import gen_qproj
+    p = gen_qproj(rng, E, N, K, bits, 64, sb)
+    rows = np.sort(rng.integers(0, E, M)).astype(np.uint32)
+    offsets = np.searchsorted(rows, np.arange(E + 1)).astype(np.uint32)
+    a = store(rng.normal(0, 1, (M, K)), dt)
+    lib = _lib.load()
+    q = _lib.QProj(0, 0, 0, None, bits, 64, sb, N, K, E)
+    wt, st, bt = to_torch(p.weight.view(np.int32)), to_torch(p.scales), to_torch(p.biases)
+    q.weight, q.scales, q.biases = wt.data_ptr(), st.data_ptr(), bt.data_ptr()
+    at = to_torch(a)
+    out = torch.empty(M, N, dtype=at.dtype, device="cuda")
+    wsb = lib.moe_expert_matmul_workspace_bytes(E, M)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    offt = to_torch(offsets.view(np.int32))
+    check(lib.moe_expert_matmul(C.byref(q), _p(at), dt, None, 1, M, _p(offt), _p(out), _p(ws), wsb,
+                                _stream()))
+    torch.cuda.synchronize()
+    ref = orc.round_dt(orc.qgemm_rows(p, load(a, dt), rows), dt)
+    check_close(to_numpy_f32(out), ref, dt, f"expert_matmul bits={bits}")
+
+
+# ------------------------------------------------------------ whole layer --
+
+def run_layer(spec, T, seed=0):
+    dev = spec.device()
+    x = spec.x(T, seed)
+    y, tr = dev.forward(to_torch(x), trace=True)
+    torch.cuda.synchronize()
+    logits_gpu = to_numpy_f32(tr["logits"])
+    logits_cpu = orc.router_logits(x, spec.act_dt, spec.router_weight, spec.router_dt, spec.router_bias)
+    ulp = np.abs(logits_cpu) * (2.0 ** -7 if spec.act_dt == BF16 else 2.0 ** -10 if spec.act_dt == F16
+                                else 2.0 ** -20) + 1e-6
+    # a bias add rounds twice, so allow two storage ulps
+    assert np.all(np.abs(logits_gpu - logits_cpu) <= 2.02 * ulp), "router logits"
+    y_ref, _, idx_ref, w_ref = orc.moe_layer(spec, x, given_logits=logits_gpu)
+    assert np.array_equal(_u32(tr["topk_idx"]), idx_ref), "expert ids"
+    assert np.array_equal(tr["topk_weight"].cpu().numpy().view(np.uint32), w_ref.view(np.uint32)), \
+        "combine weights"
+    _, _, rp, _ = orc.dispatch_plan(idx_ref, spec.n_experts)
+    assert np.array_equal(_u32(tr["perm"]), rp), "dispatch permutation"
+    stats = check_close(to_numpy_f32(y), load(y_ref, spec.act_dt), spec.act_dt, f"{spec.name} T={T}")
+    print(f"{spec.name} T={T}: max|d|/max(1,|ref|)={stats[0]:.3e} mean_rel={stats[1]:.3e}")
+    return dev, x, y
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_layer_scalar_kat(shared):
+    """The reference's own MoELayer KAT (MoELayerTests.swift:147-265)."""
+    from test_oracle_golden import scalar_layer_expected, scalar_layer_spec
+    spec = scalar_layer_spec(shared)
+    dev = spec.device()
+    x = np.zeros((1, 64), np.float32)
+    x[0, 0] = 2.0
+    y = dev.forward(to_torch(x)).cpu().numpy()
+    assert abs(y[0, 0] - scalar_layer_expected(shared)) < 1e-3
+    assert np.all(y[0, 1:] == 0)
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    return cfg_tiny()
+
+
+@pytest.mark.parametrize("T", [1, 2, 16])
+def test_layer_tiny(tiny, T):
+    run_layer(tiny, T)
+
+
+@pytest.fixture(scope="module")
+def gptoss():
+    return cfg_gptoss()
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_layer_gptoss(gptoss, T):
+    run_layer(gptoss, T, seed=T)
+
+
+def test_layer_gptoss_expert_bias():
+    run_layer(cfg_gptoss(seed=3, n_experts=8, hidden=512, inter=640, expert_bias=True), 1)
+    run_layer(cfg_gptoss(seed=3, n_experts=8, hidden=512, inter=640, expert_bias=True), 5)
+
+
+@pytest.fixture(scope="module")
+def qwen3():
+    return cfg_qwen3()
+
+
+@pytest.mark.parametrize("B", [1, 4, 16, 64])
+def test_layer_qwen3_decode(qwen3, B):
+    run_layer(qwen3, B, seed=B)
+
+
+def test_layer_qwen3_prefill_zipf():
+    spec = cfg_qwen3(seed=5, router_bias=zipf_router_bias(128, 1.1, beta=1.0))
+    run_layer(spec, 256)
+
+
+@pytest.fixture(scope="module")
+def mixed():
+    return cfg_mixed()
+
+
+@pytest.mark.parametrize("T", [1, 24])
+def test_layer_mixed_bits_shared(mixed, T):
+    run_layer(mixed, T)
+
+
+def test_layer_is_deterministic(qwen3):
+    dev = qwen3.device()
+    x = to_torch(qwen3.x(64, seed=9))
+    y1 = dev.forward(x).clone()
+    y2 = dev.forward(x)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+
+
+def test_layer_handle_matches_forward(tiny):
+    """moe_layer_create / decode / decode_many (the MoELayer instance API)."""
+    dev = tiny.device()
+    lib = _lib.load()
+    h = C.c_void_p()
+    check(lib.moe_layer_create(C.byref(dev.desc), C.byref(h)))
+    try:
+        x = to_torch(tiny.x(16))
+        ref = dev.forward(x)
+        out = torch.empty_like(x)
+        check(lib.moe_layer_decode_many(h, _p(x), 16, _p(out), _stream()))
+        one = torch.empty_like(x[:1])
+        check(lib.moe_layer_decode(h, _p(x[:1].contiguous()), _p(one), _stream()))
+        ref1 = dev.forward(x[:1].contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+        assert torch.equal(one.view(torch.int16), ref1.view(torch.int16))
+    finally:
+        lib.moe_layer_destroy(h)
