@@ -1,8 +1,8 @@
 """GPU parity tests: libmoehip.so through its C ABI against the CPU oracle.
 
 Integer outputs (expert ids, dispatch permutations, unpacked codes) must be
-bit-exact; float outputs meet moe_spec.check_close (2e-2 max-abs scaled by
-max(1,|ref|), 1e-3 mean relative, bf16/f16; 1e-3 for f32).
+bit-exact; float outputs meet moe_spec.check_close (bf16/f16: max-abs 2e-2 on
+the output's RMS scale and 1e-3 mean relative; f32: 1e-3).
 Routing is compared at the router input: the oracle routes from the logits
 the GPU produced, so ids and weights must match exactly, and the GPU logits
 themselves must be within one storage ulp of the oracle's."""
@@ -53,9 +53,11 @@ def test_dequantize_codes_bit_exact(bits):
     ones = np.ones(n // 64, np.float32)
     zeros = np.zeros(n // 64, np.float32)
     out = torch.empty(n, dtype=torch.float32, device="cuda")
-    check(_lib.load().moe_dequantize_affine(_p(to_torch(words.view(np.int32))), _p(to_torch(ones)),
-                                            _p(to_torch(zeros)), F32, bits, 64, n, _p(out), F32,
-                                            _stream()))
+    # device copies are held in locals: a temporary's memory could be reused
+    # by the next allocation before the kernel runs
+    wt, onest, zerost = to_torch(words.view(np.int32)), to_torch(ones), to_torch(zeros)
+    check(_lib.load().moe_dequantize_affine(_p(wt), _p(onest), _p(zerost), F32, bits, 64, n,
+                                            _p(out), F32, _stream()))
     torch.cuda.synchronize()
     codes = orc.unpack_codes(words, bits, n)
     assert np.array_equal(out.cpu().numpy(), codes.astype(np.float32))
@@ -63,9 +65,9 @@ def test_dequantize_codes_bit_exact(bits):
     s = store(rng.uniform(0.005, 0.02, n // 64), BF16)
     b = store(rng.uniform(-0.1, 0.1, n // 64), BF16)
     out2 = torch.empty(n, dtype=torch.bfloat16, device="cuda")
-    check(_lib.load().moe_dequantize_affine(_p(to_torch(words.view(np.int32))), _p(to_torch(s)),
-                                            _p(to_torch(b)), BF16, bits, 64, n, _p(out2), BF16,
-                                            _stream()))
+    st, bt = to_torch(s), to_torch(b)
+    check(_lib.load().moe_dequantize_affine(_p(wt), _p(st), _p(bt), BF16, bits, 64, n, _p(out2),
+                                            BF16, _stream()))
     torch.cuda.synchronize()
     ref = orc.round_dt(orc.dequantize_affine(words, s, b, BF16, bits, 64, n), BF16)
     got = out2.float().cpu().numpy()
@@ -89,7 +91,8 @@ def test_router_topk_bit_exact(E, k, mode):
     idx = torch.empty(T, k, dtype=torch.int32, device="cuda")
     w = torch.empty(T, k, dtype=torch.float32, device="cuda")
     ebt = None if eb is None else to_torch(eb)
-    check(_lib.load().moe_router_topk(_p(to_torch(lb)), BF16, T, E, k, gating, int(norm),
+    lt = to_torch(lb)
+    check(_lib.load().moe_router_topk(_p(lt), BF16, T, E, k, gating, int(norm),
                                       None if ebt is None else _p(ebt), _p(idx), _p(w), _stream()))
     torch.cuda.synchronize()
     ref_idx, ref_w = orc.route(lf, k, gating, norm, eb)
@@ -107,8 +110,9 @@ def test_router_logits_within_one_ulp(dt, wdt, E, H):
     bias = store(rng.normal(0, 0.1, E), dt)
     out = torch.empty(T, E, dtype={BF16: torch.bfloat16, F16: torch.float16, F32: torch.float32}[dt],
                       device="cuda")
-    check(_lib.load().moe_router_logits(_p(to_torch(x)), dt, T, H, _p(to_torch(W)), wdt,
-                                        _p(to_torch(bias)), E, _p(out), _stream()))
+    xt, Wt, bt = to_torch(x), to_torch(W), to_torch(bias)
+    check(_lib.load().moe_router_logits(_p(xt), dt, T, H, _p(Wt), wdt, _p(bt), E, _p(out),
+                                        _stream()))
     torch.cuda.synchronize()
     ref = orc.router_logits(x, dt, W, wdt, bias)
     got = to_numpy_f32(out)
@@ -136,7 +140,8 @@ def test_dispatch_plan_bit_exact(T, k, E):
     inv = torch.empty(M, dtype=torch.int32, device="cuda")
     wsb = lib.moe_dispatch_workspace_bytes(T, k, E)
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
-    check(lib.moe_dispatch_plan(_p(to_torch(idx.view(np.int32))), T, k, E, _p(counts), _p(offsets),
+    idxt = to_torch(idx.view(np.int32))
+    check(lib.moe_dispatch_plan(_p(idxt), T, k, E, _p(counts), _p(offsets),
                                 _p(perm), _p(inv), _p(ws), wsb, _stream()))
     torch.cuda.synchronize()
     rc, ro, rp, ri = orc.dispatch_plan(idx, E)
@@ -194,7 +199,7 @@ def run_layer(spec, T, seed=0):
     _, _, rp, _ = orc.dispatch_plan(idx_ref, spec.n_experts)
     assert np.array_equal(_u32(tr["perm"]), rp), "dispatch permutation"
     stats = check_close(to_numpy_f32(y), load(y_ref, spec.act_dt), spec.act_dt, f"{spec.name} T={T}")
-    print(f"{spec.name} T={T}: max|d|/max(1,|ref|)={stats[0]:.3e} mean_rel={stats[1]:.3e}")
+    print(f"{spec.name} T={T}: max|d|/rms={stats[0]:.3e} mean_rel={stats[1]:.3e}")
     return dev, x, y
 
 
