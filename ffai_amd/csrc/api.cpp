@@ -24,12 +24,12 @@ hipError_t launch_gemv_b4(int, int, bool, int, const GemvArgs&, int, hipStream_t
 hipError_t launch_gemv_b5(int, int, bool, int, const GemvArgs&, int, hipStream_t);
 hipError_t launch_gemv_b6(int, int, bool, int, const GemvArgs&, int, hipStream_t);
 hipError_t launch_gemv_b8(int, int, bool, int, const GemvArgs&, int, hipStream_t);
-hipError_t launch_down_combine_b2(int, int, const DownCombineArgs&, int, hipStream_t);
-hipError_t launch_down_combine_b3(int, int, const DownCombineArgs&, int, hipStream_t);
-hipError_t launch_down_combine_b4(int, int, const DownCombineArgs&, int, hipStream_t);
-hipError_t launch_down_combine_b5(int, int, const DownCombineArgs&, int, hipStream_t);
-hipError_t launch_down_combine_b6(int, int, const DownCombineArgs&, int, hipStream_t);
-hipError_t launch_down_combine_b8(int, int, const DownCombineArgs&, int, hipStream_t);
+hipError_t launch_dec1_b2(int, int, bool, int, int, const void*, int, size_t, hipStream_t);
+hipError_t launch_dec1_b3(int, int, bool, int, int, const void*, int, size_t, hipStream_t);
+hipError_t launch_dec1_b4(int, int, bool, int, int, const void*, int, size_t, hipStream_t);
+hipError_t launch_dec1_b5(int, int, bool, int, int, const void*, int, size_t, hipStream_t);
+hipError_t launch_dec1_b6(int, int, bool, int, int, const void*, int, size_t, hipStream_t);
+hipError_t launch_dec1_b8(int, int, bool, int, int, const void*, int, size_t, hipStream_t);
 
 hipError_t launch_gemv(int bits, int xdt, int sbdt, bool gateup, int tokmax, const GemvArgs& a,
                        int grid, hipStream_t st) {
@@ -44,17 +44,30 @@ hipError_t launch_gemv(int bits, int xdt, int sbdt, bool gateup, int tokmax, con
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_down_combine(int bits, int xdt, int sbdt, const DownCombineArgs& a, int grid,
-                               hipStream_t st) {
+static hipError_t launch_dec1(int bits, int xdt, int sbdt, bool down, int pr, int ur,
+                              const void* args, int grid, size_t smem, hipStream_t st) {
   switch (bits) {
-    case 2: return launch_down_combine_b2(xdt, sbdt, a, grid, st);
-    case 3: return launch_down_combine_b3(xdt, sbdt, a, grid, st);
-    case 4: return launch_down_combine_b4(xdt, sbdt, a, grid, st);
-    case 5: return launch_down_combine_b5(xdt, sbdt, a, grid, st);
-    case 6: return launch_down_combine_b6(xdt, sbdt, a, grid, st);
-    case 8: return launch_down_combine_b8(xdt, sbdt, a, grid, st);
+    case 2: return launch_dec1_b2(xdt, sbdt, down, pr, ur, args, grid, smem, st);
+    case 3: return launch_dec1_b3(xdt, sbdt, down, pr, ur, args, grid, smem, st);
+    case 4: return launch_dec1_b4(xdt, sbdt, down, pr, ur, args, grid, smem, st);
+    case 5: return launch_dec1_b5(xdt, sbdt, down, pr, ur, args, grid, smem, st);
+    case 6: return launch_dec1_b6(xdt, sbdt, down, pr, ur, args, grid, smem, st);
+    case 8: return launch_dec1_b8(xdt, sbdt, down, pr, ur, args, grid, smem, st);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_gateup1(int bits, int xdt, int sbdt, const Decode1Args& a, int grid,
+                          hipStream_t st) {
+  const int L = 1 << a.lg, ur = (a.K / 32 + L - 1) / L;
+  return launch_dec1(bits, xdt, sbdt, false, 1, ur, &a, grid, 0, st);
+}
+
+hipError_t launch_down1(int bits, int xdt, int sbdt, const Down1Args& a, int grid, size_t smem,
+                        hipStream_t st) {
+  const int L = 1 << a.lg, SG = 64 >> a.lg;
+  const int ur = (a.K / 32 + L - 1) / L, pr = (a.k + SG - 1) / SG;
+  return launch_dec1(bits, xdt, sbdt, true, pr, ur, &a, grid, smem, st);
 }
 
 size_t gemv_smem_bytes(int xdt, int K, int tok_chunk) {
@@ -62,7 +75,6 @@ size_t gemv_smem_bytes(int xdt, int K, int tok_chunk) {
   return (size_t)tok_chunk * ((size_t)K * xs + (size_t)(K / 32) * 4);
 }
 
-size_t down_combine_smem_bytes(int, int, int) { return 0; }
 }  // namespace moe
 
 using namespace moe;
@@ -212,6 +224,7 @@ moe_status validate_layer_impl(const moe_layer_desc* d) {
                 g->sb_dtype, dn->sb_dtype);
   if (d->n_experts > kMaxExperts)
     return fail(MOE_ERR_UNSUPPORTED, "MoELayer: nExperts=%d above %d", d->n_experts, kMaxExperts);
+  if (d->top_k > 64) return fail(MOE_ERR_UNSUPPORTED, "MoELayer: topK=%d above 64", d->top_k);
   if (d->has_shared) {
     MOE_TRY(validate_qproj_named(&d->shared_gate, "shared_expert.gate_proj"));
     MOE_TRY(validate_qproj_named(&d->shared_up, "shared_expert.up_proj"));
@@ -421,6 +434,7 @@ extern "C" moe_status moe_router_topk(const void* logits, int32_t dtype, int32_t
   if (!dt_ok(dtype)) return fail(MOE_ERR_INVALID, "router_topk: bad dtype");
   if (n_experts > kMaxExperts)
     return fail(MOE_ERR_UNSUPPORTED, "router_topk: nExperts=%d above %d", n_experts, kMaxExperts);
+  if (k > 64) return fail(MOE_ERR_UNSUPPORTED, "router_topk: k=%d above 64", k);
   MOE_HIP(launch_router_topk(logits, dtype, T, n_experts, k, gating, norm_topk_prob, expert_bias,
                              topk_idx, topk_weight, stream),
           "router top-k launch");
@@ -569,6 +583,35 @@ moe_status copy_trace(const moe_layer_desc* d, int T, void* ws, const Workspace&
   return MOE_OK;
 }
 
+// Shared expert (Qwen3xText.swift:928-1104; MoELayer.swift:620-624): gate/up
+// + SwiGLU, down, and the optional sigmoid gate logit, into the workspace.
+// Returns the combine mode: 0 none, 1 unconditional add, 2 sigmoid-gated.
+moe_status shared_expert(const moe_layer_desc* d, const void* x, int T, void* ws,
+                         const Workspace& w, hipStream_t st, int* smode) {
+  *smode = 0;
+  if (!d->has_shared) return MOE_OK;
+  const int xdt = d->act_dtype;
+  const bool single = (T == 1);
+  *smode = d->shared_gate_weight ? 2 : 1;
+  MOE_HIP(launch_identity_plan(at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), T, st),
+          "identity plan launch");
+  MOE_TRY(run_gemv(d->shared_gate, &d->shared_up, x, xdt, nullptr, 1, at<uint32_t>(ws, w.s_off),
+                   at<uint32_t>(ws, w.s_used), 1, T, single, at<void>(ws, w.s_act), MOE_ACT_SWIGLU,
+                   0.f, 0.f, st));
+  MOE_TRY(run_gemv(d->shared_down, nullptr, at<void>(ws, w.s_act), xdt, nullptr, 1,
+                   at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), 1, T, single,
+                   at<void>(ws, w.s_out), 0, 0.f, 0.f, st));
+  if (d->shared_gate_weight)
+    MOE_HIP(launch_router_logits(x, xdt, T, d->hidden, d->shared_gate_weight, d->router_dtype,
+                                 nullptr, 1, at<void>(ws, w.s_logit), st),
+            "shared gate launch");
+  return MOE_OK;
+}
+
+constexpr size_t kDown1MaxLds = 60 * 1024;
+constexpr int kDecodeBlocks = 512;   // gate/up blocks for one token (2 per CU)
+constexpr int kDown1Blocks = 256;    // down+combine blocks for one token (1 per CU)
+
 moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y, void* ws,
                          size_t ws_bytes, const moe_layer_trace* tr, hipStream_t st) {
   MOE_TRY(validate_layer_impl(d));
@@ -579,80 +622,99 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y,
     return fail(MOE_ERR_WORKSPACE, "MoELayer: workspace of %zu bytes needed for T=%d", w.total, T);
   const int E = d->n_experts, k = d->top_k, H = d->hidden, I = d->intermediate;
   const int M = T * k, xdt = d->act_dtype;
-
-  // 1. router projection + selection (MoELayer.swift:540-573 / 689-750)
-  MOE_HIP(launch_router_logits(x, xdt, T, H, d->router_weight, d->router_dtype, d->router_bias, E,
-                               at<void>(ws, w.logits), st),
-          "router logits launch");
-  MOE_HIP(launch_router_topk(at<void>(ws, w.logits), xdt, T, E, k, d->gating, d->norm_topk_prob,
-                             d->expert_bias, at<uint32_t>(ws, w.idx), at<float>(ws, w.w), st),
-          "router top-k launch");
-  // 2. dispatch plan (MoELayer.swift:752-792)
-  MOE_HIP(launch_dispatch_plan(at<uint32_t>(ws, w.idx), T, k, E, at<uint32_t>(ws, w.counts),
-                               at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.perm),
-                               at<uint32_t>(ws, w.inv), at<uint32_t>(ws, w.used),
-                               at<void>(ws, w.plan_scratch), dispatch_scratch_bytes(T, k, E), st),
-          "dispatch plan launch");
-  const bool single = (T == 1);
-  const int slots = std::min(E, M);
   auto mark = [&](int i) -> moe_status {
     if (!tr || !tr->events[i]) return MOE_OK;
     return hip_check(hipEventRecord(reinterpret_cast<hipEvent_t>(tr->events[i]), st),
                      "trace event");
   };
-  // 3. gate/up + activation (MoELayer.swift:883-893)
-  MOE_TRY(mark(0));
-  MOE_TRY(run_gemv(d->gate, &d->up, x, xdt, at<uint32_t>(ws, w.perm), k,
-                   at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, single,
-                   at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st));
-  MOE_TRY(mark(1));
 
-  // shared expert first so the combine can fold it in (Qwen3xText.swift:1047-1104)
-  int smode = 0;
-  if (d->has_shared) {
-    smode = d->shared_gate_weight ? 2 : 1;
-    MOE_HIP(launch_identity_plan(at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), T, st),
-            "identity plan launch");
-    MOE_TRY(run_gemv(d->shared_gate, &d->shared_up, x, xdt, nullptr, 1, at<uint32_t>(ws, w.s_off),
-                     at<uint32_t>(ws, w.s_used), 1, T, single, at<void>(ws, w.s_act),
-                     MOE_ACT_SWIGLU, 0.f, 0.f, st));
-    MOE_TRY(run_gemv(d->shared_down, nullptr, at<void>(ws, w.s_act), xdt, nullptr, 1,
-                     at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), 1, T, single,
-                     at<void>(ws, w.s_out), 0, 0.f, 0.f, st));
-    if (d->shared_gate_weight)
-      MOE_HIP(launch_router_logits(x, xdt, T, H, d->shared_gate_weight, d->router_dtype, nullptr, 1,
-                                   at<void>(ws, w.s_logit), st),
-              "shared gate launch");
-  }
+  // 1. router projection (MoELayer.swift:540 / 689-690)
+  MOE_HIP(launch_router_logits(x, xdt, T, H, d->router_weight, d->router_dtype, d->router_bias, E,
+                               at<void>(ws, w.logits), st),
+          "router logits launch");
 
-  // 4. down projection + weighted combine (MoELayer.swift:899-939)
   const int lgc = pick_lg_combine(I / 32, k);
-  if (single && lgc >= 0) {
-    DownCombineArgs a{};
-    a.p = to_proj(d->down);
-    a.act = at<void>(ws, w.act);
-    a.perm = at<uint32_t>(ws, w.perm);
-    a.idx = at<uint32_t>(ws, w.idx);
-    a.w = at<float>(ws, w.w);
-    a.out = y;
-    a.k = k;
-    a.N = H;
-    a.K = I;
-    a.gs = d->down.group_size;
-    a.lg = lgc;
-    const int rpb = std::max(4, (H + 511) / 512);
-    a.rows_per_block = rpb;
-    const int grid = (H + rpb - 1) / rpb;
-    MOE_HIP(launch_down_combine(d->down.bits, xdt, d->down.sb_dtype, a, grid, st),
-            "down+combine launch");
+  const bool dec1 = (T == 1 && xdt != MOE_F32 && lgc >= 0 &&
+                     (size_t)k * I * dt_size(xdt) <= kDown1MaxLds);
+  int smode = 0;
+  if (dec1) {
+    // 2. one token: routing inside the gate/up kernel (MoELayer.swift:1167-1282
+    //    without a host round trip), then the fused down + combine
+    Decode1Args g{};
+    g.logits = at<void>(ws, w.logits);
+    g.E = E;
+    g.k = k;
+    g.gating = d->gating;
+    g.norm = d->norm_topk_prob;
+    g.ebias = d->expert_bias;
+    g.idx = at<uint32_t>(ws, w.idx);
+    g.w = at<float>(ws, w.w);
+    g.perm = at<uint32_t>(ws, w.perm);
+    g.offsets = at<uint32_t>(ws, w.offsets);
+    g.x = x;
+    g.g = to_proj(d->gate);
+    g.u = to_proj(d->up);
+    g.act = at<void>(ws, w.act);
+    g.N = I;
+    g.K = H;
+    g.gs = d->gate.group_size;
+    g.lg = pick_lg(H / 32, 4);
+    const int SG = 64 >> g.lg;
+    const int max_rb = std::max(1, (I + 4 * SG - 1) / (4 * SG));
+    int rb = std::min(max_rb, std::max(1, (kDecodeBlocks + k - 1) / k));
+    g.rows_per_block = (I + rb - 1) / rb;
+    g.row_blocks = (I + g.rows_per_block - 1) / g.rows_per_block;
+    g.act_kind = d->activation;
+    g.alpha = d->act_alpha;
+    g.limit = d->act_limit;
+    MOE_TRY(mark(0));
+    MOE_HIP(launch_gateup1(d->gate.bits, xdt, d->gate.sb_dtype, g, k * g.row_blocks, st),
+            "gate/up decode launch");
+    MOE_TRY(mark(1));
+    MOE_TRY(shared_expert(d, x, T, ws, w, st, &smode));
+    Down1Args dn{};
+    dn.idx = g.idx;
+    dn.w = g.w;
+    dn.perm = g.perm;
+    dn.act = g.act;
+    dn.p = to_proj(d->down);
+    dn.out = y;
+    dn.k = k;
+    dn.N = H;
+    dn.K = I;
+    dn.gs = d->down.group_size;
+    dn.lg = lgc;
+    dn.rows_per_block = std::max(1, (H + kDown1Blocks - 1) / kDown1Blocks);
+    const int grid = (H + dn.rows_per_block - 1) / dn.rows_per_block;
+    MOE_HIP(launch_down1(d->down.bits, xdt, d->down.sb_dtype, dn, grid,
+                         (size_t)k * I * dt_size(xdt), st),
+            "down+combine decode launch");
     MOE_TRY(mark(2));
     if (smode)
       MOE_HIP(launch_add_shared(y, at<void>(ws, w.s_out), at<void>(ws, w.s_logit), smode, T, H, xdt,
                                 st),
               "shared add launch");
   } else {
+    // 2. selection + dispatch plan (MoELayer.swift:706-792)
+    MOE_HIP(launch_router_topk(at<void>(ws, w.logits), xdt, T, E, k, d->gating, d->norm_topk_prob,
+                               d->expert_bias, at<uint32_t>(ws, w.idx), at<float>(ws, w.w), st),
+            "router top-k launch");
+    MOE_HIP(launch_dispatch_plan(at<uint32_t>(ws, w.idx), T, k, E, at<uint32_t>(ws, w.counts),
+                                 at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.perm),
+                                 at<uint32_t>(ws, w.inv), at<uint32_t>(ws, w.used),
+                                 at<void>(ws, w.plan_scratch), dispatch_scratch_bytes(T, k, E), st),
+            "dispatch plan launch");
+    const int slots = std::min(E, M);
+    // 3. gate/up + activation over the plan (MoELayer.swift:883-893)
+    MOE_TRY(mark(0));
+    MOE_TRY(run_gemv(d->gate, &d->up, x, xdt, at<uint32_t>(ws, w.perm), k,
+                     at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, T == 1,
+                     at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st));
+    MOE_TRY(mark(1));
+    MOE_TRY(shared_expert(d, x, T, ws, w, st, &smode));
+    // 4. down projection, then the weighted combine (MoELayer.swift:899-939)
     MOE_TRY(run_gemv(d->down, nullptr, at<void>(ws, w.act), xdt, nullptr, 1,
-                     at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, single,
+                     at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, T == 1,
                      at<void>(ws, w.Y), 0, 0.f, 0.f, st));
     MOE_HIP(launch_unpermute(at<void>(ws, w.Y), at<uint32_t>(ws, w.inv), at<float>(ws, w.w), T, H,
                              k, y, xdt, smode ? at<void>(ws, w.s_out) : nullptr,

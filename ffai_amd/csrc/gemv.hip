@@ -341,88 +341,272 @@ __global__ __launch_bounds__(256) void gemv_single_kernel(const GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// fused down projection + weighted combine, one token
-//   out[r] = round( sum_p round(w_p) * (W_down[e_p] . act_p)[r] )
-// Sub-group g handles sorted positions g, g + 64/L, ...; a full-wave
-// reduction adds the slots. Activations live in registers.
+// decode of one token: gate/up with in-wave routing, then down + combine
 // ---------------------------------------------------------------------------
 
-template <int BITS, typename XT, typename ST>
-__global__ __launch_bounds__(256) void down_combine_kernel(const DownCombineArgs a) {
-  const int N = a.N, K = a.K, CU = K >> 5, groups = K / a.gs, row_words = CU * BITS;
+template <int BITS, typename ST, int UR>
+__device__ __forceinline__ void load_units(const GemvProj& p, size_t row, int row_words, int groups,
+                                           int gs, int li, int L, int CU,
+                                           WUnit<BITS> (&w)[UR]) {
+#pragma unroll
+  for (int j = 0; j < UR; j++) {
+    const int u = li + j * L;
+    if (u < CU) load_w_unit<BITS, ST>(p, row, row_words, groups, gs, u, w[j]);
+  }
+}
+
+template <int BITS, typename XT, int UR>
+__device__ __forceinline__ float dot_units(const WUnit<BITS> (&w)[UR],
+                                           const XUnit<XT> (&xu)[UR], const float (&xs)[UR],
+                                           int li, int L, int CU) {
+  constexpr float MAGIC = Magic<BITS, XT>::value;
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < UR; j++) {
+    const int u = li + j * L;
+    if (u < CU) {
+      uint32_t cp[16];
+      unpack_pairs<BITS>(w[j].w, cp);
+      acc += w[j].s * dot_unit<BITS, XT>(cp, xu[j]) + (w[j].b - MAGIC * w[j].s) * xs[j];
+    }
+  }
+  return acc;
+}
+
+template <int BITS, typename XT, typename ST, int UR>
+__global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
+  __shared__ float sc[4][kTopkMaxE];
+  __shared__ int sel_lds[64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  const int slot = blockIdx.x / a.row_blocks, rb = blockIdx.x - slot * a.row_blocks;
+  const bool writer = (blockIdx.x == 0 && wave == 0);
+  const XT* logits = reinterpret_cast<const XT*>(a.logits);
+
+  // every wave routes the token itself (identical, deterministic results)
+  int sel;
+  float wgt = 0.f;
+  wave_topk<XT>(logits, a.E, a.k, a.gating, a.norm, a.ebias, sc[wave], writer, &sel, &wgt);
+  int pos = 0;
+  for (int r = 0; r < a.k; r++) pos += (__shfl(sel, r, 64) < sel) ? 1 : 0;
+  const uint64_t hit = __ballot(lane < a.k && pos == slot);
+  if (hit == 0) return;
+  const int e = __shfl(sel, __ffsll((unsigned long long)hit) - 1, 64);
+  if (writer) {
+    if (lane < a.k) {
+      a.idx[lane] = (uint32_t)sel;
+      a.w[lane] = wgt;
+      a.perm[pos] = (uint32_t)lane;
+      sel_lds[lane] = sel;
+    }
+    if (a.offsets) {
+      wave_sync();
+      for (int ee = lane; ee <= a.E; ee += 64) {
+        int c = 0;
+        for (int r = 0; r < a.k; r++) c += (sel_lds[r] < ee) ? 1 : 0;
+        a.offsets[ee] = (uint32_t)c;
+      }
+    }
+  }
+
+  const int N = a.N, K = a.K, CU = K >> 5, groups = K / a.gs, row_words = CU * BITS;
   const int L = 1 << a.lg, SG = 64 >> a.lg;
   const int sg = lane >> a.lg, li = lane & (L - 1);
-  constexpr float MAGIC = Magic<BITS, XT>::value;
-  constexpr int UR = 4;   // units per lane
-  constexpr int PR = 2;   // positions per sub-group (host: k <= 2 * 64/L)
-  const int r_begin = blockIdx.x * a.rows_per_block;
+  const int r_begin = rb * a.rows_per_block;
   const int r_end = min(N, r_begin + a.rows_per_block);
-  XT* out = reinterpret_cast<XT*>(a.out);
+  const int stride = nwaves * SG;
+  const size_t ebase = (size_t)e * N;
+  XT* act = reinterpret_cast<XT*>(a.act) + (size_t)slot * N;
 
-  XUnit<XT> xu[PR][UR];
-  float xs[PR][UR], wsl[PR];
-  uint32_t ex[PR];
+  int r = r_begin + wave * SG + sg;
+  WUnit<BITS> A0[UR], A1[UR], B0[UR], B1[UR];
+  if (r < r_end) {
+    load_units<BITS, ST, UR>(a.g, ebase + r, row_words, groups, a.gs, li, L, CU, A0);
+    load_units<BITS, ST, UR>(a.u, ebase + r, row_words, groups, a.gs, li, L, CU, A1);
+  }
+  XUnit<XT> xu[UR];
+  float xs[UR];
+  const XT* x = reinterpret_cast<const XT*>(a.x);
+#pragma unroll
+  for (int j = 0; j < UR; j++) {
+    const int u = li + j * L;
+    xs[j] = 0.f;
+    if (u < CU) xs[j] = load_x_unit<BITS, XT>(x, u, xu[j]);
+  }
+  auto finish = [&](int rr, float g, float u) {
+    g = wave_sum_width(g, L);
+    u = wave_sum_width(u, L);
+    if (li == 0) {
+      const float gv = finish_proj<XT>(g, a.g.ob, ebase + rr);
+      const float uv = finish_proj<XT>(u, a.u.ob, ebase + rr);
+      act[rr] = from_f<XT>(apply_act(gv, uv, a.act_kind, a.alpha, a.limit));
+    }
+  };
+  while (r < r_end) {
+    int rn = r + stride;
+    if (rn < r_end) {
+      load_units<BITS, ST, UR>(a.g, ebase + rn, row_words, groups, a.gs, li, L, CU, B0);
+      load_units<BITS, ST, UR>(a.u, ebase + rn, row_words, groups, a.gs, li, L, CU, B1);
+    }
+    finish(r, dot_units<BITS, XT, UR>(A0, xu, xs, li, L, CU), dot_units<BITS, XT, UR>(A1, xu, xs, li, L, CU));
+    r = rn;
+    if (r >= r_end) break;
+    rn = r + stride;
+    if (rn < r_end) {
+      load_units<BITS, ST, UR>(a.g, ebase + rn, row_words, groups, a.gs, li, L, CU, A0);
+      load_units<BITS, ST, UR>(a.u, ebase + rn, row_words, groups, a.gs, li, L, CU, A1);
+    }
+    finish(r, dot_units<BITS, XT, UR>(B0, xu, xs, li, L, CU), dot_units<BITS, XT, UR>(B1, xu, xs, li, L, CU));
+    r = rn;
+  }
+}
+
+template <int BITS, typename ST, int PR, int UR>
+__device__ __forceinline__ void down1_load_row(const GemvProj& P, int N, int k, int gs,
+                                               const uint32_t (&ex)[PR], int r, int sg, int SG,
+                                               int li, int L, int CU, int row_words, int groups,
+                                               WUnit<BITS> (&w)[PR][UR]) {
+#pragma unroll
+  for (int q = 0; q < PR; q++)
+    if (sg + q * SG < k)
+      load_units<BITS, ST, UR>(P, (size_t)ex[q] * N + r, row_words, groups, gs, li, L, CU, w[q]);
+}
+
+// One output row: each expert's output is rounded to the activation dtype
+// before it is weighted, as the unfused path stores it (MoELayer.swift:
+// 895-939); a full-wave reduction adds the k experts.
+template <int BITS, typename XT, int PR, int UR>
+__device__ __forceinline__ void down1_row(const void* ob, XT* out, int N, int k,
+                                          const uint32_t (&ex)[PR], const float (&wsl)[PR],
+                                          const XUnit<XT> (&xu)[PR][UR], const float (&xs)[PR][UR],
+                                          const WUnit<BITS> (&w)[PR][UR], int r, int sg, int SG,
+                                          int li, int L, int CU, int lane) {
+  float acc = 0.f;
 #pragma unroll
   for (int q = 0; q < PR; q++) {
     const int p = sg + q * SG;
-    wsl[q] = 0.f;
+    float part = 0.f;
+    if (p < k) part = dot_units<BITS, XT, UR>(w[q], xu[q], xs[q], li, L, CU);
+    part = wave_sum_width(part, L);
+    if (p < k && li == 0) acc += wsl[q] * finish_proj<XT>(part, ob, (size_t)ex[q] * N + r);
+  }
+  acc = wave_sum_width(acc, 64);
+  if (lane == 0) out[r] = from_f<XT>(acc);
+}
+
+template <int BITS, typename XT, typename ST, int PR, int UR>
+__global__ __launch_bounds__(256) void down1_kernel(const Down1Args a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  const int N = a.N, K = a.K, CU = K >> 5, groups = K / a.gs, row_words = CU * BITS;
+  const int L = 1 << a.lg, SG = 64 >> a.lg;
+  const int sg = lane >> a.lg, li = lane & (L - 1);
+  const int r_begin = blockIdx.x * a.rows_per_block;
+  const int r_end = min(N, r_begin + a.rows_per_block);
+  XT* al = reinterpret_cast<XT*>(smem);
+  const GemvProj P = a.p;
+  const int kk = a.k, gs = a.gs;
+  XT* out = reinterpret_cast<XT*>(a.out);
+
+  // stage the k activation rows (natural order) while the weights stream in
+  constexpr int EPV = 16 / sizeof(XT);
+  constexpr int NPRE = 4;
+  const int nvec = a.k * K / EPV;
+  const uint4* src = reinterpret_cast<const uint4*>(a.act);
+  uint4* dst = reinterpret_cast<uint4*>(al);
+  uint4 stage[NPRE];
+#pragma unroll
+  for (int j = 0; j < NPRE; j++) {
+    const int i = threadIdx.x + j * blockDim.x;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (i < nvec) v = src[i];
+    stage[j] = v;
+  }
+
+  uint32_t ex[PR];
+  float wsl[PR];
+#pragma unroll
+  for (int q = 0; q < PR; q++) {
+    const int p = sg + q * SG;
     ex[q] = 0;
+    wsl[q] = 0.f;
     if (p < a.k) {
-      const uint32_t src = a.perm[p];
-      ex[q] = a.idx[src];
-      wsl[q] = round_to<XT>(a.w[src]);
-      const XT* row = reinterpret_cast<const XT*>(a.act) + (size_t)p * K;
-#pragma unroll
-      for (int j = 0; j < UR; j++) {
-        const int u = li + j * L;
-        xs[q][j] = 0.f;
-        if (u < CU) xs[q][j] = load_x_unit<BITS, XT>(row, u, xu[q][j]);
-      }
+      const uint32_t s = a.perm[p];
+      ex[q] = a.idx[s];
+      wsl[q] = round_to<XT>(a.w[s]);
     }
   }
-  for (int r = r_begin + wave; r < r_end; r += nwaves) {
-    WUnit<BITS> wu[PR][UR];
+  int r = r_begin + wave;
+  WUnit<BITS> A[PR][UR], B[PR][UR];
+  if (r < r_end) down1_load_row<BITS, ST, PR, UR>(P, N, kk, gs, ex, r, sg, SG, li, L, CU, row_words, groups, A);
+
 #pragma unroll
-    for (int q = 0; q < PR; q++) {
-      const int p = sg + q * SG;
-      if (p < a.k) {
-        const size_t row = (size_t)ex[q] * N + r;
-#pragma unroll
-        for (int j = 0; j < UR; j++) {
-          const int u = li + j * L;
-          if (u < CU) load_w_unit<BITS, ST>(a.p, row, row_words, groups, a.gs, u, wu[q][j]);
-        }
-      }
-    }
-    float acc = 0.f;
-#pragma unroll
-    for (int q = 0; q < PR; q++) {
-      const int p = sg + q * SG;
-      float part = 0.f;
-      if (p < a.k) {
-#pragma unroll
-        for (int j = 0; j < UR; j++) {
-          const int u = li + j * L;
-          if (u < CU) {
-            uint32_t cp[16];
-            unpack_pairs<BITS>(wu[q][j].w, cp);
-            part += wu[q][j].s * dot_unit<BITS, XT>(cp, xu[q][j]) +
-                    (wu[q][j].b - MAGIC * wu[q][j].s) * xs[q][j];
-          }
-        }
-      }
-      // the expert's down output is rounded to the activation dtype before
-      // it is weighted, as the unfused path stores it (MoELayer.swift:895-939)
-      part = wave_sum_width(part, L);
-      if (p < a.k && li == 0) {
-        const float yv = finish_proj<XT>(part, a.p.ob, (size_t)ex[q] * N + r);
-        acc += wsl[q] * yv;
-      }
-    }
-    acc = wave_sum_width(acc, 64);
-    if (lane == 0) out[r] = from_f<XT>(acc);
+  for (int j = 0; j < NPRE; j++) {
+    const int i = threadIdx.x + j * blockDim.x;
+    if (i < nvec) dst[i] = stage[j];
   }
+  for (int i = threadIdx.x + NPRE * blockDim.x; i < nvec; i += blockDim.x) dst[i] = src[i];
+  __syncthreads();
+
+  XUnit<XT> xu[PR][UR];
+  float xs[PR][UR];
+#pragma unroll
+  for (int q = 0; q < PR; q++) {
+    const int p = sg + q * SG;
+#pragma unroll
+    for (int j = 0; j < UR; j++) {
+      const int u = li + j * L;
+      xs[q][j] = 0.f;
+      if (p < a.k && u < CU) xs[q][j] = load_x_unit<BITS, XT>(al + (size_t)p * K, u, xu[q][j]);
+    }
+  }
+  while (r < r_end) {
+    int rn = r + nwaves;
+    if (rn < r_end) down1_load_row<BITS, ST, PR, UR>(P, N, kk, gs, ex, rn, sg, SG, li, L, CU, row_words, groups, B);
+    down1_row<BITS, XT, PR, UR>(P.ob, out, N, kk, ex, wsl, xu, xs, A, r, sg, SG, li, L, CU, lane);
+    r = rn;
+    if (r >= r_end) break;
+    rn = r + nwaves;
+    if (rn < r_end) down1_load_row<BITS, ST, PR, UR>(P, N, kk, gs, ex, rn, sg, SG, li, L, CU, row_words, groups, A);
+    down1_row<BITS, XT, PR, UR>(P.ob, out, N, kk, ex, wsl, xu, xs, B, r, sg, SG, li, L, CU, lane);
+    r = rn;
+  }
+}
+
+template <int BITS, typename XT, typename ST, int UR>
+static hipError_t launch_dec1_u(bool down, int pr, const void* args, int grid, size_t smem,
+                                hipStream_t st) {
+  if (!down)
+    hipLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR>), dim3(grid), dim3(256), 0, st,
+                       *reinterpret_cast<const Decode1Args*>(args));
+  else if (pr == 1)
+    hipLaunchKernelGGL((down1_kernel<BITS, XT, ST, 1, UR>), dim3(grid), dim3(256), smem, st,
+                       *reinterpret_cast<const Down1Args*>(args));
+  else
+    hipLaunchKernelGGL((down1_kernel<BITS, XT, ST, 2, UR>), dim3(grid), dim3(256), smem, st,
+                       *reinterpret_cast<const Down1Args*>(args));
+  return hipGetLastError();
+}
+
+template <int BITS, typename XT, typename ST>
+static hipError_t launch_dec1_t(bool down, int pr, int ur, const void* args, int grid, size_t smem,
+                                hipStream_t st) {
+  switch (ur) {
+    case 1: return launch_dec1_u<BITS, XT, ST, 1>(down, pr, args, grid, smem, st);
+    case 2: return launch_dec1_u<BITS, XT, ST, 2>(down, pr, args, grid, smem, st);
+    case 3: return launch_dec1_u<BITS, XT, ST, 3>(down, pr, args, grid, smem, st);
+    case 4: return launch_dec1_u<BITS, XT, ST, 4>(down, pr, args, grid, smem, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int BITS>
+static hipError_t launch_dec1_bits(int xdt, int sbdt, bool down, int pr, int ur, const void* args,
+                                   int grid, size_t smem, hipStream_t st) {
+  if (xdt == DT_BF16 && sbdt == DT_BF16) return launch_dec1_t<BITS, bf16_t, bf16_t>(down, pr, ur, args, grid, smem, st);
+  if (xdt == DT_BF16 && sbdt == DT_F16) return launch_dec1_t<BITS, bf16_t, f16_t>(down, pr, ur, args, grid, smem, st);
+  if (xdt == DT_F16 && sbdt == DT_F16) return launch_dec1_t<BITS, f16_t, f16_t>(down, pr, ur, args, grid, smem, st);
+  if (xdt == DT_F16 && sbdt == DT_BF16) return launch_dec1_t<BITS, f16_t, bf16_t>(down, pr, ur, args, grid, smem, st);
+  return hipErrorInvalidValue;
 }
 
 // ---------------------------------------------------------------------------
@@ -460,21 +644,6 @@ static hipError_t launch_gemv_bits(int xdt, int sbdt, bool gateup, int tokmax, c
   return hipErrorInvalidValue;
 }
 
-template <int BITS>
-static hipError_t launch_down_combine_bits(int xdt, int sbdt, const DownCombineArgs& a, int grid,
-                                           hipStream_t st) {
-#define MOE_DC(XT, ST)                                                                         \
-  hipLaunchKernelGGL((down_combine_kernel<BITS, XT, ST>), dim3(grid), dim3(256), 0, st, a); \
-  return hipGetLastError();
-  if (xdt == DT_BF16 && sbdt == DT_BF16) { MOE_DC(bf16_t, bf16_t) }
-  if (xdt == DT_BF16 && sbdt == DT_F16) { MOE_DC(bf16_t, f16_t) }
-  if (xdt == DT_F16 && sbdt == DT_F16) { MOE_DC(f16_t, f16_t) }
-  if (xdt == DT_F16 && sbdt == DT_BF16) { MOE_DC(f16_t, bf16_t) }
-  if (xdt == DT_F32 && sbdt == DT_F32) { MOE_DC(float, float) }
-#undef MOE_DC
-  return hipErrorInvalidValue;
-}
-
 // One translation unit per bit width (MOE_BITS) keeps compile times short;
 // the per-width entry points are stitched together in api.cpp.
 #define MOE_CAT2(a, b) a##b
@@ -485,9 +654,10 @@ hipError_t MOE_CAT(launch_gemv_b, MOE_BITS)(int xdt, int sbdt, bool gateup, int 
   return launch_gemv_bits<MOE_BITS>(xdt, sbdt, gateup, tokmax, a, grid, st);
 }
 
-hipError_t MOE_CAT(launch_down_combine_b, MOE_BITS)(int xdt, int sbdt, const DownCombineArgs& a,
-                                                     int grid, hipStream_t st) {
-  return launch_down_combine_bits<MOE_BITS>(xdt, sbdt, a, grid, st);
+hipError_t MOE_CAT(launch_dec1_b, MOE_BITS)(int xdt, int sbdt, bool down, int pr, int ur,
+                                             const void* args, int grid, size_t smem,
+                                             hipStream_t st) {
+  return launch_dec1_bits<MOE_BITS>(xdt, sbdt, down, pr, ur, args, grid, smem, st);
 }
 
 }  // namespace moe

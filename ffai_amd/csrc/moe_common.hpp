@@ -55,6 +55,124 @@ __device__ __forceinline__ float det_expf(float x) {
   return __builtin_ldexpf(y, (int)n);
 }
 
+// ------------------------------------------------------------ wave top-k --
+// Makes LDS writes of this wave visible to its other lanes.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+constexpr int kTopkMaxE = 512;           // experts a wave can route
+constexpr int kTopkEPL = kTopkMaxE / 64; // logits held per lane
+
+__device__ __forceinline__ bool topk_beats(float av, int ai, float bv, int bi) {
+  return av > bv || (av == bv && ai < bi);
+}
+
+// MoERouter.route for one token with one full wave (MoELayer.swift:140-205,
+// heap order of :223-296). Lane r < k returns the r-th selected expert in
+// (value desc, index asc) order in *sel and its combine weight in *w
+// (weights only when want_weights). Softmax sums run in index / rank order
+// on one lane with det_expf, so the results are reproducible bit for bit.
+// sc: this wave's LDS scratch of at least E floats (full-softmax mode).
+template <typename XT>
+__device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, int norm,
+                          const float* __restrict__ ebias, float* sc, bool want_weights,
+                          int* sel, float* w) {
+  const int lane = threadIdx.x & 63;
+  const bool on_logits = (gating == 1) || (norm && ebias == nullptr);
+  const float NEG = -__builtin_huge_valf();
+  float v[kTopkEPL];
+  float m = NEG;
+#pragma unroll
+  for (int j = 0; j < kTopkEPL; j++) {
+    const int i = lane + 64 * j;
+    v[j] = (i < E) ? to_f<XT>(row[i]) : NEG;
+    if (i < E) m = fmaxf(m, v[j]);
+  }
+  if (!on_logits) {
+    // full softmax (+ expert bias): MoELayer.swift:174-195
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+#pragma unroll
+    for (int j = 0; j < kTopkEPL; j++) {
+      const int i = lane + 64 * j;
+      if (i < E) {
+        v[j] = det_expf(v[j] - m);
+        sc[i] = v[j];
+      }
+    }
+    wave_sync();
+    float s = 0.f;
+    if (lane == 0)
+      for (int i = 0; i < E; i++) s += sc[i];
+    s = __shfl(s, 0, 64);
+#pragma unroll
+    for (int j = 0; j < kTopkEPL; j++) {
+      const int i = lane + 64 * j;
+      if (i < E) {
+        v[j] = (s > 0.f) ? v[j] / s : 1.0f / (float)E;
+        if (ebias) v[j] = v[j] + ebias[i];
+      }
+    }
+    wave_sync();
+  }
+  // NaN sorts as -inf so the order is total and every lane agrees.
+#pragma unroll
+  for (int j = 0; j < kTopkEPL; j++)
+    if (v[j] != v[j]) v[j] = NEG;
+  uint32_t taken = 0;
+  int my_sel = 0;
+  float my_val = 0.f;
+  for (int r = 0; r < k; r++) {
+    float bv = 0.f;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < kTopkEPL; j++) {
+      const int i = lane + 64 * j;
+      if (i < E && !((taken >> j) & 1u) && (bi == 0x7fffffff || topk_beats(v[j], i, bv, bi))) {
+        bv = v[j];
+        bi = i;
+      }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (oi != 0x7fffffff && (bi == 0x7fffffff || topk_beats(ov, oi, bv, bi))) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+    if (lane == r) {
+      my_sel = bi;
+      my_val = bv;
+    }
+  }
+  *sel = my_sel;
+  if (!want_weights) return;
+  // combine weights; lane 0 accumulates in rank order
+  float wv;
+  if (on_logits) {
+    // softmax over the k picked raw logits — MoELayer.swift:166-172,197-203
+    const float lv = (lane < k) ? to_f<XT>(row[my_sel]) : NEG;
+    float mx = lv;
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    const float ex = (lane < k) ? det_expf(lv - mx) : 0.f;
+    float s = 0.f;
+    for (int r = 0; r < k; r++) s += __shfl(ex, r, 64);
+    wv = (s > 0.f) ? ex / s : 1.0f / (float)k;
+  } else {
+    wv = my_val;
+    if (norm) {
+      float s = 0.f;
+      for (int r = 0; r < k; r++) s += __shfl(my_val, r, 64);
+      if (s > 0.f) wv = wv / s;
+    }
+  }
+  *w = wv;
+}
+
 // ------------------------------------------------------------ activations --
 enum { ACT_SWIGLU = 0, ACT_GPTOSS = 1 };
 

@@ -39,26 +39,43 @@ struct GemvArgs {
   float alpha, limit;
 };
 
-// Fused down projection + weighted combine for one token (T = 1): every
-// sorted position is a distinct expert.
-struct DownCombineArgs {
-  GemvProj p;                // down projection
-  const void* act;           // [k, K] activations in sorted order
-  const uint32_t* perm;      // [k]
-  const uint32_t* idx;       // [k] expert of each token-major slot
-  const float* w;            // [k] combine weight of each slot
-  void* out;                 // [N]
-  int k, N, K, gs;
-  int rows_per_block;
-  int lg;
+// Decode of one token (T = 1). gate/up kernel: every wave selects the top-k
+// from the router logits itself; block 0 publishes the routing. down kernel:
+// fused weighted combine over the k experts.
+struct Decode1Args {
+  const void* logits;        // [E] activation dtype
+  int E, k, gating, norm;
+  const float* ebias;        // nullable [E]
+  uint32_t* idx;             // [k] out: experts in rank order
+  float* w;                  // [k] out: combine weights
+  uint32_t* perm;            // [k] out: sorted position -> rank
+  uint32_t* offsets;         // nullable [E+1] out: CSR offsets of the plan
+  const void* x;             // [K]
+  GemvProj g, u;             // gate / up
+  void* act;                 // [k, N] in sorted (expert id) order
+  int N, K, gs, row_blocks, rows_per_block, lg;
+  int act_kind;
+  float alpha, limit;
 };
+
+struct Down1Args {
+  const uint32_t* idx;
+  const float* w;
+  const uint32_t* perm;
+  const void* act;           // [k, K]
+  GemvProj p;
+  void* out;                 // [N]
+  int k, N, K, gs, rows_per_block, lg;
+};
+
+hipError_t launch_gateup1(int bits, int xdt, int sbdt, const Decode1Args& a, int grid,
+                          hipStream_t st);
+hipError_t launch_down1(int bits, int xdt, int sbdt, const Down1Args& a, int grid, size_t smem,
+                        hipStream_t st);
 
 hipError_t launch_gemv(int bits, int xdt, int sbdt, bool gateup, int tokmax, const GemvArgs& a,
                        int grid, hipStream_t st);
-hipError_t launch_down_combine(int bits, int xdt, int sbdt, const DownCombineArgs& a, int grid,
-                               hipStream_t st);
 size_t gemv_smem_bytes(int xdt, int K, int tok_chunk);
-size_t down_combine_smem_bytes(int xdt, int K, int k);
 
 // ---------------------------------------------------------------- router --
 hipError_t launch_router_logits(const void* x, int xdt, int T, int H, const void* W, int wdt,

@@ -43,16 +43,24 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT* __restrict
   const int t0 = tc * 8, nt = min(8, T - t0);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   const WT* w = W + (size_t)e * H;
-  for (int h = lane * 8; h < H; h += 512) {
-    float wv[8];
-    load8<WT>(w + h, wv);
+  constexpr int UNR = 4;  // hidden chunks in flight per lane
+  for (int h0 = lane * 8; h0 < H; h0 += 512 * UNR) {
+    float wv[UNR][8];
+#pragma unroll
+    for (int u = 0; u < UNR; u++)
+      if (h0 + u * 512 < H) load8<WT>(w + h0 + u * 512, wv[u]);
 #pragma unroll
     for (int t = 0; t < 8; t++) {
       if (t < nt) {
-        float xv[8];
-        load8<XT>(x + (size_t)(t0 + t) * H + h, xv);
+        float xv[UNR][8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) acc[t] = __builtin_fmaf(wv[j], xv[j], acc[t]);
+        for (int u = 0; u < UNR; u++)
+          if (h0 + u * 512 < H) load8<XT>(x + (size_t)(t0 + t) * H + h0 + u * 512, xv[u]);
+#pragma unroll
+        for (int u = 0; u < UNR; u++)
+          if (h0 + u * 512 < H)
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[t] = __builtin_fmaf(wv[u][j], xv[u][j], acc[t]);
       }
     }
   }
@@ -68,125 +76,23 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT* __restrict
   }
 }
 
-constexpr int kMaxExperts = 512;
-constexpr int kEPL = kMaxExperts / 64;
-
-__device__ __forceinline__ bool beats(float av, int ai, float bv, int bi) {
-  return av > bv || (av == bv && ai < bi);
-}
-
-// One wave per token row. Softmax sums run in index order (the reference's
-// sequential reduce) on one lane so the weights are reproducible bit for bit.
+// One wave per token row (wave_topk); weights are reproducible bit for bit.
 template <typename XT>
 __global__ __launch_bounds__(256) void router_topk_kernel(const XT* __restrict__ logits, int T,
                                                           int E, int k, int gating, int norm,
                                                           const float* __restrict__ ebias,
                                                           uint32_t* __restrict__ idx_out,
                                                           float* __restrict__ w_out) {
-  __shared__ float sc[4][kMaxExperts];
-  __shared__ float selv[4][kMaxExperts];
-  __shared__ int seli[4][kMaxExperts];
+  __shared__ float sc[4][kTopkMaxE];
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + wv;
-  const bool active = t < T;
-  const bool on_logits = (gating == 1) || (norm && ebias == nullptr);
-  const float NEG = -__builtin_huge_valf();
-  float v[kEPL];
-  float m = NEG;
-#pragma unroll
-  for (int j = 0; j < kEPL; j++) {
-    const int i = lane + 64 * j;
-    v[j] = (active && i < E) ? to_f<XT>(logits[(size_t)t * E + i]) : NEG;
-    if (i < E) m = fmaxf(m, v[j]);
-  }
-  if (!on_logits) {
-    // full softmax (+ expert bias) — MoELayer.swift:174-195
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-#pragma unroll
-    for (int j = 0; j < kEPL; j++) {
-      const int i = lane + 64 * j;
-      if (i < E) {
-        v[j] = det_expf(v[j] - m);
-        sc[wv][i] = v[j];
-      }
-    }
-  }
-  __syncthreads();
-  if (!on_logits) {
-    float s = 0.f;
-    if (lane == 0)
-      for (int i = 0; i < E; i++) s += sc[wv][i];
-    s = __shfl(s, 0, 64);
-#pragma unroll
-    for (int j = 0; j < kEPL; j++) {
-      const int i = lane + 64 * j;
-      if (i < E) {
-        v[j] = (s > 0.f) ? v[j] / s : 1.0f / (float)E;
-        if (ebias) v[j] = v[j] + ebias[i];
-      }
-    }
-  }
-  // NaN sorts as -inf so the order is total and every lane agrees.
-#pragma unroll
-  for (int j = 0; j < kEPL; j++)
-    if (v[j] != v[j]) v[j] = NEG;
-  uint32_t taken = 0;
-  for (int r = 0; r < k; r++) {
-    float bv = 0.f;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int j = 0; j < kEPL; j++) {
-      const int i = lane + 64 * j;
-      if (i < E && !((taken >> j) & 1u)) {
-        if (bi == 0x7fffffff || beats(v[j], i, bv, bi)) {
-          bv = v[j];
-          bi = i;
-        }
-      }
-    }
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (oi != 0x7fffffff && (bi == 0x7fffffff || beats(ov, oi, bv, bi))) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if (bi != 0x7fffffff && (bi & 63) == lane) taken |= 1u << (bi >> 6);
-    if (lane == 0) {
-      seli[wv][r] = bi;
-      selv[wv][r] = bv;
-    }
-  }
-  __syncthreads();
-  if (active && lane == 0) {
-    float* w = &sc[wv][0];
-    if (on_logits) {
-      // softmax over the k picked raw logits — MoELayer.swift:166-172,197-203
-      float mx = NEG;
-      for (int r = 0; r < k; r++) {
-        w[r] = to_f<XT>(logits[(size_t)t * E + seli[wv][r]]);
-        mx = fmaxf(mx, w[r]);
-      }
-      float s = 0.f;
-      for (int r = 0; r < k; r++) {
-        w[r] = det_expf(w[r] - mx);
-        s += w[r];
-      }
-      for (int r = 0; r < k; r++) w[r] = (s > 0.f) ? w[r] / s : 1.0f / (float)k;
-    } else {
-      for (int r = 0; r < k; r++) w[r] = selv[wv][r];
-      if (norm) {
-        float s = 0.f;
-        for (int r = 0; r < k; r++) s += w[r];
-        if (s > 0.f)
-          for (int r = 0; r < k; r++) w[r] = w[r] / s;
-      }
-    }
-    for (int r = 0; r < k; r++) {
-      idx_out[(size_t)t * k + r] = (uint32_t)seli[wv][r];
-      w_out[(size_t)t * k + r] = w[r];
-    }
+  if (t >= T) return;  // wave-uniform; the kernel has no block barrier
+  int sel;
+  float w;
+  wave_topk<XT>(logits + (size_t)t * E, E, k, gating, norm, ebias, sc[wv], true, &sel, &w);
+  if (lane < k) {
+    idx_out[(size_t)t * k + lane] = (uint32_t)sel;
+    w_out[(size_t)t * k + lane] = w;
   }
 }
 
