@@ -258,22 +258,18 @@ def main():
     log(f"{steps} steps: {ms_total:.3f} ms (events), {wall * 1e3:.3f} ms (wall); "
         f"{ms_per_step * 1e3:.2f} us/step")
 
-    # kernel-level timing of the routed expert kernels (eager, GPU kept busy
-    # ahead of the host so events bracket only device work)
+    # kernel-level timing of the routed expert kernels: start/end events
+    # recorded by the kernels' own dispatch on the launch stream
     ev = HipEvents()
     reps = max(1, min(20, 480 // L))
-    marks = [[[ev.create() for _ in range(3)] for _ in range(L)] for _ in range(reps)]
+    marks = [[[ev.create() for _ in range(4)] for _ in range(L)] for _ in range(reps)]
     trace = []
     for r in range(reps):
         for l in range(L):
             t = lib.LayerTrace()
-            for i in range(3):
+            for i in range(4):
                 t.events[i] = marks[r][l][i].value
             trace.append(t)
-    # keep the GPU busy while the host queues the measured calls
-    busy = torch.ones(128 * 1024 * 1024, dtype=torch.float32, device="cuda")
-    for _ in range(200):
-        busy.mul_(1.0)
     j = 0
     stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
     for r in range(reps):
@@ -285,7 +281,7 @@ def main():
             j += 1
     torch.cuda.synchronize()
     gu = [ev.elapsed_ms(marks[r][l][0], marks[r][l][1]) for r in range(reps) for l in range(L)]
-    dn = [ev.elapsed_ms(marks[r][l][1], marks[r][l][2]) for r in range(reps) for l in range(L)]
+    dn = [ev.elapsed_ms(marks[r][l][2], marks[r][l][3]) for r in range(reps) for l in range(L)]
     for row in marks:
         for m in row:
             for e in m:
@@ -311,7 +307,8 @@ def main():
                     peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s")
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
     roof["traffic"] = None
-    roof["kernel"] = "routed gate/up grouped dequant GEMV (gemv_single_kernel / gemv_grouped_kernel)"
+    roof["kernel"] = ("gateup1_kernel (one-token gate/up with routing)" if T == 1 else
+                      "gemv_grouped_kernel (routed gate/up over the dispatch plan)")
     roof["avg_us"] = round(gu_us, 3)
     roof["algorithmic_bytes"] = gu_bytes
     log(f"gate/up kernel {gu_us:.2f} us ({gu_bytes / 1e6:.2f} MB, "

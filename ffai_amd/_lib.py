@@ -60,7 +60,7 @@ class LayerDesc(C.Structure):
 class LayerTrace(C.Structure):
     _fields_ = [
         ("logits", C.c_void_p), ("topk_idx", C.c_void_p), ("topk_weight", C.c_void_p),
-        ("perm", C.c_void_p), ("offsets", C.c_void_p), ("events", C.c_void_p * 3),
+        ("perm", C.c_void_p), ("offsets", C.c_void_p), ("events", C.c_void_p * 4),
     ]
 
 

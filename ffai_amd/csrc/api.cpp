@@ -18,56 +18,56 @@
 #include "moe_internal.hpp"
 
 namespace moe {
-hipError_t launch_gemv_b2(int, int, bool, int, const GemvArgs&, int, hipStream_t);
-hipError_t launch_gemv_b3(int, int, bool, int, const GemvArgs&, int, hipStream_t);
-hipError_t launch_gemv_b4(int, int, bool, int, const GemvArgs&, int, hipStream_t);
-hipError_t launch_gemv_b5(int, int, bool, int, const GemvArgs&, int, hipStream_t);
-hipError_t launch_gemv_b6(int, int, bool, int, const GemvArgs&, int, hipStream_t);
-hipError_t launch_gemv_b8(int, int, bool, int, const GemvArgs&, int, hipStream_t);
-hipError_t launch_dec1_b2(int, int, bool, int, int, const void*, int, size_t, hipStream_t);
-hipError_t launch_dec1_b3(int, int, bool, int, int, const void*, int, size_t, hipStream_t);
-hipError_t launch_dec1_b4(int, int, bool, int, int, const void*, int, size_t, hipStream_t);
-hipError_t launch_dec1_b5(int, int, bool, int, int, const void*, int, size_t, hipStream_t);
-hipError_t launch_dec1_b6(int, int, bool, int, int, const void*, int, size_t, hipStream_t);
-hipError_t launch_dec1_b8(int, int, bool, int, int, const void*, int, size_t, hipStream_t);
+hipError_t launch_gemv_b2(int, int, bool, int, const GemvArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemv_b3(int, int, bool, int, const GemvArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemv_b4(int, int, bool, int, const GemvArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemv_b5(int, int, bool, int, const GemvArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemv_b6(int, int, bool, int, const GemvArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemv_b8(int, int, bool, int, const GemvArgs&, int, hipStream_t, KEvents);
+hipError_t launch_dec1_b2(int, int, bool, int, int, const void*, int, size_t, hipStream_t, KEvents);
+hipError_t launch_dec1_b3(int, int, bool, int, int, const void*, int, size_t, hipStream_t, KEvents);
+hipError_t launch_dec1_b4(int, int, bool, int, int, const void*, int, size_t, hipStream_t, KEvents);
+hipError_t launch_dec1_b5(int, int, bool, int, int, const void*, int, size_t, hipStream_t, KEvents);
+hipError_t launch_dec1_b6(int, int, bool, int, int, const void*, int, size_t, hipStream_t, KEvents);
+hipError_t launch_dec1_b8(int, int, bool, int, int, const void*, int, size_t, hipStream_t, KEvents);
 
 hipError_t launch_gemv(int bits, int xdt, int sbdt, bool gateup, int tokmax, const GemvArgs& a,
-                       int grid, hipStream_t st) {
+                       int grid, hipStream_t st, KEvents ev) {
   switch (bits) {
-    case 2: return launch_gemv_b2(xdt, sbdt, gateup, tokmax, a, grid, st);
-    case 3: return launch_gemv_b3(xdt, sbdt, gateup, tokmax, a, grid, st);
-    case 4: return launch_gemv_b4(xdt, sbdt, gateup, tokmax, a, grid, st);
-    case 5: return launch_gemv_b5(xdt, sbdt, gateup, tokmax, a, grid, st);
-    case 6: return launch_gemv_b6(xdt, sbdt, gateup, tokmax, a, grid, st);
-    case 8: return launch_gemv_b8(xdt, sbdt, gateup, tokmax, a, grid, st);
+    case 2: return launch_gemv_b2(xdt, sbdt, gateup, tokmax, a, grid, st, ev);
+    case 3: return launch_gemv_b3(xdt, sbdt, gateup, tokmax, a, grid, st, ev);
+    case 4: return launch_gemv_b4(xdt, sbdt, gateup, tokmax, a, grid, st, ev);
+    case 5: return launch_gemv_b5(xdt, sbdt, gateup, tokmax, a, grid, st, ev);
+    case 6: return launch_gemv_b6(xdt, sbdt, gateup, tokmax, a, grid, st, ev);
+    case 8: return launch_gemv_b8(xdt, sbdt, gateup, tokmax, a, grid, st, ev);
   }
   return hipErrorInvalidValue;
 }
 
-static hipError_t launch_dec1(int bits, int xdt, int sbdt, bool down, int pr, int ur,
-                              const void* args, int grid, size_t smem, hipStream_t st) {
+static hipError_t launch_dec1(int bits, int xdt, int sbdt, bool down, int rm, int ur,
+                              const void* args, int grid, size_t smem, hipStream_t st,
+                              KEvents ev) {
   switch (bits) {
-    case 2: return launch_dec1_b2(xdt, sbdt, down, pr, ur, args, grid, smem, st);
-    case 3: return launch_dec1_b3(xdt, sbdt, down, pr, ur, args, grid, smem, st);
-    case 4: return launch_dec1_b4(xdt, sbdt, down, pr, ur, args, grid, smem, st);
-    case 5: return launch_dec1_b5(xdt, sbdt, down, pr, ur, args, grid, smem, st);
-    case 6: return launch_dec1_b6(xdt, sbdt, down, pr, ur, args, grid, smem, st);
-    case 8: return launch_dec1_b8(xdt, sbdt, down, pr, ur, args, grid, smem, st);
+    case 2: return launch_dec1_b2(xdt, sbdt, down, rm, ur, args, grid, smem, st, ev);
+    case 3: return launch_dec1_b3(xdt, sbdt, down, rm, ur, args, grid, smem, st, ev);
+    case 4: return launch_dec1_b4(xdt, sbdt, down, rm, ur, args, grid, smem, st, ev);
+    case 5: return launch_dec1_b5(xdt, sbdt, down, rm, ur, args, grid, smem, st, ev);
+    case 6: return launch_dec1_b6(xdt, sbdt, down, rm, ur, args, grid, smem, st, ev);
+    case 8: return launch_dec1_b8(xdt, sbdt, down, rm, ur, args, grid, smem, st, ev);
   }
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_gateup1(int bits, int xdt, int sbdt, const Decode1Args& a, int grid,
-                          hipStream_t st) {
+hipError_t launch_gateup1(int bits, int xdt, int sbdt, const Decode1Args& a, int rm, int grid,
+                          hipStream_t st, KEvents ev) {
   const int L = 1 << a.lg, ur = (a.K / 32 + L - 1) / L;
-  return launch_dec1(bits, xdt, sbdt, false, 1, ur, &a, grid, 0, st);
+  return launch_dec1(bits, xdt, sbdt, false, rm, ur, &a, grid, 0, st, ev);
 }
 
-hipError_t launch_down1(int bits, int xdt, int sbdt, const Down1Args& a, int grid, size_t smem,
-                        hipStream_t st) {
-  const int L = 1 << a.lg, SG = 64 >> a.lg;
-  const int ur = (a.K / 32 + L - 1) / L, pr = (a.k + SG - 1) / SG;
-  return launch_dec1(bits, xdt, sbdt, true, pr, ur, &a, grid, smem, st);
+hipError_t launch_down1(int bits, int xdt, int sbdt, const Down1Args& a, int rm, int grid,
+                        hipStream_t st, KEvents ev) {
+  const int L = 1 << a.lg, ur = (a.K / 32 + L - 1) / L;
+  return launch_dec1(bits, xdt, sbdt, true, rm, ur, &a, grid, 0, st, ev);
 }
 
 size_t gemv_smem_bytes(int xdt, int K, int tok_chunk) {
@@ -185,6 +185,7 @@ extern "C" moe_status moe_derive_bits(int64_t packed_cols, int64_t scale_cols, i
 namespace {
 
 constexpr int kMaxExperts = 512;
+constexpr int kMaxHidden = 8192;  // router rows are read in one round trip of 16 loads per lane
 
 moe_status validate_layer_impl(const moe_layer_desc* d) {
   if (!d) return fail(MOE_ERR_INVALID, "MoELayer: descriptor is NULL");
@@ -194,6 +195,8 @@ moe_status validate_layer_impl(const moe_layer_desc* d) {
                 d->n_experts);
   if (d->hidden <= 0 || d->intermediate <= 0)
     return fail(MOE_ERR_INVALID, "MoELayer: hidden and intermediate must be positive");
+  if (d->hidden > kMaxHidden)
+    return fail(MOE_ERR_UNSUPPORTED, "MoELayer: hidden (%d) above %d", d->hidden, kMaxHidden);
   if (!dt_ok(d->act_dtype) || !dt_ok(d->router_dtype))
     return fail(MOE_ERR_INVALID, "MoELayer: bad dtype");
   if (!d->router_weight) return fail(MOE_ERR_INVALID, "MoELayer: router weight is NULL");
@@ -252,10 +255,10 @@ moe_status validate_layer_impl(const moe_layer_desc* d) {
 // log2 of the lanes per output row: the best lane utilisation of the K/32
 // units with at most umax units per lane; ties go to fewer lanes (more rows
 // in flight per wave, fewer shuffle steps).
-int pick_lg(int CU, int umax) {
+int pick_lg(int CU, int umax, int min_lg = 0) {
   int best = 6;
   double best_eff = -1.0;
-  for (int lg = 0; lg <= 6; lg++) {
+  for (int lg = min_lg; lg <= 6; lg++) {
     const int L = 1 << lg;
     const int upl = (CU + L - 1) / L;
     if (upl > umax) continue;
@@ -274,11 +277,11 @@ struct GemvGeom {
   int lg, row_blocks, rows_per_block, grid, tokmax, tok_chunk;
 };
 
-GemvGeom gemv_geom(int N, int K, int slots, bool single, int M, int xdt) {
+GemvGeom gemv_geom(int N, int K, int gsh, int slots, bool single, int M, int xdt) {
   GemvGeom g{};
   const int CU = K / 32;
   g.tokmax = single ? 1 : 8;
-  g.lg = pick_lg(CU, single ? 4 : 8);
+  g.lg = pick_lg(CU, single ? 4 : 8, gsh);
   const int SG = 64 >> g.lg;
   g.tok_chunk = 1;
   if (!single) {
@@ -296,23 +299,8 @@ GemvGeom gemv_geom(int N, int K, int slots, bool single, int M, int xdt) {
   return g;
 }
 
-// Down+combine lanes: positions per sub-group <= 2, units per lane <= 4.
-int pick_lg_combine(int CU, int k) {
-  int best = -1;
-  double best_eff = -1.0;
-  for (int lg = 0; lg <= 6; lg++) {
-    const int L = 1 << lg, SG = 64 >> lg;
-    const int upl = (CU + L - 1) / L;
-    const int pr = (k + SG - 1) / SG;
-    if (upl > 4 || pr > 2) continue;
-    const double eff = (double)CU / (double)(L * upl) * (double)k / (double)(SG * pr);
-    if (eff > best_eff + 1e-9) {
-      best_eff = eff;
-      best = lg;
-    }
-  }
-  return best;
-}
+// log2(group size / 32); group sizes are validated to 32, 64 or 128.
+int group_shift(int gs) { return gs == 128 ? 2 : (gs == 64 ? 1 : 0); }
 
 // ---------------------------------------------------------------------------
 // workspace
@@ -369,8 +357,9 @@ GemvProj to_proj(const moe_qproj& q) { return GemvProj{q.weight, q.scales, q.bia
 moe_status run_gemv(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
                     const uint32_t* perm, int topk, const uint32_t* offsets, const uint32_t* used,
                     int slots, int M, bool single, void* out, int act, float alpha, float limit,
-                    hipStream_t st) {
-  GemvGeom g = gemv_geom(p0.n, p0.k, slots, single, M, xdt);
+                    hipStream_t st, KEvents ev = {}) {
+  const int gsh = group_shift(p0.group_size);
+  GemvGeom g = gemv_geom(p0.n, p0.k, gsh, slots, single, M, xdt);
   GemvArgs a{};
   a.p0 = to_proj(p0);
   if (p1) a.p1 = to_proj(*p1);
@@ -382,7 +371,7 @@ moe_status run_gemv(const moe_qproj& p0, const moe_qproj* p1, const void* x, int
   a.out = out;
   a.N = p0.n;
   a.K = p0.k;
-  a.gs = p0.group_size;
+  a.gsh = gsh;
   a.row_blocks = g.row_blocks;
   a.rows_per_block = g.rows_per_block;
   a.lg = g.lg;
@@ -390,7 +379,7 @@ moe_status run_gemv(const moe_qproj& p0, const moe_qproj* p1, const void* x, int
   a.act = act;
   a.alpha = alpha;
   a.limit = limit;
-  MOE_HIP(launch_gemv(p0.bits, xdt, p0.sb_dtype, p1 != nullptr, g.tokmax, a, g.grid, st),
+  MOE_HIP(launch_gemv(p0.bits, xdt, p0.sb_dtype, p1 != nullptr, g.tokmax, a, g.grid, st, ev),
           "grouped GEMV launch");
   return MOE_OK;
 }
@@ -414,6 +403,8 @@ extern "C" moe_status moe_router_logits(const void* x, int32_t x_dtype, int32_t 
     return fail(MOE_ERR_INVALID, "router_logits: T, hidden and n_experts must be positive");
   if (!dt_ok(x_dtype) || !dt_ok(w_dtype)) return fail(MOE_ERR_INVALID, "router_logits: bad dtype");
   if (hidden % 8) return fail(MOE_ERR_UNSUPPORTED, "router_logits: hidden must be a multiple of 8");
+  if (hidden > kMaxHidden)
+    return fail(MOE_ERR_UNSUPPORTED, "router_logits: hidden (%d) above %d", hidden, kMaxHidden);
   MOE_HIP(launch_router_logits(x, x_dtype, T, hidden, weight, w_dtype, bias, n_experts, logits,
                                stream),
           "router logits launch");
@@ -608,9 +599,62 @@ moe_status shared_expert(const moe_layer_desc* d, const void* x, int T, void* ws
   return MOE_OK;
 }
 
-constexpr size_t kDown1MaxLds = 60 * 1024;
-constexpr int kDecodeBlocks = 512;   // gate/up blocks for one token (2 per CU)
-constexpr int kDown1Blocks = 256;    // down+combine blocks for one token (1 per CU)
+// Decode (T = 1) launch geometry. Lanes per row: the best unit utilisation
+// with at most 4 units per lane (and whole scale groups per lane stride).
+// Rows per lane rm: every load of a lane's rows is in flight before its
+// first dot product, so rm trades waves in flight against the work each
+// wave amortises its routing and activation loads over; about 3000 waves
+// (3 per SIMD) measured best on the GPT-OSS and Qwen3 decode shapes.
+struct Dec1Geom {
+  int lg, rm, rows_per_block, grid;
+};
+
+constexpr int kDec1TargetWaves = 3000;
+
+// Lanes per row for the one-token kernels: the best unit utilisation with at
+// most 4 units per lane; among equals, 2-3 units per lane (enough loads in
+// flight per lane without long shuffle-free dot chains), then fewer lanes.
+int pick_lg_dec1(int CU, int gsh) {
+  int best = -1;
+  double best_eff = -1.0, best_pen = 0.0;
+  for (int lg = gsh; lg <= 6; lg++) {
+    const int L = 1 << lg, upl = (CU + L - 1) / L;
+    if (upl > 4) continue;
+    const double eff = (double)CU / (double)(L * upl);
+    const double pen = (upl == 2 || upl == 3) ? 0.0 : 1.0;
+    if (eff > best_eff + 1e-9 || (eff > best_eff - 1e-9 && pen < best_pen)) {
+      best = lg;
+      best_eff = eff;
+      best_pen = pen;
+    }
+  }
+  return best < 0 ? 6 : best;
+}
+
+Dec1Geom dec1_geom(int N, int K, int gsh, int k, bool down) {
+  Dec1Geom g{};
+  g.lg = pick_lg_dec1(K / 32, gsh);
+  const int SG = 64 >> g.lg;
+  const int rows_per_wave = down ? SG : 4 * SG;  // rows one rm step covers per block
+  const double waves1 = (double)k * N / SG;
+  g.rm = std::max(1, std::min(kDec1MaxRows, (int)(waves1 / kDec1TargetWaves + 0.5)));
+  g.rows_per_block = g.rm * rows_per_wave;
+  const int row_blocks = (N + g.rows_per_block - 1) / g.rows_per_block;
+  g.grid = down ? row_blocks : k * row_blocks;
+  return g;
+}
+
+bool dec1_supported(const moe_layer_desc* d) {
+  if (d->act_dtype == MOE_F32 || d->top_k > kDec1MaxK) return false;
+  if (d->hidden > 8192 || d->intermediate > 8192) return false;
+  // expert-local byte offsets stay below 2^31 (with a row block of slack)
+  const moe_qproj* ps[3] = {&d->gate, &d->up, &d->down};
+  for (const moe_qproj* p : ps) {
+    const size_t row_bytes = (size_t)p->k * p->bits / 8;
+    if (((size_t)p->n + 256) * row_bytes >= (1ull << 31)) return false;
+  }
+  return true;
+}
 
 moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y, void* ws,
                          size_t ws_bytes, const moe_layer_trace* tr, hipStream_t st) {
@@ -622,10 +666,14 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y,
     return fail(MOE_ERR_WORKSPACE, "MoELayer: workspace of %zu bytes needed for T=%d", w.total, T);
   const int E = d->n_experts, k = d->top_k, H = d->hidden, I = d->intermediate;
   const int M = T * k, xdt = d->act_dtype;
-  auto mark = [&](int i) -> moe_status {
-    if (!tr || !tr->events[i]) return MOE_OK;
-    return hip_check(hipEventRecord(reinterpret_cast<hipEvent_t>(tr->events[i]), st),
-                     "trace event");
+  // dispatch-timestamped events of the routed gate/up and down kernels
+  auto kev = [&](int i) -> KEvents {
+    KEvents ev;
+    if (tr) {
+      ev.start = reinterpret_cast<hipEvent_t>(tr->events[2 * i]);
+      ev.stop = reinterpret_cast<hipEvent_t>(tr->events[2 * i + 1]);
+    }
+    return ev;
   };
 
   // 1. router projection (MoELayer.swift:540 / 689-690)
@@ -633,13 +681,12 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y,
                                at<void>(ws, w.logits), st),
           "router logits launch");
 
-  const int lgc = pick_lg_combine(I / 32, k);
-  const bool dec1 = (T == 1 && xdt != MOE_F32 && lgc >= 0 &&
-                     (size_t)k * I * dt_size(xdt) <= kDown1MaxLds);
+  const bool dec1 = (T == 1 && dec1_supported(d));
   int smode = 0;
   if (dec1) {
     // 2. one token: routing inside the gate/up kernel (MoELayer.swift:1167-1282
     //    without a host round trip), then the fused down + combine
+    const Dec1Geom gg = dec1_geom(I, H, group_shift(d->gate.group_size), k, false);
     Decode1Args g{};
     g.logits = at<void>(ws, w.logits);
     g.E = E;
@@ -657,39 +704,31 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y,
     g.act = at<void>(ws, w.act);
     g.N = I;
     g.K = H;
-    g.gs = d->gate.group_size;
-    g.lg = pick_lg(H / 32, 4);
-    const int SG = 64 >> g.lg;
-    const int max_rb = std::max(1, (I + 4 * SG - 1) / (4 * SG));
-    int rb = std::min(max_rb, std::max(1, (kDecodeBlocks + k - 1) / k));
-    g.rows_per_block = (I + rb - 1) / rb;
-    g.row_blocks = (I + g.rows_per_block - 1) / g.rows_per_block;
+    g.gsh = group_shift(d->gate.group_size);
+    g.lg = gg.lg;
+    g.rows_per_block = gg.rows_per_block;
+    g.row_blocks = gg.grid / k;
     g.act_kind = d->activation;
     g.alpha = d->act_alpha;
     g.limit = d->act_limit;
-    MOE_TRY(mark(0));
-    MOE_HIP(launch_gateup1(d->gate.bits, xdt, d->gate.sb_dtype, g, k * g.row_blocks, st),
+    MOE_HIP(launch_gateup1(d->gate.bits, xdt, d->gate.sb_dtype, g, gg.rm, gg.grid, st, kev(0)),
             "gate/up decode launch");
-    MOE_TRY(mark(1));
     MOE_TRY(shared_expert(d, x, T, ws, w, st, &smode));
+    const Dec1Geom dg = dec1_geom(H, I, group_shift(d->down.group_size), k, true);
     Down1Args dn{};
     dn.idx = g.idx;
     dn.w = g.w;
-    dn.perm = g.perm;
     dn.act = g.act;
     dn.p = to_proj(d->down);
     dn.out = y;
     dn.k = k;
     dn.N = H;
     dn.K = I;
-    dn.gs = d->down.group_size;
-    dn.lg = lgc;
-    dn.rows_per_block = std::max(1, (H + kDown1Blocks - 1) / kDown1Blocks);
-    const int grid = (H + dn.rows_per_block - 1) / dn.rows_per_block;
-    MOE_HIP(launch_down1(d->down.bits, xdt, d->down.sb_dtype, dn, grid,
-                         (size_t)k * I * dt_size(xdt), st),
+    dn.gsh = group_shift(d->down.group_size);
+    dn.lg = dg.lg;
+    dn.rows_per_block = dg.rows_per_block;
+    MOE_HIP(launch_down1(d->down.bits, xdt, d->down.sb_dtype, dn, dg.rm, dg.grid, st, kev(1)),
             "down+combine decode launch");
-    MOE_TRY(mark(2));
     if (smode)
       MOE_HIP(launch_add_shared(y, at<void>(ws, w.s_out), at<void>(ws, w.s_logit), smode, T, H, xdt,
                                 st),
@@ -706,21 +745,18 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y,
             "dispatch plan launch");
     const int slots = std::min(E, M);
     // 3. gate/up + activation over the plan (MoELayer.swift:883-893)
-    MOE_TRY(mark(0));
     MOE_TRY(run_gemv(d->gate, &d->up, x, xdt, at<uint32_t>(ws, w.perm), k,
                      at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, T == 1,
-                     at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st));
-    MOE_TRY(mark(1));
+                     at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st, kev(0)));
     MOE_TRY(shared_expert(d, x, T, ws, w, st, &smode));
     // 4. down projection, then the weighted combine (MoELayer.swift:899-939)
     MOE_TRY(run_gemv(d->down, nullptr, at<void>(ws, w.act), xdt, nullptr, 1,
                      at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, T == 1,
-                     at<void>(ws, w.Y), 0, 0.f, 0.f, st));
+                     at<void>(ws, w.Y), 0, 0.f, 0.f, st, kev(1)));
     MOE_HIP(launch_unpermute(at<void>(ws, w.Y), at<uint32_t>(ws, w.inv), at<float>(ws, w.w), T, H,
                              k, y, xdt, smode ? at<void>(ws, w.s_out) : nullptr,
                              smode ? at<void>(ws, w.s_logit) : nullptr, smode, st),
             "unpermute launch");
-    MOE_TRY(mark(2));
   }
   MOE_TRY(copy_trace(d, T, ws, w, tr, st));
   return MOE_OK;

@@ -17,6 +17,8 @@
 // Lane layout: a wave is split into 64/L sub-groups of L lanes; a sub-group
 // owns one output row and its lanes stride over the row's K/32 units; a
 // shuffle reduction over L lanes finishes the row.
+#include <hip/hip_ext.h>
+
 #include "moe_common.hpp"
 #include "moe_internal.hpp"
 
@@ -127,19 +129,36 @@ __device__ __forceinline__ void lds_x_unit(const XT* row, int u, XUnit<XT>& x) {
   }
 }
 
-// One weight unit with its group scale and folded bias.
-template <int BITS> struct WUnit {
+// One weight unit with its group scale and bias. Scale and bias stay in
+// their storage type until use, so loads are not forced to complete early.
+template <int BITS, typename ST> struct WUnit {
   uint32_t w[BITS];
-  float s, b;
+  ST s_raw, b_raw;
+  __device__ __forceinline__ float s() const { return to_f<ST>(s_raw); }
+  __device__ __forceinline__ float b() const { return to_f<ST>(b_raw); }
 };
 
+// p points at one expert (see expert_proj); row < N, so the offsets fit in
+// 32 bits and the loads use a scalar base with a 32-bit vector offset.
 template <int BITS, typename ST>
-__device__ __forceinline__ void load_w_unit(const GemvProj& p, size_t row, int row_words, int groups,
-                                            int gs, int u, WUnit<BITS>& wu) {
-  load_unit<BITS>(p.w + row * row_words + u * BITS, wu.w);
-  const size_t gi = row * groups + (u * 32) / gs;
-  wu.s = ld_sb<ST>(p.s, gi);
-  wu.b = ld_sb<ST>(p.b, gi);
+__device__ __forceinline__ void load_w_unit(const GemvProj& p, uint32_t row, int row_words, int groups,
+                                            int gsh, int u, WUnit<BITS, ST>& wu) {
+  load_unit<BITS>(p.w + (row * (uint32_t)row_words + (uint32_t)(u * BITS)), wu.w);
+  const uint32_t gi = row * (uint32_t)groups + (uint32_t)(u >> gsh);
+  wu.s_raw = reinterpret_cast<const ST*>(p.s)[gi];
+  wu.b_raw = reinterpret_cast<const ST*>(p.b)[gi];
+}
+
+// The projection of expert e alone (pointers advanced to its first row).
+template <int BITS, typename ST>
+__device__ __forceinline__ GemvProj expert_proj(const GemvProj& p, uint32_t e, int N, int row_words,
+                                                int groups) {
+  GemvProj q;
+  q.w = p.w + (size_t)e * N * row_words;
+  q.s = reinterpret_cast<const ST*>(p.s) + (size_t)e * N * groups;
+  q.b = reinterpret_cast<const ST*>(p.b) + (size_t)e * N * groups;
+  q.ob = p.ob;
+  return q;
 }
 
 template <typename XT>
@@ -182,12 +201,14 @@ __global__ __launch_bounds__(256) void gemv_grouped_kernel(const GemvArgs a) {
   if ((uint32_t)slot >= a.used[0]) return;
   const uint32_t e = a.used[1 + slot];
   const uint32_t pbeg = a.offsets[e], pend = a.offsets[e + 1];
-  const int N = a.N, K = a.K, CU = K >> 5, groups = K / a.gs, row_words = CU * BITS;
+  const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
   const int r_begin = rb * a.rows_per_block;
   const int r_end = min(N, r_begin + a.rows_per_block);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
   const int L = 1 << a.lg, SG = 64 >> a.lg;
   const int sg = lane >> a.lg, li = lane & (L - 1);
+  const GemvProj p0 = expert_proj<BITS, ST>(a.p0, e, N, row_words, groups);
+  const GemvProj p1 = expert_proj<BITS, ST>(a.p1, e, N, row_words, groups);
   XT* xs = reinterpret_cast<XT*>(smem);
   float* xsum = reinterpret_cast<float*>(smem + (size_t)a.tok_chunk * K * sizeof(XT));
   const XT* x = reinterpret_cast<const XT*>(a.x);
@@ -202,17 +223,17 @@ __global__ __launch_bounds__(256) void gemv_grouped_kernel(const GemvArgs a) {
     for (int r0 = r_begin + wave * SG; r0 < r_end; r0 += nwaves * SG) {
       const int r = r0 + sg;
       if (r >= r_end) continue;
-      const size_t row = ebase + (size_t)r;
+      const uint32_t row = (uint32_t)r;
       float acc0[TOKMAX], acc1[TOKMAX];
 #pragma unroll
       for (int t = 0; t < TOKMAX; t++) acc0[t] = acc1[t] = 0.f;
-      WUnit<BITS> w0[kUMax], w1[kUMax];
+      WUnit<BITS, ST> w0[kUMax], w1[kUMax];
 #pragma unroll
       for (int j = 0; j < kUMax; j++) {
         const int u = li + j * L;
         if (u < CU) {
-          load_w_unit<BITS, ST>(a.p0, row, row_words, groups, a.gs, u, w0[j]);
-          if constexpr (GATEUP) load_w_unit<BITS, ST>(a.p1, row, row_words, groups, a.gs, u, w1[j]);
+          load_w_unit<BITS, ST>(p0, row, row_words, groups, a.gsh, u, w0[j]);
+          if constexpr (GATEUP) load_w_unit<BITS, ST>(p1, row, row_words, groups, a.gsh, u, w1[j]);
         }
       }
 #pragma unroll
@@ -220,12 +241,12 @@ __global__ __launch_bounds__(256) void gemv_grouped_kernel(const GemvArgs a) {
         const int u = li + j * L;
         if (u < CU) {
           uint32_t cp0[16], cp1[16];
-          unpack_pairs<BITS>(w0[j].w, cp0);
-          const float bb0 = w0[j].b - MAGIC * w0[j].s;
+          unpack_pairs<BITS, Magic<BITS, XT>::bits>(w0[j].w, cp0);
+          const float bb0 = w0[j].b() - MAGIC * w0[j].s();
           float bb1 = 0.f;
           if constexpr (GATEUP) {
-            unpack_pairs<BITS>(w1[j].w, cp1);
-            bb1 = w1[j].b - MAGIC * w1[j].s;
+            unpack_pairs<BITS, Magic<BITS, XT>::bits>(w1[j].w, cp1);
+            bb1 = w1[j].b() - MAGIC * w1[j].s();
           }
 #pragma unroll
           for (int t = 0; t < TOKMAX; t++) {
@@ -233,8 +254,8 @@ __global__ __launch_bounds__(256) void gemv_grouped_kernel(const GemvArgs a) {
               XUnit<XT> xu;
               lds_x_unit<XT>(xs + t * K, u, xu);
               const float xsu = xsum[t * CU + u];
-              acc0[t] += w0[j].s * dot_unit<BITS, XT>(cp0, xu) + bb0 * xsu;
-              if constexpr (GATEUP) acc1[t] += w1[j].s * dot_unit<BITS, XT>(cp1, xu) + bb1 * xsu;
+              acc0[t] += w0[j].s() * dot_unit<BITS, XT>(cp0, xu) + bb0 * xsu;
+              if constexpr (GATEUP) acc1[t] += w1[j].s() * dot_unit<BITS, XT>(cp1, xu) + bb1 * xsu;
             }
           }
         }
@@ -251,9 +272,9 @@ __global__ __launch_bounds__(256) void gemv_grouped_kernel(const GemvArgs a) {
         for (int t = 0; t < TOKMAX; t++) {
           if (t < nt) {
             const size_t o = (size_t)(pc + t) * N + r;
-            const float g = finish_proj<XT>(acc0[t], a.p0.ob, row);
+            const float g = finish_proj<XT>(acc0[t], a.p0.ob, ebase + r);
             if constexpr (GATEUP) {
-              const float u = finish_proj<XT>(acc1[t], a.p1.ob, row);
+              const float u = finish_proj<XT>(acc1[t], a.p1.ob, ebase + r);
               out[o] = from_f<XT>(apply_act(g, u, a.act, a.alpha, a.limit));
             } else {
               out[o] = from_f<XT>(g);
@@ -277,12 +298,14 @@ __global__ __launch_bounds__(256) void gemv_single_kernel(const GemvArgs a) {
   const uint32_t e = a.used[1 + slot];
   const uint32_t p = a.offsets[e];
   if (a.offsets[e + 1] == p) return;
-  const int N = a.N, K = a.K, CU = K >> 5, groups = K / a.gs, row_words = CU * BITS;
+  const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
   const int r_begin = rb * a.rows_per_block;
   const int r_end = min(N, r_begin + a.rows_per_block);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
   const int L = 1 << a.lg, SG = 64 >> a.lg;
   const int sg = lane >> a.lg, li = lane & (L - 1);
+  const GemvProj p0 = expert_proj<BITS, ST>(a.p0, e, N, row_words, groups);
+  const GemvProj p1 = expert_proj<BITS, ST>(a.p1, e, N, row_words, groups);
   constexpr float MAGIC = Magic<BITS, XT>::value;
   constexpr int UR = 4;  // host guarantees ceil(CU / L) <= 4 for this kernel
   const uint32_t xrow = a.perm ? a.perm[p] / (uint32_t)a.topk : p;
@@ -301,14 +324,14 @@ __global__ __launch_bounds__(256) void gemv_single_kernel(const GemvArgs a) {
   for (int r0 = r_begin + wave * SG; r0 < r_end; r0 += nwaves * SG) {
     const int r = r0 + sg;
     if (r >= r_end) continue;
-    const size_t row = ebase + (size_t)r;
-    WUnit<BITS> w0[UR], w1[UR];
+    const uint32_t row = (uint32_t)r;
+    WUnit<BITS, ST> w0[UR], w1[UR];
 #pragma unroll
     for (int j = 0; j < UR; j++) {
       const int u = li + j * L;
       if (u < CU) {
-        load_w_unit<BITS, ST>(a.p0, row, row_words, groups, a.gs, u, w0[j]);
-        if constexpr (GATEUP) load_w_unit<BITS, ST>(a.p1, row, row_words, groups, a.gs, u, w1[j]);
+        load_w_unit<BITS, ST>(p0, row, row_words, groups, a.gsh, u, w0[j]);
+        if constexpr (GATEUP) load_w_unit<BITS, ST>(p1, row, row_words, groups, a.gsh, u, w1[j]);
       }
     }
     float acc0 = 0.f, acc1 = 0.f;
@@ -317,11 +340,11 @@ __global__ __launch_bounds__(256) void gemv_single_kernel(const GemvArgs a) {
       const int u = li + j * L;
       if (u < CU) {
         uint32_t cp[16];
-        unpack_pairs<BITS>(w0[j].w, cp);
-        acc0 += w0[j].s * dot_unit<BITS, XT>(cp, xu[j]) + (w0[j].b - MAGIC * w0[j].s) * xs[j];
+        unpack_pairs<BITS, Magic<BITS, XT>::bits>(w0[j].w, cp);
+        acc0 += w0[j].s() * dot_unit<BITS, XT>(cp, xu[j]) + (w0[j].b() - MAGIC * w0[j].s()) * xs[j];
         if constexpr (GATEUP) {
-          unpack_pairs<BITS>(w1[j].w, cp);
-          acc1 += w1[j].s * dot_unit<BITS, XT>(cp, xu[j]) + (w1[j].b - MAGIC * w1[j].s) * xs[j];
+          unpack_pairs<BITS, Magic<BITS, XT>::bits>(w1[j].w, cp);
+          acc1 += w1[j].s() * dot_unit<BITS, XT>(cp, xu[j]) + (w1[j].b() - MAGIC * w1[j].s()) * xs[j];
         }
       }
     }
@@ -329,9 +352,9 @@ __global__ __launch_bounds__(256) void gemv_single_kernel(const GemvArgs a) {
     if constexpr (GATEUP) acc1 = wave_sum_width(acc1, L);
     if (li == 0) {
       const size_t o = (size_t)p * N + r;
-      const float g = finish_proj<XT>(acc0, a.p0.ob, row);
+      const float g = finish_proj<XT>(acc0, a.p0.ob, ebase + r);
       if constexpr (GATEUP) {
-        const float u = finish_proj<XT>(acc1, a.p1.ob, row);
+        const float u = finish_proj<XT>(acc1, a.p1.ob, ebase + r);
         out[o] = from_f<XT>(apply_act(g, u, a.act, a.alpha, a.limit));
       } else {
         out[o] = from_f<XT>(g);
@@ -342,270 +365,283 @@ __global__ __launch_bounds__(256) void gemv_single_kernel(const GemvArgs a) {
 
 // ---------------------------------------------------------------------------
 // decode of one token: gate/up with in-wave routing, then down + combine
+//
+// Both kernels hold one expert per wave at a time, so the expert's weight,
+// scale and bias arrays are addressed through wave-uniform buffer resources
+// and every load is a 32-bit lane offset (no per-unit 64-bit address math).
+// A lane's units are u = li + j L; units at or past CU read the next row's
+// bytes, or zeros past the expert's end, and are masked out of the sums.
 // ---------------------------------------------------------------------------
 
+struct ProjView {
+  rsrc_t w, s, b;
+};
+
+template <int BITS, typename ST>
+__device__ __forceinline__ ProjView proj_view(const GemvProj& p, uint32_t e, int N, int row_words,
+                                              int groups) {
+  const size_t rows = (size_t)e * (size_t)N;
+  ProjView v;
+  v.w = make_rsrc(p.w + rows * row_words, (uint32_t)N * (uint32_t)row_words * 4u);
+  v.s = make_rsrc(reinterpret_cast<const ST*>(p.s) + rows * groups,
+                  (uint32_t)N * (uint32_t)groups * (uint32_t)sizeof(ST));
+  v.b = make_rsrc(reinterpret_cast<const ST*>(p.b) + rows * groups,
+                  (uint32_t)N * (uint32_t)groups * (uint32_t)sizeof(ST));
+  return v;
+}
+
+// Byte offsets of a lane's first unit in `row`; unit j adds j * wstep and
+// j * sstep (wstep = L * BITS * 4, sstep = (L >> gsh) * sizeof(ST); the host
+// keeps L a multiple of the units per scale group, 1 << gsh).
+struct UnitAddr {
+  uint32_t w0, s0;
+};
+
+template <int BITS, typename ST>
+__device__ __forceinline__ UnitAddr unit_addr(uint32_t row, int row_words, int groups, int li,
+                                              int gsh) {
+  UnitAddr a;
+  a.w0 = row * (uint32_t)(row_words * 4) + (uint32_t)(li * BITS * 4);
+  a.s0 = (row * (uint32_t)groups + (uint32_t)(li >> gsh)) * (uint32_t)sizeof(ST);
+  return a;
+}
+
 template <int BITS, typename ST, int UR>
-__device__ __forceinline__ void load_units(const GemvProj& p, size_t row, int row_words, int groups,
-                                           int gs, int li, int L, int CU,
-                                           WUnit<BITS> (&w)[UR]) {
+__device__ __forceinline__ void bload_units(const ProjView& v, UnitAddr ad, uint32_t wstep,
+                                            uint32_t sstep, WUnit<BITS, ST> (&u)[UR]) {
 #pragma unroll
   for (int j = 0; j < UR; j++) {
-    const int u = li + j * L;
-    if (u < CU) load_w_unit<BITS, ST>(p, row, row_words, groups, gs, u, w[j]);
+    bload_unit<BITS>(v.w, ad.w0 + (uint32_t)j * wstep, u[j].w);
+    u[j].s_raw = __builtin_bit_cast(ST, bload16(v.s, ad.s0 + (uint32_t)j * sstep));
+    u[j].b_raw = __builtin_bit_cast(ST, bload16(v.b, ad.s0 + (uint32_t)j * sstep));
   }
 }
 
-template <int BITS, typename XT, int UR>
-__device__ __forceinline__ float dot_units(const WUnit<BITS> (&w)[UR],
+template <int BITS, typename XT, typename ST, int UR>
+__device__ __forceinline__ float dot_units(const WUnit<BITS, ST> (&w)[UR],
                                            const XUnit<XT> (&xu)[UR], const float (&xs)[UR],
                                            int li, int L, int CU) {
   constexpr float MAGIC = Magic<BITS, XT>::value;
   float acc = 0.f;
 #pragma unroll
   for (int j = 0; j < UR; j++) {
-    const int u = li + j * L;
-    if (u < CU) {
-      uint32_t cp[16];
-      unpack_pairs<BITS>(w[j].w, cp);
-      acc += w[j].s * dot_unit<BITS, XT>(cp, xu[j]) + (w[j].b - MAGIC * w[j].s) * xs[j];
-    }
+    uint32_t cp[16];
+    unpack_pairs<BITS, Magic<BITS, XT>::bits>(w[j].w, cp);
+    const float sc = w[j].s();
+    const float v = sc * dot_unit<BITS, XT>(cp, xu[j]) + (w[j].b() - MAGIC * sc) * xs[j];
+    acc += (li + j * L < CU) ? v : 0.f;
   }
   return acc;
 }
 
-template <int BITS, typename XT, typename ST, int UR>
-__global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
-  __shared__ float sc[4][kTopkMaxE];
-  __shared__ int sel_lds[64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-  const int slot = blockIdx.x / a.row_blocks, rb = blockIdx.x - slot * a.row_blocks;
-  const bool writer = (blockIdx.x == 0 && wave == 0);
-  const XT* logits = reinterpret_cast<const XT*>(a.logits);
-
-  // every wave routes the token itself (identical, deterministic results)
-  int sel;
-  float wgt = 0.f;
-  wave_topk<XT>(logits, a.E, a.k, a.gating, a.norm, a.ebias, sc[wave], writer, &sel, &wgt);
-  int pos = 0;
-  for (int r = 0; r < a.k; r++) pos += (__shfl(sel, r, 64) < sel) ? 1 : 0;
-  const uint64_t hit = __ballot(lane < a.k && pos == slot);
-  if (hit == 0) return;
-  const int e = __shfl(sel, __ffsll((unsigned long long)hit) - 1, 64);
-  if (writer) {
-    if (lane < a.k) {
-      a.idx[lane] = (uint32_t)sel;
-      a.w[lane] = wgt;
-      a.perm[pos] = (uint32_t)lane;
-      sel_lds[lane] = sel;
+// One activation row (16-bit types) into registers in pair order; units past
+// the row read zeros.
+template <int BITS, typename XT, int UR>
+__device__ __forceinline__ void bload_x_units(rsrc_t xr, int li, int L, XUnit<XT> (&xu)[UR],
+                                              float (&xs)[UR]) {
+#pragma unroll
+  for (int j = 0; j < UR; j++) {
+    const uint32_t off = (uint32_t)(li + j * L) * 64u;
+    uint32_t n[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const u32x4_t v = bload128(xr, off + 16u * q);
+      n[4 * q] = v[0]; n[4 * q + 1] = v[1]; n[4 * q + 2] = v[2]; n[4 * q + 3] = v[3];
     }
-    if (a.offsets) {
-      wave_sync();
-      for (int ee = lane; ee <= a.E; ee += 64) {
-        int c = 0;
-        for (int r = 0; r < a.k; r++) c += (sel_lds[r] < ee) ? 1 : 0;
-        a.offsets[ee] = (uint32_t)c;
-      }
-    }
+    natural_to_pairs<BITS>(n, xu[j].v);
+    xs[j] = sum16(n, __is_same(XT, bf16_t));
   }
+}
 
-  const int N = a.N, K = a.K, CU = K >> 5, groups = K / a.gs, row_words = CU * BITS;
+// gate/up for one token. Block (slot, rb): the slot-th smallest selected
+// expert, rows [rb * rows_per_block, ...). Wave w, sub-group sg owns rows
+// r_begin + w SG + sg + it 4 SG for it < RM; every load of those rows is
+// issued before the first dot product. The routing runs once per block, in
+// wave 0, while the other waves load the activations.
+template <int BITS, typename XT, typename ST, int UR, int RM>
+__global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
+  __shared__ float sc[kTopkMaxE];
+  __shared__ int route[2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int slot = blockIdx.x / a.row_blocks, rb = blockIdx.x - slot * a.row_blocks;
+  const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
   const int L = 1 << a.lg, SG = 64 >> a.lg;
   const int sg = lane >> a.lg, li = lane & (L - 1);
   const int r_begin = rb * a.rows_per_block;
   const int r_end = min(N, r_begin + a.rows_per_block);
-  const int stride = nwaves * SG;
-  const size_t ebase = (size_t)e * N;
-  XT* act = reinterpret_cast<XT*>(a.act) + (size_t)slot * N;
+  const int r0 = r_begin + wave * SG + sg, stride = 4 * SG;
+  const XT* ob_g = reinterpret_cast<const XT*>(a.g.ob);
+  const XT* ob_u = reinterpret_cast<const XT*>(a.u.ob);
 
-  int r = r_begin + wave * SG + sg;
-  WUnit<BITS> A0[UR], A1[UR], B0[UR], B1[UR];
-  if (r < r_end) {
-    load_units<BITS, ST, UR>(a.g, ebase + r, row_words, groups, a.gs, li, L, CU, A0);
-    load_units<BITS, ST, UR>(a.u, ebase + r, row_words, groups, a.gs, li, L, CU, A1);
+  // the activations do not depend on the routing
+  XUnit<XT> xu[UR];
+  float xs[UR];
+  bload_x_units<BITS, XT, UR>(make_rsrc(a.x, (uint32_t)(K * sizeof(XT))), li, L, xu, xs);
+
+  // wave 0 routes the token (every block computes identical, deterministic
+  // results); block 0 publishes the routing
+  if (wave == 0) {
+    const bool writer = blockIdx.x == 0;
+    int sel;
+    float wgt = 0.f;
+    uint64_t masks[kTopkEPL];
+    wave_topk<XT>(reinterpret_cast<const XT*>(a.logits), a.E, a.k, a.gating, a.norm, a.ebias, sc,
+                  writer, &sel, &wgt, masks);
+    const int e = __builtin_amdgcn_readfirstlane(selected_nth(masks, slot));
+    const uint64_t hit = __ballot(lane < a.k && sel == e);
+    if (lane == 0) {
+      route[0] = e;
+      route[1] = __ffsll((unsigned long long)hit) - 1;
+    }
+    if (writer) {
+      if (lane < a.k) {
+        a.idx[lane] = (uint32_t)sel;
+        a.w[lane] = wgt;
+        a.perm[selected_below(masks, sel)] = (uint32_t)lane;
+      }
+      if (a.offsets)
+        for (int ee = lane; ee <= a.E; ee += 64) a.offsets[ee] = (uint32_t)selected_below(masks, ee);
+    }
+  }
+  __syncthreads();
+  const int e = __builtin_amdgcn_readfirstlane(route[0]);
+  const int rank = __builtin_amdgcn_readfirstlane(route[1]);
+
+  // output biases first: waiting for them never waits for weight loads
+  float obg[RM], obu[RM];
+#pragma unroll
+  for (int it = 0; it < RM; it++) {
+    const int row = min(r0 + it * stride, N - 1);
+    obg[it] = ob_g ? to_f<XT>(ob_g[(size_t)e * N + row]) : 0.f;
+    obu[it] = ob_u ? to_f<XT>(ob_u[(size_t)e * N + row]) : 0.f;
+  }
+  const ProjView G = proj_view<BITS, ST>(a.g, (uint32_t)e, N, row_words, groups);
+  const ProjView U = proj_view<BITS, ST>(a.u, (uint32_t)e, N, row_words, groups);
+  const uint32_t wstep = (uint32_t)(L * BITS * 4), sstep = (uint32_t)((L >> a.gsh) * sizeof(ST));
+  WUnit<BITS, ST> gw[RM][UR], uw[RM][UR];
+#pragma unroll
+  for (int it = 0; it < RM; it++) {
+    const UnitAddr ad = unit_addr<BITS, ST>((uint32_t)(r0 + it * stride), row_words, groups, li, a.gsh);
+    bload_units<BITS, ST, UR>(G, ad, wstep, sstep, gw[it]);
+    bload_units<BITS, ST, UR>(U, ad, wstep, sstep, uw[it]);
+  }
+
+  XT* act = reinterpret_cast<XT*>(a.act) + (size_t)rank * N;
+#pragma unroll
+  for (int it = 0; it < RM; it++) {
+    float g = group_sum(dot_units<BITS, XT, ST, UR>(gw[it], xu, xs, li, L, CU), a.lg);
+    float u = group_sum(dot_units<BITS, XT, ST, UR>(uw[it], xu, xs, li, L, CU), a.lg);
+    const int row = r0 + it * stride;
+    if (li == L - 1 && row < r_end) {
+      g = round_to<XT>(g);
+      u = round_to<XT>(u);
+      if (ob_g) g = round_to<XT>(g + obg[it]);
+      if (ob_u) u = round_to<XT>(u + obu[it]);
+      act[row] = from_f<XT>(apply_act(g, u, a.act_kind, a.alpha, a.limit));
+    }
+  }
+}
+
+// down projection + weighted combine for one token. Block = k waves; wave q
+// takes the rank-q expert and its activation row (registers, pair order),
+// and all waves share the block's rows: sub-group sg owns rows
+// r_begin + sg + it SG for it < RM. Each expert's output is rounded to the
+// activation dtype (then its output bias added and rounded) before it is
+// weighted, as the unfused path stores it (MoELayer.swift:895-939); the
+// weighted outputs are added in rank order.
+template <int BITS, typename XT, typename ST, int UR, int RM>
+__global__ __launch_bounds__(512) void down1_kernel(const Down1Args a) {
+  __shared__ float ys[kDec1MaxK * kDec1MaxRows * 64];
+  __shared__ float wr[kDec1MaxK];
+  const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
+  const int L = 1 << a.lg, SG = 64 >> a.lg;
+  const int sg = lane >> a.lg, li = lane & (L - 1);
+  const int rpb = a.rows_per_block;  // RM * SG
+  const int r_begin = blockIdx.x * rpb;
+  const XT* ob = reinterpret_cast<const XT*>(a.p.ob);
+
+  const uint32_t e = __builtin_amdgcn_readfirstlane(a.idx[q]);
+  if (lane == 0) wr[q] = round_to<XT>(a.w[q]);
+  float obv[RM];
+#pragma unroll
+  for (int it = 0; it < RM; it++)
+    obv[it] = ob ? to_f<XT>(ob[(size_t)e * N + min(r_begin + sg + it * SG, N - 1)]) : 0.f;
+  const ProjView P = proj_view<BITS, ST>(a.p, e, N, row_words, groups);
+  const uint32_t wstep = (uint32_t)(L * BITS * 4), sstep = (uint32_t)((L >> a.gsh) * sizeof(ST));
+  WUnit<BITS, ST> w[RM][UR];
+#pragma unroll
+  for (int it = 0; it < RM; it++) {
+    const UnitAddr ad = unit_addr<BITS, ST>((uint32_t)(r_begin + sg + it * SG), row_words, groups, li, a.gsh);
+    bload_units<BITS, ST, UR>(P, ad, wstep, sstep, w[it]);
   }
   XUnit<XT> xu[UR];
   float xs[UR];
-  const XT* x = reinterpret_cast<const XT*>(a.x);
-#pragma unroll
-  for (int j = 0; j < UR; j++) {
-    const int u = li + j * L;
-    xs[j] = 0.f;
-    if (u < CU) xs[j] = load_x_unit<BITS, XT>(x, u, xu[j]);
-  }
-  auto finish = [&](int rr, float g, float u) {
-    g = wave_sum_width(g, L);
-    u = wave_sum_width(u, L);
-    if (li == 0) {
-      const float gv = finish_proj<XT>(g, a.g.ob, ebase + rr);
-      const float uv = finish_proj<XT>(u, a.u.ob, ebase + rr);
-      act[rr] = from_f<XT>(apply_act(gv, uv, a.act_kind, a.alpha, a.limit));
-    }
-  };
-  while (r < r_end) {
-    int rn = r + stride;
-    if (rn < r_end) {
-      load_units<BITS, ST, UR>(a.g, ebase + rn, row_words, groups, a.gs, li, L, CU, B0);
-      load_units<BITS, ST, UR>(a.u, ebase + rn, row_words, groups, a.gs, li, L, CU, B1);
-    }
-    finish(r, dot_units<BITS, XT, UR>(A0, xu, xs, li, L, CU), dot_units<BITS, XT, UR>(A1, xu, xs, li, L, CU));
-    r = rn;
-    if (r >= r_end) break;
-    rn = r + stride;
-    if (rn < r_end) {
-      load_units<BITS, ST, UR>(a.g, ebase + rn, row_words, groups, a.gs, li, L, CU, A0);
-      load_units<BITS, ST, UR>(a.u, ebase + rn, row_words, groups, a.gs, li, L, CU, A1);
-    }
-    finish(r, dot_units<BITS, XT, UR>(B0, xu, xs, li, L, CU), dot_units<BITS, XT, UR>(B1, xu, xs, li, L, CU));
-    r = rn;
-  }
-}
-
-template <int BITS, typename ST, int PR, int UR>
-__device__ __forceinline__ void down1_load_row(const GemvProj& P, int N, int k, int gs,
-                                               const uint32_t (&ex)[PR], int r, int sg, int SG,
-                                               int li, int L, int CU, int row_words, int groups,
-                                               WUnit<BITS> (&w)[PR][UR]) {
-#pragma unroll
-  for (int q = 0; q < PR; q++)
-    if (sg + q * SG < k)
-      load_units<BITS, ST, UR>(P, (size_t)ex[q] * N + r, row_words, groups, gs, li, L, CU, w[q]);
-}
-
-// One output row: each expert's output is rounded to the activation dtype
-// before it is weighted, as the unfused path stores it (MoELayer.swift:
-// 895-939); a full-wave reduction adds the k experts.
-template <int BITS, typename XT, int PR, int UR>
-__device__ __forceinline__ void down1_row(const void* ob, XT* out, int N, int k,
-                                          const uint32_t (&ex)[PR], const float (&wsl)[PR],
-                                          const XUnit<XT> (&xu)[PR][UR], const float (&xs)[PR][UR],
-                                          const WUnit<BITS> (&w)[PR][UR], int r, int sg, int SG,
-                                          int li, int L, int CU, int lane) {
-  float acc = 0.f;
-#pragma unroll
-  for (int q = 0; q < PR; q++) {
-    const int p = sg + q * SG;
-    float part = 0.f;
-    if (p < k) part = dot_units<BITS, XT, UR>(w[q], xu[q], xs[q], li, L, CU);
-    part = wave_sum_width(part, L);
-    if (p < k && li == 0) acc += wsl[q] * finish_proj<XT>(part, ob, (size_t)ex[q] * N + r);
-  }
-  acc = wave_sum_width(acc, 64);
-  if (lane == 0) out[r] = from_f<XT>(acc);
-}
-
-template <int BITS, typename XT, typename ST, int PR, int UR>
-__global__ __launch_bounds__(256) void down1_kernel(const Down1Args a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-  const int N = a.N, K = a.K, CU = K >> 5, groups = K / a.gs, row_words = CU * BITS;
-  const int L = 1 << a.lg, SG = 64 >> a.lg;
-  const int sg = lane >> a.lg, li = lane & (L - 1);
-  const int r_begin = blockIdx.x * a.rows_per_block;
-  const int r_end = min(N, r_begin + a.rows_per_block);
-  XT* al = reinterpret_cast<XT*>(smem);
-  const GemvProj P = a.p;
-  const int kk = a.k, gs = a.gs;
-  XT* out = reinterpret_cast<XT*>(a.out);
-
-  // stage the k activation rows (natural order) while the weights stream in
-  constexpr int EPV = 16 / sizeof(XT);
-  constexpr int NPRE = 4;
-  const int nvec = a.k * K / EPV;
-  const uint4* src = reinterpret_cast<const uint4*>(a.act);
-  uint4* dst = reinterpret_cast<uint4*>(al);
-  uint4 stage[NPRE];
-#pragma unroll
-  for (int j = 0; j < NPRE; j++) {
-    const int i = threadIdx.x + j * blockDim.x;
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (i < nvec) v = src[i];
-    stage[j] = v;
-  }
-
-  uint32_t ex[PR];
-  float wsl[PR];
-#pragma unroll
-  for (int q = 0; q < PR; q++) {
-    const int p = sg + q * SG;
-    ex[q] = 0;
-    wsl[q] = 0.f;
-    if (p < a.k) {
-      const uint32_t s = a.perm[p];
-      ex[q] = a.idx[s];
-      wsl[q] = round_to<XT>(a.w[s]);
-    }
-  }
-  int r = r_begin + wave;
-  WUnit<BITS> A[PR][UR], B[PR][UR];
-  if (r < r_end) down1_load_row<BITS, ST, PR, UR>(P, N, kk, gs, ex, r, sg, SG, li, L, CU, row_words, groups, A);
+  const XT* act = reinterpret_cast<const XT*>(a.act) + (size_t)q * K;
+  bload_x_units<BITS, XT, UR>(make_rsrc(act, (uint32_t)(K * sizeof(XT))), li, L, xu, xs);
 
 #pragma unroll
-  for (int j = 0; j < NPRE; j++) {
-    const int i = threadIdx.x + j * blockDim.x;
-    if (i < nvec) dst[i] = stage[j];
+  for (int it = 0; it < RM; it++) {
+    float y = group_sum(dot_units<BITS, XT, ST, UR>(w[it], xu, xs, li, L, CU), a.lg);
+    y = round_to<XT>(y);
+    if (ob) y = round_to<XT>(y + obv[it]);
+    if (li == L - 1) ys[q * rpb + sg + it * SG] = y;
   }
-  for (int i = threadIdx.x + NPRE * blockDim.x; i < nvec; i += blockDim.x) dst[i] = src[i];
   __syncthreads();
-
-  XUnit<XT> xu[PR][UR];
-  float xs[PR][UR];
-#pragma unroll
-  for (int q = 0; q < PR; q++) {
-    const int p = sg + q * SG;
-#pragma unroll
-    for (int j = 0; j < UR; j++) {
-      const int u = li + j * L;
-      xs[q][j] = 0.f;
-      if (p < a.k && u < CU) xs[q][j] = load_x_unit<BITS, XT>(al + (size_t)p * K, u, xu[q][j]);
-    }
-  }
-  while (r < r_end) {
-    int rn = r + nwaves;
-    if (rn < r_end) down1_load_row<BITS, ST, PR, UR>(P, N, kk, gs, ex, rn, sg, SG, li, L, CU, row_words, groups, B);
-    down1_row<BITS, XT, PR, UR>(P.ob, out, N, kk, ex, wsl, xu, xs, A, r, sg, SG, li, L, CU, lane);
-    r = rn;
-    if (r >= r_end) break;
-    rn = r + nwaves;
-    if (rn < r_end) down1_load_row<BITS, ST, PR, UR>(P, N, kk, gs, ex, rn, sg, SG, li, L, CU, row_words, groups, A);
-    down1_row<BITS, XT, PR, UR>(P.ob, out, N, kk, ex, wsl, xu, xs, B, r, sg, SG, li, L, CU, lane);
-    r = rn;
+  XT* out = reinterpret_cast<XT*>(a.out);
+  for (int t = threadIdx.x; t < rpb; t += blockDim.x) {
+    const int row = r_begin + t;
+    if (row >= N) break;
+    float acc = 0.f;
+    for (int qq = 0; qq < a.k; qq++) acc += wr[qq] * ys[qq * rpb + t];
+    out[row] = from_f<XT>(acc);
   }
 }
 
 template <int BITS, typename XT, typename ST, int UR>
-static hipError_t launch_dec1_u(bool down, int pr, const void* args, int grid, size_t smem,
-                                hipStream_t st) {
-  if (!down)
-    hipLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR>), dim3(grid), dim3(256), 0, st,
-                       *reinterpret_cast<const Decode1Args*>(args));
-  else if (pr == 1)
-    hipLaunchKernelGGL((down1_kernel<BITS, XT, ST, 1, UR>), dim3(grid), dim3(256), smem, st,
-                       *reinterpret_cast<const Down1Args*>(args));
-  else
-    hipLaunchKernelGGL((down1_kernel<BITS, XT, ST, 2, UR>), dim3(grid), dim3(256), smem, st,
-                       *reinterpret_cast<const Down1Args*>(args));
+static hipError_t launch_dec1_u(bool down, int var, const void* args, int grid, size_t smem,
+                                hipStream_t st, KEvents ev) {
+  if (!down) {
+    const Decode1Args& a = *reinterpret_cast<const Decode1Args*>(args);
+    switch (var) {
+      case 1: hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, 1>), dim3(grid), dim3(256), 0, st, ev.start, ev.stop, 0, a); break;
+      case 2: hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, 2>), dim3(grid), dim3(256), 0, st, ev.start, ev.stop, 0, a); break;
+      case 3: hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, 3>), dim3(grid), dim3(256), 0, st, ev.start, ev.stop, 0, a); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    const Down1Args& a = *reinterpret_cast<const Down1Args*>(args);
+    const dim3 block(64 * a.k);
+    switch (var) {
+      case 1: hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, 1>), dim3(grid), block, 0, st, ev.start, ev.stop, 0, a); break;
+      case 2: hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, 2>), dim3(grid), block, 0, st, ev.start, ev.stop, 0, a); break;
+      case 3: hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, 3>), dim3(grid), block, 0, st, ev.start, ev.stop, 0, a); break;
+      default: return hipErrorInvalidValue;
+    }
+  }
   return hipGetLastError();
 }
 
 template <int BITS, typename XT, typename ST>
-static hipError_t launch_dec1_t(bool down, int pr, int ur, const void* args, int grid, size_t smem,
-                                hipStream_t st) {
+static hipError_t launch_dec1_t(bool down, int var, int ur, const void* args, int grid, size_t smem,
+                                hipStream_t st, KEvents ev) {
   switch (ur) {
-    case 1: return launch_dec1_u<BITS, XT, ST, 1>(down, pr, args, grid, smem, st);
-    case 2: return launch_dec1_u<BITS, XT, ST, 2>(down, pr, args, grid, smem, st);
-    case 3: return launch_dec1_u<BITS, XT, ST, 3>(down, pr, args, grid, smem, st);
-    case 4: return launch_dec1_u<BITS, XT, ST, 4>(down, pr, args, grid, smem, st);
+    case 1: return launch_dec1_u<BITS, XT, ST, 1>(down, var, args, grid, smem, st, ev);
+    case 2: return launch_dec1_u<BITS, XT, ST, 2>(down, var, args, grid, smem, st, ev);
+    case 3: return launch_dec1_u<BITS, XT, ST, 3>(down, var, args, grid, smem, st, ev);
+    case 4: return launch_dec1_u<BITS, XT, ST, 4>(down, var, args, grid, smem, st, ev);
   }
   return hipErrorInvalidValue;
 }
 
+// var: rows per lane (1..3).
 template <int BITS>
-static hipError_t launch_dec1_bits(int xdt, int sbdt, bool down, int pr, int ur, const void* args,
-                                   int grid, size_t smem, hipStream_t st) {
-  if (xdt == DT_BF16 && sbdt == DT_BF16) return launch_dec1_t<BITS, bf16_t, bf16_t>(down, pr, ur, args, grid, smem, st);
-  if (xdt == DT_BF16 && sbdt == DT_F16) return launch_dec1_t<BITS, bf16_t, f16_t>(down, pr, ur, args, grid, smem, st);
-  if (xdt == DT_F16 && sbdt == DT_F16) return launch_dec1_t<BITS, f16_t, f16_t>(down, pr, ur, args, grid, smem, st);
-  if (xdt == DT_F16 && sbdt == DT_BF16) return launch_dec1_t<BITS, f16_t, bf16_t>(down, pr, ur, args, grid, smem, st);
+static hipError_t launch_dec1_bits(int xdt, int sbdt, bool down, int var, int ur, const void* args,
+                                   int grid, size_t smem, hipStream_t st, KEvents ev = {}) {
+  if (xdt == DT_BF16 && sbdt == DT_BF16) return launch_dec1_t<BITS, bf16_t, bf16_t>(down, var, ur, args, grid, smem, st, ev);
+  if (xdt == DT_BF16 && sbdt == DT_F16) return launch_dec1_t<BITS, bf16_t, f16_t>(down, var, ur, args, grid, smem, st, ev);
+  if (xdt == DT_F16 && sbdt == DT_F16) return launch_dec1_t<BITS, f16_t, f16_t>(down, var, ur, args, grid, smem, st, ev);
+  if (xdt == DT_F16 && sbdt == DT_BF16) return launch_dec1_t<BITS, f16_t, bf16_t>(down, var, ur, args, grid, smem, st, ev);
   return hipErrorInvalidValue;
 }
 
@@ -615,32 +651,35 @@ static hipError_t launch_dec1_bits(int xdt, int sbdt, bool down, int pr, int ur,
 
 template <int BITS, typename XT, typename ST>
 static hipError_t launch_gemv_t(bool gateup, int tokmax, const GemvArgs& a, int grid,
-                                hipStream_t st) {
+                                hipStream_t st, KEvents ev) {
   if (tokmax <= 1) {
     if (gateup)
-      hipLaunchKernelGGL((gemv_single_kernel<BITS, XT, ST, true>), dim3(grid), dim3(256), 0, st, a);
+      hipExtLaunchKernelGGL((gemv_single_kernel<BITS, XT, ST, true>), dim3(grid), dim3(256), 0, st,
+                            ev.start, ev.stop, 0, a);
     else
-      hipLaunchKernelGGL((gemv_single_kernel<BITS, XT, ST, false>), dim3(grid), dim3(256), 0, st, a);
+      hipExtLaunchKernelGGL((gemv_single_kernel<BITS, XT, ST, false>), dim3(grid), dim3(256), 0, st,
+                            ev.start, ev.stop, 0, a);
   } else {
-    const size_t smem = gemv_smem_bytes(__is_same(XT, float) ? DT_F32 : DT_BF16, a.K, a.tok_chunk);
+    const uint32_t smem = (uint32_t)gemv_smem_bytes(__is_same(XT, float) ? DT_F32 : DT_BF16, a.K,
+                                                    a.tok_chunk);
     if (gateup)
-      hipLaunchKernelGGL((gemv_grouped_kernel<BITS, XT, ST, true, 8>), dim3(grid), dim3(256), smem,
-                         st, a);
+      hipExtLaunchKernelGGL((gemv_grouped_kernel<BITS, XT, ST, true, 8>), dim3(grid), dim3(256),
+                            smem, st, ev.start, ev.stop, 0, a);
     else
-      hipLaunchKernelGGL((gemv_grouped_kernel<BITS, XT, ST, false, 8>), dim3(grid), dim3(256), smem,
-                         st, a);
+      hipExtLaunchKernelGGL((gemv_grouped_kernel<BITS, XT, ST, false, 8>), dim3(grid), dim3(256),
+                            smem, st, ev.start, ev.stop, 0, a);
   }
   return hipGetLastError();
 }
 
 template <int BITS>
 static hipError_t launch_gemv_bits(int xdt, int sbdt, bool gateup, int tokmax, const GemvArgs& a,
-                                   int grid, hipStream_t st) {
-  if (xdt == DT_BF16 && sbdt == DT_BF16) return launch_gemv_t<BITS, bf16_t, bf16_t>(gateup, tokmax, a, grid, st);
-  if (xdt == DT_BF16 && sbdt == DT_F16) return launch_gemv_t<BITS, bf16_t, f16_t>(gateup, tokmax, a, grid, st);
-  if (xdt == DT_F16 && sbdt == DT_F16) return launch_gemv_t<BITS, f16_t, f16_t>(gateup, tokmax, a, grid, st);
-  if (xdt == DT_F16 && sbdt == DT_BF16) return launch_gemv_t<BITS, f16_t, bf16_t>(gateup, tokmax, a, grid, st);
-  if (xdt == DT_F32 && sbdt == DT_F32) return launch_gemv_t<BITS, float, float>(gateup, tokmax, a, grid, st);
+                                   int grid, hipStream_t st, KEvents ev) {
+  if (xdt == DT_BF16 && sbdt == DT_BF16) return launch_gemv_t<BITS, bf16_t, bf16_t>(gateup, tokmax, a, grid, st, ev);
+  if (xdt == DT_BF16 && sbdt == DT_F16) return launch_gemv_t<BITS, bf16_t, f16_t>(gateup, tokmax, a, grid, st, ev);
+  if (xdt == DT_F16 && sbdt == DT_F16) return launch_gemv_t<BITS, f16_t, f16_t>(gateup, tokmax, a, grid, st, ev);
+  if (xdt == DT_F16 && sbdt == DT_BF16) return launch_gemv_t<BITS, f16_t, bf16_t>(gateup, tokmax, a, grid, st, ev);
+  if (xdt == DT_F32 && sbdt == DT_F32) return launch_gemv_t<BITS, float, float>(gateup, tokmax, a, grid, st, ev);
   return hipErrorInvalidValue;
 }
 
@@ -650,14 +689,15 @@ static hipError_t launch_gemv_bits(int xdt, int sbdt, bool gateup, int tokmax, c
 #define MOE_CAT(a, b) MOE_CAT2(a, b)
 
 hipError_t MOE_CAT(launch_gemv_b, MOE_BITS)(int xdt, int sbdt, bool gateup, int tokmax,
-                                             const GemvArgs& a, int grid, hipStream_t st) {
-  return launch_gemv_bits<MOE_BITS>(xdt, sbdt, gateup, tokmax, a, grid, st);
+                                             const GemvArgs& a, int grid, hipStream_t st,
+                                             KEvents ev) {
+  return launch_gemv_bits<MOE_BITS>(xdt, sbdt, gateup, tokmax, a, grid, st, ev);
 }
 
-hipError_t MOE_CAT(launch_dec1_b, MOE_BITS)(int xdt, int sbdt, bool down, int pr, int ur,
+hipError_t MOE_CAT(launch_dec1_b, MOE_BITS)(int xdt, int sbdt, bool down, int rm, int ur,
                                              const void* args, int grid, size_t smem,
-                                             hipStream_t st) {
-  return launch_dec1_bits<MOE_BITS>(xdt, sbdt, down, pr, ur, args, grid, smem, st);
+                                             hipStream_t st, KEvents ev) {
+  return launch_dec1_bits<MOE_BITS>(xdt, sbdt, down, rm, ur, args, grid, smem, st, ev);
 }
 
 }  // namespace moe

@@ -33,6 +33,89 @@ __device__ __forceinline__ float wave_sum_width(float v, int width) {
   return v;
 }
 
+// DPP lane moves (GFX9 encodings): quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] =
+// 0x4E, row_half_mirror = 0x141, row_mirror = 0x140, row_bcast:15 = 0x142,
+// row_bcast:31 = 0x143. Rows outside ROW_MASK return `old`.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f32(float old, float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(x), CTRL,
+                                                    ROW_MASK, 0xF, false));
+}
+
+// Maximum over the wave (NaN-free input), returned wave-uniform.
+__device__ __forceinline__ float wave_max_f32(float x) {
+  x = fmaxf(x, dpp_f32<0xB1, 0xF>(x, x));
+  x = fmaxf(x, dpp_f32<0x4E, 0xF>(x, x));
+  x = fmaxf(x, dpp_f32<0x141, 0xF>(x, x));
+  x = fmaxf(x, dpp_f32<0x140, 0xF>(x, x));
+  x = fmaxf(x, dpp_f32<0x142, 0xA>(x, x));
+  x = fmaxf(x, dpp_f32<0x143, 0xC>(x, x));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_i32(int old, int x) {
+  return __builtin_amdgcn_update_dpp(old, x, CTRL, ROW_MASK, 0xF, false);
+}
+
+// Maximum over the wave, returned wave-uniform.
+__device__ __forceinline__ int wave_max_i32(int x) {
+  x = max(x, dpp_i32<0xB1, 0xF>(x, x));
+  x = max(x, dpp_i32<0x4E, 0xF>(x, x));
+  x = max(x, dpp_i32<0x141, 0xF>(x, x));
+  x = max(x, dpp_i32<0x140, 0xF>(x, x));
+  x = max(x, dpp_i32<0x142, 0xA>(x, x));
+  x = max(x, dpp_i32<0x143, 0xC>(x, x));
+  return __builtin_amdgcn_readlane(x, 63);
+}
+
+// Order-preserving map of non-NaN floats onto signed ints (an involution):
+// a < b as floats iff key(a) < key(b), with -0 canonicalised to +0 first so
+// that the two zeros tie as they do in float comparisons.
+__device__ __forceinline__ int f32_key(float f) {
+  const int b = __float_as_int(f + 0.0f);
+  return b ^ ((b >> 31) & 0x7FFFFFFF);
+}
+__device__ __forceinline__ float key_f32(int k) { return __int_as_float(k ^ ((k >> 31) & 0x7FFFFFFF)); }
+
+// Sum over each aligned group of 2^lg lanes (lg wave-uniform, 0..6). The
+// sum is valid in the group's last lane (lane % 2^lg == 2^lg - 1); groups of
+// up to 16 lanes hold it in every lane. The summation tree is fixed, so the
+// result is deterministic.
+__device__ __forceinline__ float group_sum(float v, int lg) {
+  if (lg >= 1) v += dpp_f32<0xB1, 0xF>(0.f, v);
+  if (lg >= 2) v += dpp_f32<0x4E, 0xF>(0.f, v);
+  if (lg >= 3) v += dpp_f32<0x141, 0xF>(0.f, v);
+  if (lg >= 4) v += dpp_f32<0x140, 0xF>(0.f, v);
+  if (lg >= 5) v += dpp_f32<0x142, 0xA>(0.f, v);
+  if (lg >= 6) v += dpp_f32<0x143, 0xC>(0.f, v);
+  return v;
+}
+
+// ------------------------------------------------------- buffer resources --
+// Raw buffer view of [base, base + bytes): loads take a 32-bit lane offset
+// against a wave-uniform base held in SGPRs, and a load whose lane offset is
+// at or past `bytes` returns zero instead of touching memory.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x4_t bload128(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ u32x2_t bload64(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload32(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint16_t bload16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
 // ------------------------------------------------------ deterministic exp --
 // Cody-Waite reduction by ln2 plus Moshier's degree-5 polynomial (Cephes
 // expf), written as explicit fused/unfused fp32 operations so that the CPU
@@ -66,20 +149,18 @@ __device__ __forceinline__ void wave_sync() {
 constexpr int kTopkMaxE = 512;           // experts a wave can route
 constexpr int kTopkEPL = kTopkMaxE / 64; // logits held per lane
 
-__device__ __forceinline__ bool topk_beats(float av, int ai, float bv, int bi) {
-  return av > bv || (av == bv && ai < bi);
-}
-
 // MoERouter.route for one token with one full wave (MoELayer.swift:140-205,
 // heap order of :223-296). Lane r < k returns the r-th selected expert in
 // (value desc, index asc) order in *sel and its combine weight in *w
 // (weights only when want_weights). Softmax sums run in index / rank order
 // on one lane with det_expf, so the results are reproducible bit for bit.
 // sc: this wave's LDS scratch of at least E floats (full-softmax mode).
+// masks (nullable): wave-uniform selection bitmaps, bit l of masks[j] set
+// iff expert 64 j + l was selected.
 template <typename XT>
 __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, int norm,
                           const float* __restrict__ ebias, float* sc, bool want_weights,
-                          int* sel, float* w) {
+                          int* sel, float* w, uint64_t* masks = nullptr) {
   const int lane = threadIdx.x & 63;
   const bool on_logits = (gating == 1) || (norm && ebias == nullptr);
   const float NEG = -__builtin_huge_valf();
@@ -88,8 +169,12 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
 #pragma unroll
   for (int j = 0; j < kTopkEPL; j++) {
     const int i = lane + 64 * j;
-    v[j] = (i < E) ? to_f<XT>(row[i]) : NEG;
-    if (i < E) m = fmaxf(m, v[j]);
+    v[j] = NEG;
+    if (j * 64 < E) {  // wave-uniform; the load itself is clamped, not branched
+      const float lv = to_f<XT>(row[min(i, E - 1)]);
+      v[j] = (i < E) ? lv : NEG;
+      m = (i < E) ? fmaxf(m, lv) : m;
+    }
   }
   if (!on_logits) {
     // full softmax (+ expert bias): MoELayer.swift:174-195
@@ -112,42 +197,59 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
       const int i = lane + 64 * j;
       if (i < E) {
         v[j] = (s > 0.f) ? v[j] / s : 1.0f / (float)E;
-        if (ebias) v[j] = v[j] + ebias[i];
+        if (ebias) v[j] = v[j] + ebias[min(i, E - 1)];
       }
     }
     wave_sync();
   }
-  // NaN sorts as -inf so the order is total and every lane agrees.
+  // NaN sorts as -inf so the order is total and every lane agrees. k rounds
+  // of a wave argmax over integer keys: the largest remaining key by a DPP
+  // max, the smallest index holding it by ballots (index = lane + 64 j).
+  constexpr int NONE = (int)0x80000000;  // below the key of -inf
+  int key[kTopkEPL];
 #pragma unroll
-  for (int j = 0; j < kTopkEPL; j++)
-    if (v[j] != v[j]) v[j] = NEG;
+  for (int j = 0; j < kTopkEPL; j++) {
+    const bool ok = (j * 64 < E) && (lane + 64 * j < E);
+    key[j] = ok ? f32_key(v[j] != v[j] ? NEG : v[j]) : NONE;
+  }
   uint32_t taken = 0;
-  int my_sel = 0;
-  float my_val = 0.f;
+  int my_sel = 0, my_key = NONE;
   for (int r = 0; r < k; r++) {
-    float bv = 0.f;
-    int bi = 0x7fffffff;
+    int bk = key[0];
+#pragma unroll
+    for (int j = 1; j < kTopkEPL; j++)
+      if (j * 64 < E) bk = max(bk, key[j]);
+    const int mk = wave_max_i32(bk);
+    int win = 0;
 #pragma unroll
     for (int j = 0; j < kTopkEPL; j++) {
-      const int i = lane + 64 * j;
-      if (i < E && !((taken >> j) & 1u) && (bi == 0x7fffffff || topk_beats(v[j], i, bv, bi))) {
-        bv = v[j];
-        bi = i;
+      if (j * 64 < E) {
+        const uint64_t b = __ballot(key[j] == mk);
+        if (b) {
+          win = j * 64 + __ffsll((unsigned long long)b) - 1;
+          break;
+        }
       }
     }
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (oi != 0x7fffffff && (bi == 0x7fffffff || topk_beats(ov, oi, bv, bi))) {
-        bv = ov;
-        bi = oi;
+    win = __builtin_amdgcn_readfirstlane(win);
+    const int wj = win >> 6;
+    const bool mine = (win & 63) == lane;
+#pragma unroll
+    for (int j = 0; j < kTopkEPL; j++) {
+      if (j == wj && mine) {
+        key[j] = NONE;
+        taken |= 1u << j;
       }
     }
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
     if (lane == r) {
-      my_sel = bi;
-      my_val = bv;
+      my_sel = win;
+      my_key = mk;
     }
+  }
+  const float my_val = key_f32(my_key);
+  if (masks) {
+#pragma unroll
+    for (int j = 0; j < kTopkEPL; j++) masks[j] = (j * 64 < E) ? __ballot((taken >> j) & 1u) : 0ull;
   }
   *sel = my_sel;
   if (!want_weights) return;
@@ -155,7 +257,8 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
   float wv;
   if (on_logits) {
     // softmax over the k picked raw logits — MoELayer.swift:166-172,197-203
-    const float lv = (lane < k) ? to_f<XT>(row[my_sel]) : NEG;
+    const float lraw = to_f<XT>(row[my_sel]);
+    const float lv = (lane < k) ? lraw : NEG;
     float mx = lv;
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
     const float ex = (lane < k) ? det_expf(lv - mx) : 0.f;
@@ -215,23 +318,34 @@ __device__ __forceinline__ uint32_t funnel(uint32_t hi, uint32_t lo, int sh) {
   return sh == 0 ? lo : (uint32_t)((((uint64_t)hi << 32) | lo) >> sh);
 }
 
-template <int BITS>
+// A VGPR copy of c that the compiler cannot fold back into a literal: GFX9
+// VOP3 encodings take no literal operand, so `(x & M) | C` only becomes one
+// v_and_or_b32 when C already sits in a register.
+__device__ __forceinline__ uint32_t opaque_vgpr(uint32_t c) {
+  uint32_t r;
+  asm("v_mov_b32 %0, %1" : "=v"(r) : "s"(c));
+  return r;
+}
+
+// MAGIC is or-ed into every pair in the same and-or (see Magic below).
+template <int BITS, uint32_t MAGIC_C = 0u>
 __device__ __forceinline__ void unpack_pairs(const uint32_t (&w)[BITS], uint32_t (&cp)[16]) {
+  const uint32_t MAGIC = MAGIC_C ? opaque_vgpr(MAGIC_C) : 0u;
   if constexpr (BITS == 2) {
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
-      for (int i = 0; i < 8; i++) cp[j * 8 + i] = (w[j] >> (2 * i)) & 0x00030003u;
+      for (int i = 0; i < 8; i++) cp[j * 8 + i] = ((w[j] >> (2 * i)) & 0x00030003u) | MAGIC;
   } else if constexpr (BITS == 4) {
 #pragma unroll
     for (int j = 0; j < 4; j++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) cp[j * 4 + i] = (w[j] >> (4 * i)) & 0x000F000Fu;
+      for (int i = 0; i < 4; i++) cp[j * 4 + i] = ((w[j] >> (4 * i)) & 0x000F000Fu) | MAGIC;
   } else if constexpr (BITS == 8) {
 #pragma unroll
     for (int j = 0; j < 8; j++)
 #pragma unroll
-      for (int i = 0; i < 2; i++) cp[j * 2 + i] = (w[j] >> (8 * i)) & 0x00FF00FFu;
+      for (int i = 0; i < 2; i++) cp[j * 2 + i] = ((w[j] >> (8 * i)) & 0x00FF00FFu) | MAGIC;
   } else if constexpr (BITS == 3) {
     // 4 sub-blocks of 24 bits (8 values); spread the upper 12 bits to bit 16
 #pragma unroll
@@ -241,7 +355,7 @@ __device__ __forceinline__ void unpack_pairs(const uint32_t (&w)[BITS], uint32_t
       s &= 0xFFFFFFu;
       uint32_t t = (s & 0xFFFu) | ((s & 0xFFF000u) << 4);
 #pragma unroll
-      for (int i = 0; i < 4; i++) cp[j * 4 + i] = (t >> (3 * i)) & 0x00070007u;
+      for (int i = 0; i < 4; i++) cp[j * 4 + i] = ((t >> (3 * i)) & 0x00070007u) | MAGIC;
     }
   } else if constexpr (BITS == 6) {
     // 8 sub-blocks of 24 bits (4 values)
@@ -252,7 +366,7 @@ __device__ __forceinline__ void unpack_pairs(const uint32_t (&w)[BITS], uint32_t
       s &= 0xFFFFFFu;
       uint32_t t = (s & 0xFFFu) | ((s & 0xFFF000u) << 4);
 #pragma unroll
-      for (int i = 0; i < 2; i++) cp[j * 2 + i] = (t >> (6 * i)) & 0x003F003Fu;
+      for (int i = 0; i < 2; i++) cp[j * 2 + i] = ((t >> (6 * i)) & 0x003F003Fu) | MAGIC;
     }
   } else if constexpr (BITS == 5) {
     // 8 sub-blocks of 20 bits (4 values); spread the upper 10 bits to bit 16
@@ -263,7 +377,7 @@ __device__ __forceinline__ void unpack_pairs(const uint32_t (&w)[BITS], uint32_t
       s &= 0xFFFFFu;
       uint32_t t = (s & 0x3FFu) | ((s & 0xFFC00u) << 6);
 #pragma unroll
-      for (int i = 0; i < 2; i++) cp[j * 2 + i] = (t >> (5 * i)) & 0x001F001Fu;
+      for (int i = 0; i < 2; i++) cp[j * 2 + i] = ((t >> (5 * i)) & 0x001F001Fu) | MAGIC;
     }
   }
 }
@@ -296,6 +410,61 @@ __device__ __forceinline__ void load_unit(const uint32_t* __restrict__ p, uint32
   }
 }
 
+// Buffer form of load_unit: byte offset `off` of a raw buffer view.
+template <int BITS>
+__device__ __forceinline__ void bload_unit(rsrc_t r, uint32_t off, uint32_t (&w)[BITS]) {
+  if constexpr (BITS == 2) {
+    const u32x2_t v = bload64(r, off);
+    w[0] = v[0]; w[1] = v[1];
+  } else if constexpr (BITS == 3 || BITS == 5) {
+    // 12- and 20-byte units are only 4-byte aligned
+#pragma unroll
+    for (int i = 0; i < BITS; i++) w[i] = bload32(r, off + 4u * i);
+  } else if constexpr (BITS == 4) {
+    const u32x4_t v = bload128(r, off);
+    w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+  } else if constexpr (BITS == 6) {
+    const u32x2_t a = bload64(r, off), b = bload64(r, off + 8), c = bload64(r, off + 16);
+    w[0] = a[0]; w[1] = a[1]; w[2] = b[0]; w[3] = b[1]; w[4] = c[0]; w[5] = c[1];
+  } else {
+    const u32x4_t a = bload128(r, off), b = bload128(r, off + 16);
+    w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
+    w[4] = b[0]; w[5] = b[1]; w[6] = b[2]; w[7] = b[3];
+  }
+}
+
+// Number of selected experts with an id below e (selection bitmaps from
+// wave_topk); e may equal the expert count.
+__device__ __forceinline__ int selected_below(const uint64_t (&m)[kTopkEPL], int e) {
+  int c = 0;
+#pragma unroll
+  for (int j = 0; j < kTopkEPL; j++) {
+    const int lo = j * 64;
+    if (e >= lo + 64) c += __popcll(m[j]);
+    else if (e > lo) c += __popcll(m[j] & ((1ull << (e - lo)) - 1ull));
+  }
+  return c;
+}
+
+// The s-th smallest selected expert id (wave-uniform s and bitmaps).
+__device__ __forceinline__ int selected_nth(const uint64_t (&m)[kTopkEPL], int s) {
+  int e = 0;
+  bool found = false;
+#pragma unroll
+  for (int j = 0; j < kTopkEPL; j++) {
+    const int c = __popcll(m[j]);
+    if (!found && s < c) {
+      uint64_t b = m[j];
+      for (int t = 0; t < s; t++) b &= b - 1ull;
+      e = j * 64 + __ffsll((unsigned long long)b) - 1;
+      found = true;
+    } else if (!found) {
+      s -= c;
+    }
+  }
+  return e;
+}
+
 // --------------------------------------------------------- unit dot product --
 // D = sum over the unit of (MAGIC + q) * x for 16-bit activations: codes are
 // or-ed into the mantissa of MAGIC = 128.0 (bf16, exact for codes < 128) or
@@ -309,36 +478,31 @@ template <int BITS, typename XT> struct Magic {
   static constexpr float value = !dot2 ? 0.0f : (__is_same(XT, bf16_t) ? 128.0f : 1024.0f);
 };
 
-// x16: the unit's 32 activations in pair order, as 16 u32 (16-bit types).
+// x16: the unit's 32 activations in pair order, as 16 u32 (16-bit types);
+// cp: code pairs from unpack_pairs<BITS, Magic<BITS, XT>::bits>.
 template <int BITS, typename XT>
 __device__ __forceinline__ float unit_dot16(const uint32_t (&cp)[16], const uint32_t (&x16)[16]) {
-  float d0 = 0.f, d1 = 0.f;
+  float d = 0.f;
   if constexpr (Magic<BITS, XT>::dot2) {
 #pragma unroll
-    for (int i = 0; i < 16; i += 2) {
-      uint32_t a0 = cp[i] | Magic<BITS, XT>::bits, a1 = cp[i + 1] | Magic<BITS, XT>::bits;
-      if constexpr (__is_same(XT, bf16_t)) {
-        d0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a0),
-                                             __builtin_bit_cast(bf16x2_t, x16[i]), d0, false);
-        d1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a1),
-                                             __builtin_bit_cast(bf16x2_t, x16[i + 1]), d1, false);
-      } else {
-        d0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a0),
-                                    __builtin_bit_cast(f16x2_t, x16[i]), d0, false);
-        d1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a1),
-                                    __builtin_bit_cast(f16x2_t, x16[i + 1]), d1, false);
-      }
+    for (int i = 0; i < 16; i++) {
+      if constexpr (__is_same(XT, bf16_t))
+        d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, cp[i]),
+                                            __builtin_bit_cast(bf16x2_t, x16[i]), d, false);
+      else
+        d = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, cp[i]),
+                                   __builtin_bit_cast(f16x2_t, x16[i]), d, false);
     }
   } else {
     // bf16 activations with 8-bit codes
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      float xa = __uint_as_float(x16[i] << 16), xb = __uint_as_float(x16[i] & 0xFFFF0000u);
-      d0 = __builtin_fmaf((float)(cp[i] & 0xFFFFu), xa, d0);
-      d1 = __builtin_fmaf((float)(cp[i] >> 16), xb, d1);
+      const float xa = __uint_as_float(x16[i] << 16), xb = __uint_as_float(x16[i] & 0xFFFF0000u);
+      d = __builtin_fmaf((float)(cp[i] & 0xFFFFu), xa, d);
+      d = __builtin_fmaf((float)(cp[i] >> 16), xb, d);
     }
   }
-  return d0 + d1;
+  return d;
 }
 
 // f32 activations: x32 in pair order.

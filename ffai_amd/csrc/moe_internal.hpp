@@ -11,6 +11,12 @@ namespace moe {
 
 enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
 
+// Optional events recorded by the dispatch of one kernel itself (its start
+// and end timestamps, hipExtLaunchKernel); null entries record nothing.
+struct KEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+
 // ------------------------------------------------------------------ GEMV --
 // Expert-grouped dequant GEMV over a dispatch plan. Block b handles expert
 // slot b / row_blocks (the slot-th used expert) and rows
@@ -31,7 +37,8 @@ struct GemvArgs {
   const uint32_t* offsets;   // [E+1] CSR over sorted positions
   const uint32_t* used;      // [1+E]: used[0] = U, used[1..U] = expert ids
   void* out;                 // [M, N]
-  int N, K, gs;
+  int N, K;
+  int gsh;                   // log2(group size / 32)
   int row_blocks, rows_per_block;
   int lg;                    // log2(lanes per row)
   int tok_chunk;             // activation rows staged per pass (<= TOKMAX)
@@ -52,29 +59,36 @@ struct Decode1Args {
   uint32_t* offsets;         // nullable [E+1] out: CSR offsets of the plan
   const void* x;             // [K]
   GemvProj g, u;             // gate / up
-  void* act;                 // [k, N] in sorted (expert id) order
-  int N, K, gs, row_blocks, rows_per_block, lg;
+  void* act;                 // [k, N] in rank order
+  int N, K, gsh, row_blocks, rows_per_block, lg;
   int act_kind;
   float alpha, limit;
 };
 
 struct Down1Args {
-  const uint32_t* idx;
-  const float* w;
-  const uint32_t* perm;
-  const void* act;           // [k, K]
+  const uint32_t* idx;       // [k] experts in rank order
+  const float* w;            // [k] combine weights in rank order
+  const void* act;           // [k, K] in rank order
   GemvProj p;
   void* out;                 // [N]
-  int k, N, K, gs, rows_per_block, lg;
+  int k, N, K, gsh, rows_per_block, lg;
 };
 
-hipError_t launch_gateup1(int bits, int xdt, int sbdt, const Decode1Args& a, int grid,
-                          hipStream_t st);
-hipError_t launch_down1(int bits, int xdt, int sbdt, const Down1Args& a, int grid, size_t smem,
-                        hipStream_t st);
+// Launch limits of the decode kernels: a block has one wave per selected
+// expert (down) and each lane holds at most kDec1MaxRows rows of at most 4
+// units each.
+constexpr int kDec1MaxK = 8;
+constexpr int kDec1MaxRows = 3;
+
+// rm: rows per lane (rows_per_block = rm * 4 * SG for gate/up, rm * SG for
+// down).
+hipError_t launch_gateup1(int bits, int xdt, int sbdt, const Decode1Args& a, int rm, int grid,
+                          hipStream_t st, KEvents ev = {});
+hipError_t launch_down1(int bits, int xdt, int sbdt, const Down1Args& a, int rm, int grid,
+                        hipStream_t st, KEvents ev = {});
 
 hipError_t launch_gemv(int bits, int xdt, int sbdt, bool gateup, int tokmax, const GemvArgs& a,
-                       int grid, hipStream_t st);
+                       int grid, hipStream_t st, KEvents ev = {});
 size_t gemv_smem_bytes(int xdt, int K, int tok_chunk);
 
 // ---------------------------------------------------------------- router --

@@ -12,25 +12,32 @@
 
 namespace moe {
 
+// 8 consecutive elements at byte offset `off` of a raw buffer view, as fp32;
+// elements past the view read as zero.
 template <typename T>
-__device__ __forceinline__ void load8(const T* __restrict__ p, float (&v)[8]) {
+__device__ __forceinline__ void bload8(rsrc_t r, uint32_t off, float (&v)[8]) {
   if constexpr (__is_same(T, float)) {
-    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-  } else {
-    const uint4 a = *reinterpret_cast<const uint4*>(p);
-    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+    const u32x4_t a = bload128(r, off), b = bload128(r, off + 16);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      v[2 * j] = to_f<T>(__builtin_bit_cast(T, (uint16_t)(w[j] & 0xFFFFu)));
-      v[2 * j + 1] = to_f<T>(__builtin_bit_cast(T, (uint16_t)(w[j] >> 16)));
+      v[j] = __uint_as_float(a[j]);
+      v[4 + j] = __uint_as_float(b[j]);
+    }
+  } else {
+    const u32x4_t a = bload128(r, off);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      v[2 * j] = to_f<T>(__builtin_bit_cast(T, (uint16_t)(a[j] & 0xFFFFu)));
+      v[2 * j + 1] = to_f<T>(__builtin_bit_cast(T, (uint16_t)(a[j] >> 16)));
     }
   }
 }
 
 // logits[t, e] = round(W[e] . x[t]) (+ bias: round(logit + b)). One wave per
-// (expert, chunk of 8 tokens); lanes stride over hidden 8 values at a time.
-template <typename XT, typename WT>
+// (expert, chunk of up to 8 tokens); lane l takes the 8-element chunks
+// l + 64 j, j < NL, of the hidden dimension (NL * 512 >= H; chunks past H
+// read zeros), so the whole weight row is requested in one round trip.
+template <typename XT, typename WT, int NL>
 __global__ __launch_bounds__(256) void router_logits_kernel(const XT* __restrict__ x,
                                                             const WT* __restrict__ W,
                                                             const XT* __restrict__ bias,
@@ -38,39 +45,34 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT* __restrict
                                                             int E, int tchunks) {
   const int gw = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int e = gw / tchunks, tc = gw - e * tchunks;
-  if (e >= E) return;
+  if (e >= E) return;  // wave-uniform; the kernel has no block barrier
   const int lane = threadIdx.x & 63;
   const int t0 = tc * 8, nt = min(8, T - t0);
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  const WT* w = W + (size_t)e * H;
-  constexpr int UNR = 4;  // hidden chunks in flight per lane
-  for (int h0 = lane * 8; h0 < H; h0 += 512 * UNR) {
-    float wv[UNR][8];
+  const float bv = bias ? to_f<XT>(bias[e]) : 0.f;  // issued before the row loads
+  const rsrc_t wr = make_rsrc(W + (size_t)e * H, (uint32_t)(H * sizeof(WT)));
+  float wv[NL][8];
 #pragma unroll
-    for (int u = 0; u < UNR; u++)
-      if (h0 + u * 512 < H) load8<WT>(w + h0 + u * 512, wv[u]);
+  for (int j = 0; j < NL; j++) bload8<WT>(wr, (uint32_t)((lane + 64 * j) * 8 * sizeof(WT)), wv[j]);
+  float acc[8];
 #pragma unroll
-    for (int t = 0; t < 8; t++) {
-      if (t < nt) {
-        float xv[UNR][8];
+  for (int t = 0; t < 8; t++) {
+    acc[t] = 0.f;
+    if (t < nt) {  // wave-uniform
+      const rsrc_t xr = make_rsrc(x + (size_t)(t0 + t) * H, (uint32_t)(H * sizeof(XT)));
 #pragma unroll
-        for (int u = 0; u < UNR; u++)
-          if (h0 + u * 512 < H) load8<XT>(x + (size_t)(t0 + t) * H + h0 + u * 512, xv[u]);
+      for (int j = 0; j < NL; j++) {
+        float xv[8];
+        bload8<XT>(xr, (uint32_t)((lane + 64 * j) * 8 * sizeof(XT)), xv);
 #pragma unroll
-        for (int u = 0; u < UNR; u++)
-          if (h0 + u * 512 < H)
-#pragma unroll
-            for (int j = 0; j < 8; j++) acc[t] = __builtin_fmaf(wv[u][j], xv[u][j], acc[t]);
+        for (int i = 0; i < 8; i++) acc[t] = __builtin_fmaf(wv[j][i], xv[i], acc[t]);
       }
+      acc[t] = group_sum(acc[t], 6);
     }
   }
-#pragma unroll
-  for (int t = 0; t < 8; t++)
-    if (t < nt) acc[t] = wave_sum_width(acc[t], 64);
-  if (lane == 0) {
+  if (lane == 63) {
     for (int t = 0; t < nt; t++) {
       float l = round_to<XT>(acc[t]);
-      if (bias) l = round_to<XT>(l + to_f<XT>(bias[e]));
+      if (bias) l = round_to<XT>(l + bv);
       logits[(size_t)(t0 + t) * E + e] = from_f<XT>(l);
     }
   }
@@ -96,30 +98,46 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const XT* __restrict__
   }
 }
 
-hipError_t launch_router_logits(const void* x, int xdt, int T, int H, const void* W, int wdt,
-                                const void* bias, int E, void* logits, hipStream_t st) {
+template <typename XT, typename WT>
+static hipError_t launch_rl(const void* x, int T, int H, const void* W, const void* bias, int E,
+                            void* logits, hipStream_t st) {
   const int tchunks = (T + 7) / 8;
   const long waves = (long)E * tchunks;
-  const int grid = (int)((waves + 3) / 4);
-#define MOE_RL(XT, WT)                                                                      \
-  hipLaunchKernelGGL((router_logits_kernel<XT, WT>), dim3(grid), dim3(256), 0, st,         \
-                     (const XT*)x, (const WT*)W, (const XT*)bias, (XT*)logits, T, H, E,     \
-                     tchunks);                                                              \
+  // small batches: one wave per block spreads the experts over the CUs
+  const int wpb = (T <= 8) ? 1 : 4;
+  const int grid = (int)((waves + wpb - 1) / wpb);
+  const int nl = (H + 511) / 512;
+#define MOE_RL(NL)                                                                            \
+  hipLaunchKernelGGL((router_logits_kernel<XT, WT, NL>), dim3(grid), dim3(64 * wpb), 0, st,  \
+                     (const XT*)x, (const WT*)W, (const XT*)bias, (XT*)logits, T, H, E,       \
+                     tchunks);                                                                \
   return hipGetLastError();
-  if (xdt == DT_BF16) {
-    if (wdt == DT_BF16) { MOE_RL(bf16_t, bf16_t) }
-    if (wdt == DT_F16) { MOE_RL(bf16_t, f16_t) }
-    if (wdt == DT_F32) { MOE_RL(bf16_t, float) }
-  } else if (xdt == DT_F16) {
-    if (wdt == DT_BF16) { MOE_RL(f16_t, bf16_t) }
-    if (wdt == DT_F16) { MOE_RL(f16_t, f16_t) }
-    if (wdt == DT_F32) { MOE_RL(f16_t, float) }
-  } else if (xdt == DT_F32) {
-    if (wdt == DT_BF16) { MOE_RL(float, bf16_t) }
-    if (wdt == DT_F16) { MOE_RL(float, f16_t) }
-    if (wdt == DT_F32) { MOE_RL(float, float) }
-  }
+  if (nl <= 1) { MOE_RL(1) }
+  if (nl <= 2) { MOE_RL(2) }
+  if (nl <= 4) { MOE_RL(4) }
+  if (nl <= 8) { MOE_RL(8) }
+  if (nl <= 16) { MOE_RL(16) }
 #undef MOE_RL
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_router_logits(const void* x, int xdt, int T, int H, const void* W, int wdt,
+                                const void* bias, int E, void* logits, hipStream_t st) {
+#define MOE_RL2(XT, WT) return launch_rl<XT, WT>(x, T, H, W, bias, E, logits, st);
+  if (xdt == DT_BF16) {
+    if (wdt == DT_BF16) { MOE_RL2(bf16_t, bf16_t) }
+    if (wdt == DT_F16) { MOE_RL2(bf16_t, f16_t) }
+    if (wdt == DT_F32) { MOE_RL2(bf16_t, float) }
+  } else if (xdt == DT_F16) {
+    if (wdt == DT_BF16) { MOE_RL2(f16_t, bf16_t) }
+    if (wdt == DT_F16) { MOE_RL2(f16_t, f16_t) }
+    if (wdt == DT_F32) { MOE_RL2(f16_t, float) }
+  } else if (xdt == DT_F32) {
+    if (wdt == DT_BF16) { MOE_RL2(float, bf16_t) }
+    if (wdt == DT_F16) { MOE_RL2(float, f16_t) }
+    if (wdt == DT_F32) { MOE_RL2(float, float) }
+  }
+#undef MOE_RL2
   return hipErrorInvalidValue;
 }
 

@@ -113,10 +113,12 @@ typedef struct moe_layer_trace {
     float* topk_weight;    /* [T, top_k] */
     uint32_t* perm;        /* [T*top_k] sorted position -> token-major entry */
     uint32_t* offsets;     /* [n_experts + 1] */
-    /* hipEvent_t handles recorded on the stream (each nullable): [0] before
-     * the routed gate/up kernel, [1] after it, [2] after the routed down
-     * projection + combine. For timing the expert weight streaming. */
-    void* events[3];
+    /* hipEvent_t handles (each nullable) recorded by the dispatch of the
+     * routed expert kernels themselves, so that their elapsed time is the
+     * kernel's own execution: [0]/[1] start/end of the gate/up kernel,
+     * [2]/[3] start/end of the down kernel (fused with the combine on the
+     * one-token path). For timing the expert weight streaming. */
+    void* events[4];
 } moe_layer_trace;
 
 /* ---- diagnostics ------------------------------------------------------- */

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from moe_spec import (BF16, F16, F32, cfg_gptoss, cfg_mixed, cfg_qwen3, cfg_tiny, check_close, load,
+from moe_spec import (BF16, F16, F32, cfg_bits, cfg_gptoss, cfg_mixed, cfg_qwen3, cfg_tiny, check_close, load,
                       store, to_numpy_f32, to_torch, zipf_router_bias)
 
 torch = pytest.importorskip("torch")
@@ -264,6 +264,17 @@ def mixed():
 @pytest.mark.parametrize("T", [1, 24])
 def test_layer_mixed_bits_shared(mixed, T):
     run_layer(mixed, T)
+
+
+BITS_CASES = [(2, 8, 64, F16, BF16), (5, 2, 32, BF16, F16), (8, 5, 128, F16, F16),
+              (6, 3, 64, BF16, BF16), (3, 4, 128, BF16, BF16), (8, 8, 64, BF16, BF16)]
+
+
+@pytest.mark.parametrize("case", BITS_CASES, ids=lambda c: f"gu{c[0]}-d{c[1]}-gs{c[2]}-sb{c[3]}-x{c[4]}")
+@pytest.mark.parametrize("T", [1, 5])
+def test_layer_bit_widths(case, T):
+    """Decode (T=1) and batched paths over every packed width and group size."""
+    run_layer(cfg_bits(*case), T)
 
 
 def test_layer_is_deterministic(qwen3):

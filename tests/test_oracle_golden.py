@@ -456,3 +456,39 @@ def test_layer_tiny_matches_float64_composition():
             acc = acc + np.float32(rd(np.float32(w[t, s]))) * yv.astype(np.float32)
         ref[t] = rd(acc)
     check_close(load(y, spec.act_dt), ref, spec.act_dt, "tiny layer vs float64 composition")
+
+
+def test_float_bar_catches_planted_mistakes():
+    """The layer tolerance passes storage-ulp rounding flips but fails a
+    wrong expert and a dropped expert term (mistakes planted in oracle
+    outputs on the CPU)."""
+    import copy
+    from moe_spec import cfg_tiny, load
+    spec = cfg_tiny()
+    x = spec.x(16)
+    y, logits, idx, w = orc.moe_layer(spec, x)
+    ref = load(y, spec.act_dt)
+    # one-ulp flips on 5% of the elements pass
+    rng = np.random.default_rng(3)
+    flip = y.copy().view(np.uint16)
+    sel = rng.random(flip.shape) < 0.05
+    flip[sel] = flip[sel] + np.uint16(1)  # one ulp away from zero, either sign
+    check_close(load(flip.view(y.dtype), spec.act_dt), ref, spec.act_dt, "ulp flips")
+    # token 0 routed to an expert it did not select
+    bad = logits.copy()
+    top, other = int(idx[0, 0]), int(next(e for e in range(spec.n_experts) if e not in idx[0]))
+    bad[0, top], bad[0, other] = logits[0, other], logits[0, top]
+    y_wrong = orc.moe_layer(spec, x, given_logits=bad)[0]
+    with pytest.raises(AssertionError):
+        check_close(load(y_wrong, spec.act_dt), ref, spec.act_dt, "wrong expert")
+    # one expert's down projection dropped (scales and biases zero)
+    drop = copy.copy(spec)
+    drop.down = copy.copy(spec.down)
+    e0 = int(idx[0, 1])
+    s, b = spec.down.scales.copy(), spec.down.biases.copy()
+    s[e0] = 0
+    b[e0] = 0
+    drop.down = orc.QProj(spec.down.weight, s, b, spec.down.bits, spec.down.gs, spec.down.sb_dt)
+    y_drop = orc.moe_layer(drop, x, given_logits=logits)[0]
+    with pytest.raises(AssertionError):
+        check_close(load(y_drop, spec.act_dt), ref, spec.act_dt, "dropped expert")
