@@ -31,6 +31,26 @@ hipError_t launch_dec1_b5(int, int, bool, int, int, const void*, int, size_t, hi
 hipError_t launch_dec1_b6(int, int, bool, int, int, const void*, int, size_t, hipStream_t, KEvents);
 hipError_t launch_dec1_b8(int, int, bool, int, int, const void*, int, size_t, hipStream_t, KEvents);
 
+hipError_t launch_gemm_b2(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b3(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b4(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b5(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b6(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b8(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
+
+hipError_t launch_gemm(int bits, int xdt, int sbdt, bool gateup, const GemmArgs& a, int grid,
+                       hipStream_t st, KEvents ev) {
+  switch (bits) {
+    case 2: return launch_gemm_b2(xdt, sbdt, gateup, a, grid, st, ev);
+    case 3: return launch_gemm_b3(xdt, sbdt, gateup, a, grid, st, ev);
+    case 4: return launch_gemm_b4(xdt, sbdt, gateup, a, grid, st, ev);
+    case 5: return launch_gemm_b5(xdt, sbdt, gateup, a, grid, st, ev);
+    case 6: return launch_gemm_b6(xdt, sbdt, gateup, a, grid, st, ev);
+    case 8: return launch_gemm_b8(xdt, sbdt, gateup, a, grid, st, ev);
+  }
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_gemv(int bits, int xdt, int sbdt, bool gateup, int tokmax, const GemvArgs& a,
                        int grid, hipStream_t st, KEvents ev) {
   switch (bits) {
@@ -307,7 +327,7 @@ int group_shift(int gs) { return gs == 128 ? 2 : (gs == 64 ? 1 : 0); }
 // ---------------------------------------------------------------------------
 
 struct Workspace {
-  size_t logits, idx, w, counts, offsets, used, perm, inv, act, Y, plan_scratch;
+  size_t logits, idx, w, counts, offsets, used, perm, inv, act, Y, plan_scratch, tiles;
   size_t s_off, s_used, s_act, s_out, s_logit;
   size_t total;
 };
@@ -334,6 +354,7 @@ Workspace layout(const moe_layer_desc* d, int T) {
   w.act = take(M * I * ds);
   w.Y = take(M * H * ds);
   w.plan_scratch = take(dispatch_scratch_bytes(T, (int)k, (int)E));
+  w.tiles = take((1 + 2 * (size_t)gemm_max_tiles((int)M, (int)E)) * 4);
   if (d->has_shared) {
     const size_t SI = (size_t)d->shared_gate.n;
     w.s_off = take(2 * 4);
@@ -381,6 +402,46 @@ moe_status run_gemv(const moe_qproj& p0, const moe_qproj* p1, const void* x, int
   a.limit = limit;
   MOE_HIP(launch_gemv(p0.bits, xdt, p0.sb_dtype, p1 != nullptr, g.tokmax, a, g.grid, st, ev),
           "grouped GEMV launch");
+  return MOE_OK;
+}
+
+// The MFMA grouped GEMM pays off once the used experts average enough rows
+// to fill a good part of its 128-row tiles; below that the HBM-streaming
+// GEMV, which reads every weight once per 8 rows, is faster.
+constexpr int kGemmMinRows = 32;
+
+bool gemm_ok(const moe_qproj& p, int xdt, int M) {
+  const int slots = std::min(p.n_experts, M);
+  return xdt != MOE_F32 && p.k % 64 == 0 && p.n_experts <= 1024 && M >= kGemmMinRows * slots;
+}
+
+// out[p] = W[e(p)] . a[row(p)] (or the gate/up pair with the activation)
+// over the row tiles of a plan, on the matrix cores. `tiles` must hold the
+// list written by launch_gemm_tiles for the same offsets.
+moe_status run_gemm(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
+                    const uint32_t* perm, int topk, const uint32_t* offsets,
+                    const uint32_t* tiles, int M, void* out, int act, float alpha, float limit,
+                    hipStream_t st, KEvents ev = {}) {
+  GemmArgs a{};
+  a.p0 = to_proj(p0);
+  if (p1) a.p1 = to_proj(*p1);
+  a.x = x;
+  a.perm = perm;
+  a.topk = topk;
+  a.offsets = offsets;
+  a.tiles = tiles;
+  a.out = out;
+  a.N = p0.n;
+  a.K = p0.k;
+  a.gsh = group_shift(p0.group_size);
+  a.act = act;
+  a.alpha = alpha;
+  a.limit = limit;
+  const bool gu = p1 != nullptr;
+  const int cols = gemm_block_cols(gu);
+  const long items = (long)gemm_max_tiles(M, p0.n_experts) * ((p0.n + cols - 1) / cols);
+  const int grid = (int)((items + 7) / 8 * 8);  // a multiple of the 8 XCDs
+  MOE_HIP(launch_gemm(p0.bits, xdt, p0.sb_dtype, gu, a, grid, st, ev), "grouped GEMM launch");
   return MOE_OK;
 }
 
@@ -494,7 +555,8 @@ extern "C" moe_status moe_dequantize_affine(const uint32_t* weight, const void* 
 
 extern "C" size_t moe_expert_matmul_workspace_bytes(int32_t n_experts, int32_t M) {
   if (n_experts <= 0 || M <= 0) return 0;
-  return align_up((size_t)(n_experts + 1) * 4, 256);
+  return align_up((size_t)(n_experts + 1) * 4, 256) +
+         align_up((1 + 2 * (size_t)gemm_max_tiles(M, n_experts)) * 4, 256);
 }
 
 extern "C" moe_status moe_expert_matmul(const moe_qproj* p, const void* a, int32_t a_dtype,
@@ -511,6 +573,14 @@ extern "C" moe_status moe_expert_matmul(const moe_qproj* p, const void* a, int32
   const size_t need = moe_expert_matmul_workspace_bytes(p->n_experts, M);
   if (!workspace || workspace_bytes < need)
     return fail(MOE_ERR_WORKSPACE, "expert_matmul: workspace of %zu bytes needed", need);
+  if (gemm_ok(*p, a_dtype, M)) {
+    uint32_t* tiles = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(workspace) +
+                                                  align_up((size_t)(p->n_experts + 1) * 4, 256));
+    MOE_HIP(launch_gemm_tiles(offsets, p->n_experts, kGemmRows, tiles, stream), "tile list launch");
+    MOE_TRY(run_gemm(*p, nullptr, a, a_dtype, perm, top_k, offsets, tiles, M, out, 0, 0.f, 0.f,
+                     stream));
+    return ok();
+  }
   uint32_t* used = reinterpret_cast<uint32_t*>(workspace);
   MOE_HIP(launch_used_from_offsets(offsets, p->n_experts, used, stream), "used list launch");
   const int slots = std::min(p->n_experts, M);
@@ -744,15 +814,31 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y,
                                  at<void>(ws, w.plan_scratch), dispatch_scratch_bytes(T, k, E), st),
             "dispatch plan launch");
     const int slots = std::min(E, M);
+    const bool gemm = gemm_ok(d->gate, xdt, M) && gemm_ok(d->down, xdt, M);
     // 3. gate/up + activation over the plan (MoELayer.swift:883-893)
-    MOE_TRY(run_gemv(d->gate, &d->up, x, xdt, at<uint32_t>(ws, w.perm), k,
-                     at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, T == 1,
-                     at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st, kev(0)));
+    if (gemm) {
+      MOE_HIP(launch_gemm_tiles(at<uint32_t>(ws, w.offsets), E, kGemmRows, at<uint32_t>(ws, w.tiles),
+                                st),
+              "tile list launch");
+      MOE_TRY(run_gemm(d->gate, &d->up, x, xdt, at<uint32_t>(ws, w.perm), k,
+                       at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.tiles), M,
+                       at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st, kev(0)));
+    } else {
+      MOE_TRY(run_gemv(d->gate, &d->up, x, xdt, at<uint32_t>(ws, w.perm), k,
+                       at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, T == 1,
+                       at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st, kev(0)));
+    }
     MOE_TRY(shared_expert(d, x, T, ws, w, st, &smode));
     // 4. down projection, then the weighted combine (MoELayer.swift:899-939)
-    MOE_TRY(run_gemv(d->down, nullptr, at<void>(ws, w.act), xdt, nullptr, 1,
-                     at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, T == 1,
-                     at<void>(ws, w.Y), 0, 0.f, 0.f, st, kev(1)));
+    if (gemm) {
+      MOE_TRY(run_gemm(d->down, nullptr, at<void>(ws, w.act), xdt, nullptr, 1,
+                       at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.tiles), M, at<void>(ws, w.Y),
+                       0, 0.f, 0.f, st, kev(1)));
+    } else {
+      MOE_TRY(run_gemv(d->down, nullptr, at<void>(ws, w.act), xdt, nullptr, 1,
+                       at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, T == 1,
+                       at<void>(ws, w.Y), 0, 0.f, 0.f, st, kev(1)));
+    }
     MOE_HIP(launch_unpermute(at<void>(ws, w.Y), at<uint32_t>(ws, w.inv), at<float>(ws, w.w), T, H,
                              k, y, xdt, smode ? at<void>(ws, w.s_out) : nullptr,
                              smode ? at<void>(ws, w.s_logit) : nullptr, smode, st),

@@ -243,6 +243,51 @@ hipError_t launch_dispatch_plan(const uint32_t* idx, int T, int k, int E, uint32
   return hipGetLastError();
 }
 
+// Row tiles of an expert-sorted plan for the grouped GEMM: tiles[0] = count,
+// then (expert, first sorted position) pairs, experts ascending, tiles of
+// bm positions (the last tile of an expert may be partial).
+__global__ __launch_bounds__(kPlanThreads) void gemm_tiles_kernel(const uint32_t* __restrict__ offsets,
+                                                                  int E, int bm,
+                                                                  uint32_t* __restrict__ tiles) {
+  __shared__ uint32_t scan[kPlanThreads];
+  constexpr int EPT = kPlanMaxE / kPlanThreads;  // experts per thread
+  const int t = threadIdx.x;
+  uint32_t n[EPT], tot = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int e = t * EPT + j;
+    n[j] = 0;
+    if (e < E) n[j] = (offsets[e + 1] - offsets[e] + (uint32_t)bm - 1) / (uint32_t)bm;
+    tot += n[j];
+  }
+  scan[t] = tot;
+  __syncthreads();
+  for (int off = 1; off < kPlanThreads; off <<= 1) {
+    const uint32_t v = t >= off ? scan[t - off] : 0u;
+    __syncthreads();
+    scan[t] += v;
+    __syncthreads();
+  }
+  uint32_t base = scan[t] - tot;
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int e = t * EPT + j;
+    for (uint32_t i = 0; i < n[j]; i++) {
+      tiles[1 + 2 * (base + i)] = (uint32_t)e;
+      tiles[2 + 2 * (base + i)] = offsets[e] + i * (uint32_t)bm;
+    }
+    base += n[j];
+  }
+  if (t == kPlanThreads - 1) tiles[0] = scan[t];
+}
+
+hipError_t launch_gemm_tiles(const uint32_t* offsets, int E, int bm, uint32_t* tiles,
+                             hipStream_t st) {
+  if (E > kPlanMaxE) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gemm_tiles_kernel, dim3(1), dim3(kPlanThreads), 0, st, offsets, E, bm, tiles);
+  return hipGetLastError();
+}
+
 hipError_t launch_identity_plan(uint32_t* offsets, uint32_t* used, int M, hipStream_t st) {
   hipLaunchKernelGGL(identity_plan_kernel, dim3(1), dim3(64), 0, st, offsets, used, M);
   return hipGetLastError();

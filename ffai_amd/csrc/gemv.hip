@@ -553,7 +553,9 @@ template <int BITS, typename XT, typename ST, int UR, int RM>
 __global__ __launch_bounds__(512) void down1_kernel(const Down1Args a) {
   __shared__ float ys[kDec1MaxK * kDec1MaxRows * 64];
   __shared__ float wr[kDec1MaxK];
-  const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+  // wave-uniform by construction; readfirstlane tells the compiler, so the
+  // buffer resources built from it stay scalar
+  const int lane = threadIdx.x & 63, q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
   const int L = 1 << a.lg, SG = 64 >> a.lg;
   const int sg = lane >> a.lg, li = lane & (L - 1);

@@ -123,17 +123,26 @@ hipError_t launch_dequantize(const uint32_t* w, const void* s, const void* b, in
                              int gs, int64_t numel, void* out, int odt, hipStream_t st);
 
 // ----------------------------------------------------------------- GEMM --
+// Grouped dequant GEMM over row tiles of a dispatch plan (MFMA).
 struct GemmArgs {
-  GemvProj p0, p1;
-  const void* x;
-  const uint32_t* perm;
+  GemvProj p0, p1;           // gate/up pair (p1 = up) or a single projection
+  const void* x;             // activation rows [rows, K]
+  const uint32_t* perm;      // nullable: row(p) = perm[p] / topk, else p
   int topk;
-  const uint32_t* offsets;
-  const uint32_t* tiles;     // work list: [1 + max_tiles] (count, packed expert/m-tile)
-  void* out;
-  int N, K, gs, M;
+  const uint32_t* offsets;   // [E+1] CSR over sorted positions
+  const uint32_t* tiles;     // [1 + 2 * max_tiles]: count, (expert, first position)
+  void* out;                 // [M, N]
+  int N, K, gsh;
   int act;
   float alpha, limit;
 };
+constexpr int kGemmRows = 128;  // rows per tile
+// Output columns per block: 128 (gate/up pairs) or 256 (single projection).
+inline int gemm_block_cols(bool gateup) { return gateup ? 128 : 256; }
+inline int gemm_max_tiles(int M, int E) { return (M + kGemmRows - 1) / kGemmRows + E; }
+hipError_t launch_gemm_tiles(const uint32_t* offsets, int E, int bm, uint32_t* tiles,
+                             hipStream_t st);
+hipError_t launch_gemm(int bits, int xdt, int sbdt, bool gateup, const GemmArgs& a, int grid,
+                       hipStream_t st, KEvents ev = {});
 
 }  // namespace moe

@@ -43,9 +43,10 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT* __restrict
                                                             const XT* __restrict__ bias,
                                                             XT* __restrict__ logits, int T, int H,
                                                             int E, int tchunks) {
-  const int gw = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  // wave-uniform (readfirstlane keeps the buffer resources below scalar)
+  const int gw = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
   const int e = gw / tchunks, tc = gw - e * tchunks;
-  if (e >= E) return;  // wave-uniform; the kernel has no block barrier
+  if (e >= E) return;  // the kernel has no block barrier
   const int lane = threadIdx.x & 63;
   const int t0 = tc * 8, nt = min(8, T - t0);
   const float bv = bias ? to_f<XT>(bias[e]) : 0.f;  // issued before the row loads

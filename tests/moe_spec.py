@@ -212,7 +212,7 @@ def cfg_bits(gu_bits, down_bits, gs, sb_dt, act_dt, seed=0, hidden=512, inter=38
 
 # ------------------------------------------------------------- tolerance --
 
-def check_close(got, ref, dt, label=""):
+def check_close(got, ref, dt, label="", mean_tol=1e-3):
     """The layer's float bar against the fp32-accumulated oracle.
 
     fp16/bf16: max |d| <= 2e-2 on each element's own scale, max(1, |ref|,
@@ -224,7 +224,9 @@ def check_close(got, ref, dt, label=""):
     the error to order 1 on the RMS scale. Elements below the RMS are judged on
     the RMS scale, since the combine adds rounded per-expert outputs whose
     rounding is set by the summands, not by a cancelled result.
-    f32: |d| <= 1e-3 * max(1, |ref|) elementwise (MoELayerTests.swift:224)."""
+    f32: |d| <= 1e-3 * max(1, |ref|) elementwise (MoELayerTests.swift:224).
+    mean_tol overrides the mean bar for single products whose operands the
+    kernel rounds on purpose (the matrix-core path); layer tests keep 1e-3."""
     got = np.asarray(got, dtype=np.float64).ravel()
     ref = np.asarray(ref, dtype=np.float64).ravel()
     assert got.shape == ref.shape, (got.shape, ref.shape)
@@ -239,5 +241,5 @@ def check_close(got, ref, dt, label=""):
     scale = np.maximum(np.maximum(1.0, rms), np.abs(ref))
     max_scaled = float((d / scale).max()) if d.size else 0.0
     assert max_scaled <= 2e-2, f"{label}: max |d| / max(1, |ref|, rms) = {max_scaled:.3e} > 2e-2"
-    assert mean_rel <= 1e-3, f"{label}: mean relative error {mean_rel:.3e} > 1e-3"
+    assert mean_rel <= mean_tol, f"{label}: mean relative error {mean_rel:.3e} > {mean_tol:.1e}"
     return max_scaled, mean_rel

@@ -179,6 +179,56 @@ def test_expert_matmul_all_widths(bits, dt, sb):
     check_close(to_numpy_f32(out), ref, dt, f"expert_matmul bits={bits}")
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("dt,sb,gs", [(BF16, BF16, 64), (BF16, F16, 128), (F16, F16, 32),
+                                      (F16, BF16, 64)])
+@pytest.mark.parametrize("gather", [False, True])
+def test_expert_matmul_mfma(bits, dt, sb, gs, gather):
+    """The matrix-core path (enough rows per expert): uneven experts, an
+    empty expert, partial row tiles, a partial column block, and the
+    activation gather through a permutation."""
+    rng = np.random.default_rng(bits * 100 + dt * 10 + gs + gather)
+    from moe_spec import gen_qproj
+    E, N, K, topk = 5, 200, 384, 4
+    counts = np.array([300, 0, 131, 57, 212])  # M = 700 = 175 tokens x 4
+    M = int(counts.sum())
+    f = 15.0 / (2 ** bits - 1)
+    p = gen_qproj(rng, E, N, K, bits, gs, sb, s_range=(0.005 * f, 0.02 * f))
+    experts = np.repeat(np.arange(E), counts).astype(np.uint32)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.uint32)
+    if gather:
+        T = M // topk
+        a = store(rng.normal(0, 1, (T, K)), dt)
+        perm = rng.permutation(M).astype(np.uint32)  # sorted position -> t*topk + s
+        src = load(a, dt)[perm // topk]
+    else:
+        a = store(rng.normal(0, 1, (M, K)), dt)
+        perm = None
+        src = load(a, dt)
+    lib = _lib.load()
+    q = _lib.QProj(0, 0, 0, None, bits, gs, sb, N, K, E)
+    wt, st, bt = to_torch(p.weight.view(np.int32)), to_torch(p.scales), to_torch(p.biases)
+    q.weight, q.scales, q.biases = wt.data_ptr(), st.data_ptr(), bt.data_ptr()
+    at = to_torch(a)
+    out = torch.empty(M, N, dtype=at.dtype, device="cuda")
+    wsb = lib.moe_expert_matmul_workspace_bytes(E, M)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    offt = to_torch(offsets.view(np.int32))
+    pt = to_torch(perm.view(np.int32)) if gather else None
+    check(lib.moe_expert_matmul(C.byref(q), _p(at), dt, _p(pt) if gather else None, topk, M, _p(offt),
+                                _p(out), _p(ws), wsb, _stream()))
+    torch.cuda.synchronize()
+    ref = orc.round_dt(orc.qgemm_rows(p, src, experts), dt)
+    # The matrix-core path rounds every dequantised weight to the MFMA operand
+    # type (bf16: 2^-9, f16: 2^-12 relative), as the reference's simdgroup
+    # matrix kernels do in the input dtype (Ops.swift:4553-4600); the
+    # reference tests those kernels at cosine >= 0.99
+    # (MoEBgemmBm64MppTests.swift:82-114). One product is held to one bf16 ulp
+    # (2^-8) of mean relative error; whole layers keep the 1e-3 bar.
+    check_close(to_numpy_f32(out), ref, dt, f"mfma expert_matmul bits={bits} gs={gs}",
+                mean_tol=2.0 ** -8 if dt == BF16 else 1e-3)
+
+
 # ------------------------------------------------------------ whole layer --
 
 def run_layer(spec, T, seed=0):
@@ -275,6 +325,20 @@ BITS_CASES = [(2, 8, 64, F16, BF16), (5, 2, 32, BF16, F16), (8, 5, 128, F16, F16
 def test_layer_bit_widths(case, T):
     """Decode (T=1) and batched paths over every packed width and group size."""
     run_layer(cfg_bits(*case), T)
+
+
+@pytest.mark.parametrize("case", [(4, 4, 64, BF16, BF16), (3, 6, 64, BF16, BF16),
+                                  (5, 8, 128, F16, F16), (2, 4, 32, F16, BF16)],
+                         ids=lambda c: f"gu{c[0]}-d{c[1]}-gs{c[2]}-sb{c[3]}-x{c[4]}")
+def test_layer_mfma_path(case):
+    """Whole layers with enough rows per expert for the matrix-core GEMMs."""
+    run_layer(cfg_bits(*case, n_experts=4, top_k=2), 160)
+
+
+def test_layer_qwen3_mfma_zipf():
+    """Qwen3-MoE shape (16 experts) on the matrix-core path, Zipf routing."""
+    spec = cfg_qwen3(seed=11, n_experts=16, router_bias=zipf_router_bias(16, 1.1, beta=1.0))
+    run_layer(spec, 96)
 
 
 def test_layer_is_deterministic(qwen3):
