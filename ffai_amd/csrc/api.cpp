@@ -328,7 +328,7 @@ int group_shift(int gs) { return gs == 128 ? 2 : (gs == 64 ? 1 : 0); }
 
 struct Workspace {
   size_t logits, idx, w, counts, offsets, used, perm, inv, act, Y, plan_scratch, tiles;
-  size_t s_off, s_used, s_act, s_out, s_logit;
+  size_t s_off, s_used, s_act, s_out, s_logit, s_tiles;
   size_t total;
 };
 
@@ -362,6 +362,7 @@ Workspace layout(const moe_layer_desc* d, int T) {
     w.s_act = take((size_t)T * SI * ds);
     w.s_out = take((size_t)T * H * ds);
     w.s_logit = take((size_t)T * ds);
+    w.s_tiles = take((1 + 2 * (size_t)gemm_max_tiles(T, 1)) * 4);
   }
   w.total = o;
   return w;
@@ -412,7 +413,10 @@ constexpr int kGemmMinRows = 32;
 
 bool gemm_ok(const moe_qproj& p, int xdt, int M) {
   const int slots = std::min(p.n_experts, M);
-  return xdt != MOE_F32 && p.k % 64 == 0 && p.n_experts <= 1024 && M >= kGemmMinRows * slots;
+  // activation rows are addressed with 32-bit byte offsets
+  const bool fits = (size_t)M * (size_t)p.k * 2 < (1ull << 32);
+  return xdt != MOE_F32 && p.k % 64 == 0 && p.n_experts <= 1024 && fits &&
+         M >= kGemmMinRows * slots;
 }
 
 // out[p] = W[e(p)] . a[row(p)] (or the gate/up pair with the activation)
@@ -426,6 +430,7 @@ moe_status run_gemm(const moe_qproj& p0, const moe_qproj* p1, const void* x, int
   a.p0 = to_proj(p0);
   if (p1) a.p1 = to_proj(*p1);
   a.x = x;
+  a.x_rows = perm ? (M + topk - 1) / topk : M;
   a.perm = perm;
   a.topk = topk;
   a.offsets = offsets;
@@ -656,12 +661,25 @@ moe_status shared_expert(const moe_layer_desc* d, const void* x, int T, void* ws
   *smode = d->shared_gate_weight ? 2 : 1;
   MOE_HIP(launch_identity_plan(at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), T, st),
           "identity plan launch");
-  MOE_TRY(run_gemv(d->shared_gate, &d->shared_up, x, xdt, nullptr, 1, at<uint32_t>(ws, w.s_off),
-                   at<uint32_t>(ws, w.s_used), 1, T, single, at<void>(ws, w.s_act), MOE_ACT_SWIGLU,
-                   0.f, 0.f, st));
-  MOE_TRY(run_gemv(d->shared_down, nullptr, at<void>(ws, w.s_act), xdt, nullptr, 1,
-                   at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), 1, T, single,
-                   at<void>(ws, w.s_out), 0, 0.f, 0.f, st));
+  if (gemm_ok(d->shared_gate, xdt, T) && gemm_ok(d->shared_down, xdt, T)) {
+    // many tokens through one expert: the matrix-core path
+    MOE_HIP(launch_gemm_tiles(at<uint32_t>(ws, w.s_off), 1, kGemmRows, at<uint32_t>(ws, w.s_tiles),
+                              st),
+            "shared tile list launch");
+    MOE_TRY(run_gemm(d->shared_gate, &d->shared_up, x, xdt, nullptr, 1, at<uint32_t>(ws, w.s_off),
+                     at<uint32_t>(ws, w.s_tiles), T, at<void>(ws, w.s_act), MOE_ACT_SWIGLU, 0.f,
+                     0.f, st));
+    MOE_TRY(run_gemm(d->shared_down, nullptr, at<void>(ws, w.s_act), xdt, nullptr, 1,
+                     at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_tiles), T,
+                     at<void>(ws, w.s_out), 0, 0.f, 0.f, st));
+  } else {
+    MOE_TRY(run_gemv(d->shared_gate, &d->shared_up, x, xdt, nullptr, 1, at<uint32_t>(ws, w.s_off),
+                     at<uint32_t>(ws, w.s_used), 1, T, single, at<void>(ws, w.s_act),
+                     MOE_ACT_SWIGLU, 0.f, 0.f, st));
+    MOE_TRY(run_gemv(d->shared_down, nullptr, at<void>(ws, w.s_act), xdt, nullptr, 1,
+                     at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), 1, T, single,
+                     at<void>(ws, w.s_out), 0, 0.f, 0.f, st));
+  }
   if (d->shared_gate_weight)
     MOE_HIP(launch_router_logits(x, xdt, T, d->hidden, d->shared_gate_weight, d->router_dtype,
                                  nullptr, 1, at<void>(ws, w.s_logit), st),

@@ -97,23 +97,6 @@ __device__ __forceinline__ typename MfmaOp<XT>::V dequant8(const uint32_t (&w)[B
   return r;
 }
 
-// One weight matrix slice held by a lane for one K chunk.
-template <int BITS, typename ST> struct BFrag {
-  uint32_t w[BITS];
-  ST s, b;
-};
-
-template <int BITS, typename ST>
-__device__ __forceinline__ void load_bfrag(const ProjViewG& v, uint32_t row, int row_words,
-                                           int groups, int chunk, int h, int gsh,
-                                           BFrag<BITS, ST>& f) {
-  const int unit = 2 * chunk + h;  // 32-value unit index within the row
-  bload_unit<BITS>(v.w, (row * (uint32_t)row_words + (uint32_t)(unit * BITS)) * 4u, f.w);
-  const uint32_t gi = row * (uint32_t)groups + (uint32_t)(unit >> gsh);
-  f.s = __builtin_bit_cast(ST, bload16(v.s, gi * (uint32_t)sizeof(ST)));
-  f.b = __builtin_bit_cast(ST, bload16(v.b, gi * (uint32_t)sizeof(ST)));
-}
-
 template <int BITS, typename ST>
 __device__ __forceinline__ ProjViewG proj_view_g(const GemvProj& p, uint32_t e, int N,
                                                  int row_words, int groups) {
@@ -127,15 +110,47 @@ __device__ __forceinline__ ProjViewG proj_view_g(const GemvProj& p, uint32_t e, 
   return v;
 }
 
-// GATEUP: matrix 0 = gate, matrix 1 = up, both for columns n0 + lane%32
-// (the activation is applied in the epilogue, output [M, N]); otherwise
-// one matrix with two 32-column sets n0 + lane%32 and n0 + 32 + lane%32.
+// LDS tile of 256 rows x 64 values (16-bit), 128 B per row; the 16-byte
+// chunk c of row r sits at slot c ^ (r & 7), so that 8 consecutive rows
+// reading the same chunk hit 8 different bank groups.
+constexpr int kTR = 256;
+__device__ __forceinline__ uint32_t tile_off(int r, int c) {
+  return (uint32_t)(r * 128 + ((c ^ (r & 7)) << 4));
+}
+
+// Block barrier ordering LDS only: loads from global memory stay in flight
+// across it (a full __syncthreads would wait for them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Block tile: 256 rows x 256 weight rows (gate/up: 128 output columns of
+// gate and of up; otherwise 256 output columns), 8 waves in a 4 x 2 grid:
+// wave (wm, wn) owns rows [64 wm, +64) as 2 MFMA row tiles and 4 MFMA column
+// tiles (gate/up: gate columns [64 wn, +64) and the matching up columns), so
+// its accumulators fit 128 AGPRs and two waves share each SIMD. Row tiles
+// past the expert's last position skip their MFMAs.
+//
+// Per 64-value chunk: every thread copies 64 bytes of activation rows and
+// dequantises one 32-value unit of one weight row into LDS, once for the
+// whole block, and each wave runs 4 steps x 8 v_mfma_f32_32x32x16. Global
+// loads run two chunks ahead of the MFMAs; chunk c + 1 is written to LDS
+// (its weights dequantised between the MFMA steps) while chunk c is
+// multiplied.
+// All operand rows of a lane are congruent mod 8, so one swizzled chunk
+// offset per step serves every LDS read (immediate row offsets).
 template <int BITS, typename XT, typename ST, bool GATEUP>
-__global__ __launch_bounds__(256) void gemm_grouped_kernel(const GemmArgs a) {
-  __shared__ __align__(16) XT As[2][kGBM * kGAS];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nb_cols = GATEUP ? 128 : 256;  // output columns per block
-  const int n_tiles = (a.N + nb_cols - 1) / nb_cols;
+__global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
+  __shared__ __align__(16) unsigned char As[2][kTR * 128];
+  __shared__ __align__(16) unsigned char Bs[2][kTR * 128];
+  typedef typename MfmaOp<XT>::V V;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int ncols = GATEUP ? 128 : 256;  // output columns per block
+  const int n_tiles = (a.N + ncols - 1) / ncols;
 
   // blocks b, b + 8, b + 16, ... share an XCD (and its L2): give them
   // consecutive work items, column slices of one row tile first
@@ -153,77 +168,136 @@ __global__ __launch_bounds__(256) void gemm_grouped_kernel(const GemmArgs a) {
 
   const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
   const int nchunks = K / kGBK;
-  const int col = lane & 31, h = lane >> 5;
-  const int n0 = bn * nb_cols + wave * (GATEUP ? 32 : 64);
-  // B rows of the two column sets (clamped: columns past N compute garbage
-  // that is never stored)
-  const uint32_t r0 = (uint32_t)min(n0 + col, N - 1);
-  const uint32_t r1 = GATEUP ? r0 : (uint32_t)min(n0 + 32 + col, N - 1);
-  const ProjViewG P0 = proj_view_g<BITS, ST>(a.p0, e, N, row_words, groups);
-  const ProjViewG P1 = GATEUP ? proj_view_g<BITS, ST>(a.p1, e, N, row_words, groups) : P0;
 
-  // A staging: thread t copies row t/2, values [32 (t%2), +32) of a chunk
-  const int arow = threadIdx.x >> 1, ahalf = threadIdx.x & 1;
-  const uint32_t ap = min(m0 + (uint32_t)arow, pend - 1);
-  const uint32_t xrow = a.perm ? a.perm[ap] / (uint32_t)a.topk : ap;
-  // rows differ per lane, so these are plain global loads (a buffer
-  // resource must be wave-uniform)
-  const u32x4_t* xsrc = reinterpret_cast<const u32x4_t*>(reinterpret_cast<const XT*>(a.x) +
-                                                         (size_t)xrow * K + 32 * ahalf);
-  auto load_a = [&](int c, u32x4_t (&v)[4]) {
+  // ---- activation rows: thread (wave, lane) copies, for i < 4, 16 bytes
+  // of LDS row 32 wave + 8 i + lane / 8, slot lane % 8 (logical chunk
+  // (lane % 8) ^ (row & 7)); two register sets keep chunk c + 2 in flight
+  // one wave-uniform buffer resource over all activation rows; per-lane
+  // 32-bit byte offsets of the four rows this lane copies
+  const rsrc_t xr = make_rsrc(a.x, (uint32_t)min((size_t)a.x_rows * K * sizeof(XT), (size_t)0xFFFFFFFFu));
+  uint32_t xoff[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) v[j] = xsrc[c * (kGBK * (int)sizeof(XT) / 16) + j];
-  };
-  auto store_a = [&](int buf, const u32x4_t (&v)[4]) {
-    u32x4_t* dst = reinterpret_cast<u32x4_t*>(&As[buf][arow * kGAS + 32 * ahalf]);
-#pragma unroll
-    for (int j = 0; j < 4; j++) dst[j] = v[j];
-  };
-
-  f32x16_t acc0[4], acc1[4];
-#pragma unroll
-  for (int t = 0; t < 4; t++) {
-    acc0[t] = f32x16_t{};
-    acc1[t] = f32x16_t{};
+  for (int i = 0; i < 4; i++) {
+    const int r = 32 * wave + 8 * i + (lane >> 3);
+    const uint32_t p = min(m0 + (uint32_t)r, pend - 1);
+    const uint32_t xrow = a.perm ? a.perm[p] / (uint32_t)a.topk : p;
+    const int c = (lane & 7) ^ (r & 7);
+    xoff[i] = (xrow * (uint32_t)K + (uint32_t)(8 * c)) * (uint32_t)sizeof(XT);
   }
+  // LDS byte offset of load i: row 32 wave + 8 i + lane / 8, slot lane % 8
+  const uint32_t aoff0 = (uint32_t)((32 * wave + (lane >> 3)) * 128 + ((lane & 7) << 4));
+  struct ARegs {
+    u32x4_t v[4];
+  };
+  auto load_a = [&](int chunk, ARegs& ar) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      ar.v[i] = bload128(xr, xoff[i] + (uint32_t)(chunk * kGBK * (int)sizeof(XT)));
+  };
+  auto store_a = [&](const ARegs& ar, int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4_t*>(&As[buf][aoff0 + 1024 * i]) = ar.v[i];
+  };
 
-  BFrag<BITS, ST> f0, f1, g0, g1;
-  u32x4_t av[4];
-  load_a(0, av);
-  load_bfrag<BITS, ST>(P0, r0, row_words, groups, 0, h, a.gsh, f0);
-  load_bfrag<BITS, ST>(P1, r1, row_words, groups, 0, h, a.gsh, f1);
-  store_a(0, av);
-  __syncthreads();
+  // ---- weights: thread t dequantises unit t % 2 (values [32 (t % 2), +32)
+  // of the chunk) of LDS weight row t / 2
+  const int brl = threadIdx.x >> 1, bu = threadIdx.x & 1;
+  const bool upper = GATEUP && wave >= 4;  // LDS rows 128..255 hold up (wave-uniform)
+  const int wrow = GATEUP ? bn * 128 + (brl & 127) : bn * 256 + brl;
+  const uint32_t brow = (uint32_t)min(wrow, N - 1);
+  const ProjViewG PB = proj_view_g<BITS, ST>(upper ? a.p1 : a.p0, e, N, row_words, groups);
+  // packed codes, scale and bias of one unit: two register sets so that
+  // chunk c + 2 is in flight while chunk c + 1 is dequantised
+  struct BUnit {
+    uint32_t w[BITS];
+    ST s, b;
+  };
+  auto load_b = [&](int chunk, BUnit& u) {
+    const int unit = 2 * chunk + bu;
+    bload_unit<BITS>(PB.w, (brow * (uint32_t)row_words + (uint32_t)(unit * BITS)) * 4u, u.w);
+    const uint32_t gi = brow * (uint32_t)groups + (uint32_t)(unit >> a.gsh);
+    u.s = __builtin_bit_cast(ST, bload16(PB.s, gi * (uint32_t)sizeof(ST)));
+    u.b = __builtin_bit_cast(ST, bload16(PB.b, gi * (uint32_t)sizeof(ST)));
+  };
+  // 8 values [8 s, 8 s + 8) of the unit -> LDS chunk 4 bu + s
+  auto store_b = [&](const BUnit& u, int s, int buf) {
+    const V v = dequant8<BITS, XT>(u.w, s, to_f<ST>(u.s), to_f<ST>(u.b));
+    *reinterpret_cast<V*>(&Bs[buf][tile_off(brl, 4 * bu + s)]) = v;
+  };
 
-  typedef typename MfmaOp<XT>::V V;
-  for (int c = 0; c < nchunks; c++) {
-    const int buf = c & 1;
-    const bool more = c + 1 < nchunks;
-    if (more) {
-      load_a(c + 1, av);
-      load_bfrag<BITS, ST>(P0, r0, row_words, groups, c + 1, h, a.gsh, g0);
-      load_bfrag<BITS, ST>(P1, r1, row_words, groups, c + 1, h, a.gsh, g1);
-    }
-    const float s0 = to_f<ST>(f0.s), b0 = to_f<ST>(f0.b);
-    const float s1 = to_f<ST>(f1.s), b1 = to_f<ST>(f1.b);
-    const XT* at = &As[buf][0];
+  f32x16_t acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = f32x16_t{};
+
+  // row tiles of this wave that hold positions of the expert
+  const int mvalid = (m0 + (uint32_t)(64 * wm) >= pend) ? 0
+                   : (m0 + (uint32_t)(64 * wm + 32) >= pend) ? 1 : 2;
+
+  // MFMA operand rows of this lane: A rows 64 wm + 32 i + col, B rows
+  // (gate/up) 64 wn + 32 j + col and 128 + 64 wn + 32 (j - 2) + col, or
+  // 128 wn + 32 j + col; all congruent to col mod 8
+  const int col = lane & 31, h = lane >> 5;
+  const uint32_t arow0 = (uint32_t)(64 * wm + col) * 128u;
+  const uint32_t brow0 = (uint32_t)((GATEUP ? 64 * wn : 128 * wn) + col) * 128u;
+  auto boff = [&](int j) -> uint32_t {
+    return GATEUP ? (uint32_t)((j < 2 ? 32 * j : 128 + 32 * (j - 2)) * 128) : (uint32_t)(32 * j * 128);
+  };
+
+  // One chunk: MFMAs on LDS buffer `buf`; meanwhile chunk c + 1's weights
+  // (set nb) are dequantised into the other buffer between the steps and its
+  // activations (set na) stored after them, and chunk c + 2 loads into the
+  // sets ca / cb that chunk c used.
+  // Loads and LDS writes are unconditional (past the end they repeat the
+  // last chunk, in bounds and never read) so that the compiler can count
+  // outstanding loads exactly and never waits for the newest ones.
+  auto chunk_step = [&](int c, int buf, ARegs& ca, BUnit& cb, const ARegs& na, const BUnit& nb) {
+    const int cp = min(c + 2, nchunks - 1);
+    load_a(cp, ca);
+    load_b(cp, cb);
+    const unsigned char* Ab = &As[buf][0];
+    const unsigned char* Bb = &Bs[buf][0];
+    // operand fragments of step s + 1 are read while step s multiplies
+    V bf[2][4], af[2][2];
+    auto read_frags = [&](int s, V (&b)[4], V (&a2)[2]) {
+      const uint32_t sw = (uint32_t)(((2 * s + h) ^ (col & 7)) << 4);
+#pragma unroll
+      for (int j = 0; j < 4; j++) b[j] = *reinterpret_cast<const V*>(Bb + brow0 + boff(j) + sw);
+#pragma unroll
+      for (int i = 0; i < 2; i++) a2[i] = *reinterpret_cast<const V*>(Ab + arow0 + 32 * 128 * i + sw);
+    };
+    read_frags(0, bf[0], af[0]);
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-      const V bq0 = dequant8<BITS, XT>(f0.w, s, s0, b0);
-      const V bq1 = dequant8<BITS, XT>(f1.w, s, s1, b1);
+      if (s < 3) read_frags(s + 1, bf[(s + 1) & 1], af[(s + 1) & 1]);
 #pragma unroll
-      for (int t = 0; t < 4; t++) {
-        const V av8 = *reinterpret_cast<const V*>(at + (t * 32 + col) * kGAS + 32 * h + 8 * s);
-        acc0[t] = MfmaOp<XT>::mma(av8, bq0, acc0[t]);
-        acc1[t] = MfmaOp<XT>::mma(av8, bq1, acc1[t]);
+      for (int i = 0; i < 2; i++) {
+        if (i < mvalid) {
+#pragma unroll
+          for (int j = 0; j < 4; j++) acc[i][j] = MfmaOp<XT>::mma(af[s & 1][i], bf[s & 1][j], acc[i][j]);
+        }
       }
+      store_b(nb, s, buf ^ 1);
     }
-    if (more) {
-      store_a(buf ^ 1, av);
-      f0 = g0;
-      f1 = g1;
-    }
-    __syncthreads();
+    store_a(na, buf ^ 1);
+    lds_barrier();
+  };
+
+  ARegs a0, a1;
+  BUnit u0, u1;
+  load_a(0, a0);
+  load_b(0, u0);
+  load_a(min(1, nchunks - 1), a1);
+  load_b(min(1, nchunks - 1), u1);
+  store_a(a0, 0);
+#pragma unroll
+  for (int s = 0; s < 4; s++) store_b(u0, s, 0);
+  lds_barrier();
+
+  for (int c = 0; c < nchunks; c += 2) {
+    chunk_step(c, 0, a0, u0, a1, u1);
+    if (c + 1 < nchunks) chunk_step(c + 1, 1, a1, u1, a0, u0);
   }
 
   // epilogue: lane holds column col, rows 8 (r / 4) + 4 h + r % 4 of each
@@ -231,24 +305,25 @@ __global__ __launch_bounds__(256) void gemm_grouped_kernel(const GemmArgs a) {
   XT* out = reinterpret_cast<XT*>(a.out);
   const XT* ob0 = reinterpret_cast<const XT*>(a.p0.ob);
   const XT* ob1 = reinterpret_cast<const XT*>(GATEUP ? a.p1.ob : a.p0.ob);
-  const int c0 = n0 + col, c1 = GATEUP ? c0 : n0 + 32 + col;
-  const float obv0 = (ob0 && c0 < N) ? to_f<XT>(ob0[(size_t)e * N + c0]) : 0.f;
-  const float obv1 = (ob1 && c1 < N) ? to_f<XT>(ob1[(size_t)e * N + c1]) : 0.f;
 #pragma unroll
-  for (int t = 0; t < 4; t++) {
+  for (int j = 0; j < (GATEUP ? 2 : 4); j++) {
+    const int cn = GATEUP ? bn * 128 + 64 * wn + 32 * j + col : bn * 256 + 128 * wn + 32 * j + col;
+    const float obg = (ob0 && cn < N) ? to_f<XT>(ob0[(size_t)e * N + cn]) : 0.f;
+    const float obu = (GATEUP && ob1 && cn < N) ? to_f<XT>(ob1[(size_t)e * N + cn]) : 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const uint32_t p = m0 + (uint32_t)(t * 32 + 8 * (r >> 2) + 4 * h + (r & 3));
-      if (p >= pend) continue;
-      float v0 = round_to<XT>(acc0[t][r]);
-      if (ob0) v0 = round_to<XT>(v0 + obv0);
-      float v1 = round_to<XT>(acc1[t][r]);
-      if (ob1) v1 = round_to<XT>(v1 + obv1);
-      if constexpr (GATEUP) {
-        if (c0 < N) out[(size_t)p * N + c0] = from_f<XT>(apply_act(v0, v1, a.act, a.alpha, a.limit));
-      } else {
-        if (c0 < N) out[(size_t)p * N + c0] = from_f<XT>(v0);
-        if (c1 < N) out[(size_t)p * N + c1] = from_f<XT>(v1);
+    for (int i = 0; i < 2; i++) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const uint32_t p = m0 + (uint32_t)(64 * wm + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3));
+        if (p >= pend || cn >= N) continue;
+        float v = round_to<XT>(acc[i][j][r]);
+        if (ob0) v = round_to<XT>(v + obg);
+        if constexpr (GATEUP) {
+          float u = round_to<XT>(acc[i][j + 2][r]);
+          if (ob1) u = round_to<XT>(u + obu);
+          v = apply_act(v, u, a.act, a.alpha, a.limit);
+        }
+        out[(size_t)p * N + cn] = from_f<XT>(v);
       }
     }
   }
@@ -258,10 +333,10 @@ template <int BITS, typename XT, typename ST>
 static hipError_t launch_gemm_t(bool gateup, const GemmArgs& a, int grid, hipStream_t st,
                                 KEvents ev) {
   if (gateup)
-    hipExtLaunchKernelGGL((gemm_grouped_kernel<BITS, XT, ST, true>), dim3(grid), dim3(256), 0, st,
+    hipExtLaunchKernelGGL((gemm_grouped_kernel<BITS, XT, ST, true>), dim3(grid), dim3(512), 0, st,
                           ev.start, ev.stop, 0, a);
   else
-    hipExtLaunchKernelGGL((gemm_grouped_kernel<BITS, XT, ST, false>), dim3(grid), dim3(256), 0, st,
+    hipExtLaunchKernelGGL((gemm_grouped_kernel<BITS, XT, ST, false>), dim3(grid), dim3(512), 0, st,
                           ev.start, ev.stop, 0, a);
   return hipGetLastError();
 }

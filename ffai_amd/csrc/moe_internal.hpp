@@ -126,7 +126,8 @@ hipError_t launch_dequantize(const uint32_t* w, const void* s, const void* b, in
 // Grouped dequant GEMM over row tiles of a dispatch plan (MFMA).
 struct GemmArgs {
   GemvProj p0, p1;           // gate/up pair (p1 = up) or a single projection
-  const void* x;             // activation rows [rows, K]
+  const void* x;             // activation rows [x_rows, K]
+  int x_rows;
   const uint32_t* perm;      // nullable: row(p) = perm[p] / topk, else p
   int topk;
   const uint32_t* offsets;   // [E+1] CSR over sorted positions
@@ -136,7 +137,7 @@ struct GemmArgs {
   int act;
   float alpha, limit;
 };
-constexpr int kGemmRows = 128;  // rows per tile
+constexpr int kGemmRows = 256;  // rows per tile
 // Output columns per block: 128 (gate/up pairs) or 256 (single projection).
 inline int gemm_block_cols(bool gateup) { return gateup ? 128 : 256; }
 inline int gemm_max_tiles(int M, int E) { return (M + kGemmRows - 1) / kGemmRows + E; }

@@ -311,7 +311,7 @@ def mixed():
     return cfg_mixed()
 
 
-@pytest.mark.parametrize("T", [1, 24])
+@pytest.mark.parametrize("T", [1, 24, 64])
 def test_layer_mixed_bits_shared(mixed, T):
     run_layer(mixed, T)
 
