@@ -307,7 +307,10 @@ def main():
                     peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s")
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
     roof["traffic"] = None
+    # the library's path choice: MFMA GEMM once used experts average >= 32 rows
+    gemm_path = T > 1 and M >= 32 * min(cfg["E"], M) and cfg["H"] % 64 == 0 and cfg["I"] % 64 == 0
     roof["kernel"] = ("gateup1_kernel (one-token gate/up with routing)" if T == 1 else
+                      "gemm_grouped_kernel (MFMA gate/up over the expert row tiles)" if gemm_path else
                       "gemv_grouped_kernel (routed gate/up over the dispatch plan)")
     roof["avg_us"] = round(gu_us, 3)
     roof["algorithmic_bytes"] = gu_bytes

@@ -328,6 +328,7 @@ int group_shift(int gs) { return gs == 128 ? 2 : (gs == 64 ? 1 : 0); }
 
 struct Workspace {
   size_t logits, idx, w, counts, offsets, used, perm, inv, act, Y, plan_scratch, tiles;
+  size_t r_plan, r_tiles;  // router projection on the matrix cores
   size_t s_off, s_used, s_act, s_out, s_logit, s_tiles;
   size_t total;
 };
@@ -355,6 +356,8 @@ Workspace layout(const moe_layer_desc* d, int T) {
   w.Y = take(M * H * ds);
   w.plan_scratch = take(dispatch_scratch_bytes(T, (int)k, (int)E));
   w.tiles = take((1 + 2 * (size_t)gemm_max_tiles((int)M, (int)E)) * 4);
+  w.r_plan = take(4 * 4);  // offsets {0, T} and the used list of a one-expert plan
+  w.r_tiles = take((1 + 2 * (size_t)gemm_max_tiles(T, 1)) * 4);
   if (d->has_shared) {
     const size_t SI = (size_t)d->shared_gate.n;
     w.s_off = take(2 * 4);
@@ -417,6 +420,35 @@ bool gemm_ok(const moe_qproj& p, int xdt, int M) {
   const bool fits = (size_t)M * (size_t)p.k * 2 < (1ull << 32);
   return xdt != MOE_F32 && p.k % 64 == 0 && p.n_experts <= 1024 && fits &&
          M >= kGemmMinRows * slots;
+}
+
+// Router logits on the matrix cores for many tokens: a one-expert plan over
+// the T rows with the dense router weight; the bias rounds after the product
+// as in router_logits_kernel.
+bool router_gemm_ok(const moe_layer_desc* d, int T) {
+  return T >= kGemmMinRows && d->act_dtype != MOE_F32 && d->router_dtype == d->act_dtype &&
+         d->hidden % 64 == 0 && (size_t)T * d->hidden * 2 < (1ull << 32);
+}
+
+moe_status run_router_gemm(const moe_layer_desc* d, const void* x, int T, void* logits,
+                           uint32_t* plan, uint32_t* tiles, hipStream_t st) {
+  MOE_HIP(launch_identity_plan(plan, plan + 2, T, st), "router plan launch");
+  MOE_HIP(launch_gemm_tiles(plan, 1, kGemmRows, tiles, st), "router tile list launch");
+  GemmArgs a{};
+  a.p0 = GemvProj{reinterpret_cast<const uint32_t*>(d->router_weight), nullptr, nullptr,
+                  d->router_bias};
+  a.x = x;
+  a.x_rows = T;
+  a.topk = 1;
+  a.offsets = plan;
+  a.tiles = tiles;
+  a.out = logits;
+  a.N = d->n_experts;
+  a.K = d->hidden;
+  const long items = (long)gemm_max_tiles(T, 1) * ((d->n_experts + 255) / 256);
+  const int grid = (int)((items + 7) / 8 * 8);
+  MOE_HIP(launch_gemm_dense(d->act_dtype, a, grid, st), "router GEMM launch");
+  return MOE_OK;
 }
 
 // out[p] = W[e(p)] . a[row(p)] (or the gate/up pair with the activation)
@@ -765,9 +797,14 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y,
   };
 
   // 1. router projection (MoELayer.swift:540 / 689-690)
-  MOE_HIP(launch_router_logits(x, xdt, T, H, d->router_weight, d->router_dtype, d->router_bias, E,
-                               at<void>(ws, w.logits), st),
-          "router logits launch");
+  if (router_gemm_ok(d, T)) {
+    MOE_TRY(run_router_gemm(d, x, T, at<void>(ws, w.logits), at<uint32_t>(ws, w.r_plan),
+                            at<uint32_t>(ws, w.r_tiles), st));
+  } else {
+    MOE_HIP(launch_router_logits(x, xdt, T, H, d->router_weight, d->router_dtype, d->router_bias,
+                                 E, at<void>(ws, w.logits), st),
+            "router logits launch");
+  }
 
   const bool dec1 = (T == 1 && dec1_supported(d));
   int smode = 0;

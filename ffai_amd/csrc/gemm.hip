@@ -76,6 +76,12 @@ __device__ __forceinline__ float unit_code(const uint32_t (&w)[BITS], int s, int
 template <int BITS, typename XT>
 __device__ __forceinline__ typename MfmaOp<XT>::V dequant8(const uint32_t (&w)[BITS], int s,
                                                           float sc, float bi) {
+  if constexpr (BITS == 16) {
+    // plain weights already in the operand type
+    (void)sc;
+    (void)bi;
+    return __builtin_bit_cast(typename MfmaOp<XT>::V, u32x4_t{w[4 * s], w[4 * s + 1], w[4 * s + 2], w[4 * s + 3]});
+  }
   float q[8];
   if constexpr (BITS == 4) {
     const uint32_t lo = w[s] & 0x0F0F0F0Fu, hi = (w[s] >> 4) & 0x0F0F0F0Fu;
@@ -215,13 +221,16 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
   auto load_b = [&](int chunk, BUnit& u) {
     const int unit = 2 * chunk + bu;
     bload_unit<BITS>(PB.w, (brow * (uint32_t)row_words + (uint32_t)(unit * BITS)) * 4u, u.w);
-    const uint32_t gi = brow * (uint32_t)groups + (uint32_t)(unit >> a.gsh);
-    u.s = __builtin_bit_cast(ST, bload16(PB.s, gi * (uint32_t)sizeof(ST)));
-    u.b = __builtin_bit_cast(ST, bload16(PB.b, gi * (uint32_t)sizeof(ST)));
+    if constexpr (BITS != 16) {
+      const uint32_t gi = brow * (uint32_t)groups + (uint32_t)(unit >> a.gsh);
+      u.s = __builtin_bit_cast(ST, bload16(PB.s, gi * (uint32_t)sizeof(ST)));
+      u.b = __builtin_bit_cast(ST, bload16(PB.b, gi * (uint32_t)sizeof(ST)));
+    }
   };
   // 8 values [8 s, 8 s + 8) of the unit -> LDS chunk 4 bu + s
   auto store_b = [&](const BUnit& u, int s, int buf) {
-    const V v = dequant8<BITS, XT>(u.w, s, to_f<ST>(u.s), to_f<ST>(u.b));
+    const V v = BITS == 16 ? dequant8<BITS, XT>(u.w, s, 0.f, 0.f)
+                           : dequant8<BITS, XT>(u.w, s, to_f<ST>(u.s), to_f<ST>(u.b));
     *reinterpret_cast<V*>(&Bs[buf][tile_off(brl, 4 * bu + s)]) = v;
   };
 
@@ -352,5 +361,21 @@ hipError_t MOE_CAT(launch_gemm_b, MOE_BITS)(int xdt, int sbdt, bool gateup, cons
   if (xdt == DT_F16 && sbdt == DT_BF16) return launch_gemm_t<MOE_BITS, f16_t, bf16_t>(gateup, a, grid, st, ev);
   return hipErrorInvalidValue;
 }
+
+#if MOE_BITS == 4
+// Dense 16-bit weights of the activation type (the router projection over
+// many tokens): the same kernel with the dequantisation replaced by a copy.
+hipError_t launch_gemm_dense(int xdt, const GemmArgs& a, int grid, hipStream_t st) {
+  if (xdt == DT_BF16)
+    hipLaunchKernelGGL((gemm_grouped_kernel<16, bf16_t, bf16_t, false>), dim3(grid), dim3(512), 0,
+                       st, a);
+  else if (xdt == DT_F16)
+    hipLaunchKernelGGL((gemm_grouped_kernel<16, f16_t, f16_t, false>), dim3(grid), dim3(512), 0,
+                       st, a);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+#endif
 
 }  // namespace moe

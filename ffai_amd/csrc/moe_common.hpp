@@ -426,10 +426,17 @@ __device__ __forceinline__ void bload_unit(rsrc_t r, uint32_t off, uint32_t (&w)
   } else if constexpr (BITS == 6) {
     const u32x2_t a = bload64(r, off), b = bload64(r, off + 8), c = bload64(r, off + 16);
     w[0] = a[0]; w[1] = a[1]; w[2] = b[0]; w[3] = b[1]; w[4] = c[0]; w[5] = c[1];
-  } else {
+  } else if constexpr (BITS == 8) {
     const u32x4_t a = bload128(r, off), b = bload128(r, off + 16);
     w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
     w[4] = b[0]; w[5] = b[1]; w[6] = b[2]; w[7] = b[3];
+  } else {
+    // 16: plain 16-bit weights (dense projections), 32 values = 64 bytes
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const u32x4_t v = bload128(r, off + 16u * q);
+      w[4 * q] = v[0]; w[4 * q + 1] = v[1]; w[4 * q + 2] = v[2]; w[4 * q + 3] = v[3];
+    }
   }
 }
 

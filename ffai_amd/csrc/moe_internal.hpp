@@ -145,5 +145,8 @@ hipError_t launch_gemm_tiles(const uint32_t* offsets, int E, int bm, uint32_t* t
                              hipStream_t st);
 hipError_t launch_gemm(int bits, int xdt, int sbdt, bool gateup, const GemmArgs& a, int grid,
                        hipStream_t st, KEvents ev = {});
+// p0.w holds dense [N, K] weights of the activation type; p0.ob an optional
+// bias added after rounding (round(round(W x) + b)).
+hipError_t launch_gemm_dense(int xdt, const GemmArgs& a, int grid, hipStream_t st);
 
 }  // namespace moe
