@@ -116,12 +116,14 @@ __device__ __forceinline__ ProjViewG proj_view_g(const GemvProj& p, uint32_t e, 
   return v;
 }
 
-// LDS tile of 256 rows x 64 values (16-bit), 128 B per row; the 16-byte
-// chunk c of row r sits at slot c ^ (r & 7), so that 8 consecutive rows
-// reading the same chunk hit 8 different bank groups.
+// LDS tile of 256 rows x 64 values (16-bit), 128 B per row. The banks
+// repeat every 256 B (two rows) and a 16-byte read serves 16 lanes per
+// cycle, so the 16-byte chunk c of row r sits at slot c ^ ((r >> 1) & 7):
+// 16 consecutive rows reading the same chunk then cover every bank once.
 constexpr int kTR = 256;
+__device__ __forceinline__ int tile_swz(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ uint32_t tile_off(int r, int c) {
-  return (uint32_t)(r * 128 + ((c ^ (r & 7)) << 4));
+  return (uint32_t)(r * 128 + ((c ^ tile_swz(r)) << 4));
 }
 
 // Block barrier ordering LDS only: loads from global memory stay in flight
@@ -145,7 +147,7 @@ __device__ __forceinline__ void lds_barrier() {
 // loads run two chunks ahead of the MFMAs; chunk c + 1 is written to LDS
 // (its weights dequantised between the MFMA steps) while chunk c is
 // multiplied.
-// All operand rows of a lane are congruent mod 8, so one swizzled chunk
+// All operand rows of a lane are congruent mod 16, so one swizzled chunk
 // offset per step serves every LDS read (immediate row offsets).
 template <int BITS, typename XT, typename ST, bool GATEUP>
 __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
@@ -177,7 +179,7 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
 
   // ---- activation rows: thread (wave, lane) copies, for i < 4, 16 bytes
   // of LDS row 32 wave + 8 i + lane / 8, slot lane % 8 (logical chunk
-  // (lane % 8) ^ (row & 7)); two register sets keep chunk c + 2 in flight
+  // (lane % 8) ^ tile_swz(row)); two register sets keep chunk c + 2 in flight
   // one wave-uniform buffer resource over all activation rows; per-lane
   // 32-bit byte offsets of the four rows this lane copies
   const rsrc_t xr = make_rsrc(a.x, (uint32_t)min((size_t)a.x_rows * K * sizeof(XT), (size_t)0xFFFFFFFFu));
@@ -187,7 +189,7 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
     const int r = 32 * wave + 8 * i + (lane >> 3);
     const uint32_t p = min(m0 + (uint32_t)r, pend - 1);
     const uint32_t xrow = a.perm ? a.perm[p] / (uint32_t)a.topk : p;
-    const int c = (lane & 7) ^ (r & 7);
+    const int c = (lane & 7) ^ tile_swz(r);
     xoff[i] = (xrow * (uint32_t)K + (uint32_t)(8 * c)) * (uint32_t)sizeof(XT);
   }
   // LDS byte offset of load i: row 32 wave + 8 i + lane / 8, slot lane % 8
@@ -246,7 +248,8 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
 
   // MFMA operand rows of this lane: A rows 64 wm + 32 i + col, B rows
   // (gate/up) 64 wn + 32 j + col and 128 + 64 wn + 32 (j - 2) + col, or
-  // 128 wn + 32 j + col; all congruent to col mod 8
+  // 128 wn + 32 j + col; all congruent to col mod 16, so they share
+  // tile_swz(col)
   const int col = lane & 31, h = lane >> 5;
   const uint32_t arow0 = (uint32_t)(64 * wm + col) * 128u;
   const uint32_t brow0 = (uint32_t)((GATEUP ? 64 * wn : 128 * wn) + col) * 128u;
@@ -270,7 +273,7 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
     // operand fragments of step s + 1 are read while step s multiplies
     V bf[2][4], af[2][2];
     auto read_frags = [&](int s, V (&b)[4], V (&a2)[2]) {
-      const uint32_t sw = (uint32_t)(((2 * s + h) ^ (col & 7)) << 4);
+      const uint32_t sw = (uint32_t)(((2 * s + h) ^ tile_swz(col)) << 4);
 #pragma unroll
       for (int j = 0; j < 4; j++) b[j] = *reinterpret_cast<const V*>(Bb + brow0 + boff(j) + sw);
 #pragma unroll
