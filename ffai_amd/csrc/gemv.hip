@@ -458,7 +458,7 @@ __device__ __forceinline__ void bload_x_units(rsrc_t xr, int li, int L, XUnit<XT
 // r_begin + w SG + sg + it 4 SG for it < RM; every load of those rows is
 // issued before the first dot product. The routing runs once per block, in
 // wave 0, while the other waves load the activations.
-template <int BITS, typename XT, typename ST, int UR, int RM>
+template <int BITS, typename XT, typename ST, int UR, int RM, int EPL>
 __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
   __shared__ float sc[kTopkMaxE];
   __shared__ int route[2];
@@ -485,8 +485,8 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
     int sel;
     float wgt = 0.f;
     uint64_t masks[kTopkEPL];
-    wave_topk<XT>(reinterpret_cast<const XT*>(a.logits), a.E, a.k, a.gating, a.norm, a.ebias, sc,
-                  writer, &sel, &wgt, masks);
+    wave_topk<XT, EPL>(reinterpret_cast<const XT*>(a.logits), a.E, a.k, a.gating, a.norm, a.ebias,
+                       sc, writer, &sel, &wgt, masks);
     const int e = __builtin_amdgcn_readfirstlane(selected_nth(masks, slot));
     const uint64_t hit = __ballot(lane < a.k && sel == e);
     if (lane == 0) {
@@ -600,26 +600,39 @@ __global__ __launch_bounds__(512) void down1_kernel(const Down1Args a) {
   }
 }
 
+template <int BITS, typename XT, typename ST, int UR, int RM>
+static hipError_t launch_gateup1_e(int E, const Decode1Args& a, int grid, hipStream_t st,
+                                   KEvents ev) {
+  if (E <= 64)
+    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, 1>), dim3(grid), dim3(256), 0, st,
+                          ev.start, ev.stop, 0, a);
+  else if (E <= 128)
+    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, 2>), dim3(grid), dim3(256), 0, st,
+                          ev.start, ev.stop, 0, a);
+  else
+    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, kTopkEPL>), dim3(grid), dim3(256), 0,
+                          st, ev.start, ev.stop, 0, a);
+  return hipGetLastError();
+}
+
 template <int BITS, typename XT, typename ST, int UR>
 static hipError_t launch_dec1_u(bool down, int var, const void* args, int grid, size_t smem,
                                 hipStream_t st, KEvents ev) {
+  (void)smem;
   if (!down) {
     const Decode1Args& a = *reinterpret_cast<const Decode1Args*>(args);
     switch (var) {
-      case 1: hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, 1>), dim3(grid), dim3(256), 0, st, ev.start, ev.stop, 0, a); break;
-      case 2: hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, 2>), dim3(grid), dim3(256), 0, st, ev.start, ev.stop, 0, a); break;
-      case 3: hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, 3>), dim3(grid), dim3(256), 0, st, ev.start, ev.stop, 0, a); break;
+      case 1: return launch_gateup1_e<BITS, XT, ST, UR, 1>(a.E, a, grid, st, ev);
+      case 2: return launch_gateup1_e<BITS, XT, ST, UR, 2>(a.E, a, grid, st, ev);
       default: return hipErrorInvalidValue;
     }
-  } else {
-    const Down1Args& a = *reinterpret_cast<const Down1Args*>(args);
-    const dim3 block(64 * a.k);
-    switch (var) {
-      case 1: hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, 1>), dim3(grid), block, 0, st, ev.start, ev.stop, 0, a); break;
-      case 2: hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, 2>), dim3(grid), block, 0, st, ev.start, ev.stop, 0, a); break;
-      case 3: hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, 3>), dim3(grid), block, 0, st, ev.start, ev.stop, 0, a); break;
-      default: return hipErrorInvalidValue;
-    }
+  }
+  const Down1Args& a = *reinterpret_cast<const Down1Args*>(args);
+  const dim3 block(64 * a.k);
+  switch (var) {
+    case 1: hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, 1>), dim3(grid), block, 0, st, ev.start, ev.stop, 0, a); break;
+    case 2: hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, 2>), dim3(grid), block, 0, st, ev.start, ev.stop, 0, a); break;
+    default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
@@ -636,7 +649,7 @@ static hipError_t launch_dec1_t(bool down, int var, int ur, const void* args, in
   return hipErrorInvalidValue;
 }
 
-// var: rows per lane (1..3).
+// var: rows per lane (1..kDec1MaxRows).
 template <int BITS>
 static hipError_t launch_dec1_bits(int xdt, int sbdt, bool down, int var, int ur, const void* args,
                                    int grid, size_t smem, hipStream_t st, KEvents ev = {}) {

@@ -156,18 +156,20 @@ constexpr int kTopkEPL = kTopkMaxE / 64; // logits held per lane
 // on one lane with det_expf, so the results are reproducible bit for bit.
 // sc: this wave's LDS scratch of at least E floats (full-softmax mode).
 // masks (nullable): wave-uniform selection bitmaps, bit l of masks[j] set
-// iff expert 64 j + l was selected.
-template <typename XT>
+// iff expert 64 j + l was selected (kTopkEPL entries). EPL: logits per lane,
+// a compile-time bound on E (E <= 64 EPL) that removes the per-slot range
+// checks from the k selection rounds.
+template <typename XT, int EPL = kTopkEPL>
 __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, int norm,
                           const float* __restrict__ ebias, float* sc, bool want_weights,
                           int* sel, float* w, uint64_t* masks = nullptr) {
   const int lane = threadIdx.x & 63;
   const bool on_logits = (gating == 1) || (norm && ebias == nullptr);
   const float NEG = -__builtin_huge_valf();
-  float v[kTopkEPL];
+  float v[EPL];
   float m = NEG;
 #pragma unroll
-  for (int j = 0; j < kTopkEPL; j++) {
+  for (int j = 0; j < EPL; j++) {
     const int i = lane + 64 * j;
     v[j] = NEG;
     if (j * 64 < E) {  // wave-uniform; the load itself is clamped, not branched
@@ -180,7 +182,7 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
     // full softmax (+ expert bias): MoELayer.swift:174-195
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
 #pragma unroll
-    for (int j = 0; j < kTopkEPL; j++) {
+    for (int j = 0; j < EPL; j++) {
       const int i = lane + 64 * j;
       if (i < E) {
         v[j] = det_expf(v[j] - m);
@@ -193,7 +195,7 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
       for (int i = 0; i < E; i++) s += sc[i];
     s = __shfl(s, 0, 64);
 #pragma unroll
-    for (int j = 0; j < kTopkEPL; j++) {
+    for (int j = 0; j < EPL; j++) {
       const int i = lane + 64 * j;
       if (i < E) {
         v[j] = (s > 0.f) ? v[j] / s : 1.0f / (float)E;
@@ -206,9 +208,9 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
   // of a wave argmax over integer keys: the largest remaining key by a DPP
   // max, the smallest index holding it by ballots (index = lane + 64 j).
   constexpr int NONE = (int)0x80000000;  // below the key of -inf
-  int key[kTopkEPL];
+  int key[EPL];
 #pragma unroll
-  for (int j = 0; j < kTopkEPL; j++) {
+  for (int j = 0; j < EPL; j++) {
     const bool ok = (j * 64 < E) && (lane + 64 * j < E);
     key[j] = ok ? f32_key(v[j] != v[j] ? NEG : v[j]) : NONE;
   }
@@ -217,12 +219,12 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
   for (int r = 0; r < k; r++) {
     int bk = key[0];
 #pragma unroll
-    for (int j = 1; j < kTopkEPL; j++)
+    for (int j = 1; j < EPL; j++)
       if (j * 64 < E) bk = max(bk, key[j]);
     const int mk = wave_max_i32(bk);
     int win = 0;
 #pragma unroll
-    for (int j = 0; j < kTopkEPL; j++) {
+    for (int j = 0; j < EPL; j++) {
       if (j * 64 < E) {
         const uint64_t b = __ballot(key[j] == mk);
         if (b) {
@@ -235,7 +237,7 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
     const int wj = win >> 6;
     const bool mine = (win & 63) == lane;
 #pragma unroll
-    for (int j = 0; j < kTopkEPL; j++) {
+    for (int j = 0; j < EPL; j++) {
       if (j == wj && mine) {
         key[j] = NONE;
         taken |= 1u << j;
@@ -249,7 +251,7 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
   const float my_val = key_f32(my_key);
   if (masks) {
 #pragma unroll
-    for (int j = 0; j < kTopkEPL; j++) masks[j] = (j * 64 < E) ? __ballot((taken >> j) & 1u) : 0ull;
+    for (int j = 0; j < kTopkEPL; j++) masks[j] = (j < EPL && j * 64 < E) ? __ballot((taken >> j) & 1u) : 0ull;
   }
   *sel = my_sel;
   if (!want_weights) return;

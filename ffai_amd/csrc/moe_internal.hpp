@@ -78,7 +78,7 @@ struct Down1Args {
 // expert (down) and each lane holds at most kDec1MaxRows rows of at most 4
 // units each.
 constexpr int kDec1MaxK = 8;
-constexpr int kDec1MaxRows = 3;
+constexpr int kDec1MaxRows = 2;
 
 // rm: rows per lane (rows_per_block = rm * 4 * SG for gate/up, rm * SG for
 // down).
