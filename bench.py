@@ -136,6 +136,18 @@ def proj_bytes(p, experts):
     return experts * (n * k * p.bits // 8 + 2 * n * (k // p.group_size) * sb)
 
 
+def measured_traffic(workload, T):
+    """HBM bytes per launch of the dominant kernel from the committed FETCH_SIZE
+    / WRITE_SIZE passes (profiles/<workload>_traffic.json), or None."""
+    path = os.path.join(ROOT, "profiles", f"{workload}_traffic.json")
+    if T != 1 or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        data = json.load(f)
+    k = data.get("kernels", {}).get("gateup1_kernel")
+    return None if k is None else k["hbm_bytes"]
+
+
 # ------------------------------------------------------------ CPU oracle --
 def cpu_baseline(layer, cfg, torch, budget_s=12.0):
     """Times the C oracle (oracle/) on layer 0, one token per call."""
@@ -200,6 +212,9 @@ def main():
     ap.add_argument("--batch", type=int, default=None, help="tokens per step (overrides config)")
     ap.add_argument("--layers", type=int, default=24, help="resident layers rotated per step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run 10 plain device copies of BYTES each (calibrates the "
+                         "FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -209,6 +224,15 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_probe:
+        n = args.copy_probe // 4
+        src = torch.ones(n, dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: 10 copies of {n * 4} bytes")
+        return
     from ffai_amd import _lib as lib
     from ffai_amd import layer as fl
 
@@ -306,7 +330,7 @@ def main():
         roof = dict(bound="mfma", achieved=round(gu_flops / (gu_us * 1e-6) / 1e12, 2),
                     peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s")
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
-    roof["traffic"] = None
+    roof["traffic"] = measured_traffic(cfg["workload"], T)
     # the library's path choice: MFMA GEMM once used experts average >= 32 rows
     gemm_path = T > 1 and M >= 32 * min(cfg["E"], M) and cfg["H"] % 64 == 0 and cfg["I"] % 64 == 0
     roof["kernel"] = ("gateup1_kernel (one-token gate/up with routing)" if T == 1 else
