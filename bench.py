@@ -323,8 +323,9 @@ def main():
     dn_bytes = proj_bytes(lay0.down, U) + T * cfg["k"] * cfg["I"] * 2 + T * cfg["H"] * 2
     M = T * cfg["k"]
     gu_flops = 2.0 * M * 2 * cfg["H"] * cfg["I"]
+    k_bytes = gu_bytes
     if T <= 64:
-        roof = dict(bound="hbm", achieved=round(gu_bytes / (gu_us * 1e-6) / 1e9, 1),
+        roof = dict(bound="hbm", achieved=round(k_bytes / (gu_us * 1e-6) / 1e9, 1),
                     peak=HBM_PEAK_GBS, unit="GB/s")
     else:
         roof = dict(bound="mfma", achieved=round(gu_flops / (gu_us * 1e-6) / 1e12, 2),
@@ -337,9 +338,9 @@ def main():
                       "gemm_grouped_kernel (MFMA gate/up over the expert row tiles)" if gemm_path else
                       "gemv_grouped_kernel (routed gate/up over the dispatch plan)")
     roof["avg_us"] = round(gu_us, 3)
-    roof["algorithmic_bytes"] = gu_bytes
-    log(f"gate/up kernel {gu_us:.2f} us ({gu_bytes / 1e6:.2f} MB, "
-        f"{gu_bytes / (gu_us * 1e-6) / 1e9:.0f} GB/s); down+combine {dn_us:.2f} us "
+    roof["algorithmic_bytes"] = k_bytes
+    log(f"gate/up kernel {gu_us:.2f} us ({k_bytes / 1e6:.2f} MB, "
+        f"{k_bytes / (gu_us * 1e-6) / 1e9:.0f} GB/s); down+combine {dn_us:.2f} us "
         f"({dn_bytes / 1e6:.2f} MB, {dn_bytes / (dn_us * 1e-6) / 1e9:.0f} GB/s); U={U}")
 
     cpu = None

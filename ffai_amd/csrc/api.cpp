@@ -31,6 +31,7 @@ hipError_t launch_dec1_b5(int, int, bool, int, int, const void*, int, size_t, hi
 hipError_t launch_dec1_b6(int, int, bool, int, int, const void*, int, size_t, hipStream_t, KEvents);
 hipError_t launch_dec1_b8(int, int, bool, int, int, const void*, int, size_t, hipStream_t, KEvents);
 
+
 hipError_t launch_gemm_b2(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
 hipError_t launch_gemm_b3(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
 hipError_t launch_gemm_b4(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
@@ -776,6 +777,28 @@ bool dec1_supported(const moe_layer_desc* d) {
   return true;
 }
 
+// down projection + weighted combine of one token (down1_kernel).
+moe_status run_down1(const moe_layer_desc* d, void* y, const uint32_t* idx, const float* w,
+                     const void* act, hipStream_t st, KEvents ev) {
+  const int k = d->top_k, H = d->hidden, I = d->intermediate;
+  const Dec1Geom dg = dec1_geom(H, I, group_shift(d->down.group_size), k, true);
+  Down1Args dn{};
+  dn.idx = idx;
+  dn.w = w;
+  dn.act = act;
+  dn.p = to_proj(d->down);
+  dn.out = y;
+  dn.k = k;
+  dn.N = H;
+  dn.K = I;
+  dn.gsh = group_shift(d->down.group_size);
+  dn.lg = dg.lg;
+  dn.rows_per_block = dg.rows_per_block;
+  MOE_HIP(launch_down1(d->down.bits, d->act_dtype, d->down.sb_dtype, dn, dg.rm, dg.grid, st, ev),
+          "down+combine decode launch");
+  return MOE_OK;
+}
+
 moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y, void* ws,
                          size_t ws_bytes, const moe_layer_trace* tr, hipStream_t st) {
   MOE_TRY(validate_layer_impl(d));
@@ -839,21 +862,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y,
     MOE_HIP(launch_gateup1(d->gate.bits, xdt, d->gate.sb_dtype, g, gg.rm, gg.grid, st, kev(0)),
             "gate/up decode launch");
     MOE_TRY(shared_expert(d, x, T, ws, w, st, &smode));
-    const Dec1Geom dg = dec1_geom(H, I, group_shift(d->down.group_size), k, true);
-    Down1Args dn{};
-    dn.idx = g.idx;
-    dn.w = g.w;
-    dn.act = g.act;
-    dn.p = to_proj(d->down);
-    dn.out = y;
-    dn.k = k;
-    dn.N = H;
-    dn.K = I;
-    dn.gsh = group_shift(d->down.group_size);
-    dn.lg = dg.lg;
-    dn.rows_per_block = dg.rows_per_block;
-    MOE_HIP(launch_down1(d->down.bits, xdt, d->down.sb_dtype, dn, dg.rm, dg.grid, st, kev(1)),
-            "down+combine decode launch");
+    MOE_TRY(run_down1(d, y, g.idx, g.w, g.act, st, kev(1)));
     if (smode)
       MOE_HIP(launch_add_shared(y, at<void>(ws, w.s_out), at<void>(ws, w.s_logit), smode, T, H, xdt,
                                 st),

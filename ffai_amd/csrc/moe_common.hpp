@@ -216,6 +216,7 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
   }
   uint32_t taken = 0;
   int my_sel = 0, my_key = NONE;
+  float my_raw = NEG;  // the selected value as stored (NaN kept), lane r < k
   for (int r = 0; r < k; r++) {
     int bk = key[0];
 #pragma unroll
@@ -236,6 +237,10 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
     win = __builtin_amdgcn_readfirstlane(win);
     const int wj = win >> 6;
     const bool mine = (win & 63) == lane;
+    float rv = v[0];
+#pragma unroll
+    for (int j = 1; j < EPL; j++) rv = (j == wj) ? v[j] : rv;
+    rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rv), win & 63));
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
       if (j == wj && mine) {
@@ -246,6 +251,7 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
     if (lane == r) {
       my_sel = win;
       my_key = mk;
+      my_raw = rv;
     }
   }
   const float my_val = key_f32(my_key);
@@ -259,8 +265,8 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
   float wv;
   if (on_logits) {
     // softmax over the k picked raw logits — MoELayer.swift:166-172,197-203
-    const float lraw = to_f<XT>(row[my_sel]);
-    const float lv = (lane < k) ? lraw : NEG;
+    // (the values travelled with the selection: no second read of the row)
+    const float lv = (lane < k) ? my_raw : NEG;
     float mx = lv;
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
     const float ex = (lane < k) ? det_expf(lv - mx) : 0.f;
@@ -486,6 +492,18 @@ template <int BITS, typename XT> struct Magic {
   static constexpr uint32_t bits = !dot2 ? 0u : (__is_same(XT, bf16_t) ? 0x43004300u : 0x64006400u);
   static constexpr float value = !dot2 ? 0.0f : (__is_same(XT, bf16_t) ? 128.0f : 1024.0f);
 };
+
+// a.lo b.lo + a.hi b.hi + c for two packed 16-bit pairs of type T
+// (v_dot2_f32_bf16 / v_dot2_f32_f16).
+template <typename T>
+__device__ __forceinline__ float dot2_16(uint32_t a, uint32_t b, float c) {
+  if constexpr (__is_same(T, bf16_t))
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c,
+                                  false);
+}
 
 // x16: the unit's 32 activations in pair order, as 16 u32 (16-bit types);
 // cp: code pairs from unpack_pairs<BITS, Magic<BITS, XT>::bits>.

@@ -79,6 +79,7 @@ struct Down1Args {
 // units each.
 constexpr int kDec1MaxK = 8;
 constexpr int kDec1MaxRows = 2;
+constexpr int kDec1MaxHidden = 8192;  // activation row staged in LDS
 
 // rm: rows per lane (rows_per_block = rm * 4 * SG for gate/up, rm * SG for
 // down).

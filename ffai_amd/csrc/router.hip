@@ -37,6 +37,8 @@ __device__ __forceinline__ void bload8(rsrc_t r, uint32_t off, float (&v)[8]) {
 // (expert, chunk of up to 8 tokens); lane l takes the 8-element chunks
 // l + 64 j, j < NL, of the hidden dimension (NL * 512 >= H; chunks past H
 // read zeros), so the whole weight row is requested in one round trip.
+// Weights and activations of one 16-bit type multiply pairwise with v_dot2
+// (fp32 accumulate) in chunk order; other type pairs use fp32 fma.
 template <typename XT, typename WT, int NL>
 __global__ __launch_bounds__(256) void router_logits_kernel(const XT* __restrict__ x,
                                                             const WT* __restrict__ W,
@@ -51,23 +53,43 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT* __restrict
   const int t0 = tc * 8, nt = min(8, T - t0);
   const float bv = bias ? to_f<XT>(bias[e]) : 0.f;  // issued before the row loads
   const rsrc_t wr = make_rsrc(W + (size_t)e * H, (uint32_t)(H * sizeof(WT)));
-  float wv[NL][8];
-#pragma unroll
-  for (int j = 0; j < NL; j++) bload8<WT>(wr, (uint32_t)((lane + 64 * j) * 8 * sizeof(WT)), wv[j]);
   float acc[8];
+  if constexpr (__is_same(XT, WT) && !__is_same(XT, float)) {
+    u32x4_t wv[NL];
 #pragma unroll
-  for (int t = 0; t < 8; t++) {
-    acc[t] = 0.f;
-    if (t < nt) {  // wave-uniform
-      const rsrc_t xr = make_rsrc(x + (size_t)(t0 + t) * H, (uint32_t)(H * sizeof(XT)));
+    for (int j = 0; j < NL; j++) wv[j] = bload128(wr, (uint32_t)((lane + 64 * j) * 16));
 #pragma unroll
-      for (int j = 0; j < NL; j++) {
-        float xv[8];
-        bload8<XT>(xr, (uint32_t)((lane + 64 * j) * 8 * sizeof(XT)), xv);
+    for (int t = 0; t < 8; t++) {
+      acc[t] = 0.f;
+      if (t < nt) {  // wave-uniform
+        const rsrc_t xr = make_rsrc(x + (size_t)(t0 + t) * H, (uint32_t)(H * sizeof(XT)));
 #pragma unroll
-        for (int i = 0; i < 8; i++) acc[t] = __builtin_fmaf(wv[j][i], xv[i], acc[t]);
+        for (int j = 0; j < NL; j++) {
+          const u32x4_t xv = bload128(xr, (uint32_t)((lane + 64 * j) * 16));
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[t] = dot2_16<XT>(wv[j][i], xv[i], acc[t]);
+        }
+        acc[t] = group_sum(acc[t], 6);
       }
-      acc[t] = group_sum(acc[t], 6);
+    }
+  } else {
+    float wv[NL][8];
+#pragma unroll
+    for (int j = 0; j < NL; j++) bload8<WT>(wr, (uint32_t)((lane + 64 * j) * 8 * sizeof(WT)), wv[j]);
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      acc[t] = 0.f;
+      if (t < nt) {  // wave-uniform
+        const rsrc_t xr = make_rsrc(x + (size_t)(t0 + t) * H, (uint32_t)(H * sizeof(XT)));
+#pragma unroll
+        for (int j = 0; j < NL; j++) {
+          float xv[8];
+          bload8<XT>(xr, (uint32_t)((lane + 64 * j) * 8 * sizeof(XT)), xv);
+#pragma unroll
+          for (int i = 0; i < 8; i++) acc[t] = __builtin_fmaf(wv[j][i], xv[i], acc[t]);
+        }
+        acc[t] = group_sum(acc[t], 6);
+      }
     }
   }
   if (lane == 63) {
