@@ -415,12 +415,14 @@ moe_status run_gemv(const moe_qproj& p0, const moe_qproj* p1, const void* x, int
 // GEMV, which reads every weight once per 8 rows, is faster.
 constexpr int kGemmMinRows = 32;
 
-bool gemm_ok(const moe_qproj& p, int xdt, int M) {
+// The matrix-core GEMM writes whole 16-byte groups of an output row: N is a
+// multiple of 8 and the output 16-byte aligned (workspace buffers always are).
+bool gemm_ok(const moe_qproj& p, int xdt, int M, const void* out = nullptr) {
   const int slots = std::min(p.n_experts, M);
   // activation rows are addressed with 32-bit byte offsets
   const bool fits = (size_t)M * (size_t)p.k * 2 < (1ull << 32);
-  return xdt != MOE_F32 && p.k % 64 == 0 && p.n_experts <= 1024 && fits &&
-         M >= kGemmMinRows * slots;
+  return xdt != MOE_F32 && p.k % 64 == 0 && p.n % 8 == 0 && p.n_experts <= 1024 && fits &&
+         M >= kGemmMinRows * slots && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
 }
 
 // Router logits on the matrix cores for many tokens: a one-expert plan over
@@ -428,7 +430,7 @@ bool gemm_ok(const moe_qproj& p, int xdt, int M) {
 // as in router_logits_kernel.
 bool router_gemm_ok(const moe_layer_desc* d, int T) {
   return T >= kGemmMinRows && d->act_dtype != MOE_F32 && d->router_dtype == d->act_dtype &&
-         d->hidden % 64 == 0 && (size_t)T * d->hidden * 2 < (1ull << 32);
+         d->hidden % 64 == 0 && d->n_experts % 8 == 0 && (size_t)T * d->hidden * 2 < (1ull << 32);
 }
 
 moe_status run_router_gemm(const moe_layer_desc* d, const void* x, int T, void* logits,
@@ -611,7 +613,7 @@ extern "C" moe_status moe_expert_matmul(const moe_qproj* p, const void* a, int32
   const size_t need = moe_expert_matmul_workspace_bytes(p->n_experts, M);
   if (!workspace || workspace_bytes < need)
     return fail(MOE_ERR_WORKSPACE, "expert_matmul: workspace of %zu bytes needed", need);
-  if (gemm_ok(*p, a_dtype, M)) {
+  if (gemm_ok(*p, a_dtype, M, out)) {
     uint32_t* tiles = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(workspace) +
                                                   align_up((size_t)(p->n_experts + 1) * 4, 256));
     MOE_HIP(launch_gemm_tiles(offsets, p->n_experts, kGemmRows, tiles, stream), "tile list launch");

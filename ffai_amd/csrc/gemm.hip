@@ -10,19 +10,17 @@
 //   single:   out[p, n] = round(W[e(p)][n] . a[p])
 // over the expert-sorted positions p of a dispatch plan.
 //
-// Work: a tile list of (expert, 128 consecutive sorted positions); block =
-// one tile x one column slice. The block stages the tile's 128 activation
-// rows, 64 values at a time, in LDS (padded rows, double-buffered); every
-// wave owns 32 output columns for one or two weight matrices and all 128
-// rows (4 x v_mfma_f32_32x32x16 tiles per matrix). A wave dequantises its
-// weight fragments straight from HBM into the MFMA B-operand registers, so
-// each weight value is converted exactly once per tile and no LDS traffic is
-// spent on weights: codes -> fp32 (exact) -> s*q + b (fp32) -> bf16 / f16.
+// Work: a tile list of (expert, 256 consecutive sorted positions); block =
+// one tile x one column slice (256 weight rows). Per 64-value chunk of K the
+// block stages the tile's activation rows and the slice's weights,
+// dequantised once per block to the MFMA operand type, in double-buffered
+// LDS; 8 waves multiply with v_mfma_f32_32x32x16 (see the kernel comment).
+// Dequantisation: codes -> fp32 (exact) -> s*q + b (fp32) -> bf16 / f16.
 //
 // K order inside a 64-value chunk: lane half h of the wave takes values
-// [32h, 32h + 32) — one whole 32-value unit, a single contiguous load — and
-// step s (0..3) of the 16-deep MFMA reduction feeds values 32h + 8s + e,
-// e < 8; the A fragments are read from LDS in the same order.
+// [32h, 32h + 32) — one whole 32-value unit — and step s (0..3) of the
+// 16-deep MFMA reduction feeds values 16 s + 8 h + e, e < 8 (LDS chunk
+// 2 s + h of the row); A and B fragments are read in the same order.
 #include <hip/hip_ext.h>
 
 #include "moe_common.hpp"
@@ -313,21 +311,27 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
   }
 
   // epilogue: lane holds column col, rows 8 (r / 4) + 4 h + r % 4 of each
-  // 32 x 32 tile
+  // 32 x 32 tile. The wave's finished outputs (64 rows x OC columns) go
+  // through LDS (free after the last barrier) so that the global stores are
+  // 16 contiguous bytes of one output row per lane instead of 2-byte stores.
   XT* out = reinterpret_cast<XT*>(a.out);
   const XT* ob0 = reinterpret_cast<const XT*>(a.p0.ob);
   const XT* ob1 = reinterpret_cast<const XT*>(GATEUP ? a.p1.ob : a.p0.ob);
+  constexpr int OC = GATEUP ? 64 : 128;  // output columns per wave
+  const int cbase = GATEUP ? bn * 128 + 64 * wn : bn * 256 + 128 * wn;
+  const uint32_t prow0 = m0 + (uint32_t)(64 * wm);
+  // 8 waves x 64 x OC 16-bit values: As holds waves 0-3, Bs waves 4-7
+  XT* wt = reinterpret_cast<XT*>(wave < 4 ? &As[0][0] : &Bs[0][0]) + (wave & 3) * 64 * OC;
 #pragma unroll
   for (int j = 0; j < (GATEUP ? 2 : 4); j++) {
-    const int cn = GATEUP ? bn * 128 + 64 * wn + 32 * j + col : bn * 256 + 128 * wn + 32 * j + col;
+    const int cn = cbase + 32 * j + col;
     const float obg = (ob0 && cn < N) ? to_f<XT>(ob0[(size_t)e * N + cn]) : 0.f;
     const float obu = (GATEUP && ob1 && cn < N) ? to_f<XT>(ob1[(size_t)e * N + cn]) : 0.f;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const uint32_t p = m0 + (uint32_t)(64 * wm + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3));
-        if (p >= pend || cn >= N) continue;
+        const int row = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
         float v = round_to<XT>(acc[i][j][r]);
         if (ob0) v = round_to<XT>(v + obg);
         if constexpr (GATEUP) {
@@ -335,9 +339,22 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
           if (ob1) u = round_to<XT>(u + obu);
           v = apply_act(v, u, a.act, a.alpha, a.limit);
         }
-        out[(size_t)p * N + cn] = from_f<XT>(v);
+        wt[row * OC + 32 * j + col] = from_f<XT>(v);
       }
     }
+  }
+  // each lane: 16 bytes (8 columns) of one row per step; the wave reads only
+  // its own region, so no block barrier is needed
+  constexpr int C8 = OC / 8;
+#pragma unroll
+  for (int t = 0; t < 64 * C8 / 64; t++) {
+    const int q = 64 * t + lane;
+    const int row = q / C8, c8 = q - row * C8;
+    const uint32_t p = prow0 + (uint32_t)row;
+    const int cn0 = cbase + 8 * c8;
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(wt + row * OC + 8 * c8);
+    if (p < pend && cn0 < N)  // N % 8 == 0 (host check): whole 16-byte groups
+      *reinterpret_cast<u32x4_t*>(out + (size_t)p * N + cn0) = v;
   }
 }
 

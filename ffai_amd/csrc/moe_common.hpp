@@ -287,14 +287,16 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
 // ------------------------------------------------------------ activations --
 enum { ACT_SWIGLU = 0, ACT_GPTOSS = 1 };
 
+// The logistic uses the hardware reciprocal (v_rcp_f32, 1 ulp) in place of an
+// IEEE divide: the result is rounded to a 16-bit storage type right after.
 __device__ __forceinline__ float apply_act(float g, float u, int act, float alpha, float limit) {
   if (act == ACT_GPTOSS) {
     g = fminf(g, limit);
     u = fminf(fmaxf(u, -limit), limit);
-    float glu = g / (1.0f + __expf(-alpha * g));
+    const float glu = g * __builtin_amdgcn_rcpf(1.0f + __expf(-alpha * g));
     return glu * (u + 1.0f);
   }
-  return g / (1.0f + __expf(-g)) * u;
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }
 
 // ------------------------------------------------------ affine bit stream --
