@@ -15,16 +15,17 @@ LIB_PATH = os.path.join(_HERE, "libmoehip.so")
 
 MOE_OK, MOE_ERR_INVALID, MOE_ERR_UNSUPPORTED, MOE_ERR_WORKSPACE, MOE_ERR_HIP = range(5)
 MOE_F32, MOE_F16, MOE_BF16 = 0, 1, 2
-MOE_SOFTMAX_THEN_TOPK, MOE_TOPK_THEN_SOFTMAX = 0, 1
-MOE_ACT_SWIGLU, MOE_ACT_GPTOSS = 0, 1
+MOE_SOFTMAX_THEN_TOPK, MOE_TOPK_THEN_SOFTMAX, MOE_SIGMOID_TOPK = 0, 1, 2
+MOE_ACT_SWIGLU, MOE_ACT_GPTOSS, MOE_ACT_GEGLU, MOE_ACT_RELU2 = 0, 1, 2, 3
 
 EXPORTS = [
     "moe_last_error_string", "moe_version", "moe_validate_qproj", "moe_validate_layer",
-    "moe_derive_bits", "moe_router_logits", "moe_router_topk", "moe_dispatch_workspace_bytes",
+    "moe_derive_bits", "moe_router_logits", "moe_router_topk", "moe_router_topk_scaled",
+    "moe_dispatch_workspace_bytes",
     "moe_dispatch_plan", "moe_dequantize_affine", "moe_expert_matmul_workspace_bytes",
     "moe_expert_matmul", "moe_activation_apply", "moe_unpermute", "moe_layer_workspace_bytes",
-    "moe_layer_forward", "moe_layer_create", "moe_layer_destroy", "moe_layer_decode",
-    "moe_layer_decode_many",
+    "moe_layer_forward", "moe_layer_forward_routed", "moe_layer_create", "moe_layer_destroy",
+    "moe_layer_decode", "moe_layer_decode_many",
 ]
 
 
@@ -54,6 +55,7 @@ class LayerDesc(C.Structure):
         ("has_shared", C.c_int32),
         ("shared_gate", QProj), ("shared_up", QProj), ("shared_down", QProj),
         ("shared_gate_weight", C.c_void_p),
+        ("logit_scale", C.c_float), ("routed_scale", C.c_float), ("expert_scale", C.c_void_p),
     ]
 
 
@@ -84,6 +86,8 @@ def load():
     lib.moe_derive_bits.argtypes = [C.c_int64, C.c_int64, i32, C.POINTER(i32)]
     lib.moe_router_logits.argtypes = [vp, i32, i32, i32, vp, i32, vp, i32, vp, st]
     lib.moe_router_topk.argtypes = [vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, st]
+    lib.moe_router_topk_scaled.argtypes = [vp, i32, i32, i32, i32, i32, i32, vp, C.c_float,
+                                           C.c_float, vp, vp, vp, st]
     lib.moe_dispatch_workspace_bytes.argtypes = [i32, i32, i32]
     lib.moe_dispatch_workspace_bytes.restype = sz
     lib.moe_dispatch_plan.argtypes = [vp, i32, i32, i32, vp, vp, vp, vp, vp, sz, st]
@@ -97,15 +101,18 @@ def load():
     lib.moe_layer_workspace_bytes.restype = sz
     lib.moe_layer_forward.argtypes = [C.POINTER(LayerDesc), vp, i32, vp, vp, sz,
                                       C.POINTER(LayerTrace), st]
+    lib.moe_layer_forward_routed.argtypes = [C.POINTER(LayerDesc), vp, vp, i32, vp, vp, sz,
+                                             C.POINTER(LayerTrace), st]
     lib.moe_layer_create.argtypes = [C.POINTER(LayerDesc), C.POINTER(vp)]
     lib.moe_layer_destroy.argtypes = [vp]
     lib.moe_layer_destroy.restype = None
     lib.moe_layer_decode.argtypes = [vp, vp, vp, st]
     lib.moe_layer_decode_many.argtypes = [vp, vp, i32, vp, st]
     for name in ["moe_validate_qproj", "moe_validate_layer", "moe_derive_bits", "moe_router_logits",
-                 "moe_router_topk", "moe_dispatch_plan", "moe_dequantize_affine",
-                 "moe_expert_matmul", "moe_activation_apply", "moe_unpermute",
-                 "moe_layer_forward", "moe_layer_create", "moe_layer_decode",
+                 "moe_router_topk", "moe_router_topk_scaled", "moe_dispatch_plan",
+                 "moe_dequantize_affine", "moe_expert_matmul", "moe_activation_apply",
+                 "moe_unpermute", "moe_layer_forward", "moe_layer_forward_routed",
+                 "moe_layer_create", "moe_layer_decode",
                  "moe_layer_decode_many"]:
         getattr(lib, name).restype = C.c_int
     _lib = lib

@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cmath>
 #include <cstring>
 #include <new>
 #include <string>
@@ -147,6 +148,33 @@ bool pair_ok(int xdt, int sbdt) {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+bool gating_ok(int g) {
+  return g == MOE_SOFTMAX_THEN_TOPK || g == MOE_TOPK_THEN_SOFTMAX || g == MOE_SIGMOID_TOPK;
+}
+bool act_ok(int a) {
+  return a == MOE_ACT_SWIGLU || a == MOE_ACT_GPTOSS || a == MOE_ACT_GEGLU || a == MOE_ACT_RELU2;
+}
+bool scales_ok(float logit_scale, float routed_scale) {
+  return std::isfinite(logit_scale) && std::isfinite(routed_scale);
+}
+
+// Routing options of the device router; a zero scale reads as 1.0.
+RouteOpts route_opts(int gating, int norm, const float* ebias, float logit_scale,
+                     float routed_scale, const float* escale) {
+  RouteOpts r{};
+  r.gating = gating;
+  r.norm = norm;
+  r.ebias = ebias;
+  r.logit_scale = logit_scale == 0.f ? 1.f : logit_scale;
+  r.routed_scale = routed_scale == 0.f ? 1.f : routed_scale;
+  r.escale = escale;
+  return r;
+}
+RouteOpts route_opts(const moe_layer_desc* d) {
+  return route_opts(d->gating, d->norm_topk_prob, d->expert_bias, d->logit_scale, d->routed_scale,
+                    d->expert_scale);
+}
+
 moe_status validate_qproj_named(const moe_qproj* p, const char* name) {
   if (!p) return fail(MOE_ERR_INVALID, "%s: descriptor is NULL", name);
   if (!p->weight || !p->scales || !p->biases)
@@ -221,15 +249,20 @@ moe_status validate_layer_impl(const moe_layer_desc* d) {
   if (!dt_ok(d->act_dtype) || !dt_ok(d->router_dtype))
     return fail(MOE_ERR_INVALID, "MoELayer: bad dtype");
   if (!d->router_weight) return fail(MOE_ERR_INVALID, "MoELayer: router weight is NULL");
-  if (d->gating != MOE_SOFTMAX_THEN_TOPK && d->gating != MOE_TOPK_THEN_SOFTMAX)
-    return fail(MOE_ERR_INVALID, "MoERouter: bad gating mode %d", d->gating);
-  if (d->activation != MOE_ACT_SWIGLU && d->activation != MOE_ACT_GPTOSS)
+  if (!gating_ok(d->gating)) return fail(MOE_ERR_INVALID, "MoERouter: bad gating mode %d", d->gating);
+  if (!act_ok(d->activation))
     return fail(MOE_ERR_INVALID, "MoELayer: bad activation %d", d->activation);
-  MOE_TRY(validate_qproj_named(&d->gate, "gate_proj"));
+  if (!scales_ok(d->logit_scale, d->routed_scale))
+    return fail(MOE_ERR_INVALID, "MoERouter: logit/routed scales must be finite");
+  // squared-ReLU experts have no gate projection (NemotronHText.swift:756-761)
+  const bool gated = d->activation != MOE_ACT_RELU2;
+  if (!gated && (d->gate.weight || (d->has_shared && d->shared_gate.weight)))
+    return fail(MOE_ERR_INVALID, "MoELayer: squared-ReLU experts take no gate projection");
+  if (gated) MOE_TRY(validate_qproj_named(&d->gate, "gate_proj"));
   MOE_TRY(validate_qproj_named(&d->up, "up_proj"));
   MOE_TRY(validate_qproj_named(&d->down, "down_proj"));
-  const moe_qproj* g = &d->gate;
   const moe_qproj* u = &d->up;
+  const moe_qproj* g = gated ? &d->gate : u;
   const moe_qproj* dn = &d->down;
   if (g->n_experts != d->n_experts || u->n_experts != d->n_experts || dn->n_experts != d->n_experts)
     return fail(MOE_ERR_INVALID, "MoELayer: gate/up/down expert counts must equal nExperts (%d)",
@@ -250,11 +283,11 @@ moe_status validate_layer_impl(const moe_layer_desc* d) {
     return fail(MOE_ERR_UNSUPPORTED, "MoELayer: nExperts=%d above %d", d->n_experts, kMaxExperts);
   if (d->top_k > 64) return fail(MOE_ERR_UNSUPPORTED, "MoELayer: topK=%d above 64", d->top_k);
   if (d->has_shared) {
-    MOE_TRY(validate_qproj_named(&d->shared_gate, "shared_expert.gate_proj"));
+    if (gated) MOE_TRY(validate_qproj_named(&d->shared_gate, "shared_expert.gate_proj"));
     MOE_TRY(validate_qproj_named(&d->shared_up, "shared_expert.up_proj"));
     MOE_TRY(validate_qproj_named(&d->shared_down, "shared_expert.down_proj"));
-    const moe_qproj* sg = &d->shared_gate;
     const moe_qproj* su = &d->shared_up;
+    const moe_qproj* sg = gated ? &d->shared_gate : su;
     const moe_qproj* sd = &d->shared_down;
     if (sg->n_experts != 1 || su->n_experts != 1 || sd->n_experts != 1)
       return fail(MOE_ERR_INVALID, "MoELayer: shared expert projections hold exactly one expert");
@@ -360,7 +393,7 @@ Workspace layout(const moe_layer_desc* d, int T) {
   w.r_plan = take(4 * 4);  // offsets {0, T} and the used list of a one-expert plan
   w.r_tiles = take((1 + 2 * (size_t)gemm_max_tiles(T, 1)) * 4);
   if (d->has_shared) {
-    const size_t SI = (size_t)d->shared_gate.n;
+    const size_t SI = (size_t)d->shared_up.n;
     w.s_off = take(2 * 4);
     w.s_used = take(2 * 4);
     w.s_act = take((size_t)T * SI * ds);
@@ -516,19 +549,31 @@ extern "C" moe_status moe_router_topk(const void* logits, int32_t dtype, int32_t
                                       int32_t n_experts, int32_t k, int32_t gating,
                                       int32_t norm_topk_prob, const float* expert_bias,
                                       uint32_t* topk_idx, float* topk_weight, hipStream_t stream) {
+  return moe_router_topk_scaled(logits, dtype, T, n_experts, k, gating, norm_topk_prob,
+                                expert_bias, 1.f, 1.f, nullptr, topk_idx, topk_weight, stream);
+}
+
+extern "C" moe_status moe_router_topk_scaled(const void* logits, int32_t dtype, int32_t T,
+                                             int32_t n_experts, int32_t k, int32_t gating,
+                                             int32_t norm_topk_prob, const float* expert_bias,
+                                             float logit_scale, float routed_scale,
+                                             const float* expert_scale, uint32_t* topk_idx,
+                                             float* topk_weight, hipStream_t stream) {
   if (!logits || !topk_idx || !topk_weight) return fail(MOE_ERR_INVALID, "router_topk: NULL pointer");
   if (T <= 0) return fail(MOE_ERR_INVALID, "Ops.moeRouterTopKMany: t must be positive");
   if (n_experts <= 0) return fail(MOE_ERR_INVALID, "MoERouter: nExperts must be positive");
   if (k <= 0 || k > n_experts)
     return fail(MOE_ERR_INVALID, "MoERouter: topK (%d) must be in 1...nExperts (%d)", k, n_experts);
-  if (gating != MOE_SOFTMAX_THEN_TOPK && gating != MOE_TOPK_THEN_SOFTMAX)
-    return fail(MOE_ERR_INVALID, "router_topk: bad gating mode");
+  if (!gating_ok(gating)) return fail(MOE_ERR_INVALID, "router_topk: bad gating mode");
+  if (!scales_ok(logit_scale, routed_scale))
+    return fail(MOE_ERR_INVALID, "router_topk: logit/routed scales must be finite");
   if (!dt_ok(dtype)) return fail(MOE_ERR_INVALID, "router_topk: bad dtype");
   if (n_experts > kMaxExperts)
     return fail(MOE_ERR_UNSUPPORTED, "router_topk: nExperts=%d above %d", n_experts, kMaxExperts);
   if (k > 64) return fail(MOE_ERR_UNSUPPORTED, "router_topk: k=%d above 64", k);
-  MOE_HIP(launch_router_topk(logits, dtype, T, n_experts, k, gating, norm_topk_prob, expert_bias,
-                             topk_idx, topk_weight, stream),
+  const RouteOpts ro = route_opts(gating, norm_topk_prob, expert_bias, logit_scale, routed_scale,
+                                  expert_scale);
+  MOE_HIP(launch_router_topk(logits, dtype, T, n_experts, k, ro, topk_idx, topk_weight, stream),
           "router top-k launch");
   return ok();
 }
@@ -632,11 +677,11 @@ extern "C" moe_status moe_expert_matmul(const moe_qproj* p, const void* a, int32
 extern "C" moe_status moe_activation_apply(const void* gate, const void* up, void* out, int64_t n,
                                            int32_t dtype, int32_t activation, float alpha,
                                            float limit, hipStream_t stream) {
-  if (!gate || !up || !out) return fail(MOE_ERR_INVALID, "activation: NULL pointer");
+  if (!up || !out) return fail(MOE_ERR_INVALID, "activation: NULL pointer");
   if (n <= 0) return fail(MOE_ERR_INVALID, "activation: n must be positive");
   if (!dt_ok(dtype)) return fail(MOE_ERR_INVALID, "activation: bad dtype");
-  if (activation != MOE_ACT_SWIGLU && activation != MOE_ACT_GPTOSS)
-    return fail(MOE_ERR_INVALID, "activation: bad kind");
+  if (!act_ok(activation)) return fail(MOE_ERR_INVALID, "activation: bad kind");
+  if (!gate && activation != MOE_ACT_RELU2) return fail(MOE_ERR_INVALID, "activation: NULL gate");
   MOE_HIP(launch_activation(gate, up, out, n, dtype, activation, alpha, limit, stream),
           "activation launch");
   return ok();
@@ -684,9 +729,11 @@ moe_status copy_trace(const moe_layer_desc* d, int T, void* ws, const Workspace&
   return MOE_OK;
 }
 
-// Shared expert (Qwen3xText.swift:928-1104; MoELayer.swift:620-624): gate/up
-// + SwiGLU, down, and the optional sigmoid gate logit, into the workspace.
-// Returns the combine mode: 0 none, 1 unconditional add, 2 sigmoid-gated.
+// Shared expert (Qwen3xText.swift:928-1104; MoELayer.swift:620-624;
+// NemotronHText.swift:855-862): gate/up + the layer's activation (or the
+// single up projection with squared ReLU), down, and the optional sigmoid
+// gate logit, into the workspace. Returns the combine mode: 0 none, 1
+// unconditional add, 2 sigmoid-gated.
 moe_status shared_expert(const moe_layer_desc* d, const void* x, int T, void* ws,
                          const Workspace& w, hipStream_t st, int* smode) {
   *smode = 0;
@@ -696,21 +743,24 @@ moe_status shared_expert(const moe_layer_desc* d, const void* x, int T, void* ws
   *smode = d->shared_gate_weight ? 2 : 1;
   MOE_HIP(launch_identity_plan(at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), T, st),
           "identity plan launch");
-  if (gemm_ok(d->shared_gate, xdt, T) && gemm_ok(d->shared_down, xdt, T)) {
+  const bool gated = d->activation != MOE_ACT_RELU2;
+  const moe_qproj& p0 = gated ? d->shared_gate : d->shared_up;
+  const moe_qproj* p1 = gated ? &d->shared_up : nullptr;
+  if (gemm_ok(p0, xdt, T) && gemm_ok(d->shared_down, xdt, T)) {
     // many tokens through one expert: the matrix-core path
     MOE_HIP(launch_gemm_tiles(at<uint32_t>(ws, w.s_off), 1, kGemmRows, at<uint32_t>(ws, w.s_tiles),
                               st),
             "shared tile list launch");
-    MOE_TRY(run_gemm(d->shared_gate, &d->shared_up, x, xdt, nullptr, 1, at<uint32_t>(ws, w.s_off),
-                     at<uint32_t>(ws, w.s_tiles), T, at<void>(ws, w.s_act), MOE_ACT_SWIGLU, 0.f,
-                     0.f, st));
+    MOE_TRY(run_gemm(p0, p1, x, xdt, nullptr, 1, at<uint32_t>(ws, w.s_off),
+                     at<uint32_t>(ws, w.s_tiles), T, at<void>(ws, w.s_act), d->activation,
+                     d->act_alpha, d->act_limit, st));
     MOE_TRY(run_gemm(d->shared_down, nullptr, at<void>(ws, w.s_act), xdt, nullptr, 1,
                      at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_tiles), T,
                      at<void>(ws, w.s_out), 0, 0.f, 0.f, st));
   } else {
-    MOE_TRY(run_gemv(d->shared_gate, &d->shared_up, x, xdt, nullptr, 1, at<uint32_t>(ws, w.s_off),
+    MOE_TRY(run_gemv(p0, p1, x, xdt, nullptr, 1, at<uint32_t>(ws, w.s_off),
                      at<uint32_t>(ws, w.s_used), 1, T, single, at<void>(ws, w.s_act),
-                     MOE_ACT_SWIGLU, 0.f, 0.f, st));
+                     d->activation, d->act_alpha, d->act_limit, st));
     MOE_TRY(run_gemv(d->shared_down, nullptr, at<void>(ws, w.s_act), xdt, nullptr, 1,
                      at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), 1, T, single,
                      at<void>(ws, w.s_out), 0, 0.f, 0.f, st));
@@ -769,6 +819,7 @@ Dec1Geom dec1_geom(int N, int K, int gsh, int k, bool down) {
 
 bool dec1_supported(const moe_layer_desc* d) {
   if (d->act_dtype == MOE_F32 || d->top_k > kDec1MaxK) return false;
+  if (d->activation == MOE_ACT_RELU2) return false;  // the kernel pairs gate and up rows
   if (d->hidden > 8192 || d->intermediate > 8192) return false;
   // expert-local byte offsets stay below 2^31 (with a row block of slack)
   const moe_qproj* ps[3] = {&d->gate, &d->up, &d->down};
@@ -801,10 +852,11 @@ moe_status run_down1(const moe_layer_desc* d, void* y, const uint32_t* idx, cons
   return MOE_OK;
 }
 
-moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y, void* ws,
-                         size_t ws_bytes, const moe_layer_trace* tr, hipStream_t st) {
+// rx: the router's input rows (x for every family but Gemma 4).
+moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx, int T, void* y,
+                         void* ws, size_t ws_bytes, const moe_layer_trace* tr, hipStream_t st) {
   MOE_TRY(validate_layer_impl(d));
-  if (!x || !y) return fail(MOE_ERR_INVALID, "MoELayer: input/output is NULL");
+  if (!x || !rx || !y) return fail(MOE_ERR_INVALID, "MoELayer: input/output is NULL");
   if (T <= 0) return fail(MOE_ERR_INVALID, "MoELayer.decodeMany: T must be positive");
   const Workspace w = layout(d, T);
   if (!ws || ws_bytes < w.total)
@@ -823,10 +875,10 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y,
 
   // 1. router projection (MoELayer.swift:540 / 689-690)
   if (router_gemm_ok(d, T)) {
-    MOE_TRY(run_router_gemm(d, x, T, at<void>(ws, w.logits), at<uint32_t>(ws, w.r_plan),
+    MOE_TRY(run_router_gemm(d, rx, T, at<void>(ws, w.logits), at<uint32_t>(ws, w.r_plan),
                             at<uint32_t>(ws, w.r_tiles), st));
   } else {
-    MOE_HIP(launch_router_logits(x, xdt, T, H, d->router_weight, d->router_dtype, d->router_bias,
+    MOE_HIP(launch_router_logits(rx, xdt, T, H, d->router_weight, d->router_dtype, d->router_bias,
                                  E, at<void>(ws, w.logits), st),
             "router logits launch");
   }
@@ -841,9 +893,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y,
     g.logits = at<void>(ws, w.logits);
     g.E = E;
     g.k = k;
-    g.gating = d->gating;
-    g.norm = d->norm_topk_prob;
-    g.ebias = d->expert_bias;
+    g.ro = route_opts(d);
     g.idx = at<uint32_t>(ws, w.idx);
     g.w = at<float>(ws, w.w);
     g.perm = at<uint32_t>(ws, w.perm);
@@ -871,8 +921,8 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y,
               "shared add launch");
   } else {
     // 2. selection + dispatch plan (MoELayer.swift:706-792)
-    MOE_HIP(launch_router_topk(at<void>(ws, w.logits), xdt, T, E, k, d->gating, d->norm_topk_prob,
-                               d->expert_bias, at<uint32_t>(ws, w.idx), at<float>(ws, w.w), st),
+    MOE_HIP(launch_router_topk(at<void>(ws, w.logits), xdt, T, E, k, route_opts(d),
+                               at<uint32_t>(ws, w.idx), at<float>(ws, w.w), st),
             "router top-k launch");
     MOE_HIP(launch_dispatch_plan(at<uint32_t>(ws, w.idx), T, k, E, at<uint32_t>(ws, w.counts),
                                  at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.perm),
@@ -880,17 +930,21 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y,
                                  at<void>(ws, w.plan_scratch), dispatch_scratch_bytes(T, k, E), st),
             "dispatch plan launch");
     const int slots = std::min(E, M);
-    const bool gemm = gemm_ok(d->gate, xdt, M) && gemm_ok(d->down, xdt, M);
+    // squared-ReLU experts: the single up projection (NemotronHText.swift:756-761)
+    const bool gated = d->activation != MOE_ACT_RELU2;
+    const moe_qproj& p0 = gated ? d->gate : d->up;
+    const moe_qproj* p1 = gated ? &d->up : nullptr;
+    const bool gemm = gemm_ok(p0, xdt, M) && gemm_ok(d->down, xdt, M);
     // 3. gate/up + activation over the plan (MoELayer.swift:883-893)
     if (gemm) {
       MOE_HIP(launch_gemm_tiles(at<uint32_t>(ws, w.offsets), E, kGemmRows, at<uint32_t>(ws, w.tiles),
                                 st),
               "tile list launch");
-      MOE_TRY(run_gemm(d->gate, &d->up, x, xdt, at<uint32_t>(ws, w.perm), k,
+      MOE_TRY(run_gemm(p0, p1, x, xdt, at<uint32_t>(ws, w.perm), k,
                        at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.tiles), M,
                        at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st, kev(0)));
     } else {
-      MOE_TRY(run_gemv(d->gate, &d->up, x, xdt, at<uint32_t>(ws, w.perm), k,
+      MOE_TRY(run_gemv(p0, p1, x, xdt, at<uint32_t>(ws, w.perm), k,
                        at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, T == 1,
                        at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st, kev(0)));
     }
@@ -919,7 +973,16 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, int T, void* y,
 extern "C" moe_status moe_layer_forward(const moe_layer_desc* d, const void* x, int32_t T, void* y,
                                         void* workspace, size_t workspace_bytes,
                                         const moe_layer_trace* trace, hipStream_t stream) {
-  MOE_TRY(layer_forward(d, x, T, y, workspace, workspace_bytes, trace, stream));
+  MOE_TRY(layer_forward(d, x, x, T, y, workspace, workspace_bytes, trace, stream));
+  return ok();
+}
+
+extern "C" moe_status moe_layer_forward_routed(const moe_layer_desc* d, const void* x,
+                                               const void* router_x, int32_t T, void* y,
+                                               void* workspace, size_t workspace_bytes,
+                                               const moe_layer_trace* trace, hipStream_t stream) {
+  MOE_TRY(layer_forward(d, x, router_x ? router_x : x, T, y, workspace, workspace_bytes, trace,
+                        stream));
   return ok();
 }
 
@@ -954,7 +1017,7 @@ struct moe_layer {
   moe_status decode_many(const void* h, int T, void* out, hipStream_t st) {
     if (T <= 0) return fail(MOE_ERR_INVALID, "MoELayer.decodeMany: T must be positive");
     MOE_TRY(reserve(T));
-    return layer_forward(&desc, h, T, out, ws, ws_bytes, nullptr, st);
+    return layer_forward(&desc, h, h, T, out, ws, ws_bytes, nullptr, st);
   }
 };
 

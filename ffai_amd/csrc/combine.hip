@@ -109,9 +109,13 @@ __global__ __launch_bounds__(256) void activation_kernel(const XT* __restrict__ 
                                                          const XT* __restrict__ u,
                                                          XT* __restrict__ out, int64_t n, int act,
                                                          float alpha, float limit) {
+  // squared ReLU reads the up projection only; g may be null for it
+  const bool gated = act != ACT_RELU2;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    out[i] = from_f<XT>(apply_act(to_f<XT>(g[i]), to_f<XT>(u[i]), act, alpha, limit));
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float gv = gated ? to_f<XT>(g[i]) : 0.0f;
+    out[i] = from_f<XT>(apply_act<XT>(gv, to_f<XT>(u[i]), act, alpha, limit));
+  }
 }
 
 template <typename ST, typename OT>

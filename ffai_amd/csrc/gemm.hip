@@ -40,9 +40,7 @@ struct ProjViewG {
   rsrc_t w, s, b;
 };
 
-constexpr int kGBM = kGemmRows;  // rows per tile
-constexpr int kGBK = 64;       // values per K chunk
-constexpr int kGAS = 72;       // LDS row stride in elements (64 + 8: conflict-free b128 reads)
+constexpr int kGBK = 64;  // values per K chunk
 
 template <typename XT> struct MfmaOp;
 template <> struct MfmaOp<bf16_t> {
@@ -337,7 +335,9 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
         if constexpr (GATEUP) {
           float u = round_to<XT>(acc[i][j + 2][r]);
           if (ob1) u = round_to<XT>(u + obu);
-          v = apply_act(v, u, a.act, a.alpha, a.limit);
+          v = apply_act<XT>(v, u, a.act, a.alpha, a.limit);
+        } else if (a.act == ACT_RELU2) {  // single projection: ReLU^2 only
+          v = apply_act<XT>(0.f, v, ACT_RELU2, 0.f, 0.f);
         }
         wt[row * OC + 32 * j + col] = from_f<XT>(v);
       }

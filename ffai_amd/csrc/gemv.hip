@@ -138,9 +138,10 @@ __global__ __launch_bounds__(256) void gemv_grouped_kernel(const GemvArgs a) {
             const float g = finish_proj<XT>(acc0[t], a.p0.ob, ebase + r);
             if constexpr (GATEUP) {
               const float u = finish_proj<XT>(acc1[t], a.p1.ob, ebase + r);
-              out[o] = from_f<XT>(apply_act(g, u, a.act, a.alpha, a.limit));
+              out[o] = from_f<XT>(apply_act<XT>(g, u, a.act, a.alpha, a.limit));
             } else {
-              out[o] = from_f<XT>(g);
+              // single projection: only ReLU^2 acts on it (no gate)
+              out[o] = from_f<XT>(a.act == ACT_RELU2 ? apply_act<XT>(0.f, g, ACT_RELU2, 0.f, 0.f) : g);
             }
           }
         }
@@ -218,9 +219,9 @@ __global__ __launch_bounds__(256) void gemv_single_kernel(const GemvArgs a) {
       const float g = finish_proj<XT>(acc0, a.p0.ob, ebase + r);
       if constexpr (GATEUP) {
         const float u = finish_proj<XT>(acc1, a.p1.ob, ebase + r);
-        out[o] = from_f<XT>(apply_act(g, u, a.act, a.alpha, a.limit));
+        out[o] = from_f<XT>(apply_act<XT>(g, u, a.act, a.alpha, a.limit));
       } else {
-        out[o] = from_f<XT>(g);
+        out[o] = from_f<XT>(a.act == ACT_RELU2 ? apply_act<XT>(0.f, g, ACT_RELU2, 0.f, 0.f) : g);
       }
     }
   }
@@ -265,8 +266,8 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
     int sel;
     float wgt = 0.f;
     uint64_t masks[kTopkEPL];
-    wave_topk<XT, EPL>(reinterpret_cast<const XT*>(a.logits), a.E, a.k, a.gating, a.norm, a.ebias,
-                       sc, writer, &sel, &wgt, masks);
+    wave_topk<XT, EPL>(reinterpret_cast<const XT*>(a.logits), a.E, a.k, a.ro, sc, writer, &sel,
+                       &wgt, masks);
     const int e = __builtin_amdgcn_readfirstlane(selected_nth(masks, slot));
     const uint64_t hit = __ballot(lane < a.k && sel == e);
     if (lane == 0) {
@@ -324,7 +325,7 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
       u = round_to<XT>(u);
       if (ob_g) g = round_to<XT>(g + obg[it]);
       if (ob_u) u = round_to<XT>(u + obu[it]);
-      act[row] = from_f<XT>(apply_act(g, u, a.act_kind, a.alpha, a.limit));
+      act[row] = from_f<XT>(apply_act<XT>(g, u, a.act_kind, a.alpha, a.limit));
     }
   }
 }

@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "moe_internal.hpp"
+
 namespace moe {
 
 constexpr int kWave = 64;
@@ -160,11 +162,13 @@ constexpr int kTopkEPL = kTopkMaxE / 64; // logits held per lane
 // a compile-time bound on E (E <= 64 EPL) that removes the per-slot range
 // checks from the k selection rounds.
 template <typename XT, int EPL = kTopkEPL>
-__device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, int norm,
-                          const float* __restrict__ ebias, float* sc, bool want_weights,
-                          int* sel, float* w, uint64_t* masks = nullptr) {
+__device__ void wave_topk(const XT* __restrict__ row, int E, int k, const RouteOpts& ro, float* sc,
+                          bool want_weights, int* sel, float* w, uint64_t* masks = nullptr) {
   const int lane = threadIdx.x & 63;
-  const bool on_logits = (gating == 1) || (norm && ebias == nullptr);
+  const int gating = ro.gating, norm = ro.norm;
+  const float* __restrict__ ebias = ro.ebias;
+  const bool sigmoid = gating == 2;
+  const bool on_logits = !sigmoid && ((gating == 1) || (norm && ebias == nullptr));
   const float NEG = -__builtin_huge_valf();
   float v[EPL];
   float m = NEG;
@@ -173,12 +177,22 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
     const int i = lane + 64 * j;
     v[j] = NEG;
     if (j * 64 < E) {  // wave-uniform; the load itself is clamped, not branched
-      const float lv = to_f<XT>(row[min(i, E - 1)]);
+      const float lv = to_f<XT>(row[min(i, E - 1)]) * ro.logit_scale;
       v[j] = (i < E) ? lv : NEG;
       m = (i < E) ? fmaxf(m, lv) : m;
     }
   }
-  if (!on_logits) {
+  // sigmoid mode: v becomes the selection score, raw[] the unbiased sigmoid
+  float raw[EPL];
+  if (sigmoid) {
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+      const int i = lane + 64 * j;
+      raw[j] = 1.0f / (1.0f + det_expf(-v[j]));
+      v[j] = (i < E) ? (ebias ? raw[j] + ebias[min(i, E - 1)] : raw[j]) : NEG;
+    }
+  }
+  if (!on_logits && !sigmoid) {
     // full softmax (+ expert bias): MoELayer.swift:174-195
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
 #pragma unroll
@@ -216,7 +230,7 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
   }
   uint32_t taken = 0;
   int my_sel = 0, my_key = NONE;
-  float my_raw = NEG;  // the selected value as stored (NaN kept), lane r < k
+  float my_raw = NEG;  // the selected logit (sigmoid: unbiased score), lane r < k
   for (int r = 0; r < k; r++) {
     int bk = key[0];
 #pragma unroll
@@ -237,9 +251,9 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
     win = __builtin_amdgcn_readfirstlane(win);
     const int wj = win >> 6;
     const bool mine = (win & 63) == lane;
-    float rv = v[0];
+    float rv = sigmoid ? raw[0] : v[0];
 #pragma unroll
-    for (int j = 1; j < EPL; j++) rv = (j == wj) ? v[j] : rv;
+    for (int j = 1; j < EPL; j++) rv = (j == wj) ? (sigmoid ? raw[j] : v[j]) : rv;
     rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rv), win & 63));
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
@@ -273,6 +287,14 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
     float s = 0.f;
     for (int r = 0; r < k; r++) s += __shfl(ex, r, 64);
     wv = (s > 0.f) ? ex / s : 1.0f / (float)k;
+  } else if (sigmoid) {
+    // raw sigmoid of the pick, / (sum in rank order + 1e-20) when norm, k > 1
+    wv = my_raw;
+    if (norm && k > 1) {
+      float s = 0.f;
+      for (int r = 0; r < k; r++) s += __shfl(my_raw, r, 64);
+      wv = wv / (s + 1e-20f);
+    }
   } else {
     wv = my_val;
     if (norm) {
@@ -281,20 +303,45 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, int gating, 
       if (s > 0.f) wv = wv / s;
     }
   }
+  wv = wv * ro.routed_scale;
+  if (ro.escale) wv = wv * ro.escale[min(my_sel, E - 1)];
   *w = wv;
 }
 
 // ------------------------------------------------------------ activations --
-enum { ACT_SWIGLU = 0, ACT_GPTOSS = 1 };
+enum { ACT_SWIGLU = 0, ACT_GPTOSS = 1, ACT_GEGLU = 2, ACT_RELU2 = 3 };
 
+// Tanh-form GELU, 0.5 g (1 + tanh(y)) with y = sqrt(2/pi) (g + 0.044715 g^3),
+// evaluated as g * logistic(2y): the same function without the cancellation
+// of 1 + tanh(y) for negative g, and finite at both ends (exp overflows to
+// inf, the reciprocal to 0).
+__device__ __forceinline__ float gelu_tanh(float g) {
+  const float y = 0.7978845608f * (g + 0.044715f * g * g * g);
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * y));
+}
+
+// The gated activation of one expert row, returned in fp32 before the final
+// rounding to the storage type XT:
+//   SwiGLU silu(g) u (Ops.swift:6400-6411);
+//   GPT-OSS min(g, limit) sigma(alpha g) (clamp(u, +-limit) + 1)
+//     (GPTOSSText.swift:1415-1431);
+//   GEGLU gelu(g) rounded to XT, times u (Gemma4Text.swift:965 stores the
+//     GELU before the product);
+//   ReLU^2 max(u, 0)^2, no gate projection (NemotronHText.swift:756-761).
 // The logistic uses the hardware reciprocal (v_rcp_f32, 1 ulp) in place of an
 // IEEE divide: the result is rounded to a 16-bit storage type right after.
+template <typename XT>
 __device__ __forceinline__ float apply_act(float g, float u, int act, float alpha, float limit) {
   if (act == ACT_GPTOSS) {
     g = fminf(g, limit);
     u = fminf(fmaxf(u, -limit), limit);
     const float glu = g * __builtin_amdgcn_rcpf(1.0f + __expf(-alpha * g));
     return glu * (u + 1.0f);
+  }
+  if (act == ACT_GEGLU) return round_to<XT>(gelu_tanh(g)) * u;
+  if (act == ACT_RELU2) {
+    const float r = fmaxf(u, 0.0f);
+    return r * r;
   }
   return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }

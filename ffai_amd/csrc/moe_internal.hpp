@@ -17,6 +17,23 @@ struct KEvents {
   hipEvent_t start = nullptr, stop = nullptr;
 };
 
+// Routing options beyond the gating mode (the families after MoERouter):
+//   gating 0 softmax -> top-k, 1 top-k -> softmax (MoELayer.swift:140-205),
+//          2 sigmoid scores, ebias added for the selection only, weights the
+//          raw sigmoids, renormalised by their sum + 1e-20 when norm and
+//          k > 1 (NemotronHText.swift:700-725, 838-868);
+//   logit_scale multiplies the logits in fp32 before anything else (Gemma 4
+//          folds hidden^-0.5 there, Gemma4Text.swift:938-944);
+//   routed_scale multiplies the final weights (NemotronH
+//          routed_scaling_factor), then escale[e] (nullable, Gemma 4
+//          per_expert_scale, Gemma4Text.swift:945-950).
+struct RouteOpts {
+  int gating, norm;
+  const float* ebias;
+  float logit_scale, routed_scale;
+  const float* escale;
+};
+
 // ------------------------------------------------------------------ GEMV --
 // Expert-grouped dequant GEMV over a dispatch plan. Block b handles expert
 // slot b / row_blocks (the slot-th used expert) and rows
@@ -51,8 +68,8 @@ struct GemvArgs {
 // fused weighted combine over the k experts.
 struct Decode1Args {
   const void* logits;        // [E] activation dtype
-  int E, k, gating, norm;
-  const float* ebias;        // nullable [E]
+  int E, k;
+  RouteOpts ro;
   uint32_t* idx;             // [k] out: experts in rank order
   float* w;                  // [k] out: combine weights
   uint32_t* perm;            // [k] out: sorted position -> rank
@@ -95,9 +112,8 @@ size_t gemv_smem_bytes(int xdt, int K, int tok_chunk);
 // ---------------------------------------------------------------- router --
 hipError_t launch_router_logits(const void* x, int xdt, int T, int H, const void* W, int wdt,
                                 const void* bias, int E, void* logits, hipStream_t st);
-hipError_t launch_router_topk(const void* logits, int dt, int T, int E, int k, int gating,
-                              int norm, const float* ebias, uint32_t* idx, float* w,
-                              hipStream_t st);
+hipError_t launch_router_topk(const void* logits, int dt, int T, int E, int k,
+                              const RouteOpts& ro, uint32_t* idx, float* w, hipStream_t st);
 
 // ------------------------------------------------------------- dispatch --
 // Writes counts, offsets, perm, inv_perm and the used-expert list.

@@ -104,8 +104,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT* __restrict
 // One wave per token row (wave_topk); weights are reproducible bit for bit.
 template <typename XT>
 __global__ __launch_bounds__(256) void router_topk_kernel(const XT* __restrict__ logits, int T,
-                                                          int E, int k, int gating, int norm,
-                                                          const float* __restrict__ ebias,
+                                                          int E, int k, const RouteOpts ro,
                                                           uint32_t* __restrict__ idx_out,
                                                           float* __restrict__ w_out) {
   __shared__ float sc[4][kTopkMaxE];
@@ -114,7 +113,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const XT* __restrict__
   if (t >= T) return;  // wave-uniform; the kernel has no block barrier
   int sel;
   float w;
-  wave_topk<XT>(logits + (size_t)t * E, E, k, gating, norm, ebias, sc[wv], true, &sel, &w);
+  wave_topk<XT>(logits + (size_t)t * E, E, k, ro, sc[wv], true, &sel, &w);
   if (lane < k) {
     idx_out[(size_t)t * k + lane] = (uint32_t)sel;
     w_out[(size_t)t * k + lane] = w;
@@ -164,13 +163,12 @@ hipError_t launch_router_logits(const void* x, int xdt, int T, int H, const void
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_router_topk(const void* logits, int dt, int T, int E, int k, int gating,
-                              int norm, const float* ebias, uint32_t* idx, float* w,
-                              hipStream_t st) {
+hipError_t launch_router_topk(const void* logits, int dt, int T, int E, int k,
+                              const RouteOpts& ro, uint32_t* idx, float* w, hipStream_t st) {
   const int grid = (T + 3) / 4;
 #define MOE_TK(XT)                                                                          \
   hipLaunchKernelGGL((router_topk_kernel<XT>), dim3(grid), dim3(256), 0, st,               \
-                     (const XT*)logits, T, E, k, gating, norm, ebias, idx, w);              \
+                     (const XT*)logits, T, E, k, ro, idx, w);                              \
   return hipGetLastError();
   if (dt == DT_BF16) { MOE_TK(bf16_t) }
   if (dt == DT_F16) { MOE_TK(f16_t) }

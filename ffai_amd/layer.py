@@ -33,19 +33,27 @@ def _stream(stream=None):
 
 
 class MoEGatingMode:
-    """MoELayer.swift:71-78."""
+    """MoELayer.swift:71-78, plus the NemotronH sigmoid router
+    (NemotronHText.swift:838-868)."""
     softmaxThenTopK = _lib.MOE_SOFTMAX_THEN_TOPK
     topKThenSoftmax = _lib.MOE_TOPK_THEN_SOFTMAX
+    sigmoidTopK = _lib.MOE_SIGMOID_TOPK
 
 
 @dataclass
 class MoERouter:
-    """MoERouter (MoELayer.swift:97-124): the gating configuration."""
+    """MoERouter (MoELayer.swift:97-124): the gating configuration, with the
+    routing scales of the NemotronH (routed_scaling_factor,
+    NemotronHText.swift:867) and Gemma 4 (hidden^-0.5 logit scale and
+    per_expert_scale, Gemma4Text.swift:938-950) routers."""
     nExperts: int
     topK: int
     gatingMode: int = MoEGatingMode.softmaxThenTopK
     normTopKProb: bool = True
     expertBias: Optional[torch.Tensor] = None  # [nExperts] float32 on device
+    logitScale: float = 1.0
+    routedScale: float = 1.0
+    expertScale: Optional[torch.Tensor] = None  # [nExperts] float32 on device
 
     def __post_init__(self):
         if self.nExperts <= 0:
@@ -54,6 +62,8 @@ class MoERouter:
             raise ValueError(f"MoERouter: topK ({self.topK}) must be in 1...nExperts ({self.nExperts})")
         if self.expertBias is not None and self.expertBias.numel() != self.nExperts:
             raise ValueError("MoERouter: expertBias must have nExperts entries")
+        if self.expertScale is not None and self.expertScale.numel() != self.nExperts:
+            raise ValueError("MoERouter: expertScale must have nExperts entries")
 
 
 @dataclass
@@ -89,10 +99,11 @@ class StackedExperts:
 
 class MoELayer:
     """MoE feed-forward layer (router -> dispatch -> grouped expert products
-    -> combine [+ shared expert]) on one GPU."""
+    -> combine [+ shared expert]) on one GPU. With MOE_ACT_RELU2 the experts
+    have no gate projection: pass gate=None (and None as the shared gate)."""
 
     def __init__(self, *, router_weight: torch.Tensor, router: MoERouter,
-                 gate: StackedExperts, up: StackedExperts, down: StackedExperts,
+                 gate: Optional[StackedExperts], up: StackedExperts, down: StackedExperts,
                  hidden: int, act_dtype: torch.dtype,
                  router_bias: Optional[torch.Tensor] = None,
                  activation: int = _lib.MOE_ACT_SWIGLU, alpha: float = 1.702, limit: float = 7.0,
@@ -109,20 +120,25 @@ class MoELayer:
     def _build_desc(self) -> LayerDesc:
         d = LayerDesc()
         d.hidden, d.n_experts, d.top_k = self.hidden, self.router.nExperts, self.router.topK
-        d.intermediate = self.gate.n
+        d.intermediate = self.up.n
         d.act_dtype = moe_dtype(self.act_dtype)
         d.router_weight = self.router_weight.data_ptr()
         d.router_dtype = moe_dtype(self.router_weight.dtype)
         d.router_bias = None if self.router_bias is None else self.router_bias.data_ptr()
         d.gating, d.norm_topk_prob = self.router.gatingMode, int(bool(self.router.normTopKProb))
         d.expert_bias = None if self.router.expertBias is None else self.router.expertBias.data_ptr()
-        d.gate, d.up, d.down = self.gate.struct(), self.up.struct(), self.down.struct()
+        d.gate = QProj() if self.gate is None else self.gate.struct()
+        d.up, d.down = self.up.struct(), self.down.struct()
         d.activation, d.act_alpha, d.act_limit = self.activation, self.alpha, self.limit
         if self.shared is not None:
             d.has_shared = 1
-            d.shared_gate, d.shared_up, d.shared_down = (p.struct() for p in self.shared)
+            d.shared_gate, d.shared_up, d.shared_down = (
+                QProj() if p is None else p.struct() for p in self.shared)
             d.shared_gate_weight = (None if self.shared_gate_weight is None
                                     else self.shared_gate_weight.data_ptr())
+        r = self.router
+        d.logit_scale, d.routed_scale = r.logitScale, r.routedScale
+        d.expert_scale = None if r.expertScale is None else r.expertScale.data_ptr()
         return d
 
     @property
@@ -139,9 +155,13 @@ class MoELayer:
         return self._ws
 
     def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, trace: bool = False,
-                stream=None):
-        """decodeMany: x [T, hidden] -> [T, hidden]. With trace=True also
-        returns the routing (logits, topk_idx, topk_weight, perm, offsets)."""
+                stream=None, router_x: Optional[torch.Tensor] = None):
+        """decodeMany: x [T, hidden] -> [T, hidden]. router_x (default x) is
+        the router's input, for Gemma 4 whose router and experts read
+        differently normalised rows. With trace=True also returns the
+        routing (logits, topk_idx, topk_weight, perm, offsets)."""
+        if router_x is not None and (router_x.shape != x.shape or router_x.dtype != x.dtype):
+            raise ValueError("MoELayer: router_x must match x in shape and dtype")
         T = x.shape[0]
         if out is None:
             out = torch.empty_like(x)
@@ -159,10 +179,10 @@ class MoELayer:
                 offsets=torch.empty(E + 1, dtype=torch.int32, device=dev))
             tr = LayerTrace(*(tensors[n].data_ptr() for n in
                               ("logits", "topk_idx", "topk_weight", "perm", "offsets")))
-        check(_lib.load().moe_layer_forward(C.byref(self._desc), _ptr(x), T, _ptr(out),
-                                            _ptr(ws), ws.numel(),
-                                            C.byref(tr) if tr is not None else None,
-                                            _stream(stream)))
+        check(_lib.load().moe_layer_forward_routed(C.byref(self._desc), _ptr(x), _ptr(router_x),
+                                                   T, _ptr(out), _ptr(ws), ws.numel(),
+                                                   C.byref(tr) if tr is not None else None,
+                                                   _stream(stream)))
         return (out, tensors) if trace else out
 
     # Swift-API names

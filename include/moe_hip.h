@@ -45,16 +45,32 @@ typedef enum moe_status {
 /* Element types (Sources/FFAI/DType.swift:20-39). */
 typedef enum moe_dtype { MOE_F32 = 0, MOE_F16 = 1, MOE_BF16 = 2 } moe_dtype;
 
-/* MoEGatingMode (Sources/FFAI/Models/MoELayer.swift:71-78). */
+/* MoEGatingMode (Sources/FFAI/Models/MoELayer.swift:71-78), plus the
+ * NemotronH sigmoid router (Models/Text/NemotronHText.swift:700-725,
+ * 838-868): scores sigmoid(logit), expert_bias added for the selection
+ * only, weights the unbiased sigmoids, divided by their sum + 1e-20 when
+ * norm_topk_prob and k > 1. */
 typedef enum moe_gating {
     MOE_SOFTMAX_THEN_TOPK = 0,
-    MOE_TOPK_THEN_SOFTMAX = 1
+    MOE_TOPK_THEN_SOFTMAX = 1,
+    MOE_SIGMOID_TOPK = 2
 } moe_gating;
 
-/* Expert activation: SwiGLU silu(g)*u (Ops.swift:6400-6411) or GPT-OSS
- * clamped alpha-swish g*sigmoid(alpha*g)*(u+1) with g<=limit,
- * |u|<=limit (Models/Text/GPTOSSText.swift:1415-1431). */
-typedef enum moe_activation { MOE_ACT_SWIGLU = 0, MOE_ACT_GPTOSS = 1 } moe_activation;
+/* Expert activation:
+ *   SWIGLU  silu(g)*u (Ops.swift:6400-6411);
+ *   GPTOSS  clamped alpha-swish g*sigmoid(alpha*g)*(u+1) with g<=limit,
+ *           |u|<=limit (Models/Text/GPTOSSText.swift:1415-1431);
+ *   GEGLU   gelu(g)*u, tanh-form GELU rounded to the activation dtype
+ *           before the product (Gemma4Text.swift:965, the GELU of
+ *           Tests/FFAITests/Ops/OpsTests.swift:254-273);
+ *   RELU2   relu(u)^2 of a single up projection, no gate projection
+ *           (NemotronHText.swift:756-761). */
+typedef enum moe_activation {
+    MOE_ACT_SWIGLU = 0,
+    MOE_ACT_GPTOSS = 1,
+    MOE_ACT_GEGLU = 2,
+    MOE_ACT_RELU2 = 3
+} moe_activation;
 
 /* Stacked mlx-affine projection of n_experts experts
  * (MoELayer.StackedInt4Experts, MoELayer.swift:347-390, generalised to
@@ -80,7 +96,10 @@ typedef struct moe_qproj {
 
 /* MoELayer + MoERouter configuration (MoELayer.swift:97-124,440-498;
  * GPT-OSS GPTOSSMoELayer, GPTOSSText.swift:1302-1340; Qwen3.5 shared
- * expert Qwen35MoEFFN, Qwen3xText.swift:870-928). */
+ * expert Qwen35MoEFFN, Qwen3xText.swift:870-928; NemotronHMoELayer,
+ * NemotronHText.swift:694-868; Gemma4MoEFFN, Gemma4Text.swift:928-978).
+ * With MOE_ACT_RELU2 the gate projections (routed and shared) are absent:
+ * gate.weight and shared_gate.weight are NULL. */
 typedef struct moe_layer_desc {
     int32_t hidden;
     int32_t n_experts;
@@ -103,6 +122,17 @@ typedef struct moe_layer_desc {
     moe_qproj shared_gate, shared_up, shared_down;
     const void* shared_gate_weight; /* nullable dense [hidden] in
                                        router_dtype: sigmoid gate */
+    /* routing scales (0 reads as 1.0, so zero-initialised descriptors
+     * keep the plain MoERouter behaviour) */
+    float logit_scale;             /* logits * s in f32 before gating
+                                      (Gemma 4 hidden^-0.5,
+                                      Gemma4Text.swift:938-944) */
+    float routed_scale;            /* final weights * s (NemotronH
+                                      routed_scaling_factor) */
+    const float* expert_scale;     /* nullable [n_experts] f32: final
+                                      weight * expert_scale[e] (Gemma 4
+                                      per_expert_scale,
+                                      Gemma4Text.swift:945-950) */
 } moe_layer_desc;
 
 /* Optional device outputs of a layer call, for callers and tests that need
@@ -155,6 +185,15 @@ moe_status moe_router_topk(const void* logits, int32_t dtype, int32_t T, int32_t
                            int32_t k, int32_t gating, int32_t norm_topk_prob,
                            const float* expert_bias, uint32_t* topk_idx, float* topk_weight,
                            hipStream_t stream);
+/* moe_router_topk with the routing scales of moe_layer_desc (logit_scale,
+ * routed_scale: 0 reads as 1.0; expert_scale nullable): the NemotronH and
+ * Gemma 4 routers (NemotronHText.swift:838-868, Gemma4Text.swift:938-950). */
+moe_status moe_router_topk_scaled(const void* logits, int32_t dtype, int32_t T,
+                                  int32_t n_experts, int32_t k, int32_t gating,
+                                  int32_t norm_topk_prob, const float* expert_bias,
+                                  float logit_scale, float routed_scale,
+                                  const float* expert_scale, uint32_t* topk_idx,
+                                  float* topk_weight, hipStream_t stream);
 
 /* Deterministic token->expert plan replacing the host sort of
  * MoELayer.decodeMany (MoELayer.swift:752-792): stable order (expert asc,
@@ -188,7 +227,9 @@ moe_status moe_expert_matmul(const moe_qproj* p, const void* a, int32_t a_dtype,
                              const uint32_t* offsets, void* out, void* workspace,
                              size_t workspace_bytes, hipStream_t stream);
 
-/* Ops.swiglu (Ops.swift:6411-6460) and GPT-OSS's clamped activation. */
+/* Ops.swiglu (Ops.swift:6411-6460) and the other moe_activation kinds,
+ * elementwise over n values. MOE_ACT_RELU2 reads `up` only (gate may be
+ * NULL). */
 moe_status moe_activation_apply(const void* gate, const void* up, void* out, int64_t n,
                                 int32_t dtype, int32_t activation, float alpha, float limit,
                                 hipStream_t stream);
@@ -211,6 +252,14 @@ size_t moe_layer_workspace_bytes(const moe_layer_desc* d, int32_t max_tokens);
 moe_status moe_layer_forward(const moe_layer_desc* d, const void* x, int32_t T, void* y,
                              void* workspace, size_t workspace_bytes,
                              const moe_layer_trace* trace, hipStream_t stream);
+/* moe_layer_forward with the router reading its own input rows router_x
+ * [T, hidden] (nullable: x) while the experts read x: Gemma 4 routes on
+ * rmsNorm(h, router.scale) and feeds the experts preNorm2(h)
+ * (Gemma4Text.swift:932-936, 960). */
+moe_status moe_layer_forward_routed(const moe_layer_desc* d, const void* x,
+                                    const void* router_x, int32_t T, void* y, void* workspace,
+                                    size_t workspace_bytes, const moe_layer_trace* trace,
+                                    hipStream_t stream);
 
 /* ---- MoELayer handle (owns its workspace like the reference instance) -- */
 typedef struct moe_layer* moe_layer_t;

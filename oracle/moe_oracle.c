@@ -331,15 +331,49 @@ int or_topk_indices(const float* v, int n, int k, int* out) {
  * is the topKThenSoftmax branch. */
 int or_route(const float* logits, int T, int E, int k, int gating, int norm_topk,
              const float* expert_bias, uint32_t* idx, float* weights) {
+    return or_route_scaled(logits, T, E, k, gating, norm_topk, expert_bias, 1.0f, 1.0f, NULL,
+                           idx, weights);
+}
+
+/* NemotronH routing (NemotronHText.swift:844-867): sigmoid scores with the
+ * correction bias added for the selection only, ties to the lower index, the
+ * unbiased sigmoids as weights, divided by (their sum in rank order + 1e-20)
+ * when norm_topk and k > 1. The sigmoid uses or_expf, the exp of the
+ * softmax. */
+static void route_sigmoid(const float* l, int E, int k, int norm_topk, const float* expert_bias,
+                          float* raw, float* score, int* sel, float* ow) {
+    for (int e = 0; e < E; e++) {
+        raw[e] = 1.0f / (1.0f + or_expf(-l[e]));
+        score[e] = expert_bias ? raw[e] + expert_bias[e] : raw[e];
+    }
+    or_topk_indices(score, E, k, sel);
+    for (int j = 0; j < k; j++) ow[j] = raw[sel[j]];
+    if (k > 1 && norm_topk) {
+        float s = 0.0f;
+        for (int j = 0; j < k; j++) s += ow[j];
+        s = s + 1e-20f;
+        for (int j = 0; j < k; j++) ow[j] = ow[j] / s;
+    }
+}
+
+int or_route_scaled(const float* logits, int T, int E, int k, int gating, int norm_topk,
+                    const float* expert_bias, float logit_scale, float routed_scale,
+                    const float* expert_scale, uint32_t* idx, float* weights) {
     if (E <= 0 || k <= 0 || k > E) return -1;
+    if (gating < OR_SOFTMAX_THEN_TOPK || gating > OR_SIGMOID_TOPK) return -1;
     int* sel = (int*)malloc(sizeof(int) * (size_t)k);
     float* probs = (float*)malloc(sizeof(float) * (size_t)E);
+    float* score = (float*)malloc(sizeof(float) * (size_t)E);
     float* pick = (float*)malloc(sizeof(float) * (size_t)k);
+    float* lrow = (float*)malloc(sizeof(float) * (size_t)E);
     for (int t = 0; t < T; t++) {
-        const float* l = logits + (size_t)t * E;
+        const float* l = lrow;
+        for (int e = 0; e < E; e++) lrow[e] = logits[(size_t)t * E + e] * logit_scale;
         uint32_t* oi = idx + (size_t)t * k;
         float* ow = weights + (size_t)t * k;
-        if (gating == OR_TOPK_THEN_SOFTMAX ||
+        if (gating == OR_SIGMOID_TOPK) {
+            route_sigmoid(l, E, k, norm_topk, expert_bias, probs, score, sel, ow);
+        } else if (gating == OR_TOPK_THEN_SOFTMAX ||
             (gating == OR_SOFTMAX_THEN_TOPK && norm_topk && !expert_bias)) {
             or_topk_indices(l, E, k, sel);
             for (int j = 0; j < k; j++) pick[j] = l[sel[j]];
@@ -357,11 +391,17 @@ int or_route(const float* logits, int T, int E, int k, int gating, int norm_topk
                     for (int j = 0; j < k; j++) ow[j] = ow[j] / s;
             }
         }
-        for (int j = 0; j < k; j++) oi[j] = (uint32_t)sel[j];
+        for (int j = 0; j < k; j++) {
+            oi[j] = (uint32_t)sel[j];
+            ow[j] = ow[j] * routed_scale;
+            if (expert_scale) ow[j] = ow[j] * expert_scale[sel[j]];
+        }
     }
     free(sel);
     free(probs);
+    free(score);
     free(pick);
+    free(lrow);
     return 0;
 }
 
@@ -480,9 +520,28 @@ int or_qgemm_rows(const or_qproj* p, const float* a, int M,
 /* activations and combine                                                  */
 /* ------------------------------------------------------------------------ */
 
-/* SwiGLU silu(g)*u in fp32 (Ops.swift:6400-6411); GPT-OSS clamped
- * alpha-swish with the upper-only gate clamp (GPTOSSText.swift:1415-1431). */
+/* 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3))), the form the
+ * reference's GELU test states (OpsTests.swift:262-267). */
+float or_gelu(float g) {
+    const float c = 0.7978845608028654f; /* sqrt(2/pi) */
+    float inner = c * (g + 0.044715f * g * g * g);
+    return 0.5f * g * (1.0f + tanhf(inner));
+}
+
 float or_act(float g, float u, int act, float alpha, float limit) {
+    return or_act_dt(g, u, act, alpha, limit, OR_F32);
+}
+
+/* SwiGLU silu(g)*u in fp32 (Ops.swift:6400-6411); GPT-OSS clamped
+ * alpha-swish with the upper-only gate clamp (GPTOSSText.swift:1415-1431);
+ * GEGLU with the GELU stored in dt before the product (Gemma4Text.swift:
+ * 965); squared ReLU relu(u) * relu(u) (NemotronHText.swift:759-760). */
+float or_act_dt(float g, float u, int act, float alpha, float limit, int dt) {
+    if (act == OR_ACT_GEGLU) return or_round_dt(or_gelu(g), dt) * u;
+    if (act == OR_ACT_RELU2) {
+        float r = u > 0.0f ? u : 0.0f;
+        return r * r;
+    }
     if (act == OR_ACT_GPTOSS) {
         if (g > limit) g = limit;
         if (u > limit) u = limit;
@@ -537,6 +596,31 @@ static void finish_proj(const or_qproj* p, float* v, int M, const uint32_t* row_
 int or_moe_layer(const or_layer* L, const void* x, int T, void* y,
                  const float* given_logits,
                  float* logits_out, uint32_t* idx_out, float* w_out) {
+    return or_moe_layer_routed(L, x, x, T, y, given_logits, logits_out, idx_out, w_out);
+}
+
+/* The gate/up pair (or the single up projection of squared-ReLU experts)
+ * and the activation, rounded to dt, into g [M, I]. */
+static void expert_act(const or_layer* L, const or_qproj* gate, const or_qproj* up,
+                       const float* a, int M, const uint32_t* rexp, float* g) {
+    const int I = up->n, dt = L->act_dt;
+    float* u = (float*)malloc(sizeof(float) * (size_t)M * I);
+    or_qgemm_rows(up, a, M, rexp, u);
+    finish_proj(up, u, M, rexp, dt);
+    if (L->activation == OR_ACT_RELU2) {
+        memset(g, 0, sizeof(float) * (size_t)M * I);
+    } else {
+        or_qgemm_rows(gate, a, M, rexp, g);
+        finish_proj(gate, g, M, rexp, dt);
+    }
+    for (size_t i = 0; i < (size_t)M * I; i++)
+        g[i] = or_round_dt(or_act_dt(g[i], u[i], L->activation, L->alpha, L->limit, dt), dt);
+    free(u);
+}
+
+int or_moe_layer_routed(const or_layer* L, const void* x, const void* router_x, int T,
+                        void* y, const float* given_logits,
+                        float* logits_out, uint32_t* idx_out, float* w_out) {
     int H = L->hidden, E = L->n_experts, k = L->top_k, I = L->intermediate, dt = L->act_dt;
     if (T <= 0 || H <= 0 || E <= 0 || k <= 0 || k > E || I <= 0) return -1;
     size_t M = (size_t)T * k;
@@ -546,12 +630,15 @@ int or_moe_layer(const or_layer* L, const void* x, int T, void* y,
     /* 1. router projection */
     float* logits = (float*)malloc(sizeof(float) * (size_t)T * E);
     if (given_logits) memcpy(logits, given_logits, sizeof(float) * (size_t)T * E);
-    else or_router_logits(x, dt, T, H, L->router_weight, L->router_dt, L->router_bias, E, logits);
+    else or_router_logits(router_x, dt, T, H, L->router_weight, L->router_dt, L->router_bias, E,
+                          logits);
 
     /* 2. routing */
     uint32_t* idx = (uint32_t*)malloc(sizeof(uint32_t) * M);
     float* w = (float*)malloc(sizeof(float) * M);
-    or_route(logits, T, E, k, L->gating, L->norm_topk, L->expert_bias, idx, w);
+    or_route_scaled(logits, T, E, k, L->gating, L->norm_topk, L->expert_bias,
+                    L->logit_scale == 0.0f ? 1.0f : L->logit_scale,
+                    L->routed_scale == 0.0f ? 1.0f : L->routed_scale, L->expert_scale, idx, w);
 
     /* 3. plan */
     uint32_t* counts = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)E);
@@ -568,13 +655,7 @@ int or_moe_layer(const or_layer* L, const void* x, int T, void* y,
         memcpy(a + p * H, xf + (size_t)(perm[p] / k) * H, sizeof(float) * (size_t)H);
     }
     float* g = (float*)malloc(sizeof(float) * M * I);
-    float* u = (float*)malloc(sizeof(float) * M * I);
-    or_qgemm_rows(&L->gate, a, (int)M, rexp, g);
-    or_qgemm_rows(&L->up, a, (int)M, rexp, u);
-    finish_proj(&L->gate, g, (int)M, rexp, dt);
-    finish_proj(&L->up, u, (int)M, rexp, dt);
-    for (size_t i = 0; i < M * (size_t)I; i++)
-        g[i] = or_round_dt(or_act(g[i], u[i], L->activation, L->alpha, L->limit), dt);
+    expert_act(L, &L->gate, &L->up, a, (int)M, rexp, g);
 
     /* 5. down projection (MoELayer.swift:899-902) */
     float* Y = (float*)malloc(sizeof(float) * M * H);
@@ -586,19 +667,15 @@ int or_moe_layer(const or_layer* L, const void* x, int T, void* y,
     or_unpermute(Y, inv, w, T, H, k, dt, out);
 
     /* 7. shared expert: Granite-style unconditional add (MoELayer.swift:
-     * 620-624) or Qwen3.5's sigmoid gate (Qwen3xText.swift:1047-1104). */
+     * 620-624), Qwen3.5's sigmoid gate (Qwen3xText.swift:1047-1104), or
+     * NemotronH's squared-ReLU expert (NemotronHText.swift:855-862); the
+     * shared expert uses the routed experts' activation. */
     if (L->has_shared) {
-        int SI = L->shared_gate.n;
+        int SI = L->shared_up.n;
         uint32_t* zero = (uint32_t*)calloc((size_t)T, sizeof(uint32_t));
         float* sg = (float*)malloc(sizeof(float) * (size_t)T * SI);
-        float* su = (float*)malloc(sizeof(float) * (size_t)T * SI);
         float* so = (float*)malloc(sizeof(float) * (size_t)T * H);
-        or_qgemm_rows(&L->shared_gate, xf, T, zero, sg);
-        or_qgemm_rows(&L->shared_up, xf, T, zero, su);
-        finish_proj(&L->shared_gate, sg, T, zero, dt);
-        finish_proj(&L->shared_up, su, T, zero, dt);
-        for (size_t i = 0; i < (size_t)T * SI; i++)
-            sg[i] = or_round_dt(or_act(sg[i], su[i], OR_ACT_SWIGLU, 0.f, 0.f), dt);
+        expert_act(L, &L->shared_gate, &L->shared_up, xf, T, zero, sg);
         or_qgemm_rows(&L->shared_down, sg, T, zero, so);
         finish_proj(&L->shared_down, so, T, zero, dt);
         float* gl = NULL;
@@ -615,7 +692,7 @@ int or_moe_layer(const or_layer* L, const void* x, int T, void* y,
                 out[i] = or_round_dt(out[i] + prod, dt);
             }
         }
-        free(zero); free(sg); free(su); free(so); free(gl);
+        free(zero); free(sg); free(so); free(gl);
     }
     or_store(out, dt, (size_t)T * H, y);
 
@@ -623,6 +700,6 @@ int or_moe_layer(const or_layer* L, const void* x, int T, void* y,
     if (idx_out) memcpy(idx_out, idx, sizeof(uint32_t) * M);
     if (w_out) memcpy(w_out, w, sizeof(float) * M);
     free(xf); free(logits); free(idx); free(w); free(counts); free(offsets);
-    free(perm); free(inv); free(rexp); free(a); free(g); free(u); free(Y); free(out);
+    free(perm); free(inv); free(rexp); free(a); free(g); free(Y); free(out);
     return 0;
 }

@@ -25,12 +25,15 @@ extern "C" {
 /* Element types — same numbering as moe_dtype in include/moe_hip.h. */
 enum { OR_F32 = 0, OR_F16 = 1, OR_BF16 = 2 };
 
-/* Gating behaviours of MoERouter.route (MoELayer.swift:71-78,140-205). */
-enum { OR_SOFTMAX_THEN_TOPK = 0, OR_TOPK_THEN_SOFTMAX = 1 };
+/* Gating behaviours of MoERouter.route (MoELayer.swift:71-78,140-205) and
+ * the NemotronH sigmoid router (NemotronHText.swift:838-868). */
+enum { OR_SOFTMAX_THEN_TOPK = 0, OR_TOPK_THEN_SOFTMAX = 1, OR_SIGMOID_TOPK = 2 };
 
-/* Expert activations: SwiGLU (Ops.swift:6400-6411) and GPT-OSS clamped
- * alpha-swish (GPTOSSText.swift:1415-1431). */
-enum { OR_ACT_SWIGLU = 0, OR_ACT_GPTOSS = 1 };
+/* Expert activations: SwiGLU (Ops.swift:6400-6411), GPT-OSS clamped
+ * alpha-swish (GPTOSSText.swift:1415-1431), Gemma 4 GELU-gated
+ * (Gemma4Text.swift:965) and NemotronH squared ReLU of the single up
+ * projection (NemotronHText.swift:756-761). */
+enum { OR_ACT_SWIGLU = 0, OR_ACT_GPTOSS = 1, OR_ACT_GEGLU = 2, OR_ACT_RELU2 = 3 };
 
 /* ---- scalar conversions (Tensor.swift:146-150 for bf16 RNE) ------------ */
 float    or_bf16_to_f32(uint16_t h);
@@ -61,6 +64,13 @@ int  or_topk_indices(const float* v, int n, int k, int* out);
 void or_softmax(const float* x, int n, float* out);
 int  or_route(const float* logits, int T, int E, int k, int gating, int norm_topk,
               const float* expert_bias, uint32_t* idx, float* weights);
+/* or_route with logits * logit_scale first (Gemma4Text.swift:938-944) and
+ * the final weights * routed_scale (NemotronH routed_scaling_factor,
+ * NemotronHText.swift:867) then * expert_scale[e] when non-NULL
+ * (Gemma4Text.swift:945-950). */
+int  or_route_scaled(const float* logits, int T, int E, int k, int gating, int norm_topk,
+                     const float* expert_bias, float logit_scale, float routed_scale,
+                     const float* expert_scale, uint32_t* idx, float* weights);
 
 /* ---- dispatch plan (MoELayer.swift:752-792) ----------------------------- */
 int or_dispatch_plan(const uint32_t* idx, int T, int k, int E,
@@ -80,6 +90,12 @@ typedef struct or_qproj {
 int or_qgemm_rows(const or_qproj* p, const float* a, int M,
                   const uint32_t* row_expert, float* out);
 
+/* Tanh-form GELU (Tests/FFAITests/Ops/OpsTests.swift:254-273). */
+float or_gelu(float g);
+/* The activation before its final rounding to dt; GEGLU rounds the GELU to
+ * dt before the product (Gemma4Text.swift:965: Ops.mul(Ops.gelu(g), u)).
+ * RELU2 reads u only. or_act is or_act_dt at OR_F32. */
+float or_act_dt(float g, float u, int act, float alpha, float limit, int dt);
 float or_act(float g, float u, int act, float alpha, float limit);
 
 /* out[t,:] = Σ_s w[t,s] · Y[inv_perm[t*k+s], :] (Ops.swift:5030-5110) */
@@ -98,6 +114,8 @@ typedef struct or_layer {
     int has_shared;
     or_qproj shared_gate, shared_up, shared_down;
     const void* shared_gate_weight;   /* nullable [H] in router_dt */
+    float logit_scale, routed_scale;  /* 0 reads as 1 */
+    const float* expert_scale;        /* nullable [E] */
 } or_layer;
 
 /* If given_logits is non-NULL it replaces the router projection (used to
@@ -106,6 +124,11 @@ typedef struct or_layer {
 int or_moe_layer(const or_layer* L, const void* x, int T, void* y,
                  const float* given_logits,
                  float* logits_out, uint32_t* idx_out, float* w_out);
+/* The same with the router reading router_x while the experts read x
+ * (Gemma4Text.swift:932-936, 960). */
+int or_moe_layer_routed(const or_layer* L, const void* x, const void* router_x, int T,
+                        void* y, const float* given_logits,
+                        float* logits_out, uint32_t* idx_out, float* w_out);
 
 #ifdef __cplusplus
 }

@@ -16,8 +16,8 @@ import subprocess
 import numpy as np
 
 F32, F16, BF16 = 0, 1, 2
-SOFTMAX_THEN_TOPK, TOPK_THEN_SOFTMAX = 0, 1
-ACT_SWIGLU, ACT_GPTOSS = 0, 1
+SOFTMAX_THEN_TOPK, TOPK_THEN_SOFTMAX, SIGMOID_TOPK = 0, 1, 2
+ACT_SWIGLU, ACT_GPTOSS, ACT_GEGLU, ACT_RELU2 = 0, 1, 2, 3
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _SO = os.path.join(_HERE, "libmoe_oracle.so")
@@ -61,6 +61,7 @@ class OrLayer(C.Structure):
         ("has_shared", C.c_int),
         ("shared_gate", OrQProj), ("shared_up", OrQProj), ("shared_down", OrQProj),
         ("shared_gate_weight", C.c_void_p),
+        ("logit_scale", C.c_float), ("routed_scale", C.c_float), ("expert_scale", C.c_void_p),
     ]
 
 
@@ -85,6 +86,10 @@ def _declare(L):
     L.or_topk_indices.argtypes = [vp, i, i, vp]; L.or_topk_indices.restype = i
     L.or_softmax.argtypes = [vp, i, vp]; L.or_softmax.restype = None
     L.or_route.argtypes = [vp, i, i, i, i, i, vp, vp, vp]; L.or_route.restype = i
+    L.or_route_scaled.argtypes = [vp, i, i, i, i, i, vp, f, f, vp, vp, vp]
+    L.or_route_scaled.restype = i
+    L.or_gelu.argtypes = [f]; L.or_gelu.restype = f
+    L.or_act_dt.argtypes = [f, f, i, f, f, i]; L.or_act_dt.restype = f
     L.or_dispatch_plan.argtypes = [vp, i, i, i, vp, vp, vp, vp]
     L.or_dispatch_plan.restype = i
     L.or_qgemm_rows.argtypes = [C.POINTER(OrQProj), vp, i, vp, vp]
@@ -93,6 +98,8 @@ def _declare(L):
     L.or_unpermute.argtypes = [vp, vp, vp, i, i, i, i, vp]; L.or_unpermute.restype = None
     L.or_moe_layer.argtypes = [C.POINTER(OrLayer), vp, i, vp, vp, vp, vp, vp]
     L.or_moe_layer.restype = i
+    L.or_moe_layer_routed.argtypes = [C.POINTER(OrLayer), vp, vp, i, vp, vp, vp, vp, vp]
+    L.or_moe_layer_routed.restype = i
 
 
 def _p(a):
@@ -198,13 +205,16 @@ def softmax(v):
     return out
 
 
-def route(logits, k, gating=SOFTMAX_THEN_TOPK, norm_topk=True, expert_bias=None):
+def route(logits, k, gating=SOFTMAX_THEN_TOPK, norm_topk=True, expert_bias=None,
+          logit_scale=1.0, routed_scale=1.0, expert_scale=None):
     logits = np.ascontiguousarray(np.atleast_2d(logits), dtype=np.float32)
     T, E = logits.shape
     idx = np.zeros((T, k), dtype=np.uint32)
     w = np.zeros((T, k), dtype=np.float32)
     eb = None if expert_bias is None else np.ascontiguousarray(expert_bias, dtype=np.float32)
-    rc = lib().or_route(_p(logits), T, E, k, gating, int(bool(norm_topk)), _p(eb), _p(idx), _p(w))
+    es = None if expert_scale is None else np.ascontiguousarray(expert_scale, dtype=np.float32)
+    rc = lib().or_route_scaled(_p(logits), T, E, k, gating, int(bool(norm_topk)), _p(eb),
+                               float(logit_scale), float(routed_scale), _p(es), _p(idx), _p(w))
     if rc != 0:
         raise ValueError("invalid router arguments")
     return idx, w
@@ -262,8 +272,12 @@ def qgemm_rows(p: QProj, a: np.ndarray, row_expert: np.ndarray) -> np.ndarray:
     return out
 
 
-def act(g, u, kind=ACT_SWIGLU, alpha=1.702, limit=7.0) -> float:
-    return lib().or_act(float(g), float(u), kind, float(alpha), float(limit))
+def act(g, u, kind=ACT_SWIGLU, alpha=1.702, limit=7.0, dt=F32) -> float:
+    return lib().or_act_dt(float(g), float(u), kind, float(alpha), float(limit), dt)
+
+
+def gelu(g) -> float:
+    return lib().or_gelu(float(g))
 
 
 def unpermute(Y, inv_perm, w, T, H, k, dt):
@@ -277,10 +291,13 @@ def unpermute(Y, inv_perm, w, T, H, k, dt):
 
 # ---------------------------------------------------------------- layer ----
 
-def moe_layer(spec, x, given_logits=None):
+def moe_layer(spec, x, given_logits=None, router_x=None):
     """Run the whole layer on the CPU. ``spec`` is a tests' LayerSpec-like
-    object (see tests/moe_spec.py). Returns (y, logits, idx, weights)."""
+    object (see tests/moe_spec.py). ``router_x`` (default x) is what the
+    router reads. Returns (y, logits, idx, weights)."""
     x = np.ascontiguousarray(x)
+    rx = x if router_x is None else np.ascontiguousarray(router_x)
+    assert rx.shape == x.shape and rx.dtype == x.dtype
     T = x.shape[0]
     L = spec.oracle_struct()
     y = np.zeros((T, spec.hidden), dtype=np_dtype(spec.act_dt))
@@ -288,7 +305,8 @@ def moe_layer(spec, x, given_logits=None):
     idx = np.zeros((T, spec.top_k), dtype=np.uint32)
     w = np.zeros((T, spec.top_k), dtype=np.float32)
     gl = None if given_logits is None else np.ascontiguousarray(given_logits, dtype=np.float32)
-    rc = lib().or_moe_layer(C.byref(L), _p(x), T, _p(y), _p(gl), _p(logits), _p(idx), _p(w))
+    rc = lib().or_moe_layer_routed(C.byref(L), _p(x), _p(rx), T, _p(y), _p(gl), _p(logits),
+                                   _p(idx), _p(w))
     if rc != 0:
         raise ValueError("invalid layer description")
     return y, logits, idx, w

@@ -46,7 +46,7 @@ class LayerSpec:
     act_dt: int
     router_weight: np.ndarray
     router_dt: int
-    gate: orc.QProj
+    gate: Optional[orc.QProj]  # None for squared-ReLU experts
     up: orc.QProj
     down: orc.QProj
     gating: int = orc.SOFTMAX_THEN_TOPK
@@ -58,6 +58,10 @@ class LayerSpec:
     limit: float = 7.0
     shared: Optional[tuple] = None
     shared_gate_weight: Optional[np.ndarray] = None
+    logit_scale: float = 1.0
+    routed_scale: float = 1.0
+    expert_scale: Optional[np.ndarray] = None  # [E] float32
+    split_router_input: bool = False  # the router reads its own rows (Gemma 4)
     name: str = ""
     meta: dict = field(default_factory=dict)
 
@@ -71,13 +75,17 @@ class LayerSpec:
         L.router_bias = None if self.router_bias is None else self.router_bias.ctypes.data
         L.gating, L.norm_topk = self.gating, int(self.norm_topk)
         L.expert_bias = None if self.expert_bias is None else self.expert_bias.ctypes.data
-        L.gate, L.up, L.down = self.gate.c(), self.up.c(), self.down.c()
+        L.gate = orc.OrQProj() if self.gate is None else self.gate.c()
+        L.up, L.down = self.up.c(), self.down.c()
         L.activation, L.alpha, L.limit = self.activation, self.alpha, self.limit
         if self.shared is not None:
             L.has_shared = 1
-            L.shared_gate, L.shared_up, L.shared_down = (p.c() for p in self.shared)
+            L.shared_gate, L.shared_up, L.shared_down = (
+                orc.OrQProj() if p is None else p.c() for p in self.shared)
             L.shared_gate_weight = (None if self.shared_gate_weight is None
                                     else self.shared_gate_weight.ctypes.data)
+        L.logit_scale, L.routed_scale = self.logit_scale, self.routed_scale
+        L.expert_scale = None if self.expert_scale is None else self.expert_scale.ctypes.data
         self._keep = L
         return L
 
@@ -96,12 +104,15 @@ class LayerSpec:
             return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
         def P(q):
+            if q is None:
+                return None
             return fl.StackedExperts(T(q.weight), T(q.scales), T(q.biases), q.bits, q.gs,
                                      out_bias=T(q.out_bias))
 
         act = {F32: torch.float32, F16: torch.float16, BF16: torch.bfloat16}[self.act_dt]
         router = fl.MoERouter(self.n_experts, self.top_k, self.gating, self.norm_topk,
-                              None if self.expert_bias is None else T(self.expert_bias))
+                              T(self.expert_bias), self.logit_scale, self.routed_scale,
+                              T(self.expert_scale))
         shared = None if self.shared is None else tuple(P(q) for q in self.shared)
         return fl.MoELayer(router_weight=T(self.router_weight), router=router, gate=P(self.gate),
                            up=P(self.up), down=P(self.down), hidden=self.hidden, act_dtype=act,
@@ -111,6 +122,13 @@ class LayerSpec:
 
     def x(self, T, seed=0):
         rng = np.random.default_rng(seed + 1000)
+        return store(rng.normal(0, 1, size=(T, self.hidden)), self.act_dt)
+
+    def router_x(self, T, seed=0):
+        """The router's own input rows when split_router_input, else None."""
+        if not self.split_router_input:
+            return None
+        rng = np.random.default_rng(seed + 5000)
         return store(rng.normal(0, 1, size=(T, self.hidden)), self.act_dt)
 
 
@@ -208,6 +226,40 @@ def cfg_bits(gu_bits, down_bits, gs, sb_dt, act_dt, seed=0, hidden=512, inter=38
                      router_dt=act_dt,
                      gate=proj(I, H, gu_bits), up=proj(I, H, gu_bits), down=proj(H, I, down_bits),
                      name=f"bits{gu_bits}/{down_bits} gs{gs}")
+
+
+def cfg_nemotron(seed=0, n_experts=64, hidden=1024, inter=512, shared_inter=1024, top_k=6):
+    """NemotronH MoE (NemotronHText.swift:694-868): sigmoid router with a
+    correction bias for the selection, renormalised top-6 weights times
+    routed_scaling_factor 2.5, squared-ReLU experts with no gate projection
+    and an always-on squared-ReLU shared expert. Nemotron-3-Nano-shaped
+    ratios at a smaller width; 4-bit gs64, bf16."""
+    rng = np.random.default_rng(seed)
+    H, E, k, I = hidden, n_experts, top_k, inter
+    shared = (None, gen_qproj(rng, 1, shared_inter, H, 4, 64, BF16),
+              gen_qproj(rng, 1, H, shared_inter, 4, 64, BF16))
+    return LayerSpec(H, E, k, I, BF16,
+                     router_weight=store(rng.normal(0, 1 / np.sqrt(H), size=(E, H)), BF16),
+                     router_dt=BF16, gating=orc.SIGMOID_TOPK, norm_topk=True,
+                     expert_bias=rng.uniform(-0.05, 0.05, size=E).astype(np.float32),
+                     gate=None, up=gen_qproj(rng, E, I, H, 4, 64, BF16),
+                     down=gen_qproj(rng, E, H, I, 4, 64, BF16), activation=orc.ACT_RELU2,
+                     shared=shared, routed_scale=2.5, name="nemotron")
+
+
+def cfg_gemma4(seed=0, n_experts=64, hidden=1024, inter=384, top_k=8):
+    """Gemma 4 MoE (Gemma4Text.swift:928-978): top-8 of the logits scaled by
+    hidden^-0.5, softmax over the 8, times per_expert_scale[e]; GELU-gated
+    experts; the router reads its own normalised rows. 4-bit gs64, bf16."""
+    rng = np.random.default_rng(seed)
+    H, E, k, I = hidden, n_experts, top_k, inter
+    return LayerSpec(H, E, k, I, BF16,
+                     router_weight=store(rng.normal(0, 1, size=(E, H)), BF16), router_dt=BF16,
+                     gating=orc.TOPK_THEN_SOFTMAX, logit_scale=float(np.float32(H ** -0.5)),
+                     expert_scale=rng.uniform(0.5, 1.5, size=E).astype(np.float32),
+                     gate=gen_qproj(rng, E, I, H, 4, 64, BF16), up=gen_qproj(rng, E, I, H, 4, 64, BF16),
+                     down=gen_qproj(rng, E, H, I, 4, 64, BF16), activation=orc.ACT_GEGLU,
+                     split_router_input=True, name="gemma4")
 
 
 # ------------------------------------------------------------- tolerance --

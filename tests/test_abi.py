@@ -98,6 +98,46 @@ def test_invalid_layer_rejected_on_host(mutate, expect, needle):
     assert st2 == expect
 
 
+def relu2_layer():
+    d = layer()
+    d.activation = _lib.MOE_ACT_RELU2
+    d.gate = QProj()
+    return d
+
+
+def test_router_families_accepted():
+    lib = _lib.load()
+    d = layer()
+    d.gating, d.routed_scale = _lib.MOE_SIGMOID_TOPK, 2.5
+    assert lib.moe_validate_layer(C.byref(d)) == _lib.MOE_OK
+    d = layer()
+    d.activation, d.logit_scale = _lib.MOE_ACT_GEGLU, 64 ** -0.5
+    assert lib.moe_validate_layer(C.byref(d)) == _lib.MOE_OK
+    assert lib.moe_validate_layer(C.byref(relu2_layer())) == _lib.MOE_OK
+    d = relu2_layer()
+    d.has_shared = 1
+    d.shared_up, d.shared_down = qproj(1, 128, 64), qproj(1, 64, 128)
+    assert lib.moe_validate_layer(C.byref(d)) == _lib.MOE_OK
+    assert lib.moe_layer_workspace_bytes(C.byref(d), 8) > 0
+
+
+@pytest.mark.parametrize("mutate,needle", [
+    (lambda d: setattr(d, "gate", qproj()), "no gate"),
+    (lambda d: setattr(d, "activation", 4), "activation"),
+    (lambda d: setattr(d, "logit_scale", float("nan")), "finite"),
+    (lambda d: setattr(d, "routed_scale", float("inf")), "finite"),
+    (lambda d: setattr(d, "gating", 3), "gating"),
+])
+def test_router_family_violations_rejected(mutate, needle):
+    lib = _lib.load()
+    d = relu2_layer()
+    mutate(d)
+    assert lib.moe_validate_layer(C.byref(d)) == _lib.MOE_ERR_INVALID
+    assert needle in _lib.last_error()
+    assert lib.moe_layer_forward_routed(C.byref(d), C.c_void_p(64), None, 1, C.c_void_p(64),
+                                        C.c_void_p(64), 1 << 30, None, None) == _lib.MOE_ERR_INVALID
+
+
 def test_layer_forward_checks_workspace_and_tokens():
     lib = _lib.load()
     d = layer()
@@ -129,6 +169,11 @@ def test_kernel_entry_points_validate_before_launch():
     assert lib.moe_router_topk(p, 2, 4, 8, 9, 0, 1, None, p, p, None) == _lib.MOE_ERR_INVALID
     assert lib.moe_router_topk(p, 2, 0, 8, 2, 0, 1, None, p, p, None) == _lib.MOE_ERR_INVALID
     assert lib.moe_router_topk(p, 2, 1, 600, 2, 0, 1, None, p, p, None) == _lib.MOE_ERR_UNSUPPORTED
+    assert lib.moe_router_topk(p, 2, 4, 8, 2, 3, 1, None, p, p, None) == _lib.MOE_ERR_INVALID
+    assert lib.moe_router_topk_scaled(p, 2, 4, 8, 2, 2, 1, None, float("nan"), 1.0, None, p, p,
+                                      None) == _lib.MOE_ERR_INVALID
+    assert lib.moe_activation_apply(None, p, p, 8, 2, _lib.MOE_ACT_SWIGLU, 0.0, 0.0,
+                                    None) == _lib.MOE_ERR_INVALID
     assert lib.moe_dispatch_plan(p, 4, 2, 8, p, p, p, p, None, 0, None) == _lib.MOE_ERR_WORKSPACE
     assert lib.moe_dequantize_affine(p, p, p, 2, 4, 4, 64, p, 2, None) == _lib.MOE_ERR_INVALID
     assert lib.moe_dequantize_affine(p, p, p, 2, 3, 16, 64, p, 2, None) == _lib.MOE_ERR_INVALID

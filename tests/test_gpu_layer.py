@@ -12,8 +12,8 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from moe_spec import (BF16, F16, F32, cfg_bits, cfg_gptoss, cfg_mixed, cfg_qwen3, cfg_tiny, check_close, load,
-                      store, to_numpy_f32, to_torch, zipf_router_bias)
+from moe_spec import (BF16, F16, F32, cfg_bits, cfg_gemma4, cfg_gptoss, cfg_mixed, cfg_nemotron, cfg_qwen3,
+                      cfg_tiny, check_close, load, store, to_numpy_f32, to_torch, zipf_router_bias)
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -231,18 +231,86 @@ def test_expert_matmul_mfma(bits, dt, sb, gs, gather):
 
 # ------------------------------------------------------------ whole layer --
 
+@pytest.mark.parametrize("E,k", [(8, 1), (32, 4), (64, 6), (128, 8), (512, 16)])
+@pytest.mark.parametrize("mode", ["sigmoid_bias_scaled", "sigmoid_plain", "sigmoid_no_renorm",
+                                  "gemma_scales"])
+def test_router_topk_scaled_bit_exact(E, k, mode):
+    """NemotronH sigmoid routing and Gemma 4 scaled routing through
+    moe_router_topk_scaled: ids and f32 weights bit-exact."""
+    rng = np.random.default_rng(E * 3 + k)
+    T = 96
+    logits = np.concatenate([rng.integers(-3, 4, size=(T // 2, E)).astype(np.float32),
+                             rng.normal(0, 1.5, size=(T // 2, E)).astype(np.float32)])
+    lb = store(logits, BF16)
+    lf = load(lb, BF16)
+    eb = es = None
+    ls, rs = 1.0, 1.0
+    if mode.startswith("sigmoid"):
+        gating, norm = orc.SIGMOID_TOPK, mode != "sigmoid_no_renorm"
+        if mode == "sigmoid_bias_scaled":
+            eb = rng.uniform(-0.05, 0.05, E).astype(np.float32)
+            rs = 2.5
+    else:
+        gating, norm = orc.TOPK_THEN_SOFTMAX, True
+        ls = float(np.float32(2816 ** -0.5))
+        es = rng.uniform(0.5, 1.5, E).astype(np.float32)
+    idx = torch.empty(T, k, dtype=torch.int32, device="cuda")
+    w = torch.empty(T, k, dtype=torch.float32, device="cuda")
+    ebt = None if eb is None else to_torch(eb)
+    est = None if es is None else to_torch(es)
+    lt = to_torch(lb)
+    check(_lib.load().moe_router_topk_scaled(_p(lt), BF16, T, E, k, gating, int(norm),
+                                             None if ebt is None else _p(ebt), ls, rs,
+                                             None if est is None else _p(est), _p(idx), _p(w),
+                                             _stream()))
+    torch.cuda.synchronize()
+    ref_idx, ref_w = orc.route(lf, k, gating, norm, eb, logit_scale=ls, routed_scale=rs,
+                               expert_scale=es)
+    assert np.array_equal(_u32(idx), ref_idx)
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), ref_w.view(np.uint32))
+
+
+@pytest.mark.parametrize("act", [orc.ACT_GEGLU, orc.ACT_RELU2])
+def test_activation_apply_new_kinds(act):
+    """GELU-gated and squared-ReLU elementwise activations; the bf16 GELU
+    stays finite over the reference's [-15, 15] sweep (OpsTests.swift:
+    275-302). ReLU^2 is called without a gate buffer."""
+    xs = np.arange(-15.0, 15.0 + 0.125, 0.25)
+    rng = np.random.default_rng(act)
+    g = store(np.concatenate([xs, rng.normal(0, 3, 4096 - xs.size)]), BF16)
+    u = store(rng.normal(0, 2, g.size), BF16)
+    gt, ut = to_torch(g), to_torch(u)
+    out = torch.empty_like(ut)
+    check(_lib.load().moe_activation_apply(None if act == orc.ACT_RELU2 else _p(gt), _p(ut), _p(out),
+                                           g.size, BF16, act, 0.0, 0.0, _stream()))
+    torch.cuda.synchronize()
+    got = to_numpy_f32(out)
+    gf, uf = load(g, BF16), load(u, BF16)
+    ref = np.array([orc.act(float(a), float(b), act, dt=BF16) for a, b in zip(gf, uf)], np.float32)
+    ref = load(store(ref, BF16), BF16)
+    assert np.all(np.isfinite(got))
+    if act == orc.ACT_RELU2:
+        assert np.array_equal(got, ref)
+    else:
+        # tanh from exp and the hardware reciprocal: within one bf16 ulp of the
+        # libm-tanh oracle, after the GELU's own bf16 rounding
+        assert np.all(np.abs(got - ref) <= 2.0 ** -7 * np.abs(ref) * 2.01 + 1e-6)
+
+
 def run_layer(spec, T, seed=0):
     dev = spec.device()
     x = spec.x(T, seed)
-    y, tr = dev.forward(to_torch(x), trace=True)
+    rx = spec.router_x(T, seed)  # None unless the router reads its own rows
+    y, tr = dev.forward(to_torch(x), trace=True, router_x=None if rx is None else to_torch(rx))
     torch.cuda.synchronize()
     logits_gpu = to_numpy_f32(tr["logits"])
-    logits_cpu = orc.router_logits(x, spec.act_dt, spec.router_weight, spec.router_dt, spec.router_bias)
+    logits_cpu = orc.router_logits(x if rx is None else rx, spec.act_dt, spec.router_weight,
+                                   spec.router_dt, spec.router_bias)
     ulp = np.abs(logits_cpu) * (2.0 ** -7 if spec.act_dt == BF16 else 2.0 ** -10 if spec.act_dt == F16
                                 else 2.0 ** -20) + 1e-6
     # a bias add rounds twice, so allow two storage ulps
     assert np.all(np.abs(logits_gpu - logits_cpu) <= 2.02 * ulp), "router logits"
-    y_ref, _, idx_ref, w_ref = orc.moe_layer(spec, x, given_logits=logits_gpu)
+    y_ref, _, idx_ref, w_ref = orc.moe_layer(spec, x, given_logits=logits_gpu, router_x=rx)
     assert np.array_equal(_u32(tr["topk_idx"]), idx_ref), "expert ids"
     assert np.array_equal(tr["topk_weight"].cpu().numpy().view(np.uint32), w_ref.view(np.uint32)), \
         "combine weights"
@@ -289,6 +357,32 @@ def test_layer_gptoss(gptoss, T):
 def test_layer_gptoss_expert_bias():
     run_layer(cfg_gptoss(seed=3, n_experts=8, hidden=512, inter=640, expert_bias=True), 1)
     run_layer(cfg_gptoss(seed=3, n_experts=8, hidden=512, inter=640, expert_bias=True), 5)
+
+
+@pytest.fixture(scope="module")
+def nemotron():
+    return cfg_nemotron()
+
+
+@pytest.mark.parametrize("T", [1, 5, 400])
+def test_layer_nemotron(nemotron, T):
+    """Sigmoid router + correction bias + routed scale, squared-ReLU experts
+    without a gate projection, squared-ReLU shared expert; T=400 takes the
+    matrix-core path for the routed and shared experts."""
+    run_layer(nemotron, T, seed=T)
+
+
+@pytest.fixture(scope="module")
+def gemma4():
+    return cfg_gemma4()
+
+
+@pytest.mark.parametrize("T", [1, 5, 300])
+def test_layer_gemma4(gemma4, T):
+    """Scaled logits, per-expert scale, GELU-gated experts and a router
+    input of its own; T=1 runs the one-token kernels, T=300 the matrix
+    cores."""
+    run_layer(gemma4, T, seed=T)
 
 
 @pytest.fixture(scope="module")

@@ -232,6 +232,79 @@ def test_router_matches_brute_force(E, k):
             assert np.allclose(w[t], ref, rtol=2e-5, atol=1e-9)
 
 
+def _np_sigmoid_route(l, k, norm, eb, rs):
+    """NemotronHText.swift:844-867 restated with a full stable sort; the
+    sigmoid uses the pinned exp (or_expf, within 2 ulp of exp)."""
+    raw = np.array([np.float32(1.0) / (np.float32(1.0) + np.float32(orc.expf(-float(v))))
+                    for v in l], np.float32)
+    score = raw + eb if eb is not None else raw
+    sel = _brute_topk(score, k)
+    fw = raw[sel].astype(np.float32)
+    if k > 1 and norm:
+        s = np.float32(0)
+        for v in fw:
+            s = np.float32(s + v)
+        fw = fw / np.float32(s + np.float32(1e-20))
+    return sel, (fw * np.float32(rs)).astype(np.float32), raw
+
+
+@pytest.mark.parametrize("E,k", [(8, 1), (32, 4), (64, 6), (128, 8), (256, 8)])
+@pytest.mark.parametrize("norm,bias,rs", [(True, True, 2.5), (True, False, 1.0), (False, True, 1.0)])
+def test_sigmoid_router_matches_brute_force(E, k, norm, bias, rs):
+    rng = np.random.default_rng(E * 7 + k)
+    T = 48
+    logits = rng.integers(-3, 4, size=(T, E)).astype(np.float32)
+    logits[::2] = orc.round_dt(rng.normal(0, 1.5, size=(T // 2, E)), orc.BF16)
+    eb = rng.uniform(-0.05, 0.05, size=E).astype(np.float32) if bias else None
+    idx, w = orc.route(logits, k, orc.SIGMOID_TOPK, norm, eb, routed_scale=rs)
+    for t in range(T):
+        sel, ref, raw = _np_sigmoid_route(logits[t], k, norm, eb, rs)
+        assert idx[t].tolist() == sel
+        assert np.array_equal(w[t], ref)
+        # invariants the reference fixes: the weights follow the unbiased
+        # sigmoid of the picked logits; renormalised ones sum to the routed
+        # scale; a single pick is never renormalised
+        p = 1.0 / (1.0 + np.exp(-logits[t, sel].astype(np.float64)))
+        if k > 1 and norm:
+            assert abs(float(w[t].astype(np.float64).sum()) - rs) < 1e-5 * rs
+            assert np.allclose(w[t], rs * p / p.sum(), rtol=1e-5)
+        else:
+            assert np.allclose(w[t], rs * p, rtol=1e-5)
+    if bias:
+        # the correction bias steers the selection but never the weights: a
+        # router that weighted by the biased score would differ here
+        biased = np.array([[(1 / (1 + math.exp(-float(logits[t, e])))) + eb[e] for e in idx[t]]
+                           for t in range(T)])
+        assert not np.allclose(w / rs, biased / (biased.sum(1, keepdims=True) if norm and k > 1 else 1),
+                               rtol=1e-3)
+
+
+def test_logit_and_expert_scales():
+    """Gemma 4 routing (Gemma4Text.swift:938-950): top-k of hidden^-0.5-scaled
+    logits, softmax over the k, times per_expert_scale[e]."""
+    rng = np.random.default_rng(11)
+    T, E, k = 32, 64, 8
+    logits = orc.round_dt(rng.normal(0, 20, size=(T, E)), orc.BF16)
+    ls = float(np.float32(2816 ** -0.5))
+    es = rng.uniform(0.5, 1.5, size=E).astype(np.float32)
+    idx, w = orc.route(logits, k, orc.TOPK_THEN_SOFTMAX, True, logit_scale=ls, expert_scale=es)
+    idx0, w0 = orc.route(logits, k, orc.TOPK_THEN_SOFTMAX, True, logit_scale=ls)
+    assert np.array_equal(idx, idx0)
+    assert np.array_equal(w, (w0 * es[idx]).astype(np.float32))
+    for t in range(T):
+        sel = _brute_topk(logits[t], k)  # a positive scale keeps the order
+        z = logits[t, sel].astype(np.float64) * ls
+        p = np.exp(z - z.max())
+        assert idx[t].tolist() == sel
+        assert np.allclose(w0[t], p / p.sum(), rtol=2e-5)
+        # the scale sets the temperature: unscaled logits give other weights
+        q = np.exp(logits[t, sel].astype(np.float64) - logits[t, sel].max())
+        assert not np.allclose(w0[t], q / q.sum(), rtol=1e-2)
+    # the per-expert scale applies after the softmax: the scaled weights no
+    # longer sum to one
+    assert not np.allclose(w.sum(1), 1.0, atol=1e-3)
+
+
 def test_softmax_degenerate_is_uniform():
     out = orc.softmax(np.full(5, -np.inf, np.float32))
     assert np.allclose(out, 0.2)
@@ -351,6 +424,40 @@ def test_gptoss_activation_closed_form():
         assert abs(orc.act(gv, uv, orc.ACT_GPTOSS, a, lim) - ref) < 1e-5 * max(1, abs(ref))
 
 
+def test_gelu_kat():
+    """The reference's GELU test (OpsTests.swift:254-302): the tanh form
+    within 1e-3 at its four points, finite in bf16 over [-15, 15]."""
+    g = GOLD["gelu"]
+    c = math.sqrt(2.0 / math.pi)
+    for v in g["x"]:
+        ref = 0.5 * v * (1 + math.tanh(c * (v + 0.044715 * v ** 3)))
+        assert abs(orc.gelu(v) - ref) < g["tol"]
+    sw = g["bf16_finite_sweep"]
+    xs = np.arange(sw["from"], sw["through"] + sw["by"] / 2, sw["by"])
+    for v in orc.round_dt(xs, orc.BF16):
+        out = orc.act(float(v), 1.0, orc.ACT_GEGLU, dt=orc.BF16)
+        assert math.isfinite(out)
+        ref = 0.5 * v * (1 + math.tanh(c * (v + 0.044715 * v ** 3)))
+        assert abs(out - ref) <= 2 ** -7 * abs(ref) + 1e-6
+    # the erf form differs from the tanh form by more than a bf16 ulp near
+    # x = -2.5 .. -3.5: the oracle follows the tanh form
+    v = -3.0
+    erf_form = 0.5 * v * (1 + math.erf(v / math.sqrt(2)))
+    assert abs(orc.gelu(v) - erf_form) > 1e-4
+
+
+def test_geglu_and_relu2_closed_forms():
+    # GEGLU stores the GELU in the activation dtype before the product
+    # (Gemma4Text.swift:965)
+    for gv, uv in [(0.7, 3.0), (-1.3, 2.5), (2.2, -0.9), (9.0, 1.5)]:
+        gl = float(orc.round_dt(np.array([orc.gelu(gv)], np.float32), orc.BF16)[0])
+        assert orc.act(gv, uv, orc.ACT_GEGLU, dt=orc.BF16) == np.float32(gl * uv)
+        assert orc.act(gv, uv, orc.ACT_GEGLU) == np.float32(np.float32(orc.gelu(gv)) * np.float32(uv))
+    # squared ReLU of the up projection; no gate (NemotronHText.swift:759-760)
+    for gv, uv in [(5.0, 1.5), (-5.0, 1.5), (0.0, -2.0), (1.0, 0.0), (3.0, -0.25)]:
+        assert orc.act(gv, uv, orc.ACT_RELU2) == np.float32(max(uv, 0.0) ** 2)
+
+
 def test_unpermute_kat():
     g = GOLD["unpermute"]
     Y = np.array(g["expert_outputs"], np.float32)
@@ -456,6 +563,84 @@ def test_layer_tiny_matches_float64_composition():
             acc = acc + np.float32(rd(np.float32(w[t, s]))) * yv.astype(np.float32)
         ref[t] = rd(acc)
     check_close(load(y, spec.act_dt), ref, spec.act_dt, "tiny layer vs float64 composition")
+
+
+def _composition(spec, x, idx, w, rx=None):
+    """float64 composition of independently dequantised experts with the
+    storage rounding points of the reference: gate/up (or the single up
+    projection) rounded, the activation rounded, down rounded, the combine in
+    f32 with each weight rounded, then the shared expert added."""
+    from moe_spec import load, store
+    T, H, I = x.shape[0], spec.hidden, spec.intermediate
+    xf = load(x, spec.act_dt).astype(np.float64)
+    rd = lambda a: load(store(a, spec.act_dt), spec.act_dt).astype(np.float64)  # noqa: E731
+
+    def dense(q, e, n, kk):
+        return _dense(q.weight[e], load(q.scales[e], q.sb_dt), load(q.biases[e], q.sb_dt), q.bits,
+                      q.gs, n, kk)
+
+    def expert(gq, uq, dq, e, xv, n):
+        u = rd(dense(uq, e, n, spec.hidden) @ xv)
+        if spec.activation == orc.ACT_RELU2:
+            a = rd(np.maximum(u, 0.0) ** 2)
+        elif spec.activation == orc.ACT_GEGLU:
+            g = rd(dense(gq, e, n, spec.hidden) @ xv)
+            c = math.sqrt(2.0 / math.pi)
+            a = rd(rd(0.5 * g * (1 + np.tanh(c * (g + 0.044715 * g ** 3)))) * u)
+        else:
+            g = rd(dense(gq, e, n, spec.hidden) @ xv)
+            a = rd(g / (1 + np.exp(-g)) * u)
+        return rd(dense(dq, e, spec.hidden, n) @ a)
+
+    ref = np.zeros((T, H))
+    for t in range(T):
+        acc = np.zeros(H, np.float32)
+        for s in range(spec.top_k):
+            e = idx[t, s]
+            yv = expert(spec.gate, spec.up, spec.down, e, xf[t], I)
+            acc = acc + np.float32(rd(np.float32(w[t, s]))) * yv.astype(np.float32)
+        out = rd(acc)
+        if spec.shared is not None:
+            sg, su, sd = spec.shared
+            out = rd(out + expert(sg, su, sd, 0, xf[t], su.n))
+        ref[t] = out
+    return ref
+
+
+@pytest.mark.parametrize("family", ["nemotron", "gemma4"])
+def test_layer_family_matches_float64_composition(family):
+    """NemotronH (sigmoid router, squared-ReLU experts without a gate,
+    squared-ReLU shared expert, routed scale) and Gemma 4 (scaled logits,
+    per-expert scale, GELU-gated experts, a router input of its own) layers
+    against the float64 composition, with routing from the numpy
+    restatements above."""
+    from moe_spec import cfg_gemma4, cfg_nemotron, load
+    spec = (cfg_nemotron(hidden=256, inter=128, shared_inter=192, n_experts=16, top_k=4)
+            if family == "nemotron" else cfg_gemma4(hidden=256, inter=128, n_experts=16, top_k=4))
+    T = 6
+    x = spec.x(T)
+    rx = spec.router_x(T)
+    y, logits, idx, w = orc.moe_layer(spec, x, router_x=rx)
+    lx = x if rx is None else rx
+    ref_logits = orc.router_logits(lx, spec.act_dt, spec.router_weight, spec.router_dt)
+    assert np.array_equal(ref_logits, logits)
+    for t in range(T):
+        if family == "nemotron":
+            sel, ref_w, _ = _np_sigmoid_route(logits[t], spec.top_k, True, spec.expert_bias,
+                                              spec.routed_scale)
+        else:
+            sel = _brute_topk(logits[t], spec.top_k)
+            z = logits[t, sel].astype(np.float64) * spec.logit_scale
+            p = np.exp(z - z.max())
+            ref_w = (p / p.sum()) * spec.expert_scale[sel]
+        assert idx[t].tolist() == sel
+        assert np.allclose(w[t], ref_w, rtol=2e-5)
+    ref = _composition(spec, x, idx, w)
+    check_close(load(y, spec.act_dt), ref, spec.act_dt, f"{family} layer vs float64 composition")
+    if family == "gemma4":
+        # routing on the expert input instead of the router's rows is caught
+        y_same = orc.moe_layer(spec, x)[0]
+        assert not np.array_equal(y_same.view(np.uint16), y.view(np.uint16))
 
 
 def test_float_bar_catches_planted_mistakes():
