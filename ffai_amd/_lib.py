@@ -1,4 +1,4 @@
-"""ctypes binding of libmoehip.so (include/moe_hip.h).
+"""ctypes binding of libmoehip.so (include/moe_hip.h, include/moe_safetensors.h).
 
 This is the Python view of the C ABI that a Swift (or any FFI) caller binds;
 tests and bench.py drive the library through it with device buffers owned by
@@ -17,6 +17,9 @@ MOE_OK, MOE_ERR_INVALID, MOE_ERR_UNSUPPORTED, MOE_ERR_WORKSPACE, MOE_ERR_HIP = r
 MOE_F32, MOE_F16, MOE_BF16 = 0, 1, 2
 MOE_SOFTMAX_THEN_TOPK, MOE_TOPK_THEN_SOFTMAX, MOE_SIGMOID_TOPK = 0, 1, 2
 MOE_ACT_SWIGLU, MOE_ACT_GPTOSS, MOE_ACT_GEGLU, MOE_ACT_RELU2 = 0, 1, 2, 3
+(MOE_ST_F32, MOE_ST_F16, MOE_ST_BF16, MOE_ST_I32, MOE_ST_U32, MOE_ST_I64, MOE_ST_U64, MOE_ST_I8,
+ MOE_ST_U8) = range(9)
+MOE_ST_MAX_DIMS = 8
 
 EXPORTS = [
     "moe_last_error_string", "moe_version", "moe_validate_qproj", "moe_validate_layer",
@@ -26,6 +29,9 @@ EXPORTS = [
     "moe_expert_matmul", "moe_activation_apply", "moe_unpermute", "moe_layer_workspace_bytes",
     "moe_layer_forward", "moe_layer_forward_routed", "moe_layer_create", "moe_layer_destroy",
     "moe_layer_decode", "moe_layer_decode_many",
+    "moe_st_open", "moe_st_close", "moe_st_count", "moe_st_name", "moe_st_info", "moe_st_read_host",
+    "moe_st_upload", "moe_st_is_quantized", "moe_st_stacked_bytes", "moe_st_load_stacked",
+    "moe_st_load_stacked_many",
 ]
 
 
@@ -108,12 +114,31 @@ def load():
     lib.moe_layer_destroy.restype = None
     lib.moe_layer_decode.argtypes = [vp, vp, vp, st]
     lib.moe_layer_decode_many.argtypes = [vp, vp, i32, vp, st]
+    lib.moe_st_open.argtypes = [C.c_char_p, C.POINTER(vp)]
+    lib.moe_st_close.argtypes = [vp]
+    lib.moe_st_close.restype = None
+    lib.moe_st_count.argtypes = [vp]
+    lib.moe_st_count.restype = C.c_int64
+    lib.moe_st_name.argtypes = [vp, C.c_int64]
+    lib.moe_st_name.restype = C.c_char_p
+    lib.moe_st_info.argtypes = [vp, C.c_char_p, C.POINTER(i32), C.POINTER(i32),
+                                C.POINTER(C.c_int64), C.POINTER(sz)]
+    lib.moe_st_read_host.argtypes = [vp, C.c_char_p, vp, sz]
+    lib.moe_st_upload.argtypes = [vp, C.c_char_p, vp, sz, st]
+    lib.moe_st_is_quantized.argtypes = [vp, C.c_char_p]
+    lib.moe_st_is_quantized.restype = i32
+    lib.moe_st_stacked_bytes.argtypes = [vp, C.c_char_p, i32, C.POINTER(sz)]
+    lib.moe_st_load_stacked.argtypes = [vp, C.c_char_p, i32, vp, sz, C.POINTER(QProj), st]
+    lib.moe_st_load_stacked_many.argtypes = [vp, i32, C.POINTER(C.c_char_p), i32, C.POINTER(vp),
+                                             C.POINTER(sz), C.POINTER(QProj), st]
     for name in ["moe_validate_qproj", "moe_validate_layer", "moe_derive_bits", "moe_router_logits",
                  "moe_router_topk", "moe_router_topk_scaled", "moe_dispatch_plan",
                  "moe_dequantize_affine", "moe_expert_matmul", "moe_activation_apply",
                  "moe_unpermute", "moe_layer_forward", "moe_layer_forward_routed",
                  "moe_layer_create", "moe_layer_decode",
-                 "moe_layer_decode_many"]:
+                 "moe_layer_decode_many", "moe_st_open", "moe_st_info", "moe_st_read_host",
+                 "moe_st_upload", "moe_st_stacked_bytes", "moe_st_load_stacked",
+                 "moe_st_load_stacked_many"]:
         getattr(lib, name).restype = C.c_int
     _lib = lib
     return lib

@@ -99,14 +99,21 @@ size_t gemv_smem_bytes(int xdt, int K, int tok_chunk) {
 
 }  // namespace moe
 
-using namespace moe;
-
 // ---------------------------------------------------------------------------
 // errors
 // ---------------------------------------------------------------------------
-namespace {
+namespace moe {
 
 thread_local std::string g_err;
+
+void set_error_text(const char* msg) { g_err = msg; }
+void clear_error_text() { g_err.clear(); }
+
+}  // namespace moe
+
+using namespace moe;
+
+namespace {
 
 moe_status fail(moe_status s, const char* fmt, ...) {
   char buf[512];
@@ -114,12 +121,12 @@ moe_status fail(moe_status s, const char* fmt, ...) {
   va_start(ap, fmt);
   vsnprintf(buf, sizeof(buf), fmt, ap);
   va_end(ap);
-  g_err = buf;
+  set_error_text(buf);
   return s;
 }
 
 moe_status ok() {
-  g_err.clear();
+  clear_error_text();
   return MOE_OK;
 }
 

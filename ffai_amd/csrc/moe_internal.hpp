@@ -11,6 +11,11 @@ namespace moe {
 
 enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
 
+// The thread-local text behind moe_last_error_string() (api.cpp), shared by
+// every translation unit of the C ABI.
+void set_error_text(const char* msg);
+void clear_error_text();
+
 // Optional events recorded by the dispatch of one kernel itself (its start
 // and end timestamps, hipExtLaunchKernel); null entries record nothing.
 struct KEvents {
