@@ -27,7 +27,8 @@ EXPORTS = [
     "moe_dispatch_workspace_bytes",
     "moe_dispatch_plan", "moe_dequantize_affine", "moe_expert_matmul_workspace_bytes",
     "moe_expert_matmul", "moe_activation_apply", "moe_unpermute", "moe_layer_workspace_bytes",
-    "moe_layer_forward", "moe_layer_forward_routed", "moe_layer_create", "moe_layer_destroy",
+    "moe_layer_forward", "moe_layer_forward_routed", "moe_layer_forward_residual",
+    "moe_add_rmsnorm", "moe_layer_create", "moe_layer_destroy",
     "moe_layer_decode", "moe_layer_decode_many",
     "moe_st_open", "moe_st_close", "moe_st_count", "moe_st_name", "moe_st_info", "moe_st_read_host",
     "moe_st_upload", "moe_st_is_quantized", "moe_st_stacked_bytes", "moe_st_load_stacked",
@@ -109,6 +110,9 @@ def load():
                                       C.POINTER(LayerTrace), st]
     lib.moe_layer_forward_routed.argtypes = [C.POINTER(LayerDesc), vp, vp, i32, vp, vp, sz,
                                              C.POINTER(LayerTrace), st]
+    lib.moe_layer_forward_residual.argtypes = [C.POINTER(LayerDesc), vp, vp, vp, C.c_float, i32,
+                                               vp, vp, vp, sz, C.POINTER(LayerTrace), st]
+    lib.moe_add_rmsnorm.argtypes = [vp, vp, vp, C.c_float, i32, i32, i32, vp, vp, st]
     lib.moe_layer_create.argtypes = [C.POINTER(LayerDesc), C.POINTER(vp)]
     lib.moe_layer_destroy.argtypes = [vp]
     lib.moe_layer_destroy.restype = None
@@ -135,6 +139,7 @@ def load():
                  "moe_router_topk", "moe_router_topk_scaled", "moe_dispatch_plan",
                  "moe_dequantize_affine", "moe_expert_matmul", "moe_activation_apply",
                  "moe_unpermute", "moe_layer_forward", "moe_layer_forward_routed",
+                 "moe_layer_forward_residual", "moe_add_rmsnorm",
                  "moe_layer_create", "moe_layer_decode",
                  "moe_layer_decode_many", "moe_st_open", "moe_st_info", "moe_st_read_host",
                  "moe_st_upload", "moe_st_stacked_bytes", "moe_st_load_stacked",

@@ -371,6 +371,7 @@ struct Workspace {
   size_t logits, idx, w, counts, offsets, used, perm, inv, act, Y, plan_scratch, tiles;
   size_t r_plan, r_tiles;  // router projection on the matrix cores
   size_t s_off, s_used, s_act, s_out, s_logit, s_tiles;
+  size_t xn, res;  // decoder step before the block: normalised rows, residual
   size_t total;
 };
 
@@ -408,6 +409,8 @@ Workspace layout(const moe_layer_desc* d, int T) {
     w.s_logit = take((size_t)T * ds);
     w.s_tiles = take((1 + 2 * (size_t)gemm_max_tiles(T, 1)) * 4);
   }
+  w.xn = take((size_t)T * H * ds);
+  w.res = take((size_t)T * H * ds);
   w.total = o;
   return w;
 }
@@ -839,7 +842,7 @@ bool dec1_supported(const moe_layer_desc* d) {
 
 // down projection + weighted combine of one token (down1_kernel).
 moe_status run_down1(const moe_layer_desc* d, void* y, const uint32_t* idx, const float* w,
-                     const void* act, hipStream_t st, KEvents ev) {
+                     const void* act, hipStream_t st, KEvents ev, const void* res = nullptr) {
   const int k = d->top_k, H = d->hidden, I = d->intermediate;
   const Dec1Geom dg = dec1_geom(H, I, group_shift(d->down.group_size), k, true);
   Down1Args dn{};
@@ -848,6 +851,7 @@ moe_status run_down1(const moe_layer_desc* d, void* y, const uint32_t* idx, cons
   dn.act = act;
   dn.p = to_proj(d->down);
   dn.out = y;
+  dn.res = res;
   dn.k = k;
   dn.N = H;
   dn.K = I;
@@ -859,10 +863,33 @@ moe_status run_down1(const moe_layer_desc* d, void* y, const uint32_t* idx, cons
   return MOE_OK;
 }
 
-// rx: the router's input rows (x for every family but Gemma 4).
+// The decoder steps around the block (Qwen3xText.swift:2640-2670,
+// 1015-1035): x = rmsnorm(h + m) * nw is what the block reads, and the
+// residual h + m is added to its output before the final rounding.
+struct DecoderStep {
+  const void* h;
+  const void* m;
+  const void* nw;
+  float eps;
+  void* res_out;  // nullable: the residual row(s), else workspace
+};
+
+// rx: the router's input rows (x for every family but Gemma 4). With `step`,
+// x and rx are ignored: both read the normalised rows.
 moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx, int T, void* y,
-                         void* ws, size_t ws_bytes, const moe_layer_trace* tr, hipStream_t st) {
+                         void* ws, size_t ws_bytes, const moe_layer_trace* tr, hipStream_t st,
+                         const DecoderStep* step = nullptr) {
   MOE_TRY(validate_layer_impl(d));
+  if (step) {
+    if (!step->h || !step->m || !step->nw)
+      return fail(MOE_ERR_INVALID, "Ops.addAndRmsNorm: input is NULL");
+    if (d->hidden % 8 != 0)
+      return fail(MOE_ERR_UNSUPPORTED, "Ops.addAndRmsNorm: hidden (%d) must be a multiple of 8",
+                  d->hidden);
+    if (!(step->eps >= 0.f) || !std::isfinite(step->eps))
+      return fail(MOE_ERR_INVALID, "Ops.addAndRmsNorm: eps must be finite and non-negative");
+    x = rx = step->h;  // placeholders until the normalised rows exist
+  }
   if (!x || !rx || !y) return fail(MOE_ERR_INVALID, "MoELayer: input/output is NULL");
   if (T <= 0) return fail(MOE_ERR_INVALID, "MoELayer.decodeMany: T must be positive");
   const Workspace w = layout(d, T);
@@ -880,8 +907,30 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     return ev;
   };
 
+  // 0. the decoder step before the block: residual add + RMSNorm, fused into
+  //    the router projection for one token (Qwen3xText.swift:2650-2660)
+  const void* res = nullptr;
+  bool logits_done = false;
+  if (step) {
+    void* xn = at<void>(ws, w.xn);
+    void* rs = step->res_out ? step->res_out : at<void>(ws, w.res);
+    res = rs;
+    if (T == 1 && launch_router_logits_norm(step->h, step->m, step->nw, step->eps, xdt, H,
+                                            d->router_weight, d->router_dtype, d->router_bias, E,
+                                            at<void>(ws, w.logits), rs, xn, st) == hipSuccess) {
+      logits_done = true;
+    } else {
+      (void)hipGetLastError();  // a refused fused launch leaves no error behind
+      MOE_HIP(launch_add_rmsnorm(step->h, step->m, step->nw, step->eps, T, H, xdt, rs, xn, st),
+              "add + RMSNorm launch");
+    }
+    x = rx = xn;
+  }
+
   // 1. router projection (MoELayer.swift:540 / 689-690)
-  if (router_gemm_ok(d, T)) {
+  if (logits_done) {
+    // done above
+  } else if (router_gemm_ok(d, T)) {
     MOE_TRY(run_router_gemm(d, rx, T, at<void>(ws, w.logits), at<uint32_t>(ws, w.r_plan),
                             at<uint32_t>(ws, w.r_tiles), st));
   } else {
@@ -921,10 +970,11 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     MOE_HIP(launch_gateup1(d->gate.bits, xdt, d->gate.sb_dtype, g, gg.rm, gg.grid, st, kev(0)),
             "gate/up decode launch");
     MOE_TRY(shared_expert(d, x, T, ws, w, st, &smode));
-    MOE_TRY(run_down1(d, y, g.idx, g.w, g.act, st, kev(1)));
+    // the residual goes into the last store: down1's without a shared expert
+    MOE_TRY(run_down1(d, y, g.idx, g.w, g.act, st, kev(1), smode ? nullptr : res));
     if (smode)
       MOE_HIP(launch_add_shared(y, at<void>(ws, w.s_out), at<void>(ws, w.s_logit), smode, T, H, xdt,
-                                st),
+                                st, res),
               "shared add launch");
   } else {
     // 2. selection + dispatch plan (MoELayer.swift:706-792)
@@ -968,7 +1018,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     }
     MOE_HIP(launch_unpermute(at<void>(ws, w.Y), at<uint32_t>(ws, w.inv), at<float>(ws, w.w), T, H,
                              k, y, xdt, smode ? at<void>(ws, w.s_out) : nullptr,
-                             smode ? at<void>(ws, w.s_logit) : nullptr, smode, st),
+                             smode ? at<void>(ws, w.s_logit) : nullptr, smode, st, res),
             "unpermute launch");
   }
   MOE_TRY(copy_trace(d, T, ws, w, tr, st));
@@ -981,6 +1031,39 @@ extern "C" moe_status moe_layer_forward(const moe_layer_desc* d, const void* x, 
                                         void* workspace, size_t workspace_bytes,
                                         const moe_layer_trace* trace, hipStream_t stream) {
   MOE_TRY(layer_forward(d, x, x, T, y, workspace, workspace_bytes, trace, stream));
+  return ok();
+}
+
+extern "C" moe_status moe_layer_forward_residual(const moe_layer_desc* d, const void* h,
+                                                 const void* mixer_out, const void* norm_weight,
+                                                 float eps, int32_t T, void* y,
+                                                 void* residual_out, void* workspace,
+                                                 size_t workspace_bytes,
+                                                 const moe_layer_trace* trace,
+                                                 hipStream_t stream) {
+  const DecoderStep step{h, mixer_out, norm_weight, eps, residual_out};
+  MOE_TRY(layer_forward(d, nullptr, nullptr, T, y, workspace, workspace_bytes, trace, stream,
+                        &step));
+  return ok();
+}
+
+extern "C" moe_status moe_add_rmsnorm(const void* a, const void* b, const void* weight, float eps,
+                                      int32_t n_rows, int32_t row_size, int32_t dtype,
+                                      void* residual_out, void* normed_out, hipStream_t stream) {
+  if (!a || !b || !weight || !residual_out || !normed_out)
+    return fail(MOE_ERR_INVALID, "Ops.addAndRmsNorm: NULL pointer");
+  if (n_rows <= 0 || row_size <= 0)
+    return fail(MOE_ERR_INVALID, "Ops.addAndRmsNorm: n must be positive (got %d)", row_size);
+  if (!dt_ok(dtype)) return fail(MOE_ERR_INVALID, "Ops.addAndRmsNorm: bad dtype");
+  if (row_size % 8 != 0 || row_size > kMaxHidden)
+    return fail(MOE_ERR_UNSUPPORTED,
+                "Ops.addAndRmsNorm: row size %d must be a multiple of 8 and at most %d", row_size,
+                kMaxHidden);
+  if (!(eps >= 0.f) || !std::isfinite(eps))
+    return fail(MOE_ERR_INVALID, "Ops.addAndRmsNorm: eps must be finite and non-negative");
+  MOE_HIP(launch_add_rmsnorm(a, b, weight, eps, n_rows, row_size, dtype, residual_out, normed_out,
+                             stream),
+          "add + RMSNorm launch");
   return ok();
 }
 

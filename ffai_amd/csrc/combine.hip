@@ -9,6 +9,12 @@
 //                  1054-1103): y = round(routed + sigmoid(g) * shared)
 //   activation     Ops.swiglu (Ops.swift:6411-6460) / GPT-OSS clamped swish
 //   dequantize     QuantizedOps.dequantizeAffine (QuantizedOps.swift:62-221)
+//   add + RMSNorm  Ops.addAndRmsNorm (Ops.swift:676-730), the decoder step
+//                  before the MoE block (Qwen3xText.swift:2650-2660)
+//   residual       the decoder step after it folded into the final store:
+//                  Ops.sigmoidScalarFMAResidual (OpsFused.swift:699-753),
+//                  y = round(residual + routed + sigmoid(g) * shared), or
+//                  y = round(residual + routed) without a shared expert
 #include "moe_common.hpp"
 #include "moe_internal.hpp"
 
@@ -54,13 +60,15 @@ __device__ __forceinline__ float shared_gate(int mode, const XT* logit, int t) {
 }
 
 // One block per token; threads stride over hidden 8 values at a time.
+// res (nullable): the decoder residual added before the final rounding.
 template <typename XT>
 __global__ __launch_bounds__(256) void unpermute_kernel(const XT* __restrict__ Y,
                                                         const uint32_t* __restrict__ inv,
                                                         const float* __restrict__ w, int T, int H,
                                                         int k, XT* __restrict__ out,
                                                         const XT* __restrict__ sout,
-                                                        const XT* __restrict__ slogit, int smode) {
+                                                        const XT* __restrict__ slogit, int smode,
+                                                        const XT* __restrict__ res) {
   const int t = blockIdx.x;
   const uint32_t M = (uint32_t)T * (uint32_t)k;
   const float g = smode ? shared_gate<XT>(smode, slogit, t) : 0.f;
@@ -77,6 +85,12 @@ __global__ __launch_bounds__(256) void unpermute_kernel(const XT* __restrict__ Y
     }
 #pragma unroll
     for (int j = 0; j < 8; j++) acc[j] = round_to<XT>(acc[j]);
+    if (res) {
+      float rv[8];
+      Vec8<XT>::load(res + (size_t)t * H + h, rv);
+#pragma unroll
+      for (int j = 0; j < 8; j++) acc[j] = rv[j] + acc[j];
+    }
     if (smode) {
       float sv[8];
       Vec8<XT>::load(sout + (size_t)t * H + h, sv);
@@ -91,13 +105,19 @@ template <typename XT>
 __global__ __launch_bounds__(256) void add_shared_kernel(XT* __restrict__ y,
                                                          const XT* __restrict__ sout,
                                                          const XT* __restrict__ slogit, int smode,
-                                                         int H) {
+                                                         int H, const XT* __restrict__ res) {
   const int t = blockIdx.x;
   const float g = shared_gate<XT>(smode, slogit, t);
   for (int h = threadIdx.x * 8; h < H; h += blockDim.x * 8) {
     float a[8], b[8];
     Vec8<XT>::load(y + (size_t)t * H + h, a);
     Vec8<XT>::load(sout + (size_t)t * H + h, b);
+    if (res) {
+      float rv[8];
+      Vec8<XT>::load(res + (size_t)t * H + h, rv);
+#pragma unroll
+      for (int j = 0; j < 8; j++) a[j] = rv[j] + a[j];
+    }
 #pragma unroll
     for (int j = 0; j < 8; j++) a[j] = a[j] + g * b[j];
     Vec8<XT>::store(y + (size_t)t * H + h, a);
@@ -115,6 +135,54 @@ __global__ __launch_bounds__(256) void activation_kernel(const XT* __restrict__ 
        i += (int64_t)gridDim.x * blockDim.x) {
     const float gv = gated ? to_f<XT>(g[i]) : 0.0f;
     out[i] = from_f<XT>(apply_act<XT>(gv, to_f<XT>(u[i]), act, alpha, limit));
+  }
+}
+
+// One block per row: s = round(a + b) stored to res, then
+// xn = round(s / sqrt(mean(s^2) + eps) * w) stored to xn. A thread keeps its
+// (up to kNormChunks) 8-value chunks in registers between the two halves.
+constexpr int kNormChunks = 4;  // rows up to 256 * 8 * 4 = 8192 values
+
+template <typename XT>
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const XT* __restrict__ a,
+                                                          const XT* __restrict__ b,
+                                                          const XT* __restrict__ w, float eps,
+                                                          int H, XT* __restrict__ res,
+                                                          XT* __restrict__ xn) {
+  __shared__ float part[4];
+  const size_t row = (size_t)blockIdx.x * H;
+  float sv[kNormChunks][8];
+  float ssq = 0.f;
+#pragma unroll
+  for (int c = 0; c < kNormChunks; c++) {
+    const int h = (threadIdx.x + c * 256) * 8;
+    if (h < H) {
+      float av[8], bv[8];
+      Vec8<XT>::load(a + row + h, av);
+      Vec8<XT>::load(b + row + h, bv);
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        sv[c][j] = round_to<XT>(av[j] + bv[j]);
+        ssq = __builtin_fmaf(sv[c][j], sv[c][j], ssq);
+      }
+      Vec8<XT>::store(res + row + h, sv[c]);
+    }
+  }
+  ssq = group_sum(ssq, 6);
+  if ((threadIdx.x & 63) == 63) part[threadIdx.x >> 6] = ssq;
+  __syncthreads();
+  const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+  const float rms = sqrtf(tot / (float)H + eps);
+#pragma unroll
+  for (int c = 0; c < kNormChunks; c++) {
+    const int h = (threadIdx.x + c * 256) * 8;
+    if (h < H) {
+      float wv[8], o[8];
+      Vec8<XT>::load(w + h, wv);
+#pragma unroll
+      for (int j = 0; j < 8; j++) o[j] = sv[c][j] / rms * wv[j];
+      Vec8<XT>::store(xn + row + h, o);
+    }
   }
 }
 
@@ -146,11 +214,12 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const uint32_t* __restr
 
 hipError_t launch_unpermute(const void* Y, const uint32_t* inv, const float* w, int T, int H,
                             int k, void* out, int dt, const void* shared_out,
-                            const void* shared_logit, int shared_mode, hipStream_t st) {
+                            const void* shared_logit, int shared_mode, hipStream_t st,
+                            const void* res) {
 #define MOE_UP(XT)                                                                            \
   hipLaunchKernelGGL((unpermute_kernel<XT>), dim3(T), dim3(256), 0, st, (const XT*)Y, inv, w, \
                      T, H, k, (XT*)out, (const XT*)shared_out, (const XT*)shared_logit,       \
-                     shared_mode);                                                            \
+                     shared_mode, (const XT*)res);                                            \
   return hipGetLastError();
   MOE_BY_DT(dt, MOE_UP)
 #undef MOE_UP
@@ -158,13 +227,27 @@ hipError_t launch_unpermute(const void* Y, const uint32_t* inv, const float* w, 
 }
 
 hipError_t launch_add_shared(void* y, const void* shared_out, const void* shared_logit,
-                             int shared_mode, int T, int H, int dt, hipStream_t st) {
+                             int shared_mode, int T, int H, int dt, hipStream_t st,
+                             const void* res) {
 #define MOE_AS(XT)                                                                        \
   hipLaunchKernelGGL((add_shared_kernel<XT>), dim3(T), dim3(256), 0, st, (XT*)y,          \
-                     (const XT*)shared_out, (const XT*)shared_logit, shared_mode, H);      \
+                     (const XT*)shared_out, (const XT*)shared_logit, shared_mode, H,       \
+                     (const XT*)res);                                                      \
   return hipGetLastError();
   MOE_BY_DT(dt, MOE_AS)
 #undef MOE_AS
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_add_rmsnorm(const void* a, const void* b, const void* w, float eps, int T,
+                              int H, int dt, void* res, void* xn, hipStream_t st) {
+  if (H % 8 != 0 || H > 256 * 8 * kNormChunks) return hipErrorInvalidValue;
+#define MOE_AN(XT)                                                                          \
+  hipLaunchKernelGGL((add_rmsnorm_kernel<XT>), dim3(T), dim3(256), 0, st, (const XT*)a,     \
+                     (const XT*)b, (const XT*)w, eps, H, (XT*)res, (XT*)xn);                \
+  return hipGetLastError();
+  MOE_BY_DT(dt, MOE_AN)
+#undef MOE_AN
   return hipErrorInvalidValue;
 }
 

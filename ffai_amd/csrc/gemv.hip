@@ -385,6 +385,7 @@ __global__ __launch_bounds__(512) void down1_kernel(const Down1Args a) {
     if (row >= N) break;
     float acc = 0.f;
     for (int qq = 0; qq < a.k; qq++) acc += wr[qq] * ys[qq * rpb + t];
+    if (a.res) acc = to_f<XT>(reinterpret_cast<const XT*>(a.res)[row]) + round_to<XT>(acc);
     out[row] = from_f<XT>(acc);
   }
 }

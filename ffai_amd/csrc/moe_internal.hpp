@@ -93,6 +93,7 @@ struct Down1Args {
   const void* act;           // [k, K] in rank order
   GemvProj p;
   void* out;                 // [N]
+  const void* res;           // nullable [N]: residual added before the final rounding
   int k, N, K, gsh, rows_per_block, lg;
 };
 
@@ -119,6 +120,13 @@ hipError_t launch_router_logits(const void* x, int xdt, int T, int H, const void
                                 const void* bias, int E, void* logits, hipStream_t st);
 hipError_t launch_router_topk(const void* logits, int dt, int T, int E, int k,
                               const RouteOpts& ro, uint32_t* idx, float* w, hipStream_t st);
+// One token: res = round(h + m), xn = round(rmsnorm(res) * nw), then the
+// router logits of xn, in one launch. 16-bit x and W of one type, H <= 8192;
+// hipErrorInvalidValue otherwise (launch_add_rmsnorm + launch_router_logits).
+hipError_t launch_router_logits_norm(const void* h, const void* m, const void* nw, float eps,
+                                     int xdt, int H, const void* W, int wdt, const void* bias,
+                                     int E, void* logits, void* res_out, void* xn_out,
+                                     hipStream_t st);
 
 // ------------------------------------------------------------- dispatch --
 // Writes counts, offsets, perm, inv_perm and the used-expert list.
@@ -136,9 +144,15 @@ hipError_t launch_used_from_offsets(const uint32_t* offsets, int E, uint32_t* us
 // -------------------------------------------------------------- combine --
 hipError_t launch_unpermute(const void* Y, const uint32_t* inv, const float* w, int T, int H,
                             int k, void* out, int dt, const void* shared_out,
-                            const void* shared_logit, int shared_mode, hipStream_t st);
+                            const void* shared_logit, int shared_mode, hipStream_t st,
+                            const void* res = nullptr);
 hipError_t launch_add_shared(void* y, const void* shared_out, const void* shared_logit,
-                             int shared_mode, int T, int H, int dt, hipStream_t st);
+                             int shared_mode, int T, int H, int dt, hipStream_t st,
+                             const void* res = nullptr);
+// Per row: res = round(a + b), xn = round(res / sqrt(mean(res^2) + eps) * w);
+// H a multiple of 8, at most 8192; rows 16-byte aligned.
+hipError_t launch_add_rmsnorm(const void* a, const void* b, const void* w, float eps, int T,
+                              int H, int dt, void* res, void* xn, hipStream_t st);
 hipError_t launch_activation(const void* g, const void* u, void* out, int64_t n, int dt,
                              int act, float alpha, float limit, hipStream_t st);
 hipError_t launch_dequantize(const uint32_t* w, const void* s, const void* b, int sbdt, int bits,

@@ -101,6 +101,96 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT* __restrict
   }
 }
 
+// One token with the decoder step before the MoE block folded in: the
+// residual add and RMSNorm of Ops.addAndRmsNorm (Sources/FFAI/Ops/Ops.swift:
+// 676-730; Models/Text/Qwen3xText.swift:2650-2660), s = round(h + m),
+// xn = round(s * (1 / sqrt(mean(s^2) + eps)) * nw), then
+// logits[e] = round(W[e] . xn) (+ bias). One 256-thread block per expert;
+// thread i takes the 8-element chunks i + 256 j, j < NL, so the per-thread
+// chain is short; the sum of squares and the dot product are reduced over the
+// four waves through LDS. Every block computes the same normalised row from
+// the same loads, and the expert-0 block writes s and xn for the kernels that
+// follow. Weights, activations and the norm weight share one 16-bit type.
+template <typename XT, int NL>
+__global__ __launch_bounds__(256) void router_logits_norm_kernel(
+    const XT* __restrict__ h, const XT* __restrict__ m, const XT* __restrict__ nw, float eps,
+    const XT* __restrict__ W, const XT* __restrict__ bias, XT* __restrict__ logits,
+    XT* __restrict__ res_out, XT* __restrict__ xn_out, int H, int E) {
+  __shared__ float part[2][4];
+  const int e = blockIdx.x;  // grid == E
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const float bv = bias ? to_f<XT>(bias[e]) : 0.f;
+  const uint32_t rb = (uint32_t)(H * sizeof(XT));
+  const rsrc_t wr = make_rsrc(W + (size_t)e * H, rb);
+  const rsrc_t hr = make_rsrc(h, rb), mr = make_rsrc(m, rb), nr = make_rsrc(nw, rb);
+  u32x4_t wq[NL], hv[NL], mv[NL], nv[NL];
+#pragma unroll
+  for (int j = 0; j < NL; j++) {
+    const uint32_t off = (uint32_t)((tid + 256 * j) * 16);
+    hv[j] = bload128(hr, off);
+    mv[j] = bload128(mr, off);
+    nv[j] = bload128(nr, off);
+    wq[j] = bload128(wr, off);
+  }
+  // s = round(h + m); chunks past H read zeros and add nothing
+  float sv[NL][8];
+  float ssq = 0.f;
+#pragma unroll
+  for (int j = 0; j < NL; j++) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float h0 = to_f<XT>(__builtin_bit_cast(XT, (uint16_t)(hv[j][i] & 0xFFFFu)));
+      const float h1 = to_f<XT>(__builtin_bit_cast(XT, (uint16_t)(hv[j][i] >> 16)));
+      const float m0 = to_f<XT>(__builtin_bit_cast(XT, (uint16_t)(mv[j][i] & 0xFFFFu)));
+      const float m1 = to_f<XT>(__builtin_bit_cast(XT, (uint16_t)(mv[j][i] >> 16)));
+      sv[j][2 * i] = round_to<XT>(h0 + m0);
+      sv[j][2 * i + 1] = round_to<XT>(h1 + m1);
+      ssq = __builtin_fmaf(sv[j][2 * i], sv[j][2 * i], ssq);
+      ssq = __builtin_fmaf(sv[j][2 * i + 1], sv[j][2 * i + 1], ssq);
+    }
+  }
+  ssq = group_sum(ssq, 6);
+  if (lane == 63) part[0][wv] = ssq;
+  __syncthreads();
+  const float tot = (part[0][0] + part[0][1]) + (part[0][2] + part[0][3]);
+  const float inv = 1.0f / sqrtf(tot / (float)H + eps);
+  u32x4_t sp[NL], xp[NL];
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < NL; j++) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float n0 = to_f<XT>(__builtin_bit_cast(XT, (uint16_t)(nv[j][i] & 0xFFFFu)));
+      const float n1 = to_f<XT>(__builtin_bit_cast(XT, (uint16_t)(nv[j][i] >> 16)));
+      const uint16_t x0 = __builtin_bit_cast(uint16_t, from_f<XT>(sv[j][2 * i] * inv * n0));
+      const uint16_t x1 = __builtin_bit_cast(uint16_t, from_f<XT>(sv[j][2 * i + 1] * inv * n1));
+      const uint16_t s0 = __builtin_bit_cast(uint16_t, from_f<XT>(sv[j][2 * i]));
+      const uint16_t s1 = __builtin_bit_cast(uint16_t, from_f<XT>(sv[j][2 * i + 1]));
+      xp[j][i] = (uint32_t)x0 | ((uint32_t)x1 << 16);
+      sp[j][i] = (uint32_t)s0 | ((uint32_t)s1 << 16);
+      acc = dot2_16<XT>(wq[j][i], xp[j][i], acc);
+    }
+  }
+  acc = group_sum(acc, 6);
+  if (lane == 63) part[1][wv] = acc;
+  if (e == 0) {
+#pragma unroll
+    for (int j = 0; j < NL; j++) {
+      const int c = tid + 256 * j;  // 8-element chunk; H is a multiple of 8
+      if (c * 8 < H) {
+        *reinterpret_cast<u32x4_t*>(res_out + (size_t)c * 8) = sp[j];
+        *reinterpret_cast<u32x4_t*>(xn_out + (size_t)c * 8) = xp[j];
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float l = round_to<XT>((part[1][0] + part[1][1]) + (part[1][2] + part[1][3]));
+    if (bias) l = round_to<XT>(l + bv);
+    logits[e] = from_f<XT>(l);
+  }
+}
+
 // One wave per token row (wave_topk); weights are reproducible bit for bit.
 template <typename XT>
 __global__ __launch_bounds__(256) void router_topk_kernel(const XT* __restrict__ logits, int T,
@@ -161,6 +251,27 @@ hipError_t launch_router_logits(const void* x, int xdt, int T, int H, const void
   }
 #undef MOE_RL2
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_router_logits_norm(const void* h, const void* m, const void* nw, float eps,
+                                     int xdt, int H, const void* W, int wdt, const void* bias,
+                                     int E, void* logits, void* res_out, void* xn_out,
+                                     hipStream_t st) {
+  if (xdt != wdt || xdt == DT_F32 || H % 8 != 0 || H > 4 * 2048) return hipErrorInvalidValue;
+  const int nl = (H + 2047) / 2048;
+#define MOE_RLN(XT, NL)                                                                        \
+  hipLaunchKernelGGL((router_logits_norm_kernel<XT, NL>), dim3(E), dim3(256), 0, st,           \
+                     (const XT*)h, (const XT*)m, (const XT*)nw, eps, (const XT*)W,             \
+                     (const XT*)bias, (XT*)logits, (XT*)res_out, (XT*)xn_out, H, E);           \
+  return hipGetLastError();
+#define MOE_RLN_NL(XT)            \
+  if (nl <= 1) { MOE_RLN(XT, 1) } \
+  if (nl <= 2) { MOE_RLN(XT, 2) } \
+  MOE_RLN(XT, 4)
+  if (xdt == DT_BF16) { MOE_RLN_NL(bf16_t) }
+  MOE_RLN_NL(f16_t)
+#undef MOE_RLN_NL
+#undef MOE_RLN
 }
 
 hipError_t launch_router_topk(const void* logits, int dt, int T, int E, int k,

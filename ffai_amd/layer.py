@@ -185,6 +185,23 @@ class MoELayer:
                                                    _stream(stream)))
         return (out, tensors) if trace else out
 
+    def forward_residual(self, h: torch.Tensor, mixer_out: torch.Tensor, norm_weight: torch.Tensor,
+                         eps: float, out: Optional[torch.Tensor] = None,
+                         residual_out: Optional[torch.Tensor] = None, stream=None):
+        """The block between the decoder steps (Qwen3xText.swift:2640-2670,
+        1015-1035): r = h + mixer_out, y = r + MoE(rmsnorm(r) * norm_weight).
+        Returns y; residual_out (optional) receives r."""
+        if mixer_out.shape != h.shape or norm_weight.numel() != self.hidden:
+            raise ValueError("MoELayer.forward_residual: shape mismatch")
+        T = h.shape[0]
+        if out is None:
+            out = torch.empty_like(h)
+        ws = self.workspace(T)
+        check(_lib.load().moe_layer_forward_residual(
+            C.byref(self._desc), _ptr(h), _ptr(mixer_out), _ptr(norm_weight), float(eps), T,
+            _ptr(out), _ptr(residual_out), _ptr(ws), ws.numel(), None, _stream(stream)))
+        return out
+
     # Swift-API names
     def decode(self, h: torch.Tensor, stream=None) -> torch.Tensor:
         return self.forward(h.reshape(1, -1), stream=stream).reshape(-1)

@@ -240,6 +240,14 @@ moe_status moe_unpermute(const void* Y, const uint32_t* inv_perm, const float* t
                          int32_t T, int32_t hidden, int32_t k, void* out, int32_t dtype,
                          hipStream_t stream);
 
+/* Ops.addAndRmsNorm (Ops.swift:676-730): per row, residual = a + b and
+ * normed = residual / sqrt(mean(residual^2) + eps) * weight, each rounded to
+ * dtype. [n_rows, row_size] rows (16-byte aligned), weight [row_size];
+ * row_size a multiple of 8, at most 8192. */
+moe_status moe_add_rmsnorm(const void* a, const void* b, const void* weight, float eps,
+                           int32_t n_rows, int32_t row_size, int32_t dtype, void* residual_out,
+                           void* normed_out, hipStream_t stream);
+
 /* ---- whole layer ------------------------------------------------------- */
 
 /* Workspace for moe_layer_forward at up to max_tokens rows. */
@@ -260,6 +268,24 @@ moe_status moe_layer_forward_routed(const moe_layer_desc* d, const void* x,
                                     const void* router_x, int32_t T, void* y, void* workspace,
                                     size_t workspace_bytes, const moe_layer_trace* trace,
                                     hipStream_t stream);
+
+/* The MoE block with the decoder steps on either side folded in: the
+ * post-attention residual add + RMSNorm before it (Ops.addAndRmsNorm,
+ * Qwen3xText.swift:2640-2660) and the residual add after it
+ * (Ops.sigmoidScalarFMAResidual, OpsFused.swift:699-753; Qwen3xText.swift:
+ * 1015-1035):
+ *   r  = h + mixer_out                      (rounded; written to residual_out
+ *                                            when non-NULL)
+ *   xn = r / sqrt(mean(r^2) + eps) * norm_weight   (rounded)
+ *   y  = r + MoE(xn) [+ sigmoid(gate) * shared(xn)]   (one rounding)
+ * h, mixer_out, y [T, hidden]; norm_weight [hidden]; all in act_dtype and
+ * 16-byte aligned; hidden a multiple of 8. For one token the add and norm
+ * run inside the router launch. */
+moe_status moe_layer_forward_residual(const moe_layer_desc* d, const void* h,
+                                      const void* mixer_out, const void* norm_weight, float eps,
+                                      int32_t T, void* y, void* residual_out, void* workspace,
+                                      size_t workspace_bytes, const moe_layer_trace* trace,
+                                      hipStream_t stream);
 
 /* ---- MoELayer handle (owns its workspace like the reference instance) -- */
 typedef struct moe_layer* moe_layer_t;

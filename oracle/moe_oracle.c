@@ -618,9 +618,79 @@ static void expert_act(const or_layer* L, const or_qproj* gate, const or_qproj* 
     free(u);
 }
 
+/* Ops.addAndRmsNorm (Ops.swift:676-730; the reference's CPU check in
+ * OpsTests.swift:1009-1060): r = round(a + b), ssq summed in row order,
+ * xn = round(r / sqrt(ssq / n + eps) * w). */
+void or_add_rmsnorm(const float* a, const float* b, const float* w, float eps, int T, int H,
+                    int dt, float* res_out, float* xn_out) {
+    for (int t = 0; t < T; t++) {
+        const float* ar = a + (size_t)t * H;
+        const float* br = b + (size_t)t * H;
+        float* rr = res_out + (size_t)t * H;
+        float ssq = 0.0f;
+        for (int i = 0; i < H; i++) {
+            rr[i] = or_round_dt(ar[i] + br[i], dt);
+            ssq += rr[i] * rr[i];
+        }
+        float rms = sqrtf(ssq / (float)H + eps);
+        for (int i = 0; i < H; i++)
+            xn_out[(size_t)t * H + i] = or_round_dt(rr[i] / rms * w[i], dt);
+    }
+}
+
+/* out[i] = round((residual[i] + base[i]) + gate * value[i]): Ops.
+ * sigmoidScalarFMAResidual (OpsFused.swift:699-753) with gate = sigmoid of
+ * the shared-expert gate logit; a NULL residual is Ops.sigmoidScalarFMA, a
+ * NULL value the residual add alone. */
+void or_residual_combine(const float* res, const float* base, const float* value, float gate,
+                         int n, int dt, float* out) {
+    for (int i = 0; i < n; i++) {
+        float v = base[i];
+        if (res) v = res[i] + v;
+        if (value) v = v + gate * value[i];
+        out[i] = or_round_dt(v, dt);
+    }
+}
+
+static int layer_impl(const or_layer* L, const void* x, const void* router_x, int T, void* y,
+                      const float* given_logits, float* logits_out, uint32_t* idx_out,
+                      float* w_out, const float* res);
+
 int or_moe_layer_routed(const or_layer* L, const void* x, const void* router_x, int T,
                         void* y, const float* given_logits,
                         float* logits_out, uint32_t* idx_out, float* w_out) {
+    return layer_impl(L, x, router_x, T, y, given_logits, logits_out, idx_out, w_out, NULL);
+}
+
+/* The block between the decoder steps (Qwen3xText.swift:2640-2670,
+ * 1015-1035): r = round(h + m), xn = rmsnorm(r) * nw, y = round(r + MoE(xn)
+ * [+ gate * shared(xn)]). xn_out and res_out (nullable) receive the rows. */
+int or_moe_layer_residual(const or_layer* L, const void* h, const void* m, const float* nw,
+                          float eps, int T, void* y, const float* given_logits,
+                          float* xn_out, float* res_out, float* logits_out, uint32_t* idx_out,
+                          float* w_out) {
+    int H = L->hidden, dt = L->act_dt;
+    if (T <= 0 || H <= 0) return -1;
+    size_t n = (size_t)T * H;
+    float* hf = (float*)malloc(sizeof(float) * n);
+    float* mf = (float*)malloc(sizeof(float) * n);
+    float* r = (float*)malloc(sizeof(float) * n);
+    float* xn = (float*)malloc(sizeof(float) * n);
+    void* xs = malloc(n * (dt == OR_F32 ? 4 : 2));
+    or_load(h, dt, n, hf);
+    or_load(m, dt, n, mf);
+    or_add_rmsnorm(hf, mf, nw, eps, T, H, dt, r, xn);
+    or_store(xn, dt, n, xs);
+    int rc = layer_impl(L, xs, xs, T, y, given_logits, logits_out, idx_out, w_out, r);
+    if (xn_out) memcpy(xn_out, xn, sizeof(float) * n);
+    if (res_out) memcpy(res_out, r, sizeof(float) * n);
+    free(hf); free(mf); free(r); free(xn); free(xs);
+    return rc;
+}
+
+static int layer_impl(const or_layer* L, const void* x, const void* router_x, int T, void* y,
+                      const float* given_logits, float* logits_out, uint32_t* idx_out,
+                      float* w_out, const float* res) {
     int H = L->hidden, E = L->n_experts, k = L->top_k, I = L->intermediate, dt = L->act_dt;
     if (T <= 0 || H <= 0 || E <= 0 || k <= 0 || k > E || I <= 0) return -1;
     size_t M = (size_t)T * k;
@@ -669,7 +739,12 @@ int or_moe_layer_routed(const or_layer* L, const void* x, const void* router_x, 
     /* 7. shared expert: Granite-style unconditional add (MoELayer.swift:
      * 620-624), Qwen3.5's sigmoid gate (Qwen3xText.swift:1047-1104), or
      * NemotronH's squared-ReLU expert (NemotronHText.swift:855-862); the
-     * shared expert uses the routed experts' activation. */
+     * shared expert uses the routed experts' activation. The decoder
+     * residual, when given, joins the same final rounding. */
+    if (res && !L->has_shared)
+        for (int t = 0; t < T; t++)
+            or_residual_combine(res + (size_t)t * H, out + (size_t)t * H, NULL, 0.0f, H, dt,
+                                out + (size_t)t * H);
     if (L->has_shared) {
         int SI = L->shared_up.n;
         uint32_t* zero = (uint32_t*)calloc((size_t)T, sizeof(uint32_t));
@@ -686,11 +761,8 @@ int or_moe_layer_routed(const or_layer* L, const void* x, const void* router_x, 
         for (int t = 0; t < T; t++) {
             float gate = 1.0f;
             if (gl) gate = 1.0f / (1.0f + expf(-gl[t]));
-            for (int h = 0; h < H; h++) {
-                size_t i = (size_t)t * H + h;
-                float prod = gate * so[i];
-                out[i] = or_round_dt(out[i] + prod, dt);
-            }
+            or_residual_combine(res ? res + (size_t)t * H : NULL, out + (size_t)t * H,
+                                so + (size_t)t * H, gate, H, dt, out + (size_t)t * H);
         }
         free(zero); free(sg); free(so); free(gl);
     }

@@ -130,6 +130,17 @@ int or_moe_layer_routed(const or_layer* L, const void* x, const void* router_x, 
                         void* y, const float* given_logits,
                         float* logits_out, uint32_t* idx_out, float* w_out);
 
+/* ---- decoder steps around the block (Qwen3xText.swift:2640-2670,
+ *      1015-1035) --------------------------------------------------------- */
+void or_add_rmsnorm(const float* a, const float* b, const float* w, float eps, int T, int H,
+                    int dt, float* res_out, float* xn_out);
+void or_residual_combine(const float* res, const float* base, const float* value, float gate,
+                         int n, int dt, float* out);
+int or_moe_layer_residual(const or_layer* L, const void* h, const void* m, const float* nw,
+                          float eps, int T, void* y, const float* given_logits,
+                          float* xn_out, float* res_out, float* logits_out, uint32_t* idx_out,
+                          float* w_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -100,6 +100,13 @@ def _declare(L):
     L.or_moe_layer.restype = i
     L.or_moe_layer_routed.argtypes = [C.POINTER(OrLayer), vp, vp, i, vp, vp, vp, vp, vp]
     L.or_moe_layer_routed.restype = i
+    L.or_add_rmsnorm.argtypes = [vp, vp, vp, f, i, i, i, vp, vp]
+    L.or_add_rmsnorm.restype = None
+    L.or_residual_combine.argtypes = [vp, vp, vp, f, i, i, vp]
+    L.or_residual_combine.restype = None
+    L.or_moe_layer_residual.argtypes = [C.POINTER(OrLayer), vp, vp, vp, f, i, vp, vp, vp, vp, vp,
+                                        vp, vp]
+    L.or_moe_layer_residual.restype = i
 
 
 def _p(a):
@@ -310,3 +317,49 @@ def moe_layer(spec, x, given_logits=None, router_x=None):
     if rc != 0:
         raise ValueError("invalid layer description")
     return y, logits, idx, w
+
+
+# ------------------------------------------------------- decoder steps ----
+
+def add_rmsnorm(a, b, w, eps, dt=F32):
+    """(residual, normed) float32 arrays [T, H] (values rounded to dt)."""
+    a = np.ascontiguousarray(np.atleast_2d(a), dtype=np.float32)
+    b = np.ascontiguousarray(np.atleast_2d(b), dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    T, H = a.shape
+    res = np.zeros_like(a)
+    xn = np.zeros_like(a)
+    lib().or_add_rmsnorm(_p(a), _p(b), _p(w), float(eps), T, H, dt, _p(res), _p(xn))
+    return res, xn
+
+
+def residual_combine(res, base, value=None, gate=1.0, dt=F32):
+    base = np.ascontiguousarray(base, dtype=np.float32).ravel()
+    r = None if res is None else np.ascontiguousarray(res, dtype=np.float32).ravel()
+    v = None if value is None else np.ascontiguousarray(value, dtype=np.float32).ravel()
+    out = np.zeros_like(base)
+    lib().or_residual_combine(_p(r), _p(base), _p(v), float(gate), base.size, dt, _p(out))
+    return out
+
+
+def moe_layer_residual(spec, h, m, norm_w, eps, given_logits=None):
+    """The block between the decoder steps. h, m: storage arrays [T, H] of
+    spec.act_dt; norm_w: float32 [H] (values of the act dtype). Returns
+    (y, xn, residual, logits, idx, weights)."""
+    h = np.ascontiguousarray(h)
+    m = np.ascontiguousarray(m)
+    T, H = h.shape
+    L = spec.oracle_struct()
+    nw = np.ascontiguousarray(norm_w, dtype=np.float32)
+    y = np.zeros((T, H), dtype=np_dtype(spec.act_dt))
+    xn = np.zeros((T, H), dtype=np.float32)
+    res = np.zeros((T, H), dtype=np.float32)
+    logits = np.zeros((T, spec.n_experts), dtype=np.float32)
+    idx = np.zeros((T, spec.top_k), dtype=np.uint32)
+    w = np.zeros((T, spec.top_k), dtype=np.float32)
+    gl = None if given_logits is None else np.ascontiguousarray(given_logits, dtype=np.float32)
+    rc = lib().or_moe_layer_residual(C.byref(L), _p(h), _p(m), _p(nw), float(eps), T, _p(y),
+                                     _p(gl), _p(xn), _p(res), _p(logits), _p(idx), _p(w))
+    if rc != 0:
+        raise ValueError("invalid layer description")
+    return y, xn, res, logits, idx, w

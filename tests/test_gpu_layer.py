@@ -359,6 +359,90 @@ def test_layer_gptoss_expert_bias():
     run_layer(cfg_gptoss(seed=3, n_experts=8, hidden=512, inter=640, expert_bias=True), 5)
 
 
+@pytest.mark.parametrize("dt", [BF16, F16, F32])
+@pytest.mark.parametrize("T,H", [(1, 128), (3, 2880), (2, 4096), (1, 8192)])
+def test_add_rmsnorm_op(dt, T, H):
+    """moe_add_rmsnorm: the residual bit-exact, the normalised row within one
+    storage ulp (the sum of squares is reduced in another order)."""
+    rng = np.random.default_rng(T * 7 + H)
+    a = store(rng.normal(0, 1, (T, H)), dt)
+    b = store(rng.normal(0, 0.5, (T, H)), dt)
+    wv = store(rng.uniform(0.5, 1.5, H), dt)
+    at, bt, wt = to_torch(a), to_torch(b), to_torch(wv)
+    res, xn = torch.empty_like(at), torch.empty_like(at)
+    check(_lib.load().moe_add_rmsnorm(_p(at), _p(bt), _p(wt), 1e-6, T, H, dt, _p(res), _p(xn),
+                                      _stream()))
+    torch.cuda.synchronize()
+    r_ref, x_ref = orc.add_rmsnorm(load(a, dt), load(b, dt), load(wv, dt), 1e-6, dt)
+    assert np.array_equal(to_numpy_f32(res), r_ref)
+    # one storage ulp for 16-bit rows (the rounding of a value that moved by a
+    # few f32 ulps); f32 itself: 1e-5 relative, the drift of a sequential f32
+    # sum of up to 8192 squares against a tree-ordered one (the reference's
+    # own bar is 1e-2, OpsTests.swift:1052-1058)
+    tol = {BF16: 2.0 ** -7, F16: 2.0 ** -10, F32: 1e-5}[dt]
+    assert np.all(np.abs(to_numpy_f32(xn) - x_ref) <= 1.01 * tol * np.abs(x_ref) + 1e-30)
+
+
+def run_layer_residual(spec, T, seed=0):
+    """moe_layer_forward_residual against the oracle's block between the
+    decoder steps: the residual bit-exact, routing from the GPU's logits
+    bit-exact, the output to the float bar."""
+    dev = spec.device()
+    rng = np.random.default_rng(seed + 77)
+    H = spec.hidden
+    h = spec.x(T, seed)
+    m = store(rng.normal(0, 0.5, (T, H)), spec.act_dt)
+    nw = store(rng.uniform(0.5, 1.5, H), spec.act_dt)
+    ht, mt, nwt = to_torch(h), to_torch(m), to_torch(nw)
+    y = torch.empty_like(ht)
+    res = torch.empty_like(ht)
+    E, k = spec.n_experts, spec.top_k
+    tr_t = dict(logits=torch.empty(T, E, dtype=ht.dtype, device="cuda"),
+                topk_idx=torch.empty(T, k, dtype=torch.int32, device="cuda"),
+                topk_weight=torch.empty(T, k, dtype=torch.float32, device="cuda"))
+    tr = _lib.LayerTrace(tr_t["logits"].data_ptr(), tr_t["topk_idx"].data_ptr(),
+                         tr_t["topk_weight"].data_ptr(), None, None)
+    ws = dev.workspace(T)
+    check(_lib.load().moe_layer_forward_residual(C.byref(dev.desc), _p(ht), _p(mt), _p(nwt), 1e-6, T,
+                                                 _p(y), _p(res), _p(ws), ws.numel(), C.byref(tr),
+                                                 _stream()))
+    torch.cuda.synchronize()
+    lg = to_numpy_f32(tr_t["logits"])
+    y_ref, xn_ref, r_ref, l_ref, idx_ref, w_ref = orc.moe_layer_residual(
+        spec, h, m, load(nw, spec.act_dt), 1e-6, given_logits=lg)
+    assert np.array_equal(to_numpy_f32(res), r_ref), "residual"
+    # logits of a normalised row that may differ from the oracle's by an ulp
+    # in a few elements: a few storage ulps
+    ulp = 2.0 ** -7 if spec.act_dt == BF16 else 2.0 ** -10 if spec.act_dt == F16 else 2.0 ** -20
+    l_cpu = orc.router_logits(store(xn_ref, spec.act_dt), spec.act_dt, spec.router_weight,
+                              spec.router_dt, spec.router_bias)
+    assert np.all(np.abs(lg - l_cpu) <= 4.02 * ulp * np.abs(l_cpu) + 4 * ulp), "router logits"
+    assert np.array_equal(_u32(tr_t["topk_idx"]), idx_ref), "expert ids"
+    assert np.array_equal(tr_t["topk_weight"].cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
+    stats = check_close(to_numpy_f32(y), load(y_ref, spec.act_dt), spec.act_dt,
+                        f"{spec.name} residual T={T}")
+    print(f"{spec.name} residual T={T}: max|d|/rms={stats[0]:.3e} mean_rel={stats[1]:.3e}")
+
+
+@pytest.mark.parametrize("cfg,T", [("gptoss", 1), ("gptoss", 4), ("qwen3", 1), ("qwen3", 64),
+                                   ("mixed", 1), ("mixed", 40), ("tiny_f32", 2)])
+def test_layer_residual(cfg, T):
+    """The block with the decoder steps folded in: one token runs the add and
+    norm inside the router launch (16-bit, hidden <= 4096), other calls the
+    standalone add + RMSNorm; the residual joins the last store (down + combine,
+    the shared add, or the unpermute)."""
+    spec = {"gptoss": lambda: cfg_gptoss(),
+            "qwen3": lambda: cfg_qwen3(),
+            "mixed": lambda: cfg_mixed(n_experts=64),
+            "tiny_f32": lambda: cfg_tiny(act_dt=F32)}[cfg]()
+    if cfg == "tiny_f32":
+        spec.gate, spec.up, spec.down = (
+            orc.QProj(q.weight, load(q.scales, F16), load(q.biases, F16), q.bits, q.gs, F32)
+            for q in (spec.gate, spec.up, spec.down))
+        spec.router_weight, spec.router_dt = load(spec.router_weight, F16), F32
+    run_layer_residual(spec, T, seed=T)
+
+
 @pytest.fixture(scope="module")
 def nemotron():
     return cfg_nemotron()

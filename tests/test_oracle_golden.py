@@ -458,6 +458,62 @@ def test_geglu_and_relu2_closed_forms():
         assert orc.act(gv, uv, orc.ACT_RELU2) == np.float32(max(uv, 0.0) ** 2)
 
 
+def _add_rmsnorm_inputs(g):
+    n, rows = g["n"], g["n_rows"]
+    a = np.array([_expr(g["a"], i=i) for i in range(rows * n)], np.float32).reshape(rows, n)
+    b = np.array([_expr(g["b"], i=i) for i in range(rows * n)], np.float32).reshape(rows, n)
+    w = np.array([_expr(g["w"], d=d) for d in range(n)], np.float32)
+    return a, b, w
+
+
+def test_add_rmsnorm_kat():
+    """The reference's addAndRmsNorm test (OpsTests.swift:1009-1060) with its
+    own generators and tolerances."""
+    g = GOLD["add_rmsnorm"]
+    a, b, w = _add_rmsnorm_inputs(g)
+    res, xn = orc.add_rmsnorm(a, b, w, g["eps"])
+    s = a.astype(np.float64) + b
+    rms = np.sqrt((s * s).mean(axis=1, keepdims=True) + g["eps"])
+    assert np.all(np.abs(res - s) < g["tol_residual"])
+    assert np.all(np.abs(xn - s / rms * w) < g["tol_normed"])
+    # a norm over the sum instead of the mean, or without the weight, fails
+    assert not np.all(np.abs(xn - s / np.sqrt((s * s).sum(1, keepdims=True)) * w) < g["tol_normed"])
+    assert not np.all(np.abs(xn - s / rms) < g["tol_normed"])
+
+
+def test_rmsnorm_kat():
+    """OpsTests.swift:439-468: x = 1..128, weight 1, y = x / rms(x)."""
+    g = GOLD["rmsnorm"]
+    x = np.array([_expr(g["x"], i=i) for i in range(g["n"])], np.float32)
+    _, xn = orc.add_rmsnorm(x, np.zeros_like(x), np.full(g["n"], g["w"], np.float32), g["eps"])
+    ref = x / np.sqrt((x.astype(np.float64) ** 2).mean())
+    assert np.all(np.abs(xn[0] - ref) < g["tol"])
+
+
+def test_add_rmsnorm_bf16_rounding():
+    """The residual and the normalised row are each stored in the dtype."""
+    rng = np.random.default_rng(4)
+    a = orc.round_dt(rng.normal(size=(3, 256)), orc.BF16)
+    b = orc.round_dt(rng.normal(size=(3, 256)), orc.BF16)
+    w = orc.round_dt(rng.uniform(0.5, 1.5, 256), orc.BF16)
+    res, xn = orc.add_rmsnorm(a, b, w, 1e-6, orc.BF16)
+    assert np.array_equal(res, orc.round_dt(a + b, orc.BF16))
+    assert np.array_equal(xn, orc.round_dt(xn, orc.BF16))
+    ref = res / np.sqrt((res.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6) * w
+    assert np.all(np.abs(xn - ref) <= 2 ** -8 * np.abs(ref) + 1e-30)
+
+
+def test_sigmoid_fma_residual_kat():
+    """OpsSpecialPathTests.swift:357-382."""
+    g = GOLD["sigmoid_fma_residual"]
+    gate = 1.0 / (1.0 + math.exp(-g["gate"]))
+    out = orc.residual_combine(g["residual"], g["base"], g["value"], gate)
+    assert np.all(np.abs(out - np.array(g["out"])) < g["tol"])
+    # without the residual it is sigmoidScalarFMA; without a value the plain add
+    assert np.allclose(orc.residual_combine(None, g["base"], g["value"], gate), [11, 22, 33, 44])
+    assert np.allclose(orc.residual_combine(g["residual"], g["base"]), [110, 220, 330, 440])
+
+
 def test_unpermute_kat():
     g = GOLD["unpermute"]
     Y = np.array(g["expert_outputs"], np.float32)
@@ -641,6 +697,38 @@ def test_layer_family_matches_float64_composition(family):
         # routing on the expert input instead of the router's rows is caught
         y_same = orc.moe_layer(spec, x)[0]
         assert not np.array_equal(y_same.view(np.uint16), y.view(np.uint16))
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_layer_residual_composes(shared):
+    """The block between the decoder steps: residual and normalised rows from
+    the pinned add + RMSNorm, the block on the normalised rows, and (without
+    a shared expert) y = round(residual + block output) exactly."""
+    from moe_spec import cfg_tiny, load, store
+    import copy
+    spec = cfg_tiny()
+    if shared:
+        spec = copy.copy(spec)
+        spec.shared = (spec.gate, spec.up, spec.down)
+        spec.shared = tuple(orc.QProj(q.weight[:1], q.scales[:1], q.biases[:1], q.bits, q.gs, q.sb_dt)
+                            for q in spec.shared)
+    rng = np.random.default_rng(9)
+    T, H = 5, spec.hidden
+    h = spec.x(T, seed=1)
+    m = store(rng.normal(0, 0.5, size=(T, H)), spec.act_dt)
+    nw = load(store(rng.uniform(0.5, 1.5, H), spec.act_dt), spec.act_dt)
+    y, xn, res, logits, idx, w = orc.moe_layer_residual(spec, h, m, nw, 1e-6)
+    r2, xn2 = orc.add_rmsnorm(load(h, spec.act_dt), load(m, spec.act_dt), nw, 1e-6, spec.act_dt)
+    assert np.array_equal(res, r2) and np.array_equal(xn, xn2)
+    y_plain, logits2, idx2, w2 = orc.moe_layer(spec, store(xn, spec.act_dt))
+    assert np.array_equal(logits, logits2) and np.array_equal(idx, idx2)
+    if not shared:
+        assert np.array_equal(load(y, spec.act_dt),
+                              orc.round_dt(res + load(y_plain, spec.act_dt), spec.act_dt))
+    else:
+        # the residual joins the shared add's rounding, so only tolerance-close
+        check_close(load(y, spec.act_dt), load(y_plain, spec.act_dt) + res, spec.act_dt,
+                    "residual with shared expert")
 
 
 def test_float_bar_catches_planted_mistakes():
