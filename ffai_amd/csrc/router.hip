@@ -191,6 +191,44 @@ __global__ __launch_bounds__(256) void router_logits_norm_kernel(
   }
 }
 
+// One token, one 256-thread block per expert: thread i takes the 8-element
+// chunks i + 256 j, j < NL, so each lane issues a quarter of the loads of the
+// one-wave form; the four partial sums are added through LDS in wave order.
+// Weights and activations share one 16-bit type.
+template <typename XT, int NL>
+__global__ __launch_bounds__(256) void router_logits_row_kernel(const XT* __restrict__ x,
+                                                                const XT* __restrict__ W,
+                                                                const XT* __restrict__ bias,
+                                                                XT* __restrict__ logits, int H,
+                                                                int E) {
+  __shared__ float part[4];
+  const int e = blockIdx.x;  // grid == E
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const float bv = bias ? to_f<XT>(bias[e]) : 0.f;
+  const uint32_t rb = (uint32_t)(H * sizeof(XT));
+  const rsrc_t wr = make_rsrc(W + (size_t)e * H, rb), xr = make_rsrc(x, rb);
+  u32x4_t wq[NL], xq[NL];
+#pragma unroll
+  for (int j = 0; j < NL; j++) {
+    const uint32_t off = (uint32_t)((tid + 256 * j) * 16);
+    xq[j] = bload128(xr, off);
+    wq[j] = bload128(wr, off);
+  }
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < NL; j++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc = dot2_16<XT>(wq[j][i], xq[j][i], acc);
+  acc = group_sum(acc, 6);
+  if (lane == 63) part[wv] = acc;
+  __syncthreads();
+  if (tid == 0) {
+    float l = round_to<XT>((part[0] + part[1]) + (part[2] + part[3]));
+    if (bias) l = round_to<XT>(l + bv);
+    logits[e] = from_f<XT>(l);
+  }
+}
+
 // One wave per token row (wave_topk); weights are reproducible bit for bit.
 template <typename XT>
 __global__ __launch_bounds__(256) void router_topk_kernel(const XT* __restrict__ logits, int T,
@@ -213,6 +251,19 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const XT* __restrict__
 template <typename XT, typename WT>
 static hipError_t launch_rl(const void* x, int T, int H, const void* W, const void* bias, int E,
                             void* logits, hipStream_t st) {
+  if constexpr (__is_same(XT, WT) && !__is_same(XT, float)) {
+    if (T == 1 && H <= 4 * 2048) {
+      const int nl4 = (H + 2047) / 2048;
+#define MOE_RLR(NL)                                                                         \
+  hipLaunchKernelGGL((router_logits_row_kernel<XT, NL>), dim3(E), dim3(256), 0, st,         \
+                     (const XT*)x, (const XT*)W, (const XT*)bias, (XT*)logits, H, E);       \
+  return hipGetLastError();
+      if (nl4 <= 1) { MOE_RLR(1) }
+      if (nl4 <= 2) { MOE_RLR(2) }
+      MOE_RLR(4)
+#undef MOE_RLR
+    }
+  }
   const int tchunks = (T + 7) / 8;
   const long waves = (long)E * tchunks;
   // small batches: one wave per block spreads the experts over the CUs
