@@ -393,13 +393,82 @@ def bench_decoder_step(args, torch, cfg):
     print(json.dumps(out), flush=True)
 
 
+# ------------------------------------------------------- MXFP4 transcode --
+def bench_mxfp4(args, torch):
+    """GPT-OSS-20B's expert stacks (32 experts x gate/up/down of 2880 x 2880,
+    MXFP4) transcoded in HBM to affine 4-bit with bf16 scales and biases
+    (moe_mxfp4_to_affine, in place). Algorithmic bytes per 32-code group: 16
+    packed + 1 exponent read, 16 codes + 2 + 2 scale/bias written = 37."""
+    import numpy as np
+    from ffai_amd import _lib as lib
+    E, H, I = 32, 2880, 2880
+    groups = E * (2 * I * H + H * I) // 32
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    packed = torch.randint(-2**31, 2**31 - 1, (groups * 4,), dtype=torch.int32, device="cuda",
+                           generator=g)
+    e8 = torch.randint(118, 125, (groups,), dtype=torch.uint8, device="cuda", generator=g)
+    s = torch.empty(groups, dtype=torch.bfloat16, device="cuda")
+    b = torch.empty(groups, dtype=torch.bfloat16, device="cuda")
+    st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    P = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
+
+    def run():
+        # out of place into `out` keeps every repetition on the same input
+        lib.check(lib.load().moe_mxfp4_to_affine(P(packed), P(e8), groups, P(out), P(s), P(b),
+                                                 lib.MOE_BF16, st))
+
+    out = torch.empty_like(packed)
+    for _ in range(max(1, args.warmup)):
+        run()
+    reps = max(1, args.steps)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    nbytes = groups * 37
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    # CPU baseline: the oracle's restatement of the reference loop, one thread
+    import oracle as orc
+    ns = 200000
+    pk = packed[: ns * 4].cpu().numpy().view(np.uint32)
+    ee = e8[:ns].cpu().numpy()
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < 10.0:
+        orc.mxfp4_to_affine(pk, ee, orc.BF16)
+        n += 1
+    cdt = time.perf_counter() - t0
+    out_line = {
+        "metric": "MXFP4 -> affine 4-bit transcode (GPT-OSS-20B layer experts)",
+        "value": round(groups * 32 / (ms * 1e-3) / 1e9, 2), "unit": "Gweights/s", "n_gpus": 1,
+        "steps": reps, "warmup": max(1, args.warmup), "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+        "data": "synthetic (random fp4 codes, e8m0 118..124)",
+        "config": {"workload": "gptoss20b_layer_experts_mxfp4_transcode", "experts": E,
+                   "hidden": H, "intermediate": I, "groups": groups, "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": nbytes, "kernel": "mxfp4_affine_kernel<bf16>"},
+        "cpu_baseline": {"value": round(n * ns * 32 / cdt / 1e9, 4), "unit": "Gweights/s",
+                         "cores": 1, "kind": "port",
+                         "sample": f"{n} oracle transcodes of {ns} groups ({cdt:.1f} s)"},
+    }
+    print(json.dumps(out_line), flush=True)
+
+
 # ------------------------------------------------------------------ main --
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2400)
     ap.add_argument("--warmup", type=int, default=240)
-    ap.add_argument("--config", default="gptoss", choices=sorted(CONFIGS) + ["ckpt_load"])
+    ap.add_argument("--config", default="gptoss",
+                    choices=sorted(CONFIGS) + ["ckpt_load", "mxfp4"])
     ap.add_argument("--batch", type=int, default=None, help="tokens per step (overrides config)")
     ap.add_argument("--layers", type=int, default=24, help="resident layers rotated per step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -429,6 +498,9 @@ def main():
         return
     if args.config == "ckpt_load":
         bench_ckpt_load(args, torch)
+        return
+    if args.config == "mxfp4":
+        bench_mxfp4(args, torch)
         return
     from ffai_amd import _lib as lib
     from ffai_amd import layer as fl

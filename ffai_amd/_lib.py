@@ -28,11 +28,11 @@ EXPORTS = [
     "moe_dispatch_plan", "moe_dequantize_affine", "moe_expert_matmul_workspace_bytes",
     "moe_expert_matmul", "moe_activation_apply", "moe_unpermute", "moe_layer_workspace_bytes",
     "moe_layer_forward", "moe_layer_forward_routed", "moe_layer_forward_residual",
-    "moe_add_rmsnorm", "moe_layer_create", "moe_layer_destroy",
+    "moe_add_rmsnorm", "moe_mxfp4_to_affine", "moe_layer_create", "moe_layer_destroy",
     "moe_layer_decode", "moe_layer_decode_many",
     "moe_st_open", "moe_st_close", "moe_st_count", "moe_st_name", "moe_st_info", "moe_st_read_host",
     "moe_st_upload", "moe_st_is_quantized", "moe_st_stacked_bytes", "moe_st_load_stacked",
-    "moe_st_load_stacked_many",
+    "moe_st_load_stacked_many", "moe_st_mxfp4_bytes", "moe_st_load_mxfp4",
 ]
 
 
@@ -113,6 +113,7 @@ def load():
     lib.moe_layer_forward_residual.argtypes = [C.POINTER(LayerDesc), vp, vp, vp, C.c_float, i32,
                                                vp, vp, vp, sz, C.POINTER(LayerTrace), st]
     lib.moe_add_rmsnorm.argtypes = [vp, vp, vp, C.c_float, i32, i32, i32, vp, vp, st]
+    lib.moe_mxfp4_to_affine.argtypes = [vp, vp, C.c_int64, vp, vp, vp, i32, st]
     lib.moe_layer_create.argtypes = [C.POINTER(LayerDesc), C.POINTER(vp)]
     lib.moe_layer_destroy.argtypes = [vp]
     lib.moe_layer_destroy.restype = None
@@ -135,15 +136,17 @@ def load():
     lib.moe_st_load_stacked.argtypes = [vp, C.c_char_p, i32, vp, sz, C.POINTER(QProj), st]
     lib.moe_st_load_stacked_many.argtypes = [vp, i32, C.POINTER(C.c_char_p), i32, C.POINTER(vp),
                                              C.POINTER(sz), C.POINTER(QProj), st]
+    lib.moe_st_mxfp4_bytes.argtypes = [vp, C.c_char_p, i32, C.POINTER(sz), C.POINTER(sz)]
+    lib.moe_st_load_mxfp4.argtypes = [vp, C.c_char_p, i32, vp, sz, vp, sz, C.POINTER(QProj), st]
     for name in ["moe_validate_qproj", "moe_validate_layer", "moe_derive_bits", "moe_router_logits",
                  "moe_router_topk", "moe_router_topk_scaled", "moe_dispatch_plan",
                  "moe_dequantize_affine", "moe_expert_matmul", "moe_activation_apply",
                  "moe_unpermute", "moe_layer_forward", "moe_layer_forward_routed",
-                 "moe_layer_forward_residual", "moe_add_rmsnorm",
+                 "moe_layer_forward_residual", "moe_add_rmsnorm", "moe_mxfp4_to_affine",
                  "moe_layer_create", "moe_layer_decode",
                  "moe_layer_decode_many", "moe_st_open", "moe_st_info", "moe_st_read_host",
                  "moe_st_upload", "moe_st_stacked_bytes", "moe_st_load_stacked",
-                 "moe_st_load_stacked_many"]:
+                 "moe_st_load_stacked_many", "moe_st_mxfp4_bytes", "moe_st_load_mxfp4"]:
         getattr(lib, name).restype = C.c_int
     _lib = lib
     return lib

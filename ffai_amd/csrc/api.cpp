@@ -648,6 +648,22 @@ extern "C" moe_status moe_dequantize_affine(const uint32_t* weight, const void* 
   return ok();
 }
 
+extern "C" moe_status moe_mxfp4_to_affine(const uint32_t* packed, const uint8_t* e8m0,
+                                          int64_t n_groups, uint32_t* out_weight,
+                                          void* out_scales, void* out_biases, int32_t sb_dtype,
+                                          hipStream_t stream) {
+  if (!packed || !e8m0 || !out_weight || !out_scales || !out_biases)
+    return fail(MOE_ERR_INVALID, "mxfp4_to_affine: NULL pointer");
+  if (n_groups <= 0) return fail(MOE_ERR_INVALID, "mxfp4_to_affine: n_groups must be positive");
+  if (!dt_ok(sb_dtype)) return fail(MOE_ERR_INVALID, "mxfp4_to_affine: bad scale dtype");
+  if ((reinterpret_cast<uintptr_t>(packed) & 15) || (reinterpret_cast<uintptr_t>(out_weight) & 15))
+    return fail(MOE_ERR_INVALID, "mxfp4_to_affine: packed words must be 16-byte aligned");
+  MOE_HIP(launch_mxfp4_affine(packed, e8m0, n_groups, out_weight, out_scales, out_biases, sb_dtype,
+                              stream),
+          "MXFP4 transcode launch");
+  return ok();
+}
+
 extern "C" size_t moe_expert_matmul_workspace_bytes(int32_t n_experts, int32_t M) {
   if (n_experts <= 0 || M <= 0) return 0;
   return align_up((size_t)(n_experts + 1) * 4, 256) +

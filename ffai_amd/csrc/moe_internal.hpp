@@ -158,6 +158,16 @@ hipError_t launch_activation(const void* g, const void* u, void* out, int64_t n,
 hipError_t launch_dequantize(const uint32_t* w, const void* s, const void* b, int sbdt, int bits,
                              int gs, int64_t numel, void* out, int odt, hipStream_t st);
 
+// ---------------------------------------------------------------- MXFP4 --
+// MXFP4 groups (4 packed u32 + 1 e8m0 byte each) -> affine 4-bit, group 32;
+// out_w may be `packed` itself (the codes keep their nibbles).
+hipError_t launch_mxfp4_affine(const uint32_t* packed, const uint8_t* e8m0, int64_t groups,
+                               uint32_t* out_w, void* out_s, void* out_b, int sbdt,
+                               hipStream_t st);
+// Elementwise float conversion between the DT_* types.
+hipError_t launch_convert(const void* src, int sdt, void* dst, int ddt, int64_t n,
+                          hipStream_t st);
+
 // ----------------------------------------------------------------- GEMM --
 // Grouped dequant GEMM over row tiles of a dispatch plan (MFMA).
 struct GemmArgs {

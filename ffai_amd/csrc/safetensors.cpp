@@ -852,3 +852,126 @@ extern "C" moe_status moe_st_load_stacked_many(moe_st_t bundle, int32_t count,
   for (int i = 0; i < count; i++) out[i] = qs[(size_t)i];
   return st_ok();
 }
+
+// ---------------------------------------------------------------------------
+// MXFP4 expert stacks (GPT-OSS)
+// ---------------------------------------------------------------------------
+namespace {
+
+// <base>.weight [E, N, K/8] u32, <base>.scales [E, N, K/32] u8 (e8m0),
+// <base>.bias [E, N] f16/bf16/f32 (transcodeStackedExperts,
+// GPTOSSText.swift:1071-1110); 2-D tensors are one expert.
+struct Mxfp4 {
+  const Entry* w;
+  const Entry* s;
+  const Entry* bi;
+  int64_t E, N, G;
+  size_t w_off, s_off, b_off, ob_off, total;   // device layout
+  size_t sc_e8m0, sc_bias, scratch;            // scratch layout
+};
+
+moe_status mxfp4_layout(const moe_st_bundle* b, const char* base, int act_dtype, Mxfp4* out) {
+  if (!b || !base) return st_fail(MOE_ERR_INVALID, "load_mxfp4: NULL argument");
+  if (act_dtype != MOE_ST_F32 && act_dtype != MOE_ST_F16 && act_dtype != MOE_ST_BF16)
+    return st_fail(MOE_ERR_INVALID, "load_mxfp4: bad activation dtype %d", act_dtype);
+  const std::string nb = base;
+  const std::string wn = nb + ".weight", sn = nb + ".scales", bn = nb + ".bias";
+  Mxfp4 L{};
+  L.w = find(b, wn.c_str());
+  L.s = find(b, sn.c_str());
+  L.bi = find(b, bn.c_str());
+  if (!L.w) return missing(wn.c_str());
+  if (!L.s) return missing(sn.c_str());
+  if (!L.bi) return missing(bn.c_str());
+  if (L.w->dtype != MOE_ST_U32)
+    return st_fail(MOE_ERR_INVALID, "GPT-OSS MoE: %s expected u32", wn.c_str());
+  if (L.s->dtype != MOE_ST_U8)
+    return st_fail(MOE_ERR_INVALID, "GPT-OSS MoE: %s expected u8", sn.c_str());
+  if (L.bi->dtype != MOE_ST_F32 && L.bi->dtype != MOE_ST_F16 && L.bi->dtype != MOE_ST_BF16)
+    return st_fail(MOE_ERR_INVALID, "GPT-OSS MoE: %s must be f16, bf16 or f32", bn.c_str());
+  const size_t nd = L.w->shape.size();
+  if ((nd != 2 && nd != 3) || L.s->shape.size() != nd || L.bi->shape.size() != nd - 1)
+    return st_fail(MOE_ERR_INVALID, "GPT-OSS MoE: %s expected [E, N, K/8] / [E, N, K/32] / [E, N]",
+                   nb.c_str());
+  L.E = nd == 3 ? L.w->shape[0] : 1;
+  L.N = L.w->shape[nd - 2];
+  L.G = L.s->shape[nd - 1];
+  const int64_t words = L.w->shape[nd - 1];
+  if ((nd == 3 && (L.s->shape[0] != L.E || L.bi->shape[0] != L.E)) || L.s->shape[nd - 2] != L.N ||
+      L.bi->shape[nd - 2] != L.N || words != 4 * L.G || L.E <= 0 || L.N <= 0 || L.G <= 0)
+    return st_fail(MOE_ERR_INVALID,
+                   "GPT-OSS MoE: %s weight, scales and bias shapes disagree (32 codes per scale)",
+                   nb.c_str());
+  if (L.E > INT_MAX || L.N > INT_MAX || 32 * L.G > INT_MAX)
+    return st_fail(MOE_ERR_UNSUPPORTED, "%s: dimensions above 2^31", nb.c_str());
+  const size_t ds = act_dtype == MOE_ST_F32 ? 4 : 2;
+  const size_t groups = (size_t)(L.E * L.N * L.G);
+  L.w_off = 0;
+  L.s_off = align256(L.w->nbytes);
+  L.b_off = L.s_off + align256(groups * ds);
+  L.ob_off = L.b_off + align256(groups * ds);
+  L.total = L.ob_off + align256((size_t)(L.E * L.N) * ds);
+  L.sc_e8m0 = 0;
+  L.sc_bias = align256(L.s->nbytes);
+  L.scratch = L.sc_bias + align256(L.bi->nbytes);
+  *out = L;
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" moe_status moe_st_mxfp4_bytes(moe_st_t bundle, const char* base, int32_t act_dtype,
+                                         size_t* bytes, size_t* scratch_bytes) {
+  if (!bytes || !scratch_bytes) return st_fail(MOE_ERR_INVALID, "mxfp4_bytes: NULL argument");
+  Mxfp4 L;
+  ST_TRY(mxfp4_layout(bundle, base, act_dtype, &L));
+  *bytes = L.total;
+  *scratch_bytes = L.scratch;
+  return st_ok();
+}
+
+extern "C" moe_status moe_st_load_mxfp4(moe_st_t bundle, const char* base, int32_t act_dtype,
+                                        void* dst_device, size_t dst_bytes, void* scratch_device,
+                                        size_t scratch_bytes, moe_qproj* out,
+                                        hipStream_t stream) {
+  if (!out) return st_fail(MOE_ERR_INVALID, "load_mxfp4: NULL output descriptor");
+  Mxfp4 L;
+  ST_TRY(mxfp4_layout(bundle, base, act_dtype, &L));
+  if (!dst_device || dst_bytes < L.total)
+    return st_fail(MOE_ERR_INVALID, "load_mxfp4: %s needs %zu device bytes", base, L.total);
+  if (!scratch_device || scratch_bytes < L.scratch)
+    return st_fail(MOE_ERR_INVALID, "load_mxfp4: %s needs %zu scratch bytes", base, L.scratch);
+  if ((reinterpret_cast<uintptr_t>(dst_device) & 255) ||
+      (reinterpret_cast<uintptr_t>(scratch_device) & 255))
+    return st_fail(MOE_ERR_INVALID, "load_mxfp4: buffers must be 256-byte aligned");
+  unsigned char* d = static_cast<unsigned char*>(dst_device);
+  unsigned char* sc = static_cast<unsigned char*>(scratch_device);
+  moe_qproj q{};
+  q.weight = reinterpret_cast<const uint32_t*>(d + L.w_off);
+  q.scales = d + L.s_off;
+  q.biases = d + L.b_off;
+  q.out_bias = d + L.ob_off;
+  q.bits = 4;
+  q.group_size = 32;
+  q.sb_dtype = act_dtype;
+  q.n = (int32_t)L.N;
+  q.k = (int32_t)(32 * L.G);
+  q.n_experts = (int32_t)L.E;
+  ST_TRY(moe_validate_qproj(&q));
+  ST_TRY(upload_ranges({entry_range(bundle, *L.w, d + L.w_off),
+                        entry_range(bundle, *L.s, sc + L.sc_e8m0),
+                        entry_range(bundle, *L.bi, sc + L.sc_bias)},
+                       stream));
+  // the codes transcode in place; scales and biases land in act_dtype
+  hipError_t e = moe::launch_mxfp4_affine(reinterpret_cast<const uint32_t*>(d + L.w_off),
+                                          sc + L.sc_e8m0, L.E * L.N * L.G,
+                                          reinterpret_cast<uint32_t*>(d + L.w_off), d + L.s_off,
+                                          d + L.b_off, act_dtype, stream);
+  if (e == hipSuccess)
+    e = moe::launch_convert(sc + L.sc_bias, L.bi->dtype, d + L.ob_off, act_dtype, L.E * L.N,
+                            stream);
+  if (e != hipSuccess) return hip_fail(e, "MXFP4 transcode launch");
+  *out = q;
+  return st_ok();
+}
+

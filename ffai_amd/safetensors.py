@@ -40,6 +40,16 @@ def _stream(device: torch.device):
     return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+def _mx_views(q: QProj, buf: torch.Tensor, dtype: torch.dtype) -> StackedExperts:
+    """StackedExperts views of an MXFP4 projection moe_st_load_mxfp4 placed in
+    buf (affine 4-bit, group 32, per-row bias as out_bias)."""
+    se = _views(q, buf, 32)
+    ob = q.out_bias - buf.data_ptr()
+    esz = torch.tensor([], dtype=dtype).element_size()
+    se.out_bias = buf[ob:ob + q.n_experts * q.n * esz].view(dtype).view(q.n_experts, q.n)
+    return se
+
+
 def _views(q: QProj, buf: torch.Tensor, groupSize: int) -> StackedExperts:
     """StackedExperts views of a triplet that moe_st_load_stacked placed in buf."""
     E, N, K = q.n_experts, q.n, q.k
@@ -127,6 +137,26 @@ class SafeTensorsBundle:
         """The stacked triplet at ``base`` (``<base>.weight/.scales/.biases``)
         in one device allocation, bits derived from the shapes."""
         return self.stackedExpertsMany([base], groupSize, device)[0]
+
+    def mxfp4Experts(self, base: str, dtype: torch.dtype = torch.bfloat16,
+                     device="cuda") -> StackedExperts:
+        """A GPT-OSS MXFP4 stack (``<base>.weight/.scales/.bias``) transcoded
+        on the GPU to affine 4-bit with group size 32, scales, biases and
+        the per-row bias in ``dtype`` (transcodeStackedExperts,
+        GPTOSSText.swift:1071-1236)."""
+        adt = {torch.float32: _lib.MOE_F32, torch.float16: _lib.MOE_F16,
+               torch.bfloat16: _lib.MOE_BF16}[dtype]
+        nb, ns = C.c_size_t(), C.c_size_t()
+        check(self._lib.moe_st_mxfp4_bytes(self._h, base.encode(), adt, C.byref(nb), C.byref(ns)))
+        dev = torch.device(device)
+        buf = torch.empty(nb.value, dtype=torch.uint8, device=dev)
+        scratch = torch.empty(ns.value, dtype=torch.uint8, device=dev)
+        q = QProj()
+        check(self._lib.moe_st_load_mxfp4(self._h, base.encode(), adt, C.c_void_p(buf.data_ptr()),
+                                          nb.value, C.c_void_p(scratch.data_ptr()), ns.value,
+                                          C.byref(q), _stream(dev)))
+        torch.cuda.current_stream(dev).synchronize()  # the scratch is freed on return
+        return _mx_views(q, buf, dtype)
 
     def stackedExpertsMany(self, bases: List[str], groupSize: int,
                            device="cuda") -> List[StackedExperts]:

@@ -240,6 +240,23 @@ moe_status moe_unpermute(const void* Y, const uint32_t* inv_perm, const float* t
                          int32_t T, int32_t hidden, int32_t k, void* out, int32_t dtype,
                          hipStream_t stream);
 
+/* GPT-OSS's MXFP4 -> affine 4-bit transcode (transcodeStackedExperts,
+ * Models/Text/GPTOSSText.swift:1040-1236), on the GPU. n_groups groups of 32
+ * fp4 codes: packed [n_groups * 4] u32 (8 codes per word, low nibble first),
+ * e8m0 [n_groups] exponent bytes (value = LUT[code] * 2^(e8m0 - 127)). Per
+ * group: lo/hi = min/max table value, bias = lo * 2^(e-127), scale =
+ * (hi - lo) * 2^(e-127) / 15, code = clamp(round((LUT[code] - lo) *
+ * 2^(e-127) / scale), 0, 15) in the same nibble. Writes an mlx affine 4-bit
+ * triplet with group size 32: out_weight (may equal packed), out_scales and
+ * out_biases [n_groups] in sb_dtype. packed and out_weight 16-byte aligned.
+ * Bit-exact with the reference's f32 arithmetic for e8m0 in 3..254; for
+ * e8m0 0..2 (magnitudes below 2^-124) the reference's intermediates are
+ * subnormal and the GPU flushes them (the result stays finite); e8m0 = 255
+ * (2^128) is outside the format's finite range. */
+moe_status moe_mxfp4_to_affine(const uint32_t* packed, const uint8_t* e8m0, int64_t n_groups,
+                               uint32_t* out_weight, void* out_scales, void* out_biases,
+                               int32_t sb_dtype, hipStream_t stream);
+
 /* Ops.addAndRmsNorm (Ops.swift:676-730): per row, residual = a + b and
  * normed = residual / sqrt(mean(residual^2) + eps) * weight, each rounded to
  * dtype. [n_rows, row_size] rows (16-byte aligned), weight [row_size];

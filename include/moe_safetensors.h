@@ -114,6 +114,23 @@ moe_status moe_st_load_stacked_many(moe_st_t bundle, int32_t count, const char* 
                                     int32_t group_size, void* const* dst_device,
                                     const size_t* dst_bytes, moe_qproj* out, hipStream_t stream);
 
+/* GPT-OSS MXFP4 expert stacks (transcodeStackedExperts, Models/Text/
+ * GPTOSSText.swift:1071-1236): <base>.weight [E, N, K/8] u32 (fp4 codes),
+ * <base>.scales [E, N, K/32] u8 (e8m0 exponents) and <base>.bias [E, N]
+ * (f16, bf16 or f32; 2-D tensors are one expert). moe_st_mxfp4_bytes gives
+ * the device bytes of the loaded projection and the scratch bytes the load
+ * stages through; moe_st_load_mxfp4 uploads the three tensors, transcodes
+ * them on the GPU to an affine 4-bit triplet with group size 32 (scales and
+ * biases in act_dtype, moe_mxfp4_to_affine) and converts the per-row bias to
+ * act_dtype as out_bias. *out describes the result for moe_hip.h. The
+ * transcode is queued on `stream` after the copies: keep the scratch until
+ * the stream has passed it. */
+moe_status moe_st_mxfp4_bytes(moe_st_t bundle, const char* base, int32_t act_dtype,
+                              size_t* bytes, size_t* scratch_bytes);
+moe_status moe_st_load_mxfp4(moe_st_t bundle, const char* base, int32_t act_dtype,
+                             void* dst_device, size_t dst_bytes, void* scratch_device,
+                             size_t scratch_bytes, moe_qproj* out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -775,3 +775,56 @@ static int layer_impl(const or_layer* L, const void* x, const void* router_x, in
     free(perm); free(inv); free(rexp); free(a); free(g); free(Y); free(out);
     return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* MXFP4 -> affine 4-bit (GPTOSSText.swift:1040-1236)                       */
+/* ------------------------------------------------------------------------ */
+
+/* The mlx-lm gpt_oss MXFP4 table (GPTOSSText.swift:947-954). */
+static const float kMxfp4Lut[16] = {+0.0f, +0.5f, +1.0f, +1.5f, +2.0f, +3.0f, +4.0f, +6.0f,
+                                    -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+
+float or_mxfp4_value(int code) { return kMxfp4Lut[code & 15]; }
+
+/* Per 32-code group, the reference's two passes: min / max of the table
+ * values in byte order (low nibble first), bias = lo * 2^(e - 127),
+ * scale = (hi - lo) * mx / 15 (0 when flat), q = clamp(round((v - lo) *
+ * (mx * (1 / scale))), 0, 15) into the same nibble; scale and bias stored in
+ * sb_dt. packed/out_w hold groups * 4 words, e8m0 one byte per group. */
+void or_mxfp4_to_affine(const uint32_t* packed, const uint8_t* e8m0, long groups,
+                        uint32_t* out_w, void* out_s, void* out_b, int sb_dt) {
+    for (long g = 0; g < groups; g++) {
+        const uint8_t* bytes = (const uint8_t*)(packed + 4 * g);
+        float mx = (float)exp2((double)((int)e8m0[g] - 127));
+        float lo = 1e30f, hi = -1e30f;
+        for (int b = 0; b < 16; b++) {
+            float v0 = kMxfp4Lut[bytes[b] & 0x0F];
+            float v1 = kMxfp4Lut[bytes[b] >> 4];
+            if (v0 < lo) lo = v0;
+            if (v0 > hi) hi = v0;
+            if (v1 < lo) lo = v1;
+            if (v1 > hi) hi = v1;
+        }
+        float bias = lo * mx;
+        float span = (hi - lo) * mx;
+        float scale = span > 0 ? span / 15.0f : 0;
+        float inv = scale > 0 ? 1.0f / scale : 0;
+        float cs = mx * inv;
+        uint8_t* ob = (uint8_t*)(out_w + 4 * g);
+        uint8_t src[16];
+        memcpy(src, bytes, 16); /* out_w may alias packed */
+        for (int b = 0; b < 16; b++) {
+            long q0 = lroundf((kMxfp4Lut[src[b] & 0x0F] - lo) * cs);
+            long q1 = lroundf((kMxfp4Lut[src[b] >> 4] - lo) * cs);
+            if (q0 < 0) q0 = 0;
+            if (q0 > 15) q0 = 15;
+            if (q1 < 0) q1 = 0;
+            if (q1 > 15) q1 = 15;
+            ob[b] = (uint8_t)(q0 | (q1 << 4));
+        }
+        float sv = scale, bv = bias;
+        or_store(&sv, sb_dt, 1, (char*)out_s + (size_t)g * (sb_dt == OR_F32 ? 4 : 2));
+        or_store(&bv, sb_dt, 1, (char*)out_b + (size_t)g * (sb_dt == OR_F32 ? 4 : 2));
+    }
+}
+

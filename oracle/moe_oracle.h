@@ -141,6 +141,11 @@ int or_moe_layer_residual(const or_layer* L, const void* h, const void* m, const
                           float* xn_out, float* res_out, float* logits_out, uint32_t* idx_out,
                           float* w_out);
 
+/* ---- MXFP4 -> affine 4-bit transcode (GPTOSSText.swift:941-1236) ------- */
+float or_mxfp4_value(int code);
+void or_mxfp4_to_affine(const uint32_t* packed, const uint8_t* e8m0, long groups,
+                        uint32_t* out_w, void* out_s, void* out_b, int sb_dt);
+
 #ifdef __cplusplus
 }
 #endif

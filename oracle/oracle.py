@@ -107,6 +107,9 @@ def _declare(L):
     L.or_moe_layer_residual.argtypes = [C.POINTER(OrLayer), vp, vp, vp, f, i, vp, vp, vp, vp, vp,
                                         vp, vp]
     L.or_moe_layer_residual.restype = i
+    L.or_mxfp4_value.argtypes = [i]; L.or_mxfp4_value.restype = f
+    L.or_mxfp4_to_affine.argtypes = [vp, vp, C.c_long, vp, vp, vp, i]
+    L.or_mxfp4_to_affine.restype = None
 
 
 def _p(a):
@@ -363,3 +366,25 @@ def moe_layer_residual(spec, h, m, norm_w, eps, given_logits=None):
     if rc != 0:
         raise ValueError("invalid layer description")
     return y, xn, res, logits, idx, w
+
+
+# ----------------------------------------------------- MXFP4 transcode ----
+
+def mxfp4_value(code: int) -> float:
+    return lib().or_mxfp4_value(int(code))
+
+
+def mxfp4_to_affine(packed, e8m0, sb_dt=BF16):
+    """packed: u32 [..., K/8], e8m0: u8 [..., K/32] -> (codes u32 like packed,
+    scales, biases [..., K/32] as sb_dt storage arrays)."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint32)
+    e8m0 = np.ascontiguousarray(e8m0, dtype=np.uint8)
+    groups = e8m0.size
+    assert packed.size == 4 * groups
+    out_w = np.zeros_like(packed)
+    sdt = np_dtype(sb_dt)
+    out_s = np.zeros(e8m0.shape, dtype=sdt)
+    out_b = np.zeros(e8m0.shape, dtype=sdt)
+    lib().or_mxfp4_to_affine(_p(packed), _p(e8m0), groups, _p(out_w), _p(out_s), _p(out_b), sb_dt)
+    return out_w, out_s, out_b
+
