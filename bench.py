@@ -139,14 +139,18 @@ def proj_bytes(p, experts):
 
 def measured_traffic(workload, T):
     """HBM bytes per launch of the dominant kernel from the committed FETCH_SIZE
-    / WRITE_SIZE passes (profiles/<workload>_traffic.json), or None."""
-    path = os.path.join(ROOT, "profiles", f"{workload}_traffic.json")
-    if T != 1 or not os.path.exists(path):
+    / WRITE_SIZE passes (the profiles/*_traffic.json whose "workload" is this
+    one), or None."""
+    import glob
+    if T != 1:
         return None
-    with open(path) as f:
-        data = json.load(f)
-    k = data.get("kernels", {}).get("gateup1_kernel")
-    return None if k is None else k["hbm_bytes"]
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_traffic.json"))):
+        with open(path) as f:
+            data = json.load(f)
+        if data.get("workload") == workload:
+            k = data.get("kernels", {}).get("gateup1_kernel")
+            return None if k is None else k["hbm_bytes"]
+    return None
 
 
 # ------------------------------------------------------------ CPU oracle --
