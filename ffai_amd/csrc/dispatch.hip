@@ -249,9 +249,13 @@ hipError_t launch_dispatch_plan(const uint32_t* idx, int T, int k, int E, uint32
 __global__ __launch_bounds__(kPlanThreads) void gemm_tiles_kernel(const uint32_t* __restrict__ offsets,
                                                                   int E, int bm,
                                                                   uint32_t* __restrict__ tiles) {
+  // An expert's rows are covered by bm-row tiles; a last partial tile of at
+  // most bm / 2 rows is a half tile (its expert id carries kHalfTile), so
+  // the kernel spreads it over all its waves instead of leaving half idle.
   __shared__ uint32_t scan[kPlanThreads];
   constexpr int EPT = kPlanMaxE / kPlanThreads;  // experts per thread
   const int t = threadIdx.x;
+  const uint32_t hb = (uint32_t)bm / 2u;
   uint32_t n[EPT], tot = 0;
 #pragma unroll
   for (int j = 0; j < EPT; j++) {
@@ -272,8 +276,10 @@ __global__ __launch_bounds__(kPlanThreads) void gemm_tiles_kernel(const uint32_t
 #pragma unroll
   for (int j = 0; j < EPT; j++) {
     const int e = t * EPT + j;
+    const uint32_t rows = e < E ? offsets[e + 1] - offsets[e] : 0u;
     for (uint32_t i = 0; i < n[j]; i++) {
-      tiles[1 + 2 * (base + i)] = (uint32_t)e;
+      const uint32_t left = rows - i * (uint32_t)bm;
+      tiles[1 + 2 * (base + i)] = (uint32_t)e | (left <= hb ? kHalfTile : 0u);
       tiles[2 + 2 * (base + i)] = offsets[e] + i * (uint32_t)bm;
     }
     base += n[j];

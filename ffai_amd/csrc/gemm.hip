@@ -10,8 +10,9 @@
 //   single:   out[p, n] = round(W[e(p)][n] . a[p])
 // over the expert-sorted positions p of a dispatch plan.
 //
-// Work: a tile list of (expert, 256 consecutive sorted positions); block =
-// one tile x one column slice (256 weight rows). Per 64-value chunk of K the
+// Work: a tile list of (expert, up to 256 consecutive sorted positions; the
+// last tile of an expert with at most 128 rows is a half tile); block = one
+// tile x one column slice (256 weight rows). Per 64-value chunk of K the
 // block stages the tile's activation rows and the slice's weights,
 // dequantised once per block to the MFMA operand type, in double-buffered
 // LDS; 8 waves multiply with v_mfma_f32_32x32x16 (see the kernel comment).
@@ -22,6 +23,8 @@
 // 16-deep MFMA reduction feeds values 16 s + 8 h + e, e < 8 (LDS chunk
 // 2 s + h of the row); A and B fragments are read in the same order.
 #include <hip/hip_ext.h>
+
+#include <type_traits>
 
 #include "moe_common.hpp"
 #include "moe_internal.hpp"
@@ -134,8 +137,10 @@ __device__ __forceinline__ void lds_barrier() {
 // gate and of up; otherwise 256 output columns), 8 waves in a 4 x 2 grid:
 // wave (wm, wn) owns rows [64 wm, +64) as 2 MFMA row tiles and 4 MFMA column
 // tiles (gate/up: gate columns [64 wn, +64) and the matching up columns), so
-// its accumulators fit 128 AGPRs and two waves share each SIMD. Row tiles
-// past the expert's last position skip their MFMAs.
+// its accumulators fit 128 registers and two waves share each SIMD. Row
+// tiles past the expert's last position skip their MFMAs. A half tile (the
+// last tile of an expert, at most 128 rows) gives each wave the 32-row band
+// [32 wm, +32) instead, so its rows are spread over all four SIMDs.
 //
 // Per 64-value chunk: every thread copies 64 bytes of activation rows and
 // dequantises one 32-value unit of one weight row into LDS, once for the
@@ -166,8 +171,12 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
   const int bn = (int)(wi - tile * (uint32_t)n_tiles);
   // tile fields are block-uniform; readfirstlane keeps the buffer resources
   // built from them scalar
-  const uint32_t e = __builtin_amdgcn_readfirstlane(a.tiles[1 + 2 * tile]);
+  const uint32_t ef = __builtin_amdgcn_readfirstlane(a.tiles[1 + 2 * tile]);
+  const uint32_t e = ef & ~kHalfTile;
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(a.tiles[2 + 2 * tile]);
+  // rows per wave band: 64 (two MFMA row tiles) in a full 256-row tile, 32
+  // (one) in a half tile, so that all four SIMDs share a short tile's rows
+  const int band = (ef & kHalfTile) ? 32 : 64;
   const uint32_t pend = __builtin_amdgcn_readfirstlane(a.offsets[e + 1]);
 
   const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
@@ -238,32 +247,44 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = f32x16_t{};
 
-  // row tiles of this wave that hold positions of the expert
-  const int mvalid = (m0 + (uint32_t)(64 * wm) >= pend) ? 0
-                   : (m0 + (uint32_t)(64 * wm + 32) >= pend) ? 1 : 2;
+  // row tiles of this wave's band that hold positions of the expert
+  const uint32_t bstart = m0 + (uint32_t)(band * wm);
+  const int mvalid = (bstart >= pend) ? 0 : (band == 32 || bstart + 32u >= pend) ? 1 : 2;
 
-  // MFMA operand rows of this lane: A rows 64 wm + 32 i + col, B rows
+  // MFMA operand rows of this lane: A rows band wm + 32 i + col, B rows
   // (gate/up) 64 wn + 32 j + col and 128 + 64 wn + 32 (j - 2) + col, or
   // 128 wn + 32 j + col; all congruent to col mod 16, so they share
   // tile_swz(col)
   const int col = lane & 31, h = lane >> 5;
-  const uint32_t arow0 = (uint32_t)(64 * wm + col) * 128u;
+  const uint32_t arow0 = (uint32_t)(band * wm + col) * 128u;
   const uint32_t brow0 = (uint32_t)((GATEUP ? 64 * wn : 128 * wn) + col) * 128u;
   auto boff = [&](int j) -> uint32_t {
     return GATEUP ? (uint32_t)((j < 2 ? 32 * j : 128 + 32 * (j - 2)) * 128) : (uint32_t)(32 * j * 128);
   };
 
-  // One chunk: MFMAs on LDS buffer `buf`; meanwhile chunk c + 1's weights
-  // (set nb) are dequantised into the other buffer between the steps and its
-  // activations (set na) stored after them, and chunk c + 2 loads into the
-  // sets ca / cb that chunk c used.
+  // One chunk: MFMAs on LDS buffer `buf`. First chunk c + 1's activations
+  // (loaded during chunk c - 1) go from `ar` to the other buffer, which
+  // chunk c - 1's closing barrier freed, and `ar` takes chunk c + 2's loads;
+  // chunk c + 1's weights (set nb) are dequantised into the other buffer
+  // between the MFMA steps, and chunk c + 2's weights load into the set cb
+  // that chunk c used. One activation register set suffices.
   // Loads and LDS writes are unconditional (past the end they repeat the
   // last chunk, in bounds and never read) so that the compiler can count
   // outstanding loads exactly and never waits for the newest ones.
-  auto chunk_step = [&](int c, int buf, ARegs& ca, BUnit& cb, const ARegs& na, const BUnit& nb) {
+  // MV: row tiles of this wave with positions of the expert (0..2), a
+  // compile-time constant so that each version of the loop is straight-line
+  // code the compiler can schedule across steps (a branch per row tile split
+  // every step into blocks that serialised LDS reads and MFMAs)
+  auto chunk_step = [&](auto mv, int c, int buf, ARegs& ar, BUnit& cb, const BUnit& nb) {
+    constexpr int MV = decltype(mv)::value;
     const int cp = min(c + 2, nchunks - 1);
-    load_a(cp, ca);
+    store_a(ar, buf ^ 1);
+    load_a(cp, ar);
     load_b(cp, cb);
+    // keep chunk c + 2's loads issued here: sunk below the first weight
+    // dequantisation they turned its wait for chunk c + 1's weights into a
+    // wait for every load in flight
+    __builtin_amdgcn_sched_barrier(0);
     const unsigned char* Ab = &As[buf][0];
     const unsigned char* Bb = &Bs[buf][0];
     // operand fragments of step s + 1 are read while step s multiplies
@@ -280,33 +301,36 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
     for (int s = 0; s < 4; s++) {
       if (s < 3) read_frags(s + 1, bf[(s + 1) & 1], af[(s + 1) & 1]);
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
-        if (i < mvalid) {
+      for (int i = 0; i < MV; i++) {
 #pragma unroll
-          for (int j = 0; j < 4; j++) acc[i][j] = MfmaOp<XT>::mma(af[s & 1][i], bf[s & 1][j], acc[i][j]);
-        }
+        for (int j = 0; j < 4; j++) acc[i][j] = MfmaOp<XT>::mma(af[s & 1][i], bf[s & 1][j], acc[i][j]);
       }
       store_b(nb, s, buf ^ 1);
     }
-    store_a(na, buf ^ 1);
     lds_barrier();
   };
 
-  ARegs a0, a1;
+  ARegs ar;
   BUnit u0, u1;
-  load_a(0, a0);
+  load_a(0, ar);
   load_b(0, u0);
-  load_a(min(1, nchunks - 1), a1);
   load_b(min(1, nchunks - 1), u1);
-  store_a(a0, 0);
+  store_a(ar, 0);
+  load_a(min(1, nchunks - 1), ar);
 #pragma unroll
   for (int s = 0; s < 4; s++) store_b(u0, s, 0);
   lds_barrier();
 
-  for (int c = 0; c < nchunks; c += 2) {
-    chunk_step(c, 0, a0, u0, a1, u1);
-    if (c + 1 < nchunks) chunk_step(c + 1, 1, a1, u1, a0, u0);
-  }
+  auto run = [&](auto mv) {
+    for (int c = 0; c < nchunks; c += 2) {
+      chunk_step(mv, c, 0, ar, u0, u1);
+      if (c + 1 < nchunks) chunk_step(mv, c + 1, 1, ar, u1, u0);
+    }
+  };
+  // mvalid is wave-uniform: one scalar branch picks the loop
+  if (mvalid == 2) run(std::integral_constant<int, 2>{});
+  else if (mvalid == 1) run(std::integral_constant<int, 1>{});
+  else run(std::integral_constant<int, 0>{});
 
   // epilogue: lane holds column col, rows 8 (r / 4) + 4 h + r % 4 of each
   // 32 x 32 tile. The wave's finished outputs (64 rows x OC columns) go
@@ -317,7 +341,7 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
   const XT* ob1 = reinterpret_cast<const XT*>(GATEUP ? a.p1.ob : a.p0.ob);
   constexpr int OC = GATEUP ? 64 : 128;  // output columns per wave
   const int cbase = GATEUP ? bn * 128 + 64 * wn : bn * 256 + 128 * wn;
-  const uint32_t prow0 = m0 + (uint32_t)(64 * wm);
+  const uint32_t prow0 = bstart;
   // 8 waves x 64 x OC 16-bit values: As holds waves 0-3, Bs waves 4-7
   XT* wt = reinterpret_cast<XT*>(wave < 4 ? &As[0][0] : &Bs[0][0]) + (wave & 3) * 64 * OC;
 #pragma unroll
@@ -353,7 +377,8 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
     const uint32_t p = prow0 + (uint32_t)row;
     const int cn0 = cbase + 8 * c8;
     const u32x4_t v = *reinterpret_cast<const u32x4_t*>(wt + row * OC + 8 * c8);
-    if (p < pend && cn0 < N)  // N % 8 == 0 (host check): whole 16-byte groups
+    // rows past the band belong to the next wave (half tiles)
+    if (row < band && p < pend && cn0 < N)  // N % 8 == 0 (host check): whole 16-byte groups
       *reinterpret_cast<u32x4_t*>(out + (size_t)p * N + cn0) = v;
   }
 }

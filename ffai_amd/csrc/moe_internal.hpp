@@ -177,13 +177,16 @@ struct GemmArgs {
   const uint32_t* perm;      // nullable: row(p) = perm[p] / topk, else p
   int topk;
   const uint32_t* offsets;   // [E+1] CSR over sorted positions
-  const uint32_t* tiles;     // [1 + 2 * max_tiles]: count, (expert, first position)
+  const uint32_t* tiles;     // [1 + 2 * max_tiles]: count, (expert | kHalfTile?, first position)
   void* out;                 // [M, N]
   int N, K, gsh;
   int act;
   float alpha, limit;
 };
 constexpr int kGemmRows = 256;  // rows per tile
+// Expert-id flag of a tile list entry: a half tile (at most kGemmRows / 2
+// rows, the last of its expert).
+constexpr uint32_t kHalfTile = 0x80000000u;
 // Output columns per block: 128 (gate/up pairs) or 256 (single projection).
 inline int gemm_block_cols(bool gateup) { return gateup ? 128 : 256; }
 inline int gemm_max_tiles(int M, int E) { return (M + kGemmRows - 1) / kGemmRows + E; }
