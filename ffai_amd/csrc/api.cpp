@@ -845,10 +845,9 @@ Dec1Geom dec1_geom(int N, int K, int gsh, int k, bool down) {
 
 bool dec1_supported(const moe_layer_desc* d) {
   if (d->act_dtype == MOE_F32 || d->top_k > kDec1MaxK) return false;
-  if (d->activation == MOE_ACT_RELU2) return false;  // the kernel pairs gate and up rows
   if (d->hidden > 8192 || d->intermediate > 8192) return false;
   // expert-local byte offsets stay below 2^31 (with a row block of slack)
-  const moe_qproj* ps[3] = {&d->gate, &d->up, &d->down};
+  const moe_qproj* ps[2] = {&d->up, &d->down};  // gate, when present, is shaped as up
   for (const moe_qproj* p : ps) {
     const size_t row_bytes = (size_t)p->k * p->bits / 8;
     if (((size_t)p->n + 256) * row_bytes >= (1ull << 31)) return false;
@@ -960,7 +959,10 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
   if (dec1) {
     // 2. one token: routing inside the gate/up kernel (MoELayer.swift:1167-1282
     //    without a host round trip), then the fused down + combine
-    const Dec1Geom gg = dec1_geom(I, H, group_shift(d->gate.group_size), k, false);
+    // gate/up rows (the up projection alone for squared-ReLU experts: the
+    // kernel reads zeros for the missing gate)
+    const moe_qproj& gu = d->activation == MOE_ACT_RELU2 ? d->up : d->gate;
+    const Dec1Geom gg = dec1_geom(I, H, group_shift(gu.group_size), k, false);
     Decode1Args g{};
     g.logits = at<void>(ws, w.logits);
     g.E = E;
@@ -976,14 +978,14 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     g.act = at<void>(ws, w.act);
     g.N = I;
     g.K = H;
-    g.gsh = group_shift(d->gate.group_size);
+    g.gsh = group_shift(gu.group_size);
     g.lg = gg.lg;
     g.rows_per_block = gg.rows_per_block;
     g.row_blocks = gg.grid / k;
     g.act_kind = d->activation;
     g.alpha = d->act_alpha;
     g.limit = d->act_limit;
-    MOE_HIP(launch_gateup1(d->gate.bits, xdt, d->gate.sb_dtype, g, gg.rm, gg.grid, st, kev(0)),
+    MOE_HIP(launch_gateup1(gu.bits, xdt, gu.sb_dtype, g, gg.rm, gg.grid, st, kev(0)),
             "gate/up decode launch");
     MOE_TRY(shared_expert(d, x, T, ws, w, st, &smode));
     // the residual goes into the last store: down1's without a shared expert

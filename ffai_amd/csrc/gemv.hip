@@ -296,8 +296,13 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
     obg[it] = ob_g ? to_f<XT>(ob_g[(size_t)e * N + row]) : 0.f;
     obu[it] = ob_u ? to_f<XT>(ob_u[(size_t)e * N + row]) : 0.f;
   }
-  const ProjView G = proj_view<BITS, ST>(a.g, (uint32_t)e, N, row_words, groups);
+  // squared-ReLU experts have no gate projection (g.w null): the gate reads
+  // go to empty buffer views, which return zeros without touching memory
+  // (no branch around the loads), and the activation reads u only
   const ProjView U = proj_view<BITS, ST>(a.u, (uint32_t)e, N, row_words, groups);
+  const rsrc_t none = make_rsrc(a.u.w, 0u);
+  const ProjView G = a.g.w ? proj_view<BITS, ST>(a.g, (uint32_t)e, N, row_words, groups)
+                           : ProjView{none, none, none};
   const uint32_t wstep = (uint32_t)(L * BITS * 4), sstep = (uint32_t)((L >> a.gsh) * sizeof(ST));
   WUnit<BITS, ST> gw[RM][UR], uw[RM][UR];
 #pragma unroll
