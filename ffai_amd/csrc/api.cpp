@@ -468,12 +468,15 @@ bool gemm_ok(const moe_qproj& p, int xdt, int M, const void* out = nullptr) {
          M >= kGemmMinRows * slots && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
 }
 
-// Router logits on the matrix cores for many tokens: a one-expert plan over
-// the T rows with the dense router weight; the bias rounds after the product
-// as in router_logits_kernel.
+// Router logits on the matrix cores for many tokens when the expert count is
+// not a multiple of 32: a one-expert plan over the T rows with the dense
+// router weight through the grouped GEMM; the bias rounds after the product
+// as in router_logits_kernel. Multiples of 32 take router_gemm_kernel inside
+// launch_router_logits instead (no plan, every CU busy).
 bool router_gemm_ok(const moe_layer_desc* d, int T) {
   return T >= kGemmMinRows && d->act_dtype != MOE_F32 && d->router_dtype == d->act_dtype &&
-         d->hidden % 64 == 0 && d->n_experts % 8 == 0 && (size_t)T * d->hidden * 2 < (1ull << 32);
+         d->hidden % 64 == 0 && d->n_experts % 8 == 0 && d->n_experts % 32 != 0 &&
+         (size_t)T * d->hidden * 2 < (1ull << 32);
 }
 
 moe_status run_router_gemm(const moe_layer_desc* d, const void* x, int T, void* logits,

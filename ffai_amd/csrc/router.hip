@@ -229,6 +229,109 @@ __global__ __launch_bounds__(256) void router_logits_row_kernel(const XT* __rest
   }
 }
 
+// Router logits for many tokens on the matrix cores. Block = one tile of 32
+// tokens x 32 experts; its 4 waves split the hidden dimension into 64-value
+// groups g = wave + 4 i and each accumulates its groups with
+// v_mfma_f32_32x32x16. Both operands come straight from global memory in
+// fragment order: lane (c, h) of step q holds values 16 q + 8 h .. + 8 of
+// token row c (A) and of expert row c (B), 16 contiguous bytes each, so no
+// LDS staging is needed; loads run two groups ahead of the MFMAs. The four
+// partial tiles are added in wave order through LDS, then rounded as
+// router_logits_kernel rounds (product, then + bias). Needs H % 64 == 0,
+// E % 32 == 0 and T * H, E * H below 2^31 elements (32-bit byte offsets).
+// Four waves per tile measured faster than eight or sixteen on the Qwen3 and
+// GPT-OSS prefill shapes (18 against 22 and 25 us for 4096 tokens, 128
+// experts).
+constexpr int kRgWaves = 4;
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+template <typename XT> struct RgMfma;
+template <> struct RgMfma<bf16_t> {
+  typedef __bf16 V __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16_t mma(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(V, a), __builtin_bit_cast(V, b), c, 0, 0, 0);
+  }
+};
+template <> struct RgMfma<f16_t> {
+  typedef _Float16 V __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16_t mma(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(V, a), __builtin_bit_cast(V, b), c, 0, 0, 0);
+  }
+};
+
+template <typename XT>
+__global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __restrict__ x,
+                                                                    const XT* __restrict__ W,
+                                                                    const XT* __restrict__ bias,
+                                                                    XT* __restrict__ logits, int T,
+                                                                    int H, int E) {
+  // partial tiles, rows padded to 33 floats
+  __shared__ float part[kRgWaves][32 * 33];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 31, h = lane >> 5;
+  const int t0 = blockIdx.x * 32, e0 = blockIdx.y * 32;
+  // rows past T repeat the last token; their outputs are not stored
+  const uint32_t row = (uint32_t)min(t0 + col, T - 1);
+  const uint32_t ex = (uint32_t)(e0 + col);
+  const rsrc_t xr = make_rsrc(x, (uint32_t)((size_t)T * H * sizeof(XT)));
+  const rsrc_t wr = make_rsrc(W, (uint32_t)((size_t)E * H * sizeof(XT)));
+  const uint32_t xo = (row * (uint32_t)H + 8u * (uint32_t)h) * 2u;
+  const uint32_t wo = (ex * (uint32_t)H + 8u * (uint32_t)h) * 2u;
+  const int G = H >> 6;
+  const int ng = (G - wv + kRgWaves - 1) / kRgWaves;  // groups wv + 4 i, i < ng (0 when wv >= G)
+
+  struct Set {
+    u32x4_t a[4], b[4];
+  };
+  // group i of this wave (clamped into the row: loads past the wave's last
+  // group are in bounds and never multiplied)
+  auto load = [&](int i, Set& s) __attribute__((always_inline)) {
+    const uint32_t kb = (uint32_t)min(wv + kRgWaves * i, G - 1) * 128u;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      s.a[q] = bload128(xr, xo + kb + 32u * (uint32_t)q);
+      s.b[q] = bload128(wr, wo + kb + 32u * (uint32_t)q);
+    }
+  };
+  f32x16_t acc = {};
+  auto mma = [&](const Set& s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) acc = RgMfma<XT>::mma(s.a[q], s.b[q], acc);
+  };
+  Set s0, s1, s2;
+  load(0, s0);
+  load(1, s1);
+  for (int i = 0; i < ng; i += 3) {  // ng is wave-uniform: scalar branches
+    load(i + 2, s2);
+    mma(s0);
+    if (i + 1 >= ng) break;
+    load(i + 3, s0);
+    mma(s1);
+    if (i + 2 >= ng) break;
+    load(i + 4, s1);
+    mma(s2);
+  }
+
+  // lane (col, h) holds rows 8 (r / 4) + 4 h + r % 4 of column col
+#pragma unroll
+  for (int r = 0; r < 16; r++) part[wv][(8 * (r >> 2) + 4 * h + (r & 3)) * 33 + col] = acc[r];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 1024 / (64 * kRgWaves); j++) {
+    const int o = threadIdx.x + 64 * kRgWaves * j;
+    const int r = o >> 5, c = o & 31;
+    float s = part[0][r * 33 + c];
+#pragma unroll
+    for (int w = 1; w < kRgWaves; w++) s += part[w][r * 33 + c];
+    if (t0 + r < T) {
+      float l = round_to<XT>(s);
+      if (bias) l = round_to<XT>(l + to_f<XT>(bias[e0 + c]));
+      logits[(size_t)(t0 + r) * E + e0 + c] = from_f<XT>(l);
+    }
+  }
+}
+
 // One wave per token row (wave_topk); weights are reproducible bit for bit.
 template <typename XT>
 __global__ __launch_bounds__(256) void router_topk_kernel(const XT* __restrict__ logits, int T,
@@ -252,6 +355,12 @@ template <typename XT, typename WT>
 static hipError_t launch_rl(const void* x, int T, int H, const void* W, const void* bias, int E,
                             void* logits, hipStream_t st) {
   if constexpr (__is_same(XT, WT) && !__is_same(XT, float)) {
+    if (T >= 32 && H % 64 == 0 && E % 32 == 0 && (size_t)T * H < (1ull << 31) &&
+        (size_t)E * H < (1ull << 31)) {
+      hipLaunchKernelGGL((router_gemm_kernel<XT>), dim3((T + 31) / 32, E / 32), dim3(64 * kRgWaves),
+                         0, st, (const XT*)x, (const XT*)W, (const XT*)bias, (XT*)logits, T, H, E);
+      return hipGetLastError();
+    }
     if (T == 1 && H <= 4 * 2048) {
       const int nl4 = (H + 2047) / 2048;
 #define MOE_RLR(NL)                                                                         \
