@@ -612,7 +612,7 @@ def main():
     gemm_path = T > 1 and M >= 32 * min(cfg["E"], M) and cfg["H"] % 64 == 0 and cfg["I"] % 64 == 0
     roof["kernel"] = ("gateup1_kernel (one-token gate/up with routing)" if T == 1 else
                       "gemm_grouped_kernel (MFMA gate/up over the expert row tiles)" if gemm_path else
-                      "gemv_grouped_kernel (routed gate/up over the dispatch plan)")
+                      "gemv_multi_kernel (routed gate/up over the dispatch plan)")
     roof["avg_us"] = round(gu_us, 3)
     roof["algorithmic_bytes"] = k_bytes
     log(f"gate/up kernel {gu_us:.2f} us ({k_bytes / 1e6:.2f} MB, "

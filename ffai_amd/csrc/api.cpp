@@ -31,6 +31,26 @@ hipError_t launch_dec1_b4(int, int, bool, int, int, const void*, int, size_t, hi
 hipError_t launch_dec1_b5(int, int, bool, int, int, const void*, int, size_t, hipStream_t, KEvents);
 hipError_t launch_dec1_b6(int, int, bool, int, int, const void*, int, size_t, hipStream_t, KEvents);
 hipError_t launch_dec1_b8(int, int, bool, int, int, const void*, int, size_t, hipStream_t, KEvents);
+hipError_t launch_multi_b2(int, int, bool, int, int, const GemvArgs&, int, size_t, hipStream_t, KEvents);
+hipError_t launch_multi_b3(int, int, bool, int, int, const GemvArgs&, int, size_t, hipStream_t, KEvents);
+hipError_t launch_multi_b4(int, int, bool, int, int, const GemvArgs&, int, size_t, hipStream_t, KEvents);
+hipError_t launch_multi_b5(int, int, bool, int, int, const GemvArgs&, int, size_t, hipStream_t, KEvents);
+hipError_t launch_multi_b6(int, int, bool, int, int, const GemvArgs&, int, size_t, hipStream_t, KEvents);
+hipError_t launch_multi_b8(int, int, bool, int, int, const GemvArgs&, int, size_t, hipStream_t, KEvents);
+
+static hipError_t launch_multi(int bits, int xdt, int sbdt, bool gateup, int ur, int tm,
+                               const GemvArgs& a, int grid, size_t smem, hipStream_t st,
+                               KEvents ev) {
+  switch (bits) {
+    case 2: return launch_multi_b2(xdt, sbdt, gateup, ur, tm, a, grid, smem, st, ev);
+    case 3: return launch_multi_b3(xdt, sbdt, gateup, ur, tm, a, grid, smem, st, ev);
+    case 4: return launch_multi_b4(xdt, sbdt, gateup, ur, tm, a, grid, smem, st, ev);
+    case 5: return launch_multi_b5(xdt, sbdt, gateup, ur, tm, a, grid, smem, st, ev);
+    case 6: return launch_multi_b6(xdt, sbdt, gateup, ur, tm, a, grid, smem, st, ev);
+    case 8: return launch_multi_b8(xdt, sbdt, gateup, ur, tm, a, grid, smem, st, ev);
+  }
+  return hipErrorInvalidValue;
+}
 
 
 hipError_t launch_gemm_b2(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
@@ -421,12 +441,83 @@ template <typename P> P* at(void* base, size_t off) {
 
 GemvProj to_proj(const moe_qproj& q) { return GemvProj{q.weight, q.scales, q.biases, q.out_bias}; }
 
+int pick_lg_dec1(int CU, int gsh);
+
+// Row iterations per gemv_multi_kernel block (each shares the block's staged
+// activation rows; two keep both iterations' weight loads in flight at once,
+// more measured slower) and the block count below which fewer are used.
+constexpr int kMultiIters = 2;
+constexpr int kMultiBlocks = 1024;
+
+// gemv_multi_kernel for a few rows per expert (16-bit activations):
+// kMultiRows weight rows per lane, lanes per row as for the one-token
+// kernels, up to 4 or 8 activation rows per pass (rows in all, max_rows at
+// most for one expert), activation units staged in at most 64 KB of LDS.
+// Returns false where the older grouped kernel has to run instead.
+bool run_multi(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
+               const uint32_t* perm, int topk, const uint32_t* offsets, const uint32_t* used,
+               int slots, int max_rows, void* out, int act, float alpha, float limit,
+               hipStream_t st, KEvents ev, moe_status* status, int rows) {
+  if (xdt == MOE_F32 || p0.sb_dtype == MOE_F32) return false;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0) return false;  // 16-byte activation loads
+  const int gsh = group_shift(p0.group_size);
+  const int CU = p0.k / 32;
+  const int lg = pick_lg_dec1(CU, gsh);
+  const int L = 1 << lg, ur = (CU + L - 1) / L;
+  if (ur > 4) return false;
+  // rows per pass: 4 when no expert, or the average used expert, has more
+  // (fewer accumulators: three blocks per CU instead of two; the few
+  // experts above the average take a second pass), else 8
+  const int tm = (max_rows <= 4 || (long)rows / std::max(1, slots) <= 4) ? 4 : 8;
+  const size_t smem = (size_t)tm * CU * 68;
+  if (smem > 65536) return false;
+  // expert-local byte offsets stay below 2^31 (with a row block of slack)
+  if (((size_t)p0.n + 256) * ((size_t)p0.k * p0.bits / 8) >= (1ull << 31)) return false;
+  // R1 rows per iteration; up to kMultiIters iterations per block, fewer
+  // while that leaves under kMultiBlocks blocks for the used experts
+  const int SG = 64 >> lg, R1 = 4 * SG * kMultiRows(p1 != nullptr);
+  const int groups_per_expert = (p0.n + R1 - 1) / R1;
+  const int nit = std::max(1, std::min(kMultiIters, groups_per_expert * slots / kMultiBlocks));
+  const int rows_per_block = nit * R1;
+  const int row_blocks = (p0.n + rows_per_block - 1) / rows_per_block;
+  GemvArgs a{};
+  a.p0 = to_proj(p0);
+  if (p1) a.p1 = to_proj(*p1);
+  a.x = x;
+  a.perm = perm;
+  a.topk = topk;
+  a.offsets = offsets;
+  a.used = used;
+  a.out = out;
+  a.N = p0.n;
+  a.K = p0.k;
+  a.gsh = gsh;
+  a.row_blocks = row_blocks;
+  a.rows_per_block = rows_per_block;
+  a.lg = lg;
+  a.tok_chunk = tm;
+  a.act = act;
+  a.alpha = alpha;
+  a.limit = limit;
+  const hipError_t err = launch_multi(p0.bits, xdt, p0.sb_dtype, p1 != nullptr, ur, tm, a,
+                                     slots * row_blocks, smem, st, ev);
+  *status = hip_check(err, "grouped GEMV launch");
+  return true;
+}
+
 // out[p] = W[e(p)] . a[row(p)] over a plan; optionally a gate/up pair with
-// the activation fused.
+// the activation fused. max_rows bounds the rows of any one expert (T for
+// routed tokens, which pick an expert at most once each).
 moe_status run_gemv(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
                     const uint32_t* perm, int topk, const uint32_t* offsets, const uint32_t* used,
                     int slots, int M, bool single, void* out, int act, float alpha, float limit,
-                    hipStream_t st, KEvents ev = {}) {
+                    hipStream_t st, KEvents ev = {}, int max_rows = 1 << 30) {
+  if (!single) {
+    moe_status status = MOE_OK;
+    if (run_multi(p0, p1, x, xdt, perm, topk, offsets, used, slots, std::min(max_rows, M), out,
+                  act, alpha, limit, st, ev, &status, M))
+      return status;
+  }
   const int gsh = group_shift(p0.group_size);
   GemvGeom g = gemv_geom(p0.n, p0.k, gsh, slots, single, M, xdt);
   GemvArgs a{};
@@ -1024,7 +1115,8 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     } else {
       MOE_TRY(run_gemv(p0, p1, x, xdt, at<uint32_t>(ws, w.perm), k,
                        at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, T == 1,
-                       at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st, kev(0)));
+                       at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st, kev(0),
+                       T));
     }
     MOE_TRY(shared_expert(d, x, T, ws, w, st, &smode));
     // 4. down projection, then the weighted combine (MoELayer.swift:899-939)
@@ -1035,7 +1127,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     } else {
       MOE_TRY(run_gemv(d->down, nullptr, at<void>(ws, w.act), xdt, nullptr, 1,
                        at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, T == 1,
-                       at<void>(ws, w.Y), 0, 0.f, 0.f, st, kev(1)));
+                       at<void>(ws, w.Y), 0, 0.f, 0.f, st, kev(1), T));
     }
     MOE_HIP(launch_unpermute(at<void>(ws, w.Y), at<uint32_t>(ws, w.inv), at<float>(ws, w.w), T, H,
                              k, y, xdt, smode ? at<void>(ws, w.s_out) : nullptr,

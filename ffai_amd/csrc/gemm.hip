@@ -125,14 +125,6 @@ __device__ __forceinline__ uint32_t tile_off(int r, int c) {
   return (uint32_t)(r * 128 + ((c ^ tile_swz(r)) << 4));
 }
 
-// Block barrier ordering LDS only: loads from global memory stay in flight
-// across it (a full __syncthreads would wait for them).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Block tile: 256 rows x 256 weight rows (gate/up: 128 output columns of
 // gate and of up; otherwise 256 output columns), 8 waves in a 4 x 2 grid:
 // wave (wm, wn) owns rows [64 wm, +64) as 2 MFMA row tiles and 4 MFMA column

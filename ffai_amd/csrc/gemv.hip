@@ -151,6 +151,211 @@ __global__ __launch_bounds__(256) void gemv_grouped_kernel(const GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// grouped GEMV for a few rows per expert (batched decode), 16-bit activations
+//
+// Block (slot, rb): expert used[1 + slot] and rows_per_block weight rows,
+// taken in iterations of R1 = 4 SG RM rows (lane rows as in gateup1_kernel:
+// wave w, sub-group sg, it < RM). The expert's sorted positions go through
+// in passes of up to TM rows; per pass the block stages the activation rows
+// into LDS once, in pair order with the per-unit sums (one thread per
+// 64-byte unit, 16-byte loads), and every iteration multiplies against them,
+// so the staging is shared by all the block's rows. Two register sets of
+// weights alternate: iteration i + 1's loads (output biases first) are in
+// flight while iteration i multiplies. The dot products run unit by unit,
+// token by token, so one LDS read of an activation unit serves every row and
+// both projections of the lane. A pass's activation loads are issued before
+// its first weight loads: loads retire in order, so staging waits for them
+// alone, and the block barriers order LDS only.
+// ---------------------------------------------------------------------------
+
+// Items q0 and q0 + 256 of a pass, (token q / CU, unit q % CU): the loads
+// (stage_load; past the pass they repeat its last item) and the pair-order
+// LDS rows with their sums (stage_store).
+template <typename XT>
+__device__ __forceinline__ void stage_load(const XT* __restrict__ x, const uint32_t* __restrict__ perm,
+                                           int topk, uint32_t pc, int nt, int K, int CU, int q0,
+                                           uint32_t (&n)[2][16]) {
+  const int total = nt * CU;
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const int q = min(q0 + 256 * r, total - 1);
+    const int t = q / CU, u = q - t * CU;
+    const uint32_t p = pc + (uint32_t)t;
+    const uint32_t row = perm ? perm[p] / (uint32_t)topk : p;
+    const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)row * K + (size_t)u * 32);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint4 v = src[j];
+      n[r][4 * j] = v.x; n[r][4 * j + 1] = v.y; n[r][4 * j + 2] = v.z; n[r][4 * j + 3] = v.w;
+    }
+  }
+}
+
+template <int BITS, typename XT>
+__device__ __forceinline__ void stage_store(const uint32_t (&n)[2][16], int nt, int CU, int q0,
+                                            uint32_t* xl, float* xsl) {
+  const int total = nt * CU;
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const int q = q0 + 256 * r;
+    if (q < total) {
+      uint32_t pw[16];
+      natural_to_pairs<BITS>(n[r], pw);
+      uint4* dst = reinterpret_cast<uint4*>(xl + (size_t)q * 16);
+#pragma unroll
+      for (int j = 0; j < 4; j++) dst[j] = make_uint4(pw[4 * j], pw[4 * j + 1], pw[4 * j + 2], pw[4 * j + 3]);
+      xsl[q] = sum16(n[r], __is_same(XT, bf16_t));
+    }
+  }
+}
+
+template <int BITS, typename XT, typename ST, bool GATEUP, int UR, int RM, int TM>
+__global__ __launch_bounds__(256, 2) void gemv_multi_kernel(const GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int slot = blockIdx.x / a.row_blocks, rb = blockIdx.x - slot * a.row_blocks;
+  if ((uint32_t)slot >= a.used[0]) return;  // block-uniform, before any barrier
+  const uint32_t e = __builtin_amdgcn_readfirstlane(a.used[1 + slot]);
+  const uint32_t pbeg = __builtin_amdgcn_readfirstlane(a.offsets[e]);
+  const uint32_t pend = __builtin_amdgcn_readfirstlane(a.offsets[e + 1]);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
+  const int L = 1 << a.lg, SG = 64 >> a.lg;
+  const int sg = lane >> a.lg, li = lane & (L - 1);
+  // the block's rows go through in iterations of R1 = 4 SG RM rows: row
+  // rbase + i R1 + it 4 SG of iteration i
+  const int R1 = 4 * SG * RM, nit = a.rows_per_block / R1;
+  const int r_end = min(N, (rb + 1) * a.rows_per_block);
+  const int rbase = rb * a.rows_per_block + wave * SG + sg, stride = 4 * SG;
+  uint32_t* xl = reinterpret_cast<uint32_t*>(smem);                         // [TM][CU][16]
+  float* xsl = reinterpret_cast<float*>(smem + (size_t)TM * CU * 64);      // [TM][CU]
+  const XT* x = reinterpret_cast<const XT*>(a.x);
+  XT* out = reinterpret_cast<XT*>(a.out);
+  constexpr float MAGIC = Magic<BITS, XT>::value;
+  const ProjView P0 = proj_view<BITS, ST>(a.p0, e, N, row_words, groups);
+  const ProjView P1 = GATEUP ? proj_view<BITS, ST>(a.p1, e, N, row_words, groups) : P0;
+  const uint32_t wstep = (uint32_t)(L * BITS * 4), sstep = (uint32_t)((L >> a.gsh) * sizeof(ST));
+  const size_t ebase = (size_t)e * N;
+  constexpr int RM1 = GATEUP ? RM : 1;
+
+  // weights (and output biases) of one iteration's rows
+  struct WSet {
+    WUnit<BITS, ST> w0[RM][UR], w1[RM1][UR];
+    float ob0[RM], ob1[RM];
+  };
+  auto load_w = [&](int i, WSet& ws) __attribute__((always_inline)) {
+#pragma unroll
+    for (int it = 0; it < RM; it++) {
+      const int row = min(rbase + i * R1 + it * stride, N - 1);
+      ws.ob0[it] = a.p0.ob ? to_f<XT>(reinterpret_cast<const XT*>(a.p0.ob)[ebase + row]) : 0.f;
+      ws.ob1[it] = (GATEUP && a.p1.ob) ? to_f<XT>(reinterpret_cast<const XT*>(a.p1.ob)[ebase + row]) : 0.f;
+      const UnitAddr ad = unit_addr<BITS, ST>((uint32_t)row, row_words, groups, li, a.gsh);
+      bload_units<BITS, ST, UR>(P0, ad, wstep, sstep, ws.w0[it]);
+      if constexpr (GATEUP) bload_units<BITS, ST, UR>(P1, ad, wstep, sstep, ws.w1[it]);
+    }
+  };
+  // iteration i's rows against the nt staged activation rows of pass pc
+  auto compute = [&](int i, const WSet& ws, uint32_t pc, int nt) __attribute__((always_inline)) {
+    float acc0[RM][TM], acc1[RM1][TM];
+#pragma unroll
+    for (int it = 0; it < RM; it++)
+#pragma unroll
+      for (int t = 0; t < TM; t++) {
+        acc0[it][t] = 0.f;
+        if constexpr (GATEUP) acc1[it][t] = 0.f;
+      }
+#pragma unroll
+    for (int j = 0; j < UR; j++) {
+      const int u = li + j * L;
+      const bool valid = u < CU;
+      const int uc = min(u, CU - 1);
+      uint32_t cp0[RM][16], cp1[RM1][16];
+      float s0[RM], b0[RM], s1[RM1], b1[RM1];
+#pragma unroll
+      for (int it = 0; it < RM; it++) {
+        unpack_pairs<BITS, Magic<BITS, XT>::bits>(ws.w0[it][j].w, cp0[it]);
+        s0[it] = ws.w0[it][j].s();
+        b0[it] = ws.w0[it][j].b() - MAGIC * s0[it];
+        if constexpr (GATEUP) {
+          unpack_pairs<BITS, Magic<BITS, XT>::bits>(ws.w1[it][j].w, cp1[it]);
+          s1[it] = ws.w1[it][j].s();
+          b1[it] = ws.w1[it][j].b() - MAGIC * s1[it];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < TM; t++) {
+        if (t < nt) {  // block-uniform
+          XUnit<XT> xu;
+          lds_x_unit<XT>(reinterpret_cast<const XT*>(xl + (size_t)(t * CU) * 16), uc, xu);
+          const float xs = xsl[t * CU + uc];
+#pragma unroll
+          for (int it = 0; it < RM; it++) {
+            const float v0 = s0[it] * dot_unit<BITS, XT>(cp0[it], xu) + b0[it] * xs;
+            acc0[it][t] += valid ? v0 : 0.f;
+            if constexpr (GATEUP) {
+              const float v1 = s1[it] * dot_unit<BITS, XT>(cp1[it], xu) + b1[it] * xs;
+              acc1[it][t] += valid ? v1 : 0.f;
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < RM; it++) {
+      const int row = rbase + i * R1 + it * stride;
+#pragma unroll
+      for (int t = 0; t < TM; t++) {
+        if (t < nt) {
+          float g = group_sum(acc0[it][t], a.lg);
+          float v;
+          if constexpr (GATEUP) {
+            float uu = group_sum(acc1[it][t], a.lg);
+            g = round_to<XT>(g);
+            uu = round_to<XT>(uu);
+            if (a.p0.ob) g = round_to<XT>(g + ws.ob0[it]);
+            if (a.p1.ob) uu = round_to<XT>(uu + ws.ob1[it]);
+            v = apply_act<XT>(g, uu, a.act, a.alpha, a.limit);
+          } else {
+            g = round_to<XT>(g);
+            if (a.p0.ob) g = round_to<XT>(g + ws.ob0[it]);
+            // single projection: only ReLU^2 acts on it (no gate)
+            v = a.act == ACT_RELU2 ? apply_act<XT>(0.f, g, ACT_RELU2, 0.f, 0.f) : g;
+          }
+          if (li == L - 1 && row < r_end) out[(size_t)(pc + t) * N + row] = from_f<XT>(v);
+        }
+      }
+    }
+  };
+
+  WSet wa, wb;
+  for (uint32_t pc = pbeg; pc < pend;) {
+    const int nt = min((int)(pend - pc), TM);
+    // this pass's first activation loads, then iteration 0's weights, then
+    // the activations into LDS once every wave is done with the last pass
+    uint32_t xn[2][16];
+    stage_load<XT>(x, a.perm, a.topk, pc, nt, K, CU, (int)threadIdx.x, xn);
+    load_w(0, wa);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();  // LDS only: the weight loads stay in flight
+    stage_store<BITS, XT>(xn, nt, CU, (int)threadIdx.x, xl, xsl);
+    for (int q0 = threadIdx.x + 512; q0 < nt * CU; q0 += 512) {
+      stage_load<XT>(x, a.perm, a.topk, pc, nt, K, CU, q0, xn);
+      stage_store<BITS, XT>(xn, nt, CU, q0, xl, xsl);
+    }
+    lds_barrier();
+    // iteration i + 1's weights load while iteration i multiplies
+    for (int i = 0; i < nit; i += 2) {
+      if (i + 1 < nit) load_w(i + 1, wb);
+      compute(i, wa, pc, nt);
+      if (i + 1 >= nit) break;
+      if (i + 2 < nit) load_w(i + 2, wa);
+      compute(i + 1, wb, pc, nt);
+    }
+    pc += (uint32_t)nt;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // one activation row per expert (decode T = 1): activations live in registers
 // for the lifetime of the wave, no LDS, no barrier.
 // ---------------------------------------------------------------------------
@@ -482,6 +687,44 @@ static hipError_t launch_gemv_t(bool gateup, int tokmax, const GemvArgs& a, int 
   return hipGetLastError();
 }
 
+// gemv_multi_kernel: ur = units per lane (1..4), tm = rows per pass (4 or 8),
+// kMultiRows(gate/up) weight rows per lane, smem = tm * (K / 32) * 68 bytes.
+template <int BITS, typename XT, typename ST, bool GU, int UR>
+static hipError_t launch_multi_u(int tm, const GemvArgs& a, int grid, size_t smem, hipStream_t st,
+                                 KEvents ev) {
+  constexpr int RM = kMultiRows(GU);
+  if (tm <= 4)
+    hipExtLaunchKernelGGL((gemv_multi_kernel<BITS, XT, ST, GU, UR, RM, 4>), dim3(grid), dim3(256),
+                          (uint32_t)smem, st, ev.start, ev.stop, 0, a);
+  else
+    hipExtLaunchKernelGGL((gemv_multi_kernel<BITS, XT, ST, GU, UR, RM, 8>), dim3(grid), dim3(256),
+                          (uint32_t)smem, st, ev.start, ev.stop, 0, a);
+  return hipGetLastError();
+}
+
+template <int BITS, typename XT, typename ST>
+static hipError_t launch_multi_t(bool gateup, int ur, int tm, const GemvArgs& a, int grid,
+                                 size_t smem, hipStream_t st, KEvents ev) {
+#define MOE_MU(UR)                                                                     \
+  case UR:                                                                             \
+    return gateup ? launch_multi_u<BITS, XT, ST, true, UR>(tm, a, grid, smem, st, ev)  \
+                  : launch_multi_u<BITS, XT, ST, false, UR>(tm, a, grid, smem, st, ev);
+  switch (ur) { MOE_MU(1) MOE_MU(2) MOE_MU(3) MOE_MU(4) }
+#undef MOE_MU
+  return hipErrorInvalidValue;
+}
+
+template <int BITS>
+static hipError_t launch_multi_bits(int xdt, int sbdt, bool gateup, int ur, int tm,
+                                    const GemvArgs& a, int grid, size_t smem, hipStream_t st,
+                                    KEvents ev) {
+  if (xdt == DT_BF16 && sbdt == DT_BF16) return launch_multi_t<BITS, bf16_t, bf16_t>(gateup, ur, tm, a, grid, smem, st, ev);
+  if (xdt == DT_BF16 && sbdt == DT_F16) return launch_multi_t<BITS, bf16_t, f16_t>(gateup, ur, tm, a, grid, smem, st, ev);
+  if (xdt == DT_F16 && sbdt == DT_F16) return launch_multi_t<BITS, f16_t, f16_t>(gateup, ur, tm, a, grid, smem, st, ev);
+  if (xdt == DT_F16 && sbdt == DT_BF16) return launch_multi_t<BITS, f16_t, bf16_t>(gateup, ur, tm, a, grid, smem, st, ev);
+  return hipErrorInvalidValue;
+}
+
 template <int BITS>
 static hipError_t launch_gemv_bits(int xdt, int sbdt, bool gateup, int tokmax, const GemvArgs& a,
                                    int grid, hipStream_t st, KEvents ev) {
@@ -502,6 +745,12 @@ hipError_t MOE_CAT(launch_gemv_b, MOE_BITS)(int xdt, int sbdt, bool gateup, int 
                                              const GemvArgs& a, int grid, hipStream_t st,
                                              KEvents ev) {
   return launch_gemv_bits<MOE_BITS>(xdt, sbdt, gateup, tokmax, a, grid, st, ev);
+}
+
+hipError_t MOE_CAT(launch_multi_b, MOE_BITS)(int xdt, int sbdt, bool gateup, int ur, int tm,
+                                              const GemvArgs& a, int grid, size_t smem,
+                                              hipStream_t st, KEvents ev) {
+  return launch_multi_bits<MOE_BITS>(xdt, sbdt, gateup, ur, tm, a, grid, smem, st, ev);
 }
 
 hipError_t MOE_CAT(launch_dec1_b, MOE_BITS)(int xdt, int sbdt, bool down, int rm, int ur,

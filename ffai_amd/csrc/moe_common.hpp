@@ -94,6 +94,14 @@ __device__ __forceinline__ float group_sum(float v, int lg) {
   return v;
 }
 
+// Block barrier ordering LDS only: loads from global memory stay in flight
+// across it (a full __syncthreads would wait for them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ------------------------------------------------------- buffer resources --
 // Raw buffer view of [base, base + bytes): loads take a 32-bit lane offset
 // against a wave-uniform base held in SGPRs, and a load whose lane offset is

@@ -103,6 +103,10 @@ struct Down1Args {
 constexpr int kDec1MaxK = 8;
 constexpr int kDec1MaxRows = 2;
 constexpr int kDec1MaxHidden = 8192;  // activation row staged in LDS
+// Weight rows per lane of gemv_multi_kernel: one for a gate/up pair (two
+// projections' units and code pairs stay in registers), two for a single
+// projection; both keep the kernel at two waves per SIMD without spills.
+constexpr int kMultiRows(bool gateup) { return gateup ? 1 : 2; }
 
 // rm: rows per lane (rows_per_block = rm * 4 * SG for gate/up, rm * SG for
 // down).
