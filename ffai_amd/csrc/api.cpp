@@ -1089,15 +1089,23 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
                                 st, res),
               "shared add launch");
   } else {
-    // 2. selection + dispatch plan (MoELayer.swift:706-792)
-    MOE_HIP(launch_router_topk(at<void>(ws, w.logits), xdt, T, E, k, route_opts(d),
-                               at<uint32_t>(ws, w.idx), at<float>(ws, w.w), st),
-            "router top-k launch");
-    MOE_HIP(launch_dispatch_plan(at<uint32_t>(ws, w.idx), T, k, E, at<uint32_t>(ws, w.counts),
-                                 at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.perm),
-                                 at<uint32_t>(ws, w.inv), at<uint32_t>(ws, w.used),
-                                 at<void>(ws, w.plan_scratch), dispatch_scratch_bytes(T, k, E), st),
-            "dispatch plan launch");
+    // 2. selection + dispatch plan (MoELayer.swift:706-792): one launch for a
+    //    small batch, else the top-k and plan kernels
+    if (launch_route_plan(at<void>(ws, w.logits), xdt, T, E, k, route_opts(d),
+                          at<uint32_t>(ws, w.idx), at<float>(ws, w.w), at<uint32_t>(ws, w.counts),
+                          at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.perm),
+                          at<uint32_t>(ws, w.inv), at<uint32_t>(ws, w.used), st) != hipSuccess) {
+      (void)hipGetLastError();  // a refused fused launch leaves no error behind
+      MOE_HIP(launch_router_topk(at<void>(ws, w.logits), xdt, T, E, k, route_opts(d),
+                                 at<uint32_t>(ws, w.idx), at<float>(ws, w.w), st),
+              "router top-k launch");
+      MOE_HIP(launch_dispatch_plan(at<uint32_t>(ws, w.idx), T, k, E, at<uint32_t>(ws, w.counts),
+                                   at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.perm),
+                                   at<uint32_t>(ws, w.inv), at<uint32_t>(ws, w.used),
+                                   at<void>(ws, w.plan_scratch), dispatch_scratch_bytes(T, k, E),
+                                   st),
+              "dispatch plan launch");
+    }
     const int slots = std::min(E, M);
     // squared-ReLU experts: the single up projection (NemotronHText.swift:756-761)
     const bool gated = d->activation != MOE_ACT_RELU2;

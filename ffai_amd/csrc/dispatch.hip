@@ -142,6 +142,67 @@ __global__ __launch_bounds__(kPlanThreads) void plan_single_kernel(
   stable_scatter(idx, 0, M, E, id_bits(E), cursor, perm, inv);
 }
 
+// Routing and dispatch plan of a small batch in one launch: the four waves
+// route tokens t = wave, wave + 4, ... exactly as router_topk_kernel does
+// (wave_topk, same results bit for bit), then the block plans the T * k
+// entries as plan_single_kernel does, reading the ids from LDS. At most two
+// tokens per wave: at 16 tokens (four per wave) the routing chain outlasts
+// the launch it saves (Qwen3 shape: 90.7 -> 96.5 us per layer step).
+constexpr int kRoutePlanMaxT = 8;
+constexpr int kRoutePlanMaxM = 1024;
+
+template <typename XT, int EPL>
+__global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(
+    const XT* __restrict__ logits, int T, int E, int k, const RouteOpts ro, uint32_t* idx, float* w,
+    uint32_t* counts, uint32_t* offsets, uint32_t* perm, uint32_t* inv, uint32_t* used) {
+  __shared__ float sc[kPlanThreads / 64][kTopkMaxE];
+  __shared__ uint32_t sidx[kRoutePlanMaxM];
+  __shared__ uint32_t cnt[kPlanMaxE], cursor[kPlanMaxE];
+  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+  const int M = T * k;
+  for (int e = tid; e < E; e += kPlanThreads) cnt[e] = 0;
+  for (int t = wv; t < T; t += kPlanThreads / 64) {  // wave-uniform
+    int sel;
+    float wt;
+    wave_topk<XT, EPL>(logits + (size_t)t * E, E, k, ro, sc[wv], true, &sel, &wt);
+    if (lane < k) {
+      idx[t * k + lane] = (uint32_t)sel;
+      w[t * k + lane] = wt;
+      sidx[t * k + lane] = (uint32_t)sel;
+    }
+  }
+  __syncthreads();
+  for (int m = tid; m < M; m += kPlanThreads) {
+    const uint32_t e = sidx[m];
+    if (e < (uint32_t)E) atomicAdd(&cnt[e], 1u);
+  }
+  __syncthreads();
+  scan_experts(cnt, E, counts, offsets, used, cursor);
+  stable_scatter(sidx, 0, M, E, id_bits(E), cursor, perm, inv);
+}
+
+hipError_t launch_route_plan(const void* logits, int dt, int T, int E, int k, const RouteOpts& ro,
+                             uint32_t* idx, float* w, uint32_t* counts, uint32_t* offsets,
+                             uint32_t* perm, uint32_t* inv, uint32_t* used, hipStream_t st) {
+  if (T > kRoutePlanMaxT || T * k > kRoutePlanMaxM || E > kTopkMaxE || k > 64)
+    return hipErrorInvalidValue;
+#define MOE_RP(XT, EPL)                                                                         \
+  hipLaunchKernelGGL((route_plan_kernel<XT, EPL>), dim3(1), dim3(kPlanThreads), 0, st,          \
+                     (const XT*)logits, T, E, k, ro, idx, w, counts, offsets, perm, inv, used); \
+  return hipGetLastError();
+#define MOE_RP_E(XT)                  \
+  if (E <= 64) { MOE_RP(XT, 1) }      \
+  if (E <= 128) { MOE_RP(XT, 2) }     \
+  if (E <= 256) { MOE_RP(XT, 4) }     \
+  MOE_RP(XT, kTopkEPL)
+  if (dt == DT_BF16) { MOE_RP_E(bf16_t) }
+  if (dt == DT_F16) { MOE_RP_E(f16_t) }
+  if (dt == DT_F32) { MOE_RP_E(float) }
+#undef MOE_RP_E
+#undef MOE_RP
+  return hipErrorInvalidValue;
+}
+
 // Multi-block pass 1: per-chunk histograms, hist[c * E + e].
 __global__ __launch_bounds__(kPlanThreads) void plan_hist_kernel(const uint32_t* __restrict__ idx,
                                                                  int M, int E,

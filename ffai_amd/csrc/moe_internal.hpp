@@ -134,6 +134,11 @@ hipError_t launch_router_logits_norm(const void* h, const void* m, const void* n
 
 // ------------------------------------------------------------- dispatch --
 // Writes counts, offsets, perm, inv_perm and the used-expert list.
+// launch_router_topk + launch_dispatch_plan in one workgroup for T <= 8
+// and T * k <= 1024 (hipErrorInvalidValue otherwise, nothing launched).
+hipError_t launch_route_plan(const void* logits, int dt, int T, int E, int k, const RouteOpts& ro,
+                             uint32_t* idx, float* w, uint32_t* counts, uint32_t* offsets,
+                             uint32_t* perm, uint32_t* inv, uint32_t* used, hipStream_t st);
 hipError_t launch_dispatch_plan(const uint32_t* idx, int T, int k, int E, uint32_t* counts,
                                 uint32_t* offsets, uint32_t* perm, uint32_t* inv_perm,
                                 uint32_t* used, void* scratch, size_t scratch_bytes,
