@@ -153,6 +153,10 @@ __global__ __launch_bounds__(256) void gemv_grouped_kernel(const GemvArgs a) {
 // ---------------------------------------------------------------------------
 // grouped GEMV for a few rows per expert (batched decode), 16-bit activations
 //
+// LDS holds a pass's activation units quad-major ([token][quad][unit], 16
+// bytes each), so the lanes of a row group, which take consecutive units,
+// read consecutive 16 bytes (a unit-major layout put them 64 bytes apart, on
+// the same banks).
 // Block (slot, rb): expert used[1 + slot] and rows_per_block weight rows,
 // taken in iterations of R1 = 4 SG RM rows (lane rows as in gateup1_kernel:
 // wave w, sub-group sg, it < RM). The expert's sorted positions go through
@@ -201,9 +205,13 @@ __device__ __forceinline__ void stage_store(const uint32_t (&n)[2][16], int nt, 
     if (q < total) {
       uint32_t pw[16];
       natural_to_pairs<BITS>(n[r], pw);
-      uint4* dst = reinterpret_cast<uint4*>(xl + (size_t)q * 16);
+      // quad j of (token t, unit u) at uint4 (4 t + j) CU + u: lanes that
+      // read consecutive units of one quad hit consecutive 16 bytes
+      const int t = q / CU, u = q - t * CU;
+      uint4* dst = reinterpret_cast<uint4*>(xl);
 #pragma unroll
-      for (int j = 0; j < 4; j++) dst[j] = make_uint4(pw[4 * j], pw[4 * j + 1], pw[4 * j + 2], pw[4 * j + 3]);
+      for (int j = 0; j < 4; j++)
+        dst[(size_t)(4 * t + j) * CU + u] = make_uint4(pw[4 * j], pw[4 * j + 1], pw[4 * j + 2], pw[4 * j + 3]);
       xsl[q] = sum16(n[r], __is_same(XT, bf16_t));
     }
   }
@@ -227,7 +235,7 @@ __global__ __launch_bounds__(256, 2) void gemv_multi_kernel(const GemvArgs a) {
   const int R1 = 4 * SG * RM, nit = a.rows_per_block / R1;
   const int r_end = min(N, (rb + 1) * a.rows_per_block);
   const int rbase = rb * a.rows_per_block + wave * SG + sg, stride = 4 * SG;
-  uint32_t* xl = reinterpret_cast<uint32_t*>(smem);                         // [TM][CU][16]
+  uint32_t* xl = reinterpret_cast<uint32_t*>(smem);                         // [TM][4][CU][4]
   float* xsl = reinterpret_cast<float*>(smem + (size_t)TM * CU * 64);      // [TM][CU]
   const XT* x = reinterpret_cast<const XT*>(a.x);
   XT* out = reinterpret_cast<XT*>(a.out);
@@ -286,7 +294,12 @@ __global__ __launch_bounds__(256, 2) void gemv_multi_kernel(const GemvArgs a) {
       for (int t = 0; t < TM; t++) {
         if (t < nt) {  // block-uniform
           XUnit<XT> xu;
-          lds_x_unit<XT>(reinterpret_cast<const XT*>(xl + (size_t)(t * CU) * 16), uc, xu);
+          const uint4* xq = reinterpret_cast<const uint4*>(xl) + (size_t)(4 * t) * CU + uc;
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const uint4 v = xq[(size_t)q * CU];
+            xu.v[4 * q] = v.x; xu.v[4 * q + 1] = v.y; xu.v[4 * q + 2] = v.z; xu.v[4 * q + 3] = v.w;
+          }
           const float xs = xsl[t * CU + uc];
 #pragma unroll
           for (int it = 0; it < RM; it++) {
