@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -854,6 +855,82 @@ moe_status copy_trace(const moe_layer_desc* d, int T, void* ws, const Workspace&
 // single up projection with squared ReLU), down, and the optional sigmoid
 // gate logit, into the workspace. Returns the combine mode: 0 none, 1
 // unconditional add, 2 sigmoid-gated.
+// Work that may overlap the routed experts (the shared expert: it reads the
+// layer input only and writes its own workspace regions) runs on a side
+// stream: forked from the caller's stream, joined back before the combine
+// that reads its output. One non-blocking, default-priority stream and two
+// events per device, created on first use and kept for the process
+// lifetime; each call's fork-to-join enqueue holds a lock, so calls from
+// several host threads never interleave the shared events. Under stream
+// capture the fork and join become graph edges. Without a side stream (its
+// creation failed) the work stays on the caller's stream, in order.
+class SideFork {
+ public:
+  SideFork(bool want, hipStream_t st) : st_(st), side_(st) {
+    if (!want) return;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+      (void)hipGetLastError();
+      return;
+    }
+    lock_ = std::unique_lock<std::mutex>(mu());
+    Slot& t = table()[dev];
+    if (!t.s) {
+      hipStream_t s = nullptr;
+      hipEvent_t f = nullptr, j = nullptr;
+      if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess ||
+          hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+          hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        if (j) (void)hipEventDestroy(j);
+        if (f) (void)hipEventDestroy(f);
+        if (s) (void)hipStreamDestroy(s);
+        lock_.unlock();
+        return;
+      }
+      t = Slot{s, f, j};
+    }
+    slot_ = &t;
+    status_ = hip_check(hipEventRecord(t.fork, st), "side stream fork");
+    if (status_ == MOE_OK) status_ = hip_check(hipStreamWaitEvent(t.s, t.fork, 0), "side stream fork");
+    if (status_ == MOE_OK) side_ = t.s;
+  }
+  moe_status status() const { return status_; }
+  hipStream_t stream() const { return side_; }
+  // after the side work: the point the caller's stream waits for
+  moe_status mark() {
+    return slot_ && side_ != st_ ? hip_check(hipEventRecord(slot_->join, side_), "side stream join")
+                                 : MOE_OK;
+  }
+  // the caller's stream waits for the side work from here on
+  moe_status join() {
+    if (!slot_ || side_ == st_) return MOE_OK;
+    const moe_status r = hip_check(hipStreamWaitEvent(st_, slot_->join, 0), "side stream join");
+    slot_ = nullptr;
+    if (lock_.owns_lock()) lock_.unlock();
+    return r;
+  }
+
+ private:
+  static constexpr int kMaxDev = 64;
+  struct Slot {
+    hipStream_t s;
+    hipEvent_t fork, join;
+  };
+  static std::mutex& mu() {
+    static std::mutex m;
+    return m;
+  }
+  static Slot* table() {
+    static Slot t[kMaxDev] = {};
+    return t;
+  }
+  hipStream_t st_, side_;
+  Slot* slot_ = nullptr;
+  std::unique_lock<std::mutex> lock_;
+  moe_status status_ = MOE_OK;
+};
+
 moe_status shared_expert(const moe_layer_desc* d, const void* x, int T, void* ws,
                          const Workspace& w, hipStream_t st, int* smode) {
   *smode = 0;
@@ -1050,6 +1127,12 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
 
   const bool dec1 = (T == 1 && dec1_supported(d));
   int smode = 0;
+  // the shared expert overlaps the routed experts (MoELayer.swift:620-624:
+  // it only joins at the combine)
+  SideFork side(d->has_shared, st);
+  MOE_TRY(side.status());
+  MOE_TRY(shared_expert(d, x, T, ws, w, side.stream(), &smode));
+  MOE_TRY(side.mark());
   if (dec1) {
     // 2. one token: routing inside the gate/up kernel (MoELayer.swift:1167-1282
     //    without a host round trip), then the fused down + combine
@@ -1081,9 +1164,9 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     g.limit = d->act_limit;
     MOE_HIP(launch_gateup1(gu.bits, xdt, gu.sb_dtype, g, gg.rm, gg.grid, st, kev(0)),
             "gate/up decode launch");
-    MOE_TRY(shared_expert(d, x, T, ws, w, st, &smode));
     // the residual goes into the last store: down1's without a shared expert
     MOE_TRY(run_down1(d, y, g.idx, g.w, g.act, st, kev(1), smode ? nullptr : res));
+    MOE_TRY(side.join());
     if (smode)
       MOE_HIP(launch_add_shared(y, at<void>(ws, w.s_out), at<void>(ws, w.s_logit), smode, T, H, xdt,
                                 st, res),
@@ -1126,7 +1209,6 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
                        at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st, kev(0),
                        T));
     }
-    MOE_TRY(shared_expert(d, x, T, ws, w, st, &smode));
     // 4. down projection, then the weighted combine (MoELayer.swift:899-939)
     if (gemm) {
       MOE_TRY(run_gemm(d->down, nullptr, at<void>(ws, w.act), xdt, nullptr, 1,
@@ -1137,6 +1219,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
                        at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, T == 1,
                        at<void>(ws, w.Y), 0, 0.f, 0.f, st, kev(1), T));
     }
+    MOE_TRY(side.join());
     MOE_HIP(launch_unpermute(at<void>(ws, w.Y), at<uint32_t>(ws, w.inv), at<float>(ws, w.w), T, H,
                              k, y, xdt, smode ? at<void>(ws, w.s_out) : nullptr,
                              smode ? at<void>(ws, w.s_logit) : nullptr, smode, st, res),

@@ -567,12 +567,16 @@ def test_decode_back_to_back(gptoss):
         assert torch.equal(y.view(torch.int16), ref[i % 4].view(torch.int16)), f"call {i}"
 
 
-@pytest.mark.parametrize("T", [1, 64])
-def test_layer_graph_replay(gptoss, T):
+@pytest.mark.parametrize("cfg,T", [("gptoss", 1), ("gptoss", 64), ("mixed", 1), ("mixed", 64),
+                                   ("nemotron", 5)])
+def test_layer_graph_replay(request, cfg, T):
     """A layer call captured in a HIP graph: every replay, with eager work
-    between replays, matches the eager result."""
-    dev = gptoss.device()
-    x = to_torch(gptoss.x(T, seed=2))
+    between replays, matches the eager result. The shared-expert layers
+    (mixed, nemotron) fork their shared expert onto a side stream and join
+    it back, which the capture records as graph edges."""
+    spec = request.getfixturevalue(cfg)
+    dev = spec.device()
+    x = to_torch(spec.x(T, seed=2))
     y_eager = dev.forward(x).clone()
     dev.workspace(T)
     out = torch.empty_like(x)
