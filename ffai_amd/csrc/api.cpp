@@ -863,7 +863,8 @@ moe_status copy_trace(const moe_layer_desc* d, int T, void* ws, const Workspace&
 // lifetime; each call's fork-to-join enqueue holds a lock, so calls from
 // several host threads never interleave the shared events. Under stream
 // capture the fork and join become graph edges. Without a side stream (its
-// creation failed) the work stays on the caller's stream, in order.
+// creation failed, or the first such call on the device is being captured)
+// the work stays on the caller's stream, in order.
 class SideFork {
  public:
   SideFork(bool want, hipStream_t st) : st_(st), side_(st) {
@@ -876,6 +877,14 @@ class SideFork {
     lock_ = std::unique_lock<std::mutex>(mu());
     Slot& t = table()[dev];
     if (!t.s) {
+      // never create the stream and events inside a stream capture: that
+      // call keeps its work in order on the caller's stream
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        lock_.unlock();
+        return;
+      }
       hipStream_t s = nullptr;
       hipEvent_t f = nullptr, j = nullptr;
       if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess ||

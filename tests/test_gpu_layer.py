@@ -596,3 +596,41 @@ def test_layer_graph_replay(request, cfg, T):
         assert torch.equal(out.view(torch.int16), y_eager.view(torch.int16)), f"replay {r}"
         dev.forward(x)  # eager work between replays
         torch.cuda.synchronize()
+
+
+_CAPTURE_FIRST = r"""
+import sys, torch
+sys.path.insert(0, "tests")
+from moe_spec import cfg_mixed, to_torch
+spec = cfg_mixed()
+dev = spec.device()
+x = to_torch(spec.x(64, seed=3))
+dev.workspace(64)
+out = torch.empty_like(x)
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):  # the process's first shared-expert call
+    dev.forward(x, out=out, stream=torch.cuda.current_stream())
+y_eager = dev.forward(x).clone()
+torch.cuda.synchronize()
+for r in range(3):
+    out.fill_(0)
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), y_eager.view(torch.int16)), r
+print("ok")
+"""
+
+
+def test_shared_expert_first_call_captured():
+    """The first call of a shared-expert layer in a process, made inside a
+    stream capture, creates no side stream there: the graph replays match
+    the eager result computed afterwards (which forks the side stream)."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_FIRST], cwd=root, capture_output=True,
+                       text=True, timeout=110)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout[-2000:] + r.stderr[-2000:]
+
