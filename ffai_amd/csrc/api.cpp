@@ -1136,9 +1136,11 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
 
   const bool dec1 = (T == 1 && dec1_supported(d));
   int smode = 0;
-  // the shared expert overlaps the routed experts (MoELayer.swift:620-624:
-  // it only joins at the combine)
-  SideFork side(d->has_shared, st);
+  // a shared expert large enough for the matrix cores overlaps the routed
+  // experts (MoELayer.swift:620-624: it only joins at the combine); a small
+  // one stays in order (the fork and join cost a one-token NemotronH-shaped
+  // layer 3.5 us more than they saved)
+  SideFork side(d->has_shared && T >= kGemmMinRows, st);
   MOE_TRY(side.status());
   MOE_TRY(shared_expert(d, x, T, ws, w, side.stream(), &smode));
   MOE_TRY(side.mark());

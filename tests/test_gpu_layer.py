@@ -568,7 +568,7 @@ def test_decode_back_to_back(gptoss):
 
 
 @pytest.mark.parametrize("cfg,T", [("gptoss", 1), ("gptoss", 64), ("mixed", 1), ("mixed", 64),
-                                   ("nemotron", 5)])
+                                   ("nemotron", 5), ("nemotron", 40)])
 def test_layer_graph_replay(request, cfg, T):
     """A layer call captured in a HIP graph: every replay, with eager work
     between replays, matches the eager result. The shared-expert layers
