@@ -610,8 +610,11 @@ def main():
     roof["traffic"] = measured_traffic(cfg["workload"], T)
     # the library's path choice: MFMA GEMM once used experts average >= 32 rows
     gemm_path = T > 1 and M >= 32 * min(cfg["E"], M) and cfg["H"] % 64 == 0 and cfg["I"] % 64 == 0
+    # and the matrix-core GEMV once the used experts average 4 rows (4-bit weights)
+    mma_path = T > 1 and not gemm_path and cfg["bits_gu"] == 4 and M >= 4 * min(cfg["E"], M)
     roof["kernel"] = ("gateup1_kernel (one-token gate/up with routing)" if T == 1 else
                       "gemm_grouped_kernel (MFMA gate/up over the expert row tiles)" if gemm_path else
+                      "gemv_mma_kernel (MFMA gate/up over the dispatch plan)" if mma_path else
                       "gemv_multi_kernel (routed gate/up over the dispatch plan)")
     roof["avg_us"] = round(gu_us, 3)
     roof["algorithmic_bytes"] = k_bytes

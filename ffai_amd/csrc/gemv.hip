@@ -368,6 +368,232 @@ __global__ __launch_bounds__(256, 2) void gemv_multi_kernel(const GemvArgs a) {
   }
 }
 
+#if MOE_BITS == 4
+// ---------------------------------------------------------------------------
+// grouped GEMV for a few rows per expert on the matrix cores (4-bit weights,
+// 16-bit activations)
+//
+// Block (slot, rb): expert used[1 + slot] and 64 LDS weight rows (a gate/up
+// pair: 32 rows of each; else 64 rows of one projection); the expert's
+// sorted positions go through in passes of up to 16 rows. Wave w owns 16
+// weight rows and computes C[t][r] = sum_k x[t][k] W[r][k] with
+// v_mfma_f32_16x16x32: A = 16 activation rows, B = the 16 weight rows' codes
+// with the magic offset (MAGIC + q exact in the 16-bit type), per 32-value
+// unit. A second MFMA against all-ones gives the unit's activation sums Q, so
+// the affine scale and bias apply per group in fp32 exactly as the one-token
+// kernels apply them: acc += s P + (b - MAGIC s) Q. Lane (r, kb) = (lane % 16,
+// lane / 16) supplies the codes of word kb of weight row r, whose pairs
+// (j, j + 4) of the 8-value block kb match the activations' pair order, and
+// quad kb of activation row r; it ends with rows 4 kb + i of output column r.
+// K runs in chunks of 8 units through double-buffered LDS: per chunk the
+// block copies 64 rows x 8 units of codes (16-byte loads), their 16-bit
+// scale/bias pairs and 16 rows x 8 units of activations (permuted to pair
+// order), with global loads two chunks ahead of the MFMAs.
+// ---------------------------------------------------------------------------
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename XT> struct Mma16;
+template <> struct Mma16<bf16_t> {
+  typedef __bf16 V __attribute__((ext_vector_type(8)));
+  static constexpr uint32_t ones = 0x3F803F80u;
+  static __device__ __forceinline__ f32x4_t mma(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(V, a), __builtin_bit_cast(V, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mma16<f16_t> {
+  typedef _Float16 V __attribute__((ext_vector_type(8)));
+  static constexpr uint32_t ones = 0x3C003C00u;
+  static __device__ __forceinline__ f32x4_t mma(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(V, a), __builtin_bit_cast(V, b), c, 0, 0, 0);
+  }
+};
+
+constexpr int kMmaU = 8;      // units per K chunk
+constexpr int kMmaRows = 64;  // LDS weight rows per block
+constexpr int kMmaTok = 16;   // activation rows per pass
+
+template <typename XT, typename ST, bool GATEUP>
+__global__ __launch_bounds__(256) void gemv_mma_kernel(const GemvArgs a) {
+  __shared__ __align__(16) uint32_t wl[2][kMmaRows * kMmaU * 4];  // [row][unit slot][4 words]
+  __shared__ __align__(16) uint32_t sl[2][kMmaRows * kMmaU];      // [row][unit]: s | b << 16
+  __shared__ __align__(16) uint32_t xl[2][kMmaU * kMmaTok * 16];  // [unit][row][quad slot][4 words]
+  __shared__ float gl[32 * kMmaTok];                              // gate outputs of a pass
+  const int slot = blockIdx.x / a.row_blocks, rb = blockIdx.x - slot * a.row_blocks;
+  if ((uint32_t)slot >= a.used[0]) return;  // block-uniform, before any barrier
+  const uint32_t e = __builtin_amdgcn_readfirstlane(a.used[1 + slot]);
+  const uint32_t pbeg = __builtin_amdgcn_readfirstlane(a.offsets[e]);
+  const uint32_t pend = __builtin_amdgcn_readfirstlane(a.offsets[e + 1]);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * 4;
+  const int upg = 1 << a.gsh;
+  const int nchunks = (CU + kMmaU - 1) / kMmaU;
+  constexpr int RPB = GATEUP ? 32 : 64;  // output rows per block
+  const int r_begin = rb * RPB;
+  const ProjView P0 = proj_view<4, ST>(a.p0, e, N, row_words, groups);
+  const ProjView P1 = GATEUP ? proj_view<4, ST>(a.p1, e, N, row_words, groups) : P0;
+  const XT* x = reinterpret_cast<const XT*>(a.x);
+  constexpr float MAGIC = Magic<4, XT>::value;
+  constexpr uint32_t MB = Magic<4, XT>::bits;
+  const int r = lane & 15, kb = lane >> 4;
+  // this lane's LDS weight row and output row
+  const int lr = GATEUP ? (wave >> 1) * 32 + (wave & 1) * 16 + r : wave * 16 + r;
+  const int orow = r_begin + (GATEUP ? (wave & 1) * 16 : wave * 16) + r;
+
+  // staging items of this thread, j < 2: codes and scales of LDS row
+  // (tid >> 3) + 32 j, unit slot tid & 7; activation quad q = tid + 256 j:
+  // unit q >> 6, row (q >> 2) & 15 (the same for both j), quad q & 3
+  const int s_lr0 = tid >> 3, s_us = tid & 7;
+  const int x_t = (tid >> 2) & 15, x_kb = tid & 3, x_us0 = tid >> 6;
+  struct Stage {
+    u32x4_t w[2], x[2];
+    uint32_t sb[2];
+  };
+  auto gw_row = [&](int slr) -> uint32_t {
+    const int g = GATEUP ? r_begin + (slr & 31) : r_begin + slr;
+    return (uint32_t)min(g, N - 1);
+  };
+  auto load_stage = [&](int c, uint32_t xrow, Stage& st) __attribute__((always_inline)) {
+    const int cc = min(c, nchunks - 1);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int slr = s_lr0 + 32 * j;
+      const ProjView& pv = (GATEUP && j == 1) ? P1 : P0;
+      const uint32_t grow = gw_row(slr);
+      const uint32_t u = (uint32_t)min(kMmaU * cc + s_us, CU - 1);
+      st.w[j] = bload128(pv.w, (grow * (uint32_t)row_words + u * 4u) * 4u);
+      const uint32_t gi = (grow * (uint32_t)groups + (u >> a.gsh)) * (uint32_t)sizeof(ST);
+      st.sb[j] = (uint32_t)bload16(pv.s, gi) | ((uint32_t)bload16(pv.b, gi) << 16);
+      const int ux = min(kMmaU * cc + x_us0 + 4 * j, CU - 1);
+      st.x[j] = *reinterpret_cast<const u32x4_t*>(x + (size_t)xrow * K + (size_t)ux * 32 + x_kb * 8);
+    }
+  };
+  auto store_stage = [&](const Stage& st, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int slr = s_lr0 + 32 * j;
+      *reinterpret_cast<u32x4_t*>(&wl[buf][(slr * kMmaU + ((s_us + slr) & 7)) * 4]) = st.w[j];
+      sl[buf][slr * kMmaU + s_us] = st.sb[j];
+      // natural values x0..x7 -> pairs (x0, x4), (x1, x5), (x2, x6), (x3, x7)
+      const u32x4_t n = st.x[j];
+      const u32x4_t pw = {(n[0] & 0xFFFFu) | (n[2] << 16), (n[0] >> 16) | (n[2] & 0xFFFF0000u),
+                          (n[1] & 0xFFFFu) | (n[3] << 16), (n[1] >> 16) | (n[3] & 0xFFFF0000u)};
+      const int us = x_us0 + 4 * j;
+      *reinterpret_cast<u32x4_t*>(&xl[buf][((us * kMmaTok + x_t) * 4 + (x_kb ^ ((x_t >> 2) & 3))) * 4]) = pw;
+    }
+  };
+  const u32x4_t ones = {Mma16<XT>::ones, Mma16<XT>::ones, Mma16<XT>::ones, Mma16<XT>::ones};
+  f32x4_t acc;
+  auto compute = [&](int c, int buf) __attribute__((always_inline)) {
+    const int nu = min(kMmaU, CU - kMmaU * c);  // block-uniform
+    f32x4_t P = {}, Q = {};
+#pragma unroll
+    for (int us = 0; us < kMmaU; us++) {
+      if (us < nu) {
+        const uint32_t w = wl[buf][(lr * kMmaU + ((us + lr) & 7)) * 4 + kb];
+        const u32x4_t bop = {(w & 0x000F000Fu) | MB, ((w >> 4) & 0x000F000Fu) | MB,
+                             ((w >> 8) & 0x000F000Fu) | MB, ((w >> 12) & 0x000F000Fu) | MB};
+        const u32x4_t aop =
+            *reinterpret_cast<const u32x4_t*>(&xl[buf][((us * kMmaTok + r) * 4 + (kb ^ ((r >> 2) & 3))) * 4]);
+        P = Mma16<XT>::mma(aop, bop, P);
+        Q = Mma16<XT>::mma(aop, ones, Q);
+        if (((kMmaU * c + us + 1) & (upg - 1)) == 0 || us == nu - 1) {
+          const uint32_t sb = sl[buf][lr * kMmaU + us];
+          const float sc = to_f<ST>(__builtin_bit_cast(ST, (uint16_t)(sb & 0xFFFFu)));
+          const float bi = to_f<ST>(__builtin_bit_cast(ST, (uint16_t)(sb >> 16))) - MAGIC * sc;
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[i] += sc * P[i] + bi * Q[i];
+          P = f32x4_t{};
+          Q = f32x4_t{};
+        }
+      }
+    }
+  };
+
+  XT* out = reinterpret_cast<XT*>(a.out);
+  for (uint32_t pc = pbeg; pc < pend; pc += kMmaTok) {
+    const int nt = min((int)(pend - pc), kMmaTok);
+    const uint32_t p = pc + (uint32_t)min(x_t, nt - 1);
+    const uint32_t xrow = a.perm ? a.perm[p] / (uint32_t)a.topk : p;
+    Stage s0, s1;
+    load_stage(0, xrow, s0);
+    load_stage(1, xrow, s1);
+    __syncthreads();  // the last pass's LDS reads (and gl) are done
+    store_stage(s0, 0);
+    load_stage(2, xrow, s0);
+    lds_barrier();
+    acc = f32x4_t{};
+    for (int c = 0; c < nchunks; c += 2) {
+      compute(c, 0);
+      store_stage(s1, 1);  // chunk c + 1
+      load_stage(c + 3, xrow, s1);
+      lds_barrier();
+      if (c + 1 >= nchunks) break;
+      compute(c + 1, 1);
+      store_stage(s0, 0);  // chunk c + 2
+      load_stage(c + 4, xrow, s0);
+      lds_barrier();
+    }
+    // lane (r, kb): output column orow, activation rows 4 kb + i of the pass
+    const size_t ob_i = (size_t)e * N + (size_t)min(orow, N - 1);
+    if constexpr (GATEUP) {
+      if (wave < 2) {
+        const float ob = a.p0.ob ? to_f<XT>(reinterpret_cast<const XT*>(a.p0.ob)[ob_i]) : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          float g = round_to<XT>(acc[i]);
+          if (a.p0.ob) g = round_to<XT>(g + ob);
+          gl[((wave & 1) * 16 + r) * kMmaTok + 4 * kb + i] = g;
+        }
+      }
+      __syncthreads();
+      if (wave >= 2) {
+        const float ob = a.p1.ob ? to_f<XT>(reinterpret_cast<const XT*>(a.p1.ob)[ob_i]) : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int t = 4 * kb + i;
+          float u = round_to<XT>(acc[i]);
+          if (a.p1.ob) u = round_to<XT>(u + ob);
+          const float g = gl[((wave & 1) * 16 + r) * kMmaTok + t];
+          if (t < nt && orow < N)
+            out[(size_t)(pc + t) * N + orow] = from_f<XT>(apply_act<XT>(g, u, a.act, a.alpha, a.limit));
+        }
+      }
+    } else {
+      const float ob = a.p0.ob ? to_f<XT>(reinterpret_cast<const XT*>(a.p0.ob)[ob_i]) : 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int t = 4 * kb + i;
+        float g = round_to<XT>(acc[i]);
+        if (a.p0.ob) g = round_to<XT>(g + ob);
+        // single projection: only ReLU^2 acts on it (no gate)
+        const float v = a.act == ACT_RELU2 ? apply_act<XT>(0.f, g, ACT_RELU2, 0.f, 0.f) : g;
+        if (t < nt && orow < N) out[(size_t)(pc + t) * N + orow] = from_f<XT>(v);
+      }
+    }
+  }
+}
+
+hipError_t launch_mma_b4(int xdt, int sbdt, bool gateup, const GemvArgs& a, int grid, hipStream_t st,
+                         KEvents ev) {
+#define MOE_MMA(XT, ST)                                                                          \
+  if (gateup)                                                                                    \
+    hipExtLaunchKernelGGL((gemv_mma_kernel<XT, ST, true>), dim3(grid), dim3(256), 0, st,         \
+                          ev.start, ev.stop, 0, a);                                              \
+  else                                                                                           \
+    hipExtLaunchKernelGGL((gemv_mma_kernel<XT, ST, false>), dim3(grid), dim3(256), 0, st,        \
+                          ev.start, ev.stop, 0, a);                                              \
+  return hipGetLastError();
+  if (xdt == DT_BF16 && sbdt == DT_BF16) { MOE_MMA(bf16_t, bf16_t) }
+  if (xdt == DT_BF16 && sbdt == DT_F16) { MOE_MMA(bf16_t, f16_t) }
+  if (xdt == DT_F16 && sbdt == DT_F16) { MOE_MMA(f16_t, f16_t) }
+  if (xdt == DT_F16 && sbdt == DT_BF16) { MOE_MMA(f16_t, bf16_t) }
+#undef MOE_MMA
+  return hipErrorInvalidValue;
+}
+#endif  // MOE_BITS == 4
+
 // ---------------------------------------------------------------------------
 // one activation row per expert (decode T = 1): activations live in registers
 // for the lifetime of the wave, no LDS, no barrier.

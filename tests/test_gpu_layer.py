@@ -352,7 +352,7 @@ def gptoss():
     return cfg_gptoss()
 
 
-@pytest.mark.parametrize("T", [1, 3])
+@pytest.mark.parametrize("T", [1, 3, 64])
 def test_layer_gptoss(gptoss, T):
     run_layer(gptoss, T, seed=T)
 
@@ -451,7 +451,7 @@ def nemotron():
     return cfg_nemotron()
 
 
-@pytest.mark.parametrize("T", [1, 5, 400])
+@pytest.mark.parametrize("T", [1, 5, 48, 400])
 def test_layer_nemotron(nemotron, T):
     """Sigmoid router + correction bias + routed scale, squared-ReLU experts
     without a gate projection, squared-ReLU shared expert; T=400 takes the
@@ -464,7 +464,7 @@ def gemma4():
     return cfg_gemma4()
 
 
-@pytest.mark.parametrize("T", [1, 5, 300])
+@pytest.mark.parametrize("T", [1, 5, 40, 300])
 def test_layer_gemma4(gemma4, T):
     """Scaled logits, per-expert scale, GELU-gated experts and a router
     input of its own; T=1 runs the one-token kernels, T=300 the matrix
