@@ -516,6 +516,17 @@ def test_layer_mfma_path(case):
     run_layer(cfg_bits(*case, n_experts=4, top_k=2), 160)
 
 
+@pytest.mark.parametrize("case", [(4, 4, 32, BF16, BF16), (4, 4, 32, F16, F16), (4, 4, 128, BF16, F16)])
+def test_layer_batched_mma_path(case):
+    """4 to 31 rows per expert with 4-bit weights: the batched GEMV on the
+    matrix cores, with a partial last block of down rows (hidden 544 is 8.5
+    blocks of 64) and passes of 16 activation rows (up to 30 rows for one
+    expert at T = 40, 8 experts, top-3)."""
+    gs = case[2]
+    hidden = 544 if gs == 32 else 640
+    run_layer(cfg_bits(*case, hidden=hidden, inter=384, n_experts=8, top_k=3), 40)
+
+
 def test_layer_qwen3_mfma_zipf():
     """Qwen3-MoE shape (16 experts) on the matrix-core path, Zipf routing."""
     spec = cfg_qwen3(seed=11, n_experts=16, router_bias=zipf_router_bias(16, 1.1, beta=1.0))
