@@ -228,19 +228,35 @@ __global__ __launch_bounds__(kPlanThreads) void plan_scan_kernel(int nchunks, in
                                                                  uint32_t* used) {
   __shared__ uint32_t cnt[kPlanMaxE], base[kPlanMaxE];
   const int tid = threadIdx.x;
+  // chunks in batches of kScanBatch: a batch's loads are all in flight
+  // before the first add (one round trip per batch, not per chunk)
+  constexpr int kScanBatch = 16;
   for (int e = tid; e < E; e += kPlanThreads) {
     uint32_t s = 0;
-    for (int c = 0; c < nchunks; c++) s += hist[(size_t)c * E + e];
+    for (int c0 = 0; c0 < nchunks; c0 += kScanBatch) {
+      uint32_t h[kScanBatch];
+#pragma unroll
+      for (int j = 0; j < kScanBatch; j++)
+        h[j] = (c0 + j < nchunks) ? hist[(size_t)(c0 + j) * E + e] : 0u;
+#pragma unroll
+      for (int j = 0; j < kScanBatch; j++) s += h[j];
+    }
     cnt[e] = s;
   }
   __syncthreads();
   scan_experts(cnt, E, counts, offsets, used, base);
   for (int e = tid; e < E; e += kPlanThreads) {
     uint32_t run = base[e];
-    for (int c = 0; c < nchunks; c++) {
-      const uint32_t h = hist[(size_t)c * E + e];
-      hist[(size_t)c * E + e] = run;
-      run += h;
+    for (int c0 = 0; c0 < nchunks; c0 += kScanBatch) {
+      uint32_t h[kScanBatch];
+#pragma unroll
+      for (int j = 0; j < kScanBatch; j++)
+        h[j] = (c0 + j < nchunks) ? hist[(size_t)(c0 + j) * E + e] : 0u;
+#pragma unroll
+      for (int j = 0; j < kScanBatch; j++) {
+        if (c0 + j < nchunks) hist[(size_t)(c0 + j) * E + e] = run;
+        run += h[j];
+      }
     }
   }
 }
