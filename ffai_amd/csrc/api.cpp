@@ -38,7 +38,23 @@ hipError_t launch_multi_b4(int, int, bool, int, int, const GemvArgs&, int, size_
 hipError_t launch_multi_b5(int, int, bool, int, int, const GemvArgs&, int, size_t, hipStream_t, KEvents);
 hipError_t launch_multi_b6(int, int, bool, int, int, const GemvArgs&, int, size_t, hipStream_t, KEvents);
 hipError_t launch_multi_b8(int, int, bool, int, int, const GemvArgs&, int, size_t, hipStream_t, KEvents);
+hipError_t launch_mma_b2(int, int, bool, const GemvArgs&, int, hipStream_t, KEvents);
+hipError_t launch_mma_b3(int, int, bool, const GemvArgs&, int, hipStream_t, KEvents);
 hipError_t launch_mma_b4(int, int, bool, const GemvArgs&, int, hipStream_t, KEvents);
+hipError_t launch_mma_b5(int, int, bool, const GemvArgs&, int, hipStream_t, KEvents);
+hipError_t launch_mma_b6(int, int, bool, const GemvArgs&, int, hipStream_t, KEvents);
+
+static hipError_t launch_mma(int bits, int xdt, int sbdt, bool gateup, const GemvArgs& a,
+                             int grid, hipStream_t st, KEvents ev) {
+  switch (bits) {
+    case 2: return launch_mma_b2(xdt, sbdt, gateup, a, grid, st, ev);
+    case 3: return launch_mma_b3(xdt, sbdt, gateup, a, grid, st, ev);
+    case 4: return launch_mma_b4(xdt, sbdt, gateup, a, grid, st, ev);
+    case 5: return launch_mma_b5(xdt, sbdt, gateup, a, grid, st, ev);
+    case 6: return launch_mma_b6(xdt, sbdt, gateup, a, grid, st, ev);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 static hipError_t launch_multi(int bits, int xdt, int sbdt, bool gateup, int ur, int tm,
                                const GemvArgs& a, int grid, size_t smem, hipStream_t st,
@@ -512,17 +528,18 @@ bool run_multi(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
 // expert: 409 -> 208 us; at 1-2 per expert gemv_multi_kernel is faster).
 constexpr int kMmaMinRows = 4;
 
-// gemv_mma_kernel (matrix cores) for 4-bit weights and 16-bit activations:
-// 32 rows of a gate/up pair or 64 rows of one projection per block, 16
-// activation rows per pass. Returns false where it does not apply.
+// gemv_mma_kernel (matrix cores) for 2- to 6-bit weights (codes exact with
+// the magic offset in either 16-bit type) and 16-bit activations: 32 rows of
+// a gate/up pair or 64 rows of one projection per block, 16 activation rows
+// per pass. Returns false where it does not apply.
 bool run_mma(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
              const uint32_t* perm, int topk, const uint32_t* offsets, const uint32_t* used, int slots,
              void* out, int act, float alpha, float limit, hipStream_t st, KEvents ev,
              moe_status* status) {
-  if (p0.bits != 4 || (p1 && p1->bits != 4)) return false;
+  if (p0.bits < 2 || p0.bits > 6 || (p1 && p1->bits != p0.bits)) return false;
   if (xdt == MOE_F32 || p0.sb_dtype == MOE_F32) return false;
   if ((reinterpret_cast<uintptr_t>(x) & 15) != 0) return false;  // 16-byte activation loads
-  if (((size_t)p0.n + 64) * ((size_t)p0.k / 2) >= (1ull << 31)) return false;
+  if (((size_t)p0.n + 64) * ((size_t)p0.k * p0.bits / 8) >= (1ull << 31)) return false;
   const int rows_per_block = p1 ? 32 : 64;
   const int row_blocks = (p0.n + rows_per_block - 1) / rows_per_block;
   GemvArgs a{};
@@ -542,7 +559,7 @@ bool run_mma(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
   a.act = act;
   a.alpha = alpha;
   a.limit = limit;
-  *status = hip_check(launch_mma_b4(xdt, p0.sb_dtype, p1 != nullptr, a, slots * row_blocks, st, ev),
+  *status = hip_check(launch_mma(p0.bits, xdt, p0.sb_dtype, p1 != nullptr, a, slots * row_blocks, st, ev),
                       "grouped GEMV launch");
   return true;
 }

@@ -368,7 +368,10 @@ __global__ __launch_bounds__(256, 2) void gemv_multi_kernel(const GemvArgs a) {
   }
 }
 
-#if MOE_BITS == 4
+#define MOE_CAT2(a, b) a##b
+#define MOE_CAT(a, b) MOE_CAT2(a, b)
+
+#if MOE_BITS <= 6
 // ---------------------------------------------------------------------------
 // grouped GEMV for a few rows per expert on the matrix cores (4-bit weights,
 // 16-bit activations)
@@ -382,11 +385,12 @@ __global__ __launch_bounds__(256, 2) void gemv_multi_kernel(const GemvArgs a) {
 // unit. A second MFMA against all-ones gives the unit's activation sums Q, so
 // the affine scale and bias apply per group in fp32 exactly as the one-token
 // kernels apply them: acc += s P + (b - MAGIC s) Q. Lane (r, kb) = (lane % 16,
-// lane / 16) supplies the codes of word kb of weight row r, whose pairs
-// (j, j + 4) of the 8-value block kb match the activations' pair order, and
+// lane / 16) supplies the codes of 8-value block kb of weight row r (bits
+// [8 kb BITS, +8 BITS) of the unit's BITS words; for 4 bits, word kb), whose
+// pairs (j, j + 4) match the activations' pair order, and
 // quad kb of activation row r; it ends with rows 4 kb + i of output column r.
 // K runs in chunks of 8 units through double-buffered LDS: per chunk the
-// block copies 64 rows x 8 units of codes (16-byte loads), their 16-bit
+// block copies 64 rows x 8 units of codes (BITS words each), their 16-bit
 // scale/bias pairs and 16 rows x 8 units of activations (permuted to pair
 // order), with global loads two chunks ahead of the MFMAs.
 // ---------------------------------------------------------------------------
@@ -413,9 +417,31 @@ constexpr int kMmaU = 8;      // units per K chunk
 constexpr int kMmaRows = 64;  // LDS weight rows per block
 constexpr int kMmaTok = 16;   // activation rows per pass
 
-template <typename XT, typename ST, bool GATEUP>
+// Codes of 8-value block kb of a unit as four magic-offset pairs (j, j + 4).
+template <int BITS>
+__device__ __forceinline__ u32x4_t mma_codes(const uint32_t* unit, int kb, uint32_t MB) {
+  if constexpr (BITS == 4) {
+    const uint32_t w = unit[kb];
+    return u32x4_t{(w & 0x000F000Fu) | MB, ((w >> 4) & 0x000F000Fu) | MB,
+                   ((w >> 8) & 0x000F000Fu) | MB, ((w >> 12) & 0x000F000Fu) | MB};
+  } else {
+    // 8 BITS <= 48 bits from bit 8 kb BITS: two consecutive words of the
+    // unit hold them after the in-word shift (at most 24)
+    const int bit = 8 * kb * BITS, i0 = bit >> 5;
+    const int i1 = i0 + 1 < BITS ? i0 + 1 : BITS - 1;
+    const uint64_t v = ((uint64_t)unit[i0] | ((uint64_t)unit[i1] << 32)) >> (bit & 31);
+    constexpr uint32_t m = (1u << BITS) - 1u;
+    u32x4_t r;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      r[j] = ((uint32_t)(v >> (BITS * j)) & m) | (((uint32_t)(v >> (BITS * (j + 4))) & m) << 16) | MB;
+    return r;
+  }
+}
+
+template <int BITS, typename XT, typename ST, bool GATEUP>
 __global__ __launch_bounds__(256) void gemv_mma_kernel(const GemvArgs a) {
-  __shared__ __align__(16) uint32_t wl[2][kMmaRows * kMmaU * 4];  // [row][unit slot][4 words]
+  __shared__ __align__(16) uint32_t wl[2][kMmaRows * kMmaU * BITS];  // [row][unit slot][BITS words]
   __shared__ __align__(16) uint32_t sl[2][kMmaRows * kMmaU];      // [row][unit]: s | b << 16
   __shared__ __align__(16) uint32_t xl[2][kMmaU * kMmaTok * 16];  // [unit][row][quad slot][4 words]
   __shared__ float gl[32 * kMmaTok];                              // gate outputs of a pass
@@ -426,16 +452,18 @@ __global__ __launch_bounds__(256) void gemv_mma_kernel(const GemvArgs a) {
   const uint32_t pend = __builtin_amdgcn_readfirstlane(a.offsets[e + 1]);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * 4;
+  const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
   const int upg = 1 << a.gsh;
   const int nchunks = (CU + kMmaU - 1) / kMmaU;
   constexpr int RPB = GATEUP ? 32 : 64;  // output rows per block
   const int r_begin = rb * RPB;
-  const ProjView P0 = proj_view<4, ST>(a.p0, e, N, row_words, groups);
-  const ProjView P1 = GATEUP ? proj_view<4, ST>(a.p1, e, N, row_words, groups) : P0;
+  const ProjView P0 = proj_view<BITS, ST>(a.p0, e, N, row_words, groups);
+  const ProjView P1 = GATEUP ? proj_view<BITS, ST>(a.p1, e, N, row_words, groups) : P0;
   const XT* x = reinterpret_cast<const XT*>(a.x);
-  constexpr float MAGIC = Magic<4, XT>::value;
-  constexpr uint32_t MB = Magic<4, XT>::bits;
+  // MAGIC + q is exact in the 16-bit type for q < 128 (bf16) / 1024 (f16)
+  constexpr float MAGIC = Magic<BITS, XT>::value;
+  constexpr uint32_t MB = Magic<BITS, XT>::bits;
+  static_assert(Magic<BITS, XT>::dot2, "magic-offset codes");
   const int r = lane & 15, kb = lane >> 4;
   // this lane's LDS weight row and output row
   const int lr = GATEUP ? (wave >> 1) * 32 + (wave & 1) * 16 + r : wave * 16 + r;
@@ -447,7 +475,8 @@ __global__ __launch_bounds__(256) void gemv_mma_kernel(const GemvArgs a) {
   const int s_lr0 = tid >> 3, s_us = tid & 7;
   const int x_t = (tid >> 2) & 15, x_kb = tid & 3, x_us0 = tid >> 6;
   struct Stage {
-    u32x4_t w[2], x[2];
+    uint32_t w[2][BITS];
+    u32x4_t x[2];
     uint32_t sb[2];
   };
   auto gw_row = [&](int slr) -> uint32_t {
@@ -462,7 +491,7 @@ __global__ __launch_bounds__(256) void gemv_mma_kernel(const GemvArgs a) {
       const ProjView& pv = (GATEUP && j == 1) ? P1 : P0;
       const uint32_t grow = gw_row(slr);
       const uint32_t u = (uint32_t)min(kMmaU * cc + s_us, CU - 1);
-      st.w[j] = bload128(pv.w, (grow * (uint32_t)row_words + u * 4u) * 4u);
+      bload_unit<BITS>(pv.w, (grow * (uint32_t)row_words + u * (uint32_t)BITS) * 4u, st.w[j]);
       const uint32_t gi = (grow * (uint32_t)groups + (u >> a.gsh)) * (uint32_t)sizeof(ST);
       st.sb[j] = (uint32_t)bload16(pv.s, gi) | ((uint32_t)bload16(pv.b, gi) << 16);
       const int ux = min(kMmaU * cc + x_us0 + 4 * j, CU - 1);
@@ -473,7 +502,13 @@ __global__ __launch_bounds__(256) void gemv_mma_kernel(const GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int slr = s_lr0 + 32 * j;
-      *reinterpret_cast<u32x4_t*>(&wl[buf][(slr * kMmaU + ((s_us + slr) & 7)) * 4]) = st.w[j];
+      uint32_t* wd = &wl[buf][(slr * kMmaU + ((s_us + slr) & 7)) * BITS];
+      if constexpr (BITS == 4) {
+        *reinterpret_cast<u32x4_t*>(wd) = u32x4_t{st.w[j][0], st.w[j][1], st.w[j][2], st.w[j][3]};
+      } else {
+#pragma unroll
+        for (int q = 0; q < BITS; q++) wd[q] = st.w[j][q];
+      }
       sl[buf][slr * kMmaU + s_us] = st.sb[j];
       // natural values x0..x7 -> pairs (x0, x4), (x1, x5), (x2, x6), (x3, x7)
       const u32x4_t n = st.x[j];
@@ -491,9 +526,7 @@ __global__ __launch_bounds__(256) void gemv_mma_kernel(const GemvArgs a) {
 #pragma unroll
     for (int us = 0; us < kMmaU; us++) {
       if (us < nu) {
-        const uint32_t w = wl[buf][(lr * kMmaU + ((us + lr) & 7)) * 4 + kb];
-        const u32x4_t bop = {(w & 0x000F000Fu) | MB, ((w >> 4) & 0x000F000Fu) | MB,
-                             ((w >> 8) & 0x000F000Fu) | MB, ((w >> 12) & 0x000F000Fu) | MB};
+        const u32x4_t bop = mma_codes<BITS>(&wl[buf][(lr * kMmaU + ((us + lr) & 7)) * BITS], kb, MB);
         const u32x4_t aop =
             *reinterpret_cast<const u32x4_t*>(&xl[buf][((us * kMmaTok + r) * 4 + (kb ^ ((r >> 2) & 3))) * 4]);
         P = Mma16<XT>::mma(aop, bop, P);
@@ -575,15 +608,15 @@ __global__ __launch_bounds__(256) void gemv_mma_kernel(const GemvArgs a) {
   }
 }
 
-hipError_t launch_mma_b4(int xdt, int sbdt, bool gateup, const GemvArgs& a, int grid, hipStream_t st,
-                         KEvents ev) {
+hipError_t MOE_CAT(launch_mma_b, MOE_BITS)(int xdt, int sbdt, bool gateup, const GemvArgs& a,
+                                            int grid, hipStream_t st, KEvents ev) {
 #define MOE_MMA(XT, ST)                                                                          \
   if (gateup)                                                                                    \
-    hipExtLaunchKernelGGL((gemv_mma_kernel<XT, ST, true>), dim3(grid), dim3(256), 0, st,         \
-                          ev.start, ev.stop, 0, a);                                              \
+    hipExtLaunchKernelGGL((gemv_mma_kernel<MOE_BITS, XT, ST, true>), dim3(grid), dim3(256), 0,   \
+                          st, ev.start, ev.stop, 0, a);                                          \
   else                                                                                           \
-    hipExtLaunchKernelGGL((gemv_mma_kernel<XT, ST, false>), dim3(grid), dim3(256), 0, st,        \
-                          ev.start, ev.stop, 0, a);                                              \
+    hipExtLaunchKernelGGL((gemv_mma_kernel<MOE_BITS, XT, ST, false>), dim3(grid), dim3(256), 0,  \
+                          st, ev.start, ev.stop, 0, a);                                          \
   return hipGetLastError();
   if (xdt == DT_BF16 && sbdt == DT_BF16) { MOE_MMA(bf16_t, bf16_t) }
   if (xdt == DT_BF16 && sbdt == DT_F16) { MOE_MMA(bf16_t, f16_t) }
@@ -592,7 +625,7 @@ hipError_t launch_mma_b4(int xdt, int sbdt, bool gateup, const GemvArgs& a, int 
 #undef MOE_MMA
   return hipErrorInvalidValue;
 }
-#endif  // MOE_BITS == 4
+#endif  // MOE_BITS <= 6
 
 // ---------------------------------------------------------------------------
 // one activation row per expert (decode T = 1): activations live in registers
@@ -977,8 +1010,6 @@ static hipError_t launch_gemv_bits(int xdt, int sbdt, bool gateup, int tokmax, c
 
 // One translation unit per bit width (MOE_BITS) keeps compile times short;
 // the per-width entry points are stitched together in api.cpp.
-#define MOE_CAT2(a, b) a##b
-#define MOE_CAT(a, b) MOE_CAT2(a, b)
 
 hipError_t MOE_CAT(launch_gemv_b, MOE_BITS)(int xdt, int sbdt, bool gateup, int tokmax,
                                              const GemvArgs& a, int grid, hipStream_t st,

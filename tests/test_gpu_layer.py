@@ -516,10 +516,14 @@ def test_layer_mfma_path(case):
     run_layer(cfg_bits(*case, n_experts=4, top_k=2), 160)
 
 
-@pytest.mark.parametrize("case", [(4, 4, 32, BF16, BF16), (4, 4, 32, F16, F16), (4, 4, 128, BF16, F16)])
+@pytest.mark.parametrize("case", [(4, 4, 32, BF16, BF16), (4, 4, 32, F16, F16), (4, 4, 128, BF16, F16),
+                                  (3, 6, 64, BF16, BF16), (2, 5, 32, F16, BF16), (6, 3, 128, F16, F16),
+                                  (5, 2, 64, BF16, F16)],
+                         ids=lambda c: f"gu{c[0]}-d{c[1]}-gs{c[2]}-sb{c[3]}-x{c[4]}")
 def test_layer_batched_mma_path(case):
-    """4 to 31 rows per expert with 4-bit weights: the batched GEMV on the
-    matrix cores, with a partial last block of down rows (hidden 544 is 8.5
+    """4 to 31 rows per expert with 2- to 6-bit weights: the batched GEMV on
+    the matrix cores (codes of 3, 5 and 6 bits straddle words inside a lane's
+    8-value block), with a partial last block of down rows (hidden 544 is 8.5
     blocks of 64) and passes of 16 activation rows (up to 30 rows for one
     expert at T = 40, 8 experts, top-3)."""
     gs = case[2]
