@@ -600,7 +600,12 @@ def main():
     M = T * cfg["k"]
     gu_flops = 2.0 * M * 2 * cfg["H"] * cfg["I"]
     k_bytes = gu_bytes
-    if T <= 64:
+    # the library's path choice: MFMA GEMM once used experts average >= 32 rows
+    gemm_path = T > 1 and M >= 32 * min(cfg["E"], M) and cfg["H"] % 64 == 0 and cfg["I"] % 64 == 0
+    # and the matrix-core GEMV once the used experts average 4 rows (2- to 6-bit weights)
+    mma_path = T > 1 and not gemm_path and 2 <= cfg["bits_gu"] <= 6 and M >= 4 * min(cfg["E"], M)
+    if not gemm_path:
+        # the GEMV paths stream each routed expert's weights once: HBM roofline
         roof = dict(bound="hbm", achieved=round(k_bytes / (gu_us * 1e-6) / 1e9, 1),
                     peak=HBM_PEAK_GBS, unit="GB/s")
     else:
@@ -608,10 +613,6 @@ def main():
                     peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s")
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
     roof["traffic"] = measured_traffic(cfg["workload"], T)
-    # the library's path choice: MFMA GEMM once used experts average >= 32 rows
-    gemm_path = T > 1 and M >= 32 * min(cfg["E"], M) and cfg["H"] % 64 == 0 and cfg["I"] % 64 == 0
-    # and the matrix-core GEMV once the used experts average 4 rows (4-bit weights)
-    mma_path = T > 1 and not gemm_path and cfg["bits_gu"] == 4 and M >= 4 * min(cfg["E"], M)
     roof["kernel"] = ("gateup1_kernel (one-token gate/up with routing)" if T == 1 else
                       "gemm_grouped_kernel (MFMA gate/up over the expert row tiles)" if gemm_path else
                       "gemv_mma_kernel (MFMA gate/up over the dispatch plan)" if mma_path else
