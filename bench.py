@@ -602,8 +602,10 @@ def main():
     k_bytes = gu_bytes
     # the library's path choice: MFMA GEMM once used experts average >= 32 rows
     gemm_path = T > 1 and M >= 32 * min(cfg["E"], M) and cfg["H"] % 64 == 0 and cfg["I"] % 64 == 0
-    # and the matrix-core GEMV once the used experts average 4 rows (2- to 6-bit weights)
-    mma_path = T > 1 and not gemm_path and 2 <= cfg["bits_gu"] <= 6 and M >= 4 * min(cfg["E"], M)
+    # and the matrix-core GEMV once the used experts average 4 rows (4-bit) or
+    # 2 rows (2-, 3-, 5- and 6-bit weights)
+    mma_path = T > 1 and not gemm_path and 2 <= cfg["bits_gu"] <= 6 and \
+        M >= (4 if cfg["bits_gu"] == 4 else 2) * min(cfg["E"], M)
     if not gemm_path:
         # the GEMV paths stream each routed expert's weights once: HBM roofline
         roof = dict(bound="hbm", achieved=round(k_bytes / (gu_us * 1e-6) / 1e9, 1),

@@ -526,7 +526,10 @@ bool run_multi(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
 // Rows per used expert from which the batched GEMV runs on the matrix cores
 // (Qwen3 shape, 4 per expert: 192 -> 154 us per layer step; GPT-OSS, 8 per
 // expert: 409 -> 208 us; at 1-2 per expert gemv_multi_kernel is faster).
+// Codes of other widths cost gemv_multi_kernel more unpacking, so they move
+// from 2 rows per expert (mixed 3/6-bit layer, 64 tokens: 317 -> 231 us).
 constexpr int kMmaMinRows = 4;
+constexpr int kMmaMinRowsOther = 2;
 
 // gemv_mma_kernel (matrix cores) for 2- to 6-bit weights (codes exact with
 // the magic offset in either 16-bit type) and 16-bit activations: 32 rows of
@@ -575,7 +578,8 @@ moe_status run_gemv(const moe_qproj& p0, const moe_qproj* p1, const void* x, int
     moe_status status = MOE_OK;
     // the matrix cores once the used experts average kMmaMinRows rows: below
     // that the K-chunk pipeline's latency outweighs the VALU it saves
-    if ((long)M >= (long)kMmaMinRows * std::max(1, slots) &&
+    const int min_rows = p0.bits == 4 ? kMmaMinRows : kMmaMinRowsOther;
+    if ((long)M >= (long)min_rows * std::max(1, slots) &&
         run_mma(p0, p1, x, xdt, perm, topk, offsets, used, slots, out, act, alpha, limit, st, ev,
                 &status))
       return status;
