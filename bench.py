@@ -45,7 +45,7 @@ CONFIGS = {
                   gating="softmax_topk", router_bias=False, T=1, SI=0,
                   workload="qwen3moe_decode"),
     "prefill": dict(H=2048, E=128, k=8, I=768, bits_gu=4, bits_d=4, sb="f16", act="swiglu",
-                    gating="softmax_topk", router_bias="zipf", T=4096, SI=0,
+                    gating="softmax_topk", router_bias="zipf", beta=0.33, T=4096, SI=0,
                     workload="qwen3moe_prefill_4096_zipf1.1"),
     "mixed": dict(H=2048, E=256, k=8, I=512, bits_gu=3, bits_d=6, sb="bf16", act="swiglu",
                   gating="softmax_topk", router_bias=False, T=2048, SI=512,
@@ -103,7 +103,7 @@ def make_layer(cfg, seed, torch, fl, lib):
     if cfg["router_bias"] is True:
         rb = (torch.randn(E, device=dev, generator=g) * 0.1).to(torch.bfloat16)
     elif cfg["router_bias"] == "zipf":
-        rb = zipf_bias(E, cfg.get("beta", 1.0), seed, torch).to(dev)
+        rb = zipf_bias(E, cfg["beta"], seed, torch).to(dev)
     gating = fl.MoEGatingMode.topKThenSoftmax if cfg["gating"] == "topk_softmax" else \
         fl.MoEGatingMode.softmaxThenTopK
     router = fl.MoERouter(E, cfg["k"], gating, True)
@@ -154,8 +154,25 @@ def measured_traffic(workload, T):
 
 
 # ------------------------------------------------------------ CPU oracle --
-def cpu_baseline(layer, cfg, torch, budget_s=12.0):
-    """Times the C oracle (oracle/) on layer 0, one token per call."""
+def cpu_threads():
+    """Worker threads for the all-core baseline: the cores this process may run
+    on, at most 16 (one GPU's share of the box)."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return max(1, min(16, avail))
+
+
+def cpu_baseline(layer, cfg, torch, budget_s=10.0):
+    """Times the C oracle (oracle/) on layer 0 in two modes on this host's
+    cores: one thread, and one thread per core over independent token rows
+    (the reference's host loop runs per token under concurrentPerform,
+    MoELayer.swift:744-748). ctypes releases the GIL for each oracle call.
+    Each mode runs calls of T rows (T = 1 for decode, 4 otherwise) for about
+    budget_s seconds."""
+    import concurrent.futures as cf
+
     import numpy as np
     import oracle as orc
 
@@ -167,9 +184,9 @@ def cpu_baseline(layer, cfg, torch, budget_s=12.0):
             return t.view(torch.int16).numpy().view(np.uint16)
         if t.dtype == torch.int32:
             return t.numpy().view(np.uint32)
+        if t.dtype == torch.float16:
+            return t.view(torch.int16).numpy().view(np.uint16)
         return t.numpy()
-
-    sbdt = orc.BF16 if layer.gate.scales.dtype == torch.bfloat16 else orc.F16
 
     def qp(p):
         return orc.QProj(host(p.weight), host(p.scales), host(p.biases), p.bits, p.group_size,
@@ -187,24 +204,57 @@ def cpu_baseline(layer, cfg, torch, budget_s=12.0):
     L.gate, L.up, L.down = keep["gate"].c(), keep["up"].c(), keep["down"].c()
     L.activation = orc.ACT_GPTOSS if cfg["act"] == "gptoss" else orc.ACT_SWIGLU
     L.alpha, L.limit = 1.702, 7.0
-    rng = np.random.default_rng(1)
+    if layer.shared is not None:
+        keep["shared"] = tuple(qp(p) for p in layer.shared)
+        keep["sgw"] = host(layer.shared_gate_weight)
+        L.has_shared = 1
+        L.shared_gate, L.shared_up, L.shared_down = (q.c() for q in keep["shared"])
+        L.shared_gate_weight = None if keep["sgw"] is None else keep["sgw"].ctypes.data
     lib = orc.lib()
     T = 1 if cfg["T"] == 1 else 4
-    x = orc.from_f32(rng.normal(0, 1, (64, T, cfg["H"])).astype(np.float32), orc.BF16)
+    rng = np.random.default_rng(1)
+    nx = 256
+    x = orc.from_f32(rng.normal(0, 1, (nx, T, cfg["H"])).astype(np.float32), orc.BF16)
+
+    def one(i, y):
+        lib.or_moe_layer(C.byref(L), x[i % nx].ctypes.data_as(C.c_void_p), T,
+                         y.ctypes.data_as(C.c_void_p), None, None, None, None)
+
+    # single thread
     y = np.zeros((T, cfg["H"]), np.uint16)
     t0 = time.perf_counter()
-    n = 0
-    while n < 64:
-        lib.or_moe_layer(C.byref(L), x[n].ctypes.data_as(C.c_void_p), T, y.ctypes.data_as(C.c_void_p),
-                         None, None, None, None)
-        n += 1
-        if time.perf_counter() - t0 > budget_s and n >= 3:
+    n1 = 0
+    while n1 < 3 or time.perf_counter() - t0 < budget_s:
+        one(n1, y)
+        n1 += 1
+        if n1 >= 4096:
             break
-    dt = time.perf_counter() - t0
-    _ = sbdt
-    return dict(value=n * T / dt, unit="tokens/s", cores=1, kind="port",
-                sample=f"{n} oracle layer calls of {T} token(s) on layer 0 (single thread, "
-                       f"{dt:.1f} s)")
+    dt1 = time.perf_counter() - t0
+    # all cores: each worker runs its own token rows
+    nt = cpu_threads()
+    stop = time.perf_counter() + budget_s
+
+    def worker(w):
+        yw = np.zeros((T, cfg["H"]), np.uint16)
+        n = 0
+        while n < 2 or time.perf_counter() < stop:
+            one(w + nt * n, yw)
+            n += 1
+        return n
+
+    t0 = time.perf_counter()
+    with cf.ThreadPoolExecutor(max_workers=nt) as ex:
+        counts = list(ex.map(worker, range(nt)))
+    dtn = time.perf_counter() - t0
+    nall = sum(counts)
+    single = n1 * T / dt1
+    allc = nall * T / dtn
+    return dict(value=round(allc, 2), unit="tokens/s", cores=nt, kind="port",
+                single_thread=round(single, 2), all_cores=round(allc, 2),
+                nproc=os.cpu_count(),
+                sample=f"C oracle on layer 0, calls of {T} token row(s): {n1} calls on one "
+                       f"thread in {dt1:.1f} s; {nall} calls on {nt} threads (one per core, "
+                       f"independent rows) in {dtn:.1f} s")
 
 
 # ------------------------------------------------------- checkpoint load --
@@ -469,13 +519,16 @@ def bench_mxfp4(args, torch):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2400)
-    ap.add_argument("--warmup", type=int, default=240)
+    ap.add_argument("--steps", type=int, default=2400,
+                    help="timed layer calls (5 repeats of steps / 5 calls, median reported)")
+    ap.add_argument("--warmup", type=int, default=240, help="untimed eager layer calls first")
     ap.add_argument("--config", default="gptoss",
                     choices=sorted(CONFIGS) + ["ckpt_load", "mxfp4"])
     ap.add_argument("--batch", type=int, default=None, help="tokens per step (overrides config)")
     ap.add_argument("--layers", type=int, default=24, help="resident layers rotated per step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="default config only: skip the prefill and mixed-bit lines")
     ap.add_argument("--decoder-step", action="store_true",
                     help="time the block with the residual add + RMSNorm before it and the "
                          "residual add after it, fused against three calls")
@@ -515,53 +568,98 @@ def main():
     if args.decoder_step:
         bench_decoder_step(args, torch, cfg)
         return
-    T = cfg["T"]
     torch.manual_seed(0)
-    L = args.layers if T <= 64 else min(args.layers, 4)
-    log(f"building {L} resident layers of {args.config} ...")
+    L = args.layers if cfg["T"] <= 64 else min(args.layers, 4)
+    res, layer0 = run_config(cfg, torch, fl, lib, steps=args.steps, warmup=args.warmup, L=L)
+    out = {
+        "metric": "MoE-layer tokens/s",
+        "value": res["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random packed codes, U-distributed scales/biases, N(0,1) activations)",
+        "config": res["config"],
+        "timing": res["timing"],
+        "roofline": res["roofline"],
+        "expert_stream": res["expert_stream"],
+    }
+    if args.config == "gptoss" and not args.batch and not args.no_extra:
+        # the metric's other two parts, on the prefill configs (configs[3],
+        # configs[4]): fixed counts, independent of --steps / --warmup
+        for name in ("prefill", "mixed"):
+            c2 = dict(CONFIGS[name])
+            r2, _ = run_config(c2, torch, fl, lib, steps=60, warmup=6, L=4)
+            out[name] = {"workload": c2["workload"], "tokens_per_s": r2["tokens_per_s"],
+                         "ms_per_step": r2["ms_per_step"], "steps": 60, "warmup": 6,
+                         "timing": r2["timing"], "roofline": r2["roofline"],
+                         "layer_roofline": r2["layer_roofline"], "paths": r2["config"]["paths"]}
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle ...")
+        cpu = cpu_baseline(layer0, cfg, torch)
+    out["cpu_baseline"] = cpu
+    print(json.dumps(out), flush=True)
+
+
+def run_config(cfg, torch, fl, lib, steps, warmup, L):
+    """Times `steps` layer calls (one step = one call of the layer on cfg["T"]
+    token rows) after `warmup` untimed eager calls. Steps rotate through L
+    resident layers. The timed steps run as 5 repeats of HIP-graph replays
+    (steps // 5 calls each, the remainder spread over the first repeats), each
+    bracketed by events on the launch stream; ms_per_step is the median over
+    the repeats of (repeat time / its calls)."""
+    T = cfg["T"]
+    log(f"building {L} resident layers of {cfg['workload']} (T={T}) ...")
     layers = [make_layer(cfg, seed=100 + l, torch=torch, fl=fl, lib=lib) for l in range(L)]
     xs = [torch.randn(T, cfg["H"], device="cuda").to(torch.bfloat16) for _ in range(L)]
     ys = [torch.empty_like(x) for x in xs]
     for l in range(L):
         layers[l].workspace(T)
     torch.cuda.synchronize()
+    paths = layers[0].paths(T)
 
-    steps = max(L, (args.steps // L) * L)
-    warm = max(L, (args.warmup // L) * L)
-
-    # eager warm-up
-    for i in range(warm):
+    # warm-up: exactly `warmup` eager calls
+    for i in range(warmup):
         layers[i % L].forward(xs[i % L], out=ys[i % L])
     torch.cuda.synchronize()
 
-    # HIP graph of one rotation through the resident layers
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for l in range(L):
-            layers[l].forward(xs[l], out=ys[l])
-    graph.replay()
+    # the timed steps: 5 repeats, each one HIP-graph replay
+    nrep = 5 if steps >= 5 else max(1, steps)
+    sizes = [steps // nrep + (1 if r < steps % nrep else 0) for r in range(nrep)]
+    graphs = {}
+    for n in sorted(set(sizes)):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                layers[i % L].forward(xs[i % L], out=ys[i % L])
+        graphs[n] = g
     torch.cuda.synchronize()
-
-    # timed region: `steps` layer calls
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(nrep)]
     w0 = time.perf_counter()
-    e0.record()
-    for _ in range(steps // L):
-        graph.replay()
-    e1.record()
+    for r, n in enumerate(sizes):
+        evs[r][0].record()
+        graphs[n].replay()
+        evs[r][1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
-    ms_total = e0.elapsed_time(e1)
-    ms_per_step = ms_total / steps
+    per_step = sorted(evs[r][0].elapsed_time(evs[r][1]) / n for r, n in enumerate(sizes))
+    ms_per_step = per_step[len(per_step) // 2]
     value = T * 1000.0 / ms_per_step
-    log(f"{steps} steps: {ms_total:.3f} ms (events), {wall * 1e3:.3f} ms (wall); "
-        f"{ms_per_step * 1e3:.2f} us/step")
+    log(f"{steps} steps in {nrep} repeats {sizes}: {ms_per_step * 1e3:.2f} us/step (median), "
+        f"repeats {[round(v * 1e3, 2) for v in per_step]} us/step; wall {wall * 1e3:.1f} ms")
+    del graphs
 
     # kernel-level timing of the routed expert kernels: start/end events
     # recorded by the kernels' own dispatch on the launch stream
     ev = HipEvents()
-    reps = max(1, min(20, 480 // L))
+    reps = max(1, min(20, 480 // L)) if T <= 64 else 4
     marks = [[[ev.create() for _ in range(4)] for _ in range(L)] for _ in range(reps)]
     trace = []
     for r in range(reps):
@@ -589,72 +687,78 @@ def main():
     gu_us = 1e3 * sum(gu) / len(gu)
     dn_us = 1e3 * sum(dn) / len(dn)
 
-    # algorithmic bytes: distinct experts actually routed (decode) or FLOPs (prefill)
+    # algorithmic bytes: distinct experts actually routed (GEMV paths) or FLOPs (GEMM)
     lay0 = layers[0]
     _, tr = lay0.forward(xs[0], trace=True)
     torch.cuda.synchronize()
     U = int(torch.unique(tr["topk_idx"]).numel())
-    gu_bytes = proj_bytes(lay0.gate, U) + proj_bytes(lay0.up, U) + \
-        T * cfg["H"] * 2 + T * cfg["k"] * cfg["I"] * 2
-    dn_bytes = proj_bytes(lay0.down, U) + T * cfg["k"] * cfg["I"] * 2 + T * cfg["H"] * 2
-    M = T * cfg["k"]
-    gu_flops = 2.0 * M * 2 * cfg["H"] * cfg["I"]
-    k_bytes = gu_bytes
-    # the library's path choice: MFMA GEMM once used experts average >= 32 rows
-    gemm_path = T > 1 and M >= 32 * min(cfg["E"], M) and cfg["H"] % 64 == 0 and cfg["I"] % 64 == 0
-    # and the matrix-core GEMV once the used experts average 4 rows (4-bit) or
-    # 2 rows (2-, 3-, 5- and 6-bit weights)
-    mma_path = T > 1 and not gemm_path and 2 <= cfg["bits_gu"] <= 6 and \
-        M >= (4 if cfg["bits_gu"] == 4 else 2) * min(cfg["E"], M)
-    if not gemm_path:
-        # the GEMV paths stream each routed expert's weights once: HBM roofline
-        roof = dict(bound="hbm", achieved=round(k_bytes / (gu_us * 1e-6) / 1e9, 1),
-                    peak=HBM_PEAK_GBS, unit="GB/s")
-    else:
+    H, I, k = cfg["H"], cfg["I"], cfg["k"]
+    gu_bytes = proj_bytes(lay0.gate, U) + proj_bytes(lay0.up, U) + T * H * 2 + T * k * I * 2
+    dn_bytes = proj_bytes(lay0.down, U) + T * k * I * 2 + T * H * 2
+    M = T * k
+    gu_flops = 2.0 * M * 2 * H * I
+    dn_flops = 2.0 * M * H * I
+    sh_flops = 0.0
+    if cfg["SI"]:
+        sh_flops = 2.0 * T * 3 * H * cfg["SI"]
+    router_bytes = cfg["E"] * H * 2
+    layer_bytes = gu_bytes + dn_bytes - T * k * I * 4 + router_bytes
+    if paths["gate_up"] == "gemm":
         roof = dict(bound="mfma", achieved=round(gu_flops / (gu_us * 1e-6) / 1e12, 2),
                     peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s")
+        layer_flops = gu_flops + dn_flops + sh_flops
+        layer_roof = dict(bound="mfma", flops=layer_flops,
+                          achieved=round(layer_flops / (ms_per_step * 1e-3) / 1e12, 2),
+                          peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s")
+    else:
+        # the GEMV paths stream each routed expert's weights once: HBM roofline
+        roof = dict(bound="hbm", achieved=round(gu_bytes / (gu_us * 1e-6) / 1e9, 1),
+                    peak=HBM_PEAK_GBS, unit="GB/s")
+        layer_roof = dict(bound="hbm", bytes=layer_bytes,
+                          achieved=round(layer_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+                          peak=HBM_PEAK_GBS, unit="GB/s")
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    layer_roof["frac"] = round(layer_roof["achieved"] / layer_roof["peak"], 4)
     roof["traffic"] = measured_traffic(cfg["workload"], T)
-    roof["kernel"] = ("gateup1_kernel (one-token gate/up with routing)" if T == 1 else
-                      "gemm_grouped_kernel (MFMA gate/up over the expert row tiles)" if gemm_path else
-                      "gemv_mma_kernel (MFMA gate/up over the dispatch plan)" if mma_path else
-                      "gemv_multi_kernel (routed gate/up over the dispatch plan)")
+    roof["kernel"] = {"decode1": "gateup1_kernel (one-token gate/up with routing)",
+                      "gemm": "gemm_grouped_kernel (MFMA gate/up over the expert row tiles)",
+                      "gemv_mma": "gemv_mma_kernel (MFMA gate/up over the dispatch plan)",
+                      "gemv": "gemv_multi_kernel (routed gate/up over the dispatch plan)"}[
+                          paths["gate_up"]]
     roof["avg_us"] = round(gu_us, 3)
-    roof["algorithmic_bytes"] = k_bytes
-    log(f"gate/up kernel {gu_us:.2f} us ({k_bytes / 1e6:.2f} MB, "
-        f"{k_bytes / (gu_us * 1e-6) / 1e9:.0f} GB/s); down+combine {dn_us:.2f} us "
-        f"({dn_bytes / 1e6:.2f} MB, {dn_bytes / (dn_us * 1e-6) / 1e9:.0f} GB/s); U={U}")
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        log("timing the CPU oracle ...")
-        cpu = cpu_baseline(layers[0], cfg, torch)
-
-    out = {
-        "metric": "MoE-layer tokens/s",
-        "value": round(value, 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": warm,
+    if roof["bound"] == "hbm":
+        roof["algorithmic_bytes"] = gu_bytes
+    else:
+        roof["algorithmic_flops"] = gu_flops
+    log(f"gate/up kernel {gu_us:.2f} us ({gu_bytes / 1e6:.2f} MB, {gu_flops / 1e9:.1f} GFLOP); "
+        f"down {dn_us:.2f} us; U={U}; paths {paths}")
+    config = {"workload": cfg["workload"], "hidden": H, "experts": cfg["E"], "top_k": k,
+              "intermediate": I, "tokens_per_step": T, "bits": [cfg["bits_gu"], cfg["bits_d"]],
+              "group_size": 64, "resident_layers": L, "parallelism": "single-gpu",
+              "paths": paths}
+    if cfg["SI"]:
+        config["shared_intermediate"] = cfg["SI"]
+    if cfg["router_bias"] == "zipf":
+        counts = torch.bincount(tr["topk_idx"].flatten().long(), minlength=cfg["E"]).float()
+        config["zipf"] = {"s": 1.1, "beta": cfg["beta"],
+                          "max_over_median": round(float(counts.max() / counts.median()), 2)}
+    res = {
+        "tokens_per_s": round(value, 1),
         "ms_per_step": round(ms_per_step, 6),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (random packed codes, U-distributed scales/biases, N(0,1) activations)",
-        "config": {"workload": cfg["workload"], "hidden": cfg["H"], "experts": cfg["E"],
-                   "top_k": cfg["k"], "intermediate": cfg["I"], "tokens_per_step": T,
-                   "bits": [cfg["bits_gu"], cfg["bits_d"]], "group_size": 64,
-                   "resident_layers": L, "parallelism": "single-gpu"},
+        "timing": {"repeats": nrep, "calls_per_repeat": sizes,
+                   "ms_per_step_each": [round(v, 6) for v in per_step],
+                   "method": "HIP-graph replay per repeat, events on the launch stream, median"},
+        "config": config,
         "roofline": roof,
-        "expert_stream": {"gate_up_us": round(gu_us, 3), "down_combine_us": round(dn_us, 3),
+        "layer_roofline": layer_roof,
+        "expert_stream": {"gate_up_us": round(gu_us, 3), "down_us": round(dn_us, 3),
                           "bytes": gu_bytes + dn_bytes, "distinct_experts": U,
                           "GBps": round((gu_bytes + dn_bytes) / ((gu_us + dn_us) * 1e-6) / 1e9, 1)},
-        "cpu_baseline": cpu,
     }
-    print(json.dumps(out), flush=True)
-
+    out_layer = layers[0]
+    del layers, xs, ys
+    torch.cuda.synchronize()
+    return res, out_layer
 
 if __name__ == "__main__":
     main()

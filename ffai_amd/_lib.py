@@ -17,18 +17,22 @@ MOE_OK, MOE_ERR_INVALID, MOE_ERR_UNSUPPORTED, MOE_ERR_WORKSPACE, MOE_ERR_HIP = r
 MOE_F32, MOE_F16, MOE_BF16 = 0, 1, 2
 MOE_SOFTMAX_THEN_TOPK, MOE_TOPK_THEN_SOFTMAX, MOE_SIGMOID_TOPK = 0, 1, 2
 MOE_ACT_SWIGLU, MOE_ACT_GPTOSS, MOE_ACT_GEGLU, MOE_ACT_RELU2 = 0, 1, 2, 3
+MOE_PATH_NONE, MOE_PATH_DECODE1, MOE_PATH_GEMV, MOE_PATH_GEMV_MMA, MOE_PATH_GEMM = range(5)
+PATH_NAMES = {MOE_PATH_NONE: "none", MOE_PATH_DECODE1: "decode1", MOE_PATH_GEMV: "gemv",
+              MOE_PATH_GEMV_MMA: "gemv_mma", MOE_PATH_GEMM: "gemm"}
 (MOE_ST_F32, MOE_ST_F16, MOE_ST_BF16, MOE_ST_I32, MOE_ST_U32, MOE_ST_I64, MOE_ST_U64, MOE_ST_I8,
  MOE_ST_U8) = range(9)
 MOE_ST_MAX_DIMS = 8
 
 EXPORTS = [
     "moe_last_error_string", "moe_version", "moe_validate_qproj", "moe_validate_layer",
-    "moe_derive_bits", "moe_router_logits", "moe_router_topk", "moe_router_topk_scaled",
+    "moe_derive_bits", "moe_router_logits", "moe_router_logits_q", "moe_router_topk",
+    "moe_router_topk_scaled",
     "moe_dispatch_workspace_bytes",
     "moe_dispatch_plan", "moe_dequantize_affine", "moe_expert_matmul_workspace_bytes",
     "moe_expert_matmul", "moe_activation_apply", "moe_unpermute", "moe_layer_workspace_bytes",
     "moe_layer_forward", "moe_layer_forward_routed", "moe_layer_forward_residual",
-    "moe_add_rmsnorm", "moe_mxfp4_to_affine", "moe_layer_create", "moe_layer_destroy",
+    "moe_layer_path", "moe_add_rmsnorm", "moe_mxfp4_to_affine", "moe_layer_create", "moe_layer_destroy",
     "moe_layer_decode", "moe_layer_decode_many",
     "moe_st_open", "moe_st_close", "moe_st_count", "moe_st_name", "moe_st_info", "moe_st_read_host",
     "moe_st_upload", "moe_st_is_quantized", "moe_st_stacked_bytes", "moe_st_load_stacked",
@@ -63,7 +67,16 @@ class LayerDesc(C.Structure):
         ("shared_gate", QProj), ("shared_up", QProj), ("shared_down", QProj),
         ("shared_gate_weight", C.c_void_p),
         ("logit_scale", C.c_float), ("routed_scale", C.c_float), ("expert_scale", C.c_void_p),
+        ("router_q", QProj), ("shared_gate_q", QProj),
     ]
+
+
+class LayerPaths(C.Structure):
+    _fields_ = [("gate_up", C.c_int32), ("down", C.c_int32), ("shared_gate_up", C.c_int32),
+                ("shared_down", C.c_int32)]
+
+    def names(self) -> dict:
+        return {f: PATH_NAMES[getattr(self, f)] for f, _ in self._fields_}
 
 
 class LayerTrace(C.Structure):
@@ -92,6 +105,7 @@ def load():
     lib.moe_validate_layer.argtypes = [C.POINTER(LayerDesc)]
     lib.moe_derive_bits.argtypes = [C.c_int64, C.c_int64, i32, C.POINTER(i32)]
     lib.moe_router_logits.argtypes = [vp, i32, i32, i32, vp, i32, vp, i32, vp, st]
+    lib.moe_router_logits_q.argtypes = [vp, i32, i32, i32, C.POINTER(QProj), vp, i32, vp, st]
     lib.moe_router_topk.argtypes = [vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, st]
     lib.moe_router_topk_scaled.argtypes = [vp, i32, i32, i32, i32, i32, i32, vp, C.c_float,
                                            C.c_float, vp, vp, vp, st]
@@ -112,6 +126,7 @@ def load():
                                              C.POINTER(LayerTrace), st]
     lib.moe_layer_forward_residual.argtypes = [C.POINTER(LayerDesc), vp, vp, vp, C.c_float, i32,
                                                vp, vp, vp, sz, C.POINTER(LayerTrace), st]
+    lib.moe_layer_path.argtypes = [C.POINTER(LayerDesc), i32, C.POINTER(LayerPaths)]
     lib.moe_add_rmsnorm.argtypes = [vp, vp, vp, C.c_float, i32, i32, i32, vp, vp, st]
     lib.moe_mxfp4_to_affine.argtypes = [vp, vp, C.c_int64, vp, vp, vp, i32, st]
     lib.moe_layer_create.argtypes = [C.POINTER(LayerDesc), C.POINTER(vp)]
@@ -139,10 +154,11 @@ def load():
     lib.moe_st_mxfp4_bytes.argtypes = [vp, C.c_char_p, i32, C.POINTER(sz), C.POINTER(sz)]
     lib.moe_st_load_mxfp4.argtypes = [vp, C.c_char_p, i32, vp, sz, vp, sz, C.POINTER(QProj), st]
     for name in ["moe_validate_qproj", "moe_validate_layer", "moe_derive_bits", "moe_router_logits",
-                 "moe_router_topk", "moe_router_topk_scaled", "moe_dispatch_plan",
+                 "moe_router_logits_q", "moe_router_topk", "moe_router_topk_scaled", "moe_dispatch_plan",
                  "moe_dequantize_affine", "moe_expert_matmul", "moe_activation_apply",
                  "moe_unpermute", "moe_layer_forward", "moe_layer_forward_routed",
-                 "moe_layer_forward_residual", "moe_add_rmsnorm", "moe_mxfp4_to_affine",
+                 "moe_layer_forward_residual", "moe_layer_path",
+                 "moe_add_rmsnorm", "moe_mxfp4_to_affine",
                  "moe_layer_create", "moe_layer_decode",
                  "moe_layer_decode_many", "moe_st_open", "moe_st_info", "moe_st_read_host",
                  "moe_st_upload", "moe_st_stacked_bytes", "moe_st_load_stacked",

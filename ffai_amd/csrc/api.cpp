@@ -12,9 +12,11 @@
 #include <cstdio>
 #include <cmath>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "../../include/moe_hip.h"
 #include "moe_internal.hpp"
@@ -70,6 +72,27 @@ static hipError_t launch_multi(int bits, int xdt, int sbdt, bool gateup, int ur,
   return hipErrorInvalidValue;
 }
 
+
+hipError_t launch_router_q_b2(const void*, int, int, int, const GemvProj&, int, int, const void*, int, void*, hipStream_t);
+hipError_t launch_router_q_b3(const void*, int, int, int, const GemvProj&, int, int, const void*, int, void*, hipStream_t);
+hipError_t launch_router_q_b4(const void*, int, int, int, const GemvProj&, int, int, const void*, int, void*, hipStream_t);
+hipError_t launch_router_q_b5(const void*, int, int, int, const GemvProj&, int, int, const void*, int, void*, hipStream_t);
+hipError_t launch_router_q_b6(const void*, int, int, int, const GemvProj&, int, int, const void*, int, void*, hipStream_t);
+hipError_t launch_router_q_b8(const void*, int, int, int, const GemvProj&, int, int, const void*, int, void*, hipStream_t);
+
+hipError_t launch_router_q(int bits, const void* x, int xdt, int T, int H, const GemvProj& W,
+                           int sbdt, int gsh, const void* bias, int E, void* logits,
+                           hipStream_t st) {
+  switch (bits) {
+    case 2: return launch_router_q_b2(x, xdt, T, H, W, sbdt, gsh, bias, E, logits, st);
+    case 3: return launch_router_q_b3(x, xdt, T, H, W, sbdt, gsh, bias, E, logits, st);
+    case 4: return launch_router_q_b4(x, xdt, T, H, W, sbdt, gsh, bias, E, logits, st);
+    case 5: return launch_router_q_b5(x, xdt, T, H, W, sbdt, gsh, bias, E, logits, st);
+    case 6: return launch_router_q_b6(x, xdt, T, H, W, sbdt, gsh, bias, E, logits, st);
+    case 8: return launch_router_q_b8(x, xdt, T, H, W, sbdt, gsh, bias, E, logits, st);
+  }
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_gemm_b2(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
 hipError_t launch_gemm_b3(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
@@ -278,6 +301,22 @@ extern "C" moe_status moe_derive_bits(int64_t packed_cols, int64_t scale_cols, i
 
 namespace {
 
+// A quantised router or shared gate: a one-expert stack [1, n, hidden].
+moe_status validate_router_q(const moe_qproj* q, int n, int hidden, int xdt, const char* name) {
+  MOE_TRY(validate_qproj_named(q, name));
+  if (q->n_experts != 1 || q->n != n || q->k != hidden)
+    return fail(MOE_ERR_INVALID, "%s: quantised weight must be [1, %d, %d] (got [%d, %d, %d])", name,
+                n, hidden, q->n_experts, q->n, q->k);
+  if (q->out_bias) return fail(MOE_ERR_INVALID, "%s: the router bias goes in router_bias", name);
+  if (xdt != MOE_F16 && xdt != MOE_BF16)
+    return fail(MOE_ERR_UNSUPPORTED, "%s: quantised router needs f16 or bf16 activations", name);
+  if (!pair_ok(xdt, q->sb_dtype))
+    return fail(MOE_ERR_UNSUPPORTED, "%s: scale dtype %d with activation dtype %d is not built",
+                name, q->sb_dtype, xdt);
+  if (hidden > 8192) return fail(MOE_ERR_UNSUPPORTED, "%s: hidden above 8192", name);
+  return MOE_OK;
+}
+
 constexpr int kMaxExperts = 512;
 constexpr int kMaxHidden = 8192;  // router rows are read in one round trip of 16 loads per lane
 
@@ -293,7 +332,12 @@ moe_status validate_layer_impl(const moe_layer_desc* d) {
     return fail(MOE_ERR_UNSUPPORTED, "MoELayer: hidden (%d) above %d", d->hidden, kMaxHidden);
   if (!dt_ok(d->act_dtype) || !dt_ok(d->router_dtype))
     return fail(MOE_ERR_INVALID, "MoELayer: bad dtype");
-  if (!d->router_weight) return fail(MOE_ERR_INVALID, "MoELayer: router weight is NULL");
+  const bool rq = d->router_q.weight != nullptr;
+  if (!d->router_weight && !rq) return fail(MOE_ERR_INVALID, "MoELayer: router weight is NULL");
+  if (d->router_weight && rq)
+    return fail(MOE_ERR_INVALID,
+                "MoELayer: give the router as a dense weight or as a quantised triplet, not both");
+  if (rq) MOE_TRY(validate_router_q(&d->router_q, d->n_experts, d->hidden, d->act_dtype, "gate"));
   if (!gating_ok(d->gating)) return fail(MOE_ERR_INVALID, "MoERouter: bad gating mode %d", d->gating);
   if (!act_ok(d->activation))
     return fail(MOE_ERR_INVALID, "MoELayer: bad activation %d", d->activation);
@@ -343,6 +387,16 @@ moe_status validate_layer_impl(const moe_layer_desc* d) {
       return fail(MOE_ERR_UNSUPPORTED, "MoELayer: shared gate/up must share bits/group/dtype");
     if (!pair_ok(d->act_dtype, sg->sb_dtype) || !pair_ok(d->act_dtype, sd->sb_dtype))
       return fail(MOE_ERR_UNSUPPORTED, "MoELayer: shared expert scale dtype not built");
+    if (d->shared_gate_q.weight) {
+      if (d->shared_gate_weight)
+        return fail(MOE_ERR_INVALID,
+                    "MoELayer: give shared_expert_gate as a dense weight or a quantised triplet, "
+                    "not both");
+      MOE_TRY(validate_router_q(&d->shared_gate_q, 1, d->hidden, d->act_dtype,
+                                "shared_expert_gate"));
+    }
+  } else if (d->shared_gate_q.weight || d->shared_gate_weight) {
+    return fail(MOE_ERR_INVALID, "MoELayer: shared_expert_gate given without a shared expert");
   }
   return MOE_OK;
 }
@@ -467,30 +521,78 @@ int pick_lg_dec1(int CU, int gsh);
 constexpr int kMultiIters = 2;
 constexpr int kMultiBlocks = 1024;
 
+// Rows per used expert from which the batched GEMV runs on the matrix cores
+// (Qwen3 shape, 4 per expert: 192 -> 154 us per layer step; GPT-OSS, 8 per
+// expert: 409 -> 208 us; at 1-2 per expert gemv_multi_kernel is faster).
+// Codes of other widths cost gemv_multi_kernel more unpacking, so they move
+// from 2 rows per expert (mixed 3/6-bit layer, 64 tokens: 317 -> 231 us).
+// One expert alone (a shared expert) gets only ceil(N / 32) matrix-core
+// blocks, so it moves only once a pass fills the 16 activation rows.
+constexpr int kMmaMinRows = 4;
+constexpr int kMmaMinRowsOther = 2;
+constexpr int kMmaMinRowsSingleExpert = 16;
+
+// gemv_mma_kernel applies: 2- to 6-bit codes (exact with the magic offset in
+// either 16-bit type), 16-bit activations at 16-byte aligned rows, and
+// expert-local byte offsets below 2^31.
+bool mma_ok(const moe_qproj& p0, const moe_qproj* p1, bool x_aligned, int xdt) {
+  if (p0.bits < 2 || p0.bits > 6 || (p1 && p1->bits != p0.bits)) return false;
+  if (xdt == MOE_F32 || p0.sb_dtype == MOE_F32 || !x_aligned) return false;
+  return ((size_t)p0.n + 64) * ((size_t)p0.k * p0.bits / 8) < (1ull << 31);
+}
+
+// gemv_multi_kernel applies: 16-bit activations at 16-byte aligned rows, at
+// most 4 units per lane, a pass of tm rows in 64 KB of LDS, expert-local byte
+// offsets below 2^31.
+bool multi_ok(const moe_qproj& p0, bool x_aligned, int xdt, int tm) {
+  if (xdt == MOE_F32 || p0.sb_dtype == MOE_F32 || !x_aligned) return false;
+  const int CU = p0.k / 32;
+  const int L = 1 << pick_lg_dec1(CU, group_shift(p0.group_size));
+  if ((CU + L - 1) / L > 4) return false;
+  if ((size_t)tm * CU * 68 > 65536) return false;
+  return ((size_t)p0.n + 256) * ((size_t)p0.k * p0.bits / 8) < (1ull << 31);
+}
+
+// Rows per pass of gemv_multi_kernel: 4 when no expert, or the average used
+// expert, has more (fewer accumulators: three blocks per CU instead of two;
+// the few experts above the average take a second pass), else 8.
+int multi_rows_per_pass(int max_rows, int rows, int slots) {
+  return (max_rows <= 4 || (long)rows / std::max(1, slots) <= 4) ? 4 : 8;
+}
+
+// The GEMV kernel run_gemv takes for M rows over `slots` used experts.
+enum GemvKind { kGemvGrouped = 0, kGemvMulti = 1, kGemvMma = 2 };
+GemvKind gemv_kind(const moe_qproj& p0, const moe_qproj* p1, bool x_aligned, int xdt, int slots,
+                   int M, bool single, int max_rows) {
+  if (single) return kGemvGrouped;
+  // the matrix cores once the used experts average enough rows: below that
+  // the K-chunk pipeline's latency outweighs the VALU it saves
+  const int min_rows = slots <= 1 ? kMmaMinRowsSingleExpert
+                                  : (p0.bits == 4 ? kMmaMinRows : kMmaMinRowsOther);
+  if ((long)M >= (long)min_rows * std::max(1, slots) && mma_ok(p0, p1, x_aligned, xdt))
+    return kGemvMma;
+  const int tm = multi_rows_per_pass(std::min(max_rows, M), M, slots);
+  if (multi_ok(p0, x_aligned, xdt, tm)) return kGemvMulti;
+  return kGemvGrouped;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 // gemv_multi_kernel for a few rows per expert (16-bit activations):
 // kMultiRows weight rows per lane, lanes per row as for the one-token
 // kernels, up to 4 or 8 activation rows per pass (rows in all, max_rows at
 // most for one expert), activation units staged in at most 64 KB of LDS.
-// Returns false where the older grouped kernel has to run instead.
-bool run_multi(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
+// The caller has checked multi_ok.
+void run_multi(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
                const uint32_t* perm, int topk, const uint32_t* offsets, const uint32_t* used,
                int slots, int max_rows, void* out, int act, float alpha, float limit,
                hipStream_t st, KEvents ev, moe_status* status, int rows) {
-  if (xdt == MOE_F32 || p0.sb_dtype == MOE_F32) return false;
-  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0) return false;  // 16-byte activation loads
   const int gsh = group_shift(p0.group_size);
   const int CU = p0.k / 32;
   const int lg = pick_lg_dec1(CU, gsh);
   const int L = 1 << lg, ur = (CU + L - 1) / L;
-  if (ur > 4) return false;
-  // rows per pass: 4 when no expert, or the average used expert, has more
-  // (fewer accumulators: three blocks per CU instead of two; the few
-  // experts above the average take a second pass), else 8
-  const int tm = (max_rows <= 4 || (long)rows / std::max(1, slots) <= 4) ? 4 : 8;
+  const int tm = multi_rows_per_pass(max_rows, rows, slots);
   const size_t smem = (size_t)tm * CU * 68;
-  if (smem > 65536) return false;
-  // expert-local byte offsets stay below 2^31 (with a row block of slack)
-  if (((size_t)p0.n + 256) * ((size_t)p0.k * p0.bits / 8) >= (1ull << 31)) return false;
   // R1 rows per iteration; up to kMultiIters iterations per block, fewer
   // while that leaves under kMultiBlocks blocks for the used experts
   const int SG = 64 >> lg, R1 = 4 * SG * kMultiRows(p1 != nullptr);
@@ -520,29 +622,15 @@ bool run_multi(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
   const hipError_t err = launch_multi(p0.bits, xdt, p0.sb_dtype, p1 != nullptr, ur, tm, a,
                                      slots * row_blocks, smem, st, ev);
   *status = hip_check(err, "grouped GEMV launch");
-  return true;
 }
 
-// Rows per used expert from which the batched GEMV runs on the matrix cores
-// (Qwen3 shape, 4 per expert: 192 -> 154 us per layer step; GPT-OSS, 8 per
-// expert: 409 -> 208 us; at 1-2 per expert gemv_multi_kernel is faster).
-// Codes of other widths cost gemv_multi_kernel more unpacking, so they move
-// from 2 rows per expert (mixed 3/6-bit layer, 64 tokens: 317 -> 231 us).
-constexpr int kMmaMinRows = 4;
-constexpr int kMmaMinRowsOther = 2;
-
-// gemv_mma_kernel (matrix cores) for 2- to 6-bit weights (codes exact with
-// the magic offset in either 16-bit type) and 16-bit activations: 32 rows of
-// a gate/up pair or 64 rows of one projection per block, 16 activation rows
-// per pass. Returns false where it does not apply.
-bool run_mma(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
+// gemv_mma_kernel (matrix cores) for 2- to 6-bit weights and 16-bit
+// activations: 32 rows of a gate/up pair or 64 rows of one projection per
+// block, 16 activation rows per pass. The caller has checked mma_ok.
+void run_mma(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
              const uint32_t* perm, int topk, const uint32_t* offsets, const uint32_t* used, int slots,
              void* out, int act, float alpha, float limit, hipStream_t st, KEvents ev,
              moe_status* status) {
-  if (p0.bits < 2 || p0.bits > 6 || (p1 && p1->bits != p0.bits)) return false;
-  if (xdt == MOE_F32 || p0.sb_dtype == MOE_F32) return false;
-  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0) return false;  // 16-byte activation loads
-  if (((size_t)p0.n + 64) * ((size_t)p0.k * p0.bits / 8) >= (1ull << 31)) return false;
   const int rows_per_block = p1 ? 32 : 64;
   const int row_blocks = (p0.n + rows_per_block - 1) / rows_per_block;
   GemvArgs a{};
@@ -564,7 +652,6 @@ bool run_mma(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
   a.limit = limit;
   *status = hip_check(launch_mma(p0.bits, xdt, p0.sb_dtype, p1 != nullptr, a, slots * row_blocks, st, ev),
                       "grouped GEMV launch");
-  return true;
 }
 
 // out[p] = W[e(p)] . a[row(p)] over a plan; optionally a gate/up pair with
@@ -574,18 +661,18 @@ moe_status run_gemv(const moe_qproj& p0, const moe_qproj* p1, const void* x, int
                     const uint32_t* perm, int topk, const uint32_t* offsets, const uint32_t* used,
                     int slots, int M, bool single, void* out, int act, float alpha, float limit,
                     hipStream_t st, KEvents ev = {}, int max_rows = 1 << 30) {
-  if (!single) {
+  const GemvKind kind = gemv_kind(p0, p1, aligned16(x), xdt, slots, M, single, max_rows);
+  if (kind == kGemvMma) {
     moe_status status = MOE_OK;
-    // the matrix cores once the used experts average kMmaMinRows rows: below
-    // that the K-chunk pipeline's latency outweighs the VALU it saves
-    const int min_rows = p0.bits == 4 ? kMmaMinRows : kMmaMinRowsOther;
-    if ((long)M >= (long)min_rows * std::max(1, slots) &&
-        run_mma(p0, p1, x, xdt, perm, topk, offsets, used, slots, out, act, alpha, limit, st, ev,
-                &status))
-      return status;
-    if (run_multi(p0, p1, x, xdt, perm, topk, offsets, used, slots, std::min(max_rows, M), out,
-                  act, alpha, limit, st, ev, &status, M))
-      return status;
+    run_mma(p0, p1, x, xdt, perm, topk, offsets, used, slots, out, act, alpha, limit, st, ev,
+            &status);
+    return status;
+  }
+  if (kind == kGemvMulti) {
+    moe_status status = MOE_OK;
+    run_multi(p0, p1, x, xdt, perm, topk, offsets, used, slots, std::min(max_rows, M), out, act,
+              alpha, limit, st, ev, &status, M);
+    return status;
   }
   const int gsh = group_shift(p0.group_size);
   GemvGeom g = gemv_geom(p0.n, p0.k, gsh, slots, single, M, xdt);
@@ -715,6 +802,19 @@ extern "C" moe_status moe_router_logits(const void* x, int32_t x_dtype, int32_t 
   MOE_HIP(launch_router_logits(x, x_dtype, T, hidden, weight, w_dtype, bias, n_experts, logits,
                                stream),
           "router logits launch");
+  return ok();
+}
+
+extern "C" moe_status moe_router_logits_q(const void* x, int32_t x_dtype, int32_t T,
+                                          int32_t hidden, const moe_qproj* w, const void* bias,
+                                          int32_t n_experts, void* logits, hipStream_t stream) {
+  if (!x || !w || !logits) return fail(MOE_ERR_INVALID, "router_logits_q: NULL pointer");
+  if (T <= 0 || hidden <= 0 || n_experts <= 0)
+    return fail(MOE_ERR_INVALID, "router_logits_q: T, hidden and n_experts must be positive");
+  MOE_TRY(validate_router_q(w, n_experts, hidden, x_dtype, "router_logits_q"));
+  MOE_HIP(launch_router_q(w->bits, x, x_dtype, T, hidden, to_proj(*w), w->sb_dtype,
+                          group_shift(w->group_size), bias, n_experts, logits, stream),
+          "quantised router launch");
   return ok();
 }
 
@@ -926,51 +1026,84 @@ moe_status copy_trace(const moe_layer_desc* d, int T, void* ws, const Workspace&
 // Work that may overlap the routed experts (the shared expert: it reads the
 // layer input only and writes its own workspace regions) runs on a side
 // stream: forked from the caller's stream, joined back before the combine
-// that reads its output. One non-blocking, default-priority stream and two
-// events per device, created on first use and kept for the process
-// lifetime; each call's fork-to-join enqueue holds a lock, so calls from
-// several host threads never interleave the shared events. Under stream
-// capture the fork and join become graph edges. Without a side stream (its
-// creation failed, or the first such call on the device is being captured)
-// the work stays on the caller's stream, in order.
+// that reads its output. Each device keeps a small pool of non-blocking,
+// default-priority side streams (each with two events), created on first use
+// outside any capture and kept for the process lifetime. A side stream that
+// joins a stream capture stays part of that capture until the capture ends,
+// so a call takes a pooled stream only if it is not being captured, or is
+// being captured by the caller's own capture (same capture id): an eager call
+// and a capture, or two captures, never share one. Each call holds its side
+// stream's lock from fork to join, so calls from several host threads never
+// interleave its events. Under stream capture the fork and join become graph
+// edges. Without a usable side stream (none idle and the caller is being
+// captured, or creation failed) the work stays on the caller's stream, in
+// order.
 class SideFork {
  public:
   SideFork(bool want, hipStream_t st) : st_(st), side_(st) {
     if (!want) return;
     int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
       (void)hipGetLastError();
       return;
     }
-    lock_ = std::unique_lock<std::mutex>(mu());
-    Slot& t = table()[dev];
-    if (!t.s) {
-      // never create the stream and events inside a stream capture: that
-      // call keeps its work in order on the caller's stream
-      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-      if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-        (void)hipGetLastError();
-        lock_.unlock();
-        return;
-      }
-      hipStream_t s = nullptr;
-      hipEvent_t f = nullptr, j = nullptr;
-      if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess ||
-          hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
-          hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
-        (void)hipGetLastError();
-        if (j) (void)hipEventDestroy(j);
-        if (f) (void)hipEventDestroy(f);
-        if (s) (void)hipStreamDestroy(s);
-        lock_.unlock();
-        return;
-      }
-      t = Slot{s, f, j};
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    unsigned long long cid = 0;
+    if (hipStreamGetCaptureInfo(st, &cs, &cid) != hipSuccess) {
+      (void)hipGetLastError();
+      return;
     }
-    slot_ = &t;
-    status_ = hip_check(hipEventRecord(t.fork, st), "side stream fork");
-    if (status_ == MOE_OK) status_ = hip_check(hipStreamWaitEvent(t.s, t.fork, 0), "side stream fork");
-    if (status_ == MOE_OK) side_ = t.s;
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    Slot* t = nullptr;
+    {
+      std::lock_guard<std::mutex> g(pool_mu());
+      std::vector<Slot*>& pool = pools()[dev];
+      for (Slot* c : pool) {
+        std::unique_lock<std::mutex> l(c->mu, std::try_to_lock);
+        if (!l.owns_lock()) continue;  // another call holds it
+        hipStreamCaptureStatus xs = hipStreamCaptureStatusNone;
+        unsigned long long xid = 0;
+        if (hipStreamGetCaptureInfo(c->s, &xs, &xid) != hipSuccess) {
+          (void)hipGetLastError();
+          continue;
+        }
+        const bool usable = xs == hipStreamCaptureStatusNone ||
+                            (capturing && xs == hipStreamCaptureStatusActive && xid == cid);
+        if (!usable) continue;
+        lock_ = std::move(l);
+        t = c;
+        break;
+      }
+      // a new side stream, never inside a capture (that call stays in order)
+      if (!t && !capturing && pool.size() < kMaxPool) {
+        hipStream_t s = nullptr;
+        hipEvent_t f = nullptr, j = nullptr;
+        if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
+          (void)hipGetLastError();
+          if (j) (void)hipEventDestroy(j);
+          if (f) (void)hipEventDestroy(f);
+          if (s) (void)hipStreamDestroy(s);
+        } else {
+          Slot* c = new (std::nothrow) Slot{s, f, j, {}};
+          if (!c) {
+            (void)hipEventDestroy(j);
+            (void)hipEventDestroy(f);
+            (void)hipStreamDestroy(s);
+          } else {
+            pool.push_back(c);
+            lock_ = std::unique_lock<std::mutex>(c->mu);
+            t = c;
+          }
+        }
+      }
+    }
+    if (!t) return;
+    slot_ = t;
+    status_ = hip_check(hipEventRecord(t->fork, st), "side stream fork");
+    if (status_ == MOE_OK) status_ = hip_check(hipStreamWaitEvent(t->s, t->fork, 0), "side stream fork");
+    if (status_ == MOE_OK) side_ = t->s;
   }
   moe_status status() const { return status_; }
   hipStream_t stream() const { return side_; }
@@ -989,18 +1122,20 @@ class SideFork {
   }
 
  private:
-  static constexpr int kMaxDev = 64;
+  static constexpr size_t kMaxPool = 8;  // side streams per device
   struct Slot {
     hipStream_t s;
     hipEvent_t fork, join;
+    std::mutex mu;
   };
-  static std::mutex& mu() {
+  static std::mutex& pool_mu() {
     static std::mutex m;
     return m;
   }
-  static Slot* table() {
-    static Slot t[kMaxDev] = {};
-    return t;
+  // never destroyed: the side streams live until the process ends
+  static std::map<int, std::vector<Slot*>>& pools() {
+    static std::map<int, std::vector<Slot*>>* m = new std::map<int, std::vector<Slot*>>();
+    return *m;
   }
   hipStream_t st_, side_;
   Slot* slot_ = nullptr;
@@ -1014,7 +1149,7 @@ moe_status shared_expert(const moe_layer_desc* d, const void* x, int T, void* ws
   if (!d->has_shared) return MOE_OK;
   const int xdt = d->act_dtype;
   const bool single = (T == 1);
-  *smode = d->shared_gate_weight ? 2 : 1;
+  *smode = (d->shared_gate_weight || d->shared_gate_q.weight) ? 2 : 1;
   MOE_HIP(launch_identity_plan(at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), T, st),
           "identity plan launch");
   const bool gated = d->activation != MOE_ACT_RELU2;
@@ -1039,7 +1174,12 @@ moe_status shared_expert(const moe_layer_desc* d, const void* x, int T, void* ws
                      at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), 1, T, single,
                      at<void>(ws, w.s_out), 0, 0.f, 0.f, st));
   }
-  if (d->shared_gate_weight)
+  if (d->shared_gate_q.weight)
+    MOE_HIP(launch_router_q(d->shared_gate_q.bits, x, xdt, T, d->hidden, to_proj(d->shared_gate_q),
+                            d->shared_gate_q.sb_dtype, group_shift(d->shared_gate_q.group_size),
+                            nullptr, 1, at<void>(ws, w.s_logit), st),
+            "shared gate launch");
+  else if (d->shared_gate_weight)
     MOE_HIP(launch_router_logits(x, xdt, T, d->hidden, d->shared_gate_weight, d->router_dtype,
                                  nullptr, 1, at<void>(ws, w.s_logit), st),
             "shared gate launch");
@@ -1139,9 +1279,11 @@ struct DecoderStep {
 
 // rx: the router's input rows (x for every family but Gemma 4). With `step`,
 // x and rx are ignored: both read the normalised rows.
+// allow_side: the shared expert may fork onto a side stream (created on a
+// stream's first such call); false keeps every launch on `st`.
 moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx, int T, void* y,
                          void* ws, size_t ws_bytes, const moe_layer_trace* tr, hipStream_t st,
-                         const DecoderStep* step = nullptr) {
+                         const DecoderStep* step = nullptr, bool allow_side = true) {
   MOE_TRY(validate_layer_impl(d));
   if (step) {
     if (!step->h || !step->m || !step->nw)
@@ -1178,7 +1320,8 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     void* xn = at<void>(ws, w.xn);
     void* rs = step->res_out ? step->res_out : at<void>(ws, w.res);
     res = rs;
-    if (T == 1 && launch_router_logits_norm(step->h, step->m, step->nw, step->eps, xdt, H,
+    if (T == 1 && !d->router_q.weight &&
+        launch_router_logits_norm(step->h, step->m, step->nw, step->eps, xdt, H,
                                             d->router_weight, d->router_dtype, d->router_bias, E,
                                             at<void>(ws, w.logits), rs, xn, st) == hipSuccess) {
       logits_done = true;
@@ -1193,6 +1336,11 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
   // 1. router projection (MoELayer.swift:540 / 689-690)
   if (logits_done) {
     // done above
+  } else if (d->router_q.weight) {
+    const moe_qproj& q = d->router_q;
+    MOE_HIP(launch_router_q(q.bits, rx, xdt, T, H, to_proj(q), q.sb_dtype, group_shift(q.group_size),
+                            d->router_bias, E, at<void>(ws, w.logits), st),
+            "quantised router launch");
   } else if (router_gemm_ok(d, T)) {
     MOE_TRY(run_router_gemm(d, rx, T, at<void>(ws, w.logits), at<uint32_t>(ws, w.r_plan),
                             at<uint32_t>(ws, w.r_tiles), st));
@@ -1208,7 +1356,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
   // experts (MoELayer.swift:620-624: it only joins at the combine); a small
   // one stays in order (the fork and join cost a one-token NemotronH-shaped
   // layer 3.5 us more than they saved)
-  SideFork side(d->has_shared && T >= kGemmMinRows, st);
+  SideFork side(allow_side && d->has_shared && T >= kGemmMinRows, st);
   MOE_TRY(side.status());
   MOE_TRY(shared_expert(d, x, T, ws, w, side.stream(), &smode));
   MOE_TRY(side.mark());
@@ -1308,7 +1456,60 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
   return MOE_OK;
 }
 
+// The kernels layer_forward runs for T rows (the same predicates it uses).
+moe_layer_paths layer_paths(const moe_layer_desc* d, int T, bool x_aligned) {
+  moe_layer_paths p{};
+  const int E = d->n_experts, k = d->top_k, M = T * k, xdt = d->act_dtype;
+  const bool gated = d->activation != MOE_ACT_RELU2;
+  auto gk = [](GemvKind kd) { return (int32_t)(kd == kGemvMma ? MOE_PATH_GEMV_MMA : MOE_PATH_GEMV); };
+  const moe_qproj& p0 = gated ? d->gate : d->up;
+  const moe_qproj* p1 = gated ? &d->up : nullptr;
+  if (T == 1 && dec1_supported(d)) {
+    p.gate_up = p.down = MOE_PATH_DECODE1;
+  } else if (gemm_ok(p0, xdt, M) && gemm_ok(d->down, xdt, M)) {
+    p.gate_up = p.down = MOE_PATH_GEMM;
+  } else {
+    const int slots = std::min(E, M);
+    p.gate_up = gk(gemv_kind(p0, p1, x_aligned, xdt, slots, M, T == 1, T));
+    p.down = gk(gemv_kind(d->down, nullptr, true, xdt, slots, M, T == 1, T));
+  }
+  if (d->has_shared) {
+    const moe_qproj& s0 = gated ? d->shared_gate : d->shared_up;
+    const moe_qproj* s1 = gated ? &d->shared_up : nullptr;
+    if (gemm_ok(s0, xdt, T) && gemm_ok(d->shared_down, xdt, T)) {
+      p.shared_gate_up = p.shared_down = MOE_PATH_GEMM;
+    } else {
+      p.shared_gate_up = gk(gemv_kind(s0, s1, x_aligned, xdt, 1, T, T == 1, 1 << 30));
+      p.shared_down = gk(gemv_kind(d->shared_down, nullptr, true, xdt, 1, T, T == 1, 1 << 30));
+    }
+  }
+  return p;
+}
+
 }  // namespace
+
+namespace moe {
+// moe_layer_forward with every launch on `stream` (no side stream is created)
+// and the workspace given by the caller; for allocation-free callers.
+moe_status layer_forward_in_order(const moe_layer_desc* d, const void* x, int32_t T, void* y,
+                                  void* ws, size_t ws_bytes, const moe_layer_trace* tr,
+                                  hipStream_t st) {
+  MOE_TRY(layer_forward(d, x, x, T, y, ws, ws_bytes, tr, st, nullptr, false));
+  return ok();
+}
+size_t layer_workspace_bytes(const moe_layer_desc* d, int32_t T) {
+  if (!d || T <= 0 || validate_layer_impl(d) != MOE_OK) return 0;
+  return layout(d, T).total;
+}
+}  // namespace moe
+
+extern "C" moe_status moe_layer_path(const moe_layer_desc* d, int32_t T, moe_layer_paths* out) {
+  MOE_TRY(validate_layer_impl(d));
+  if (!out) return fail(MOE_ERR_INVALID, "moe_layer_path: out is NULL");
+  if (T <= 0) return fail(MOE_ERR_INVALID, "MoELayer.decodeMany: T must be positive");
+  *out = layer_paths(d, T, true);
+  return ok();
+}
 
 extern "C" moe_status moe_layer_forward(const moe_layer_desc* d, const void* x, int32_t T, void* y,
                                         void* workspace, size_t workspace_bytes,
@@ -1372,14 +1573,27 @@ struct moe_layer {
   size_t ws_bytes = 0;
   int ws_tokens = 0;
 
-  moe_status reserve(int T) {
+  // Grows the scratch to T rows. Growing waits for the whole device (a
+  // previous call may still read the old scratch on any stream) and
+  // allocates, so it is refused while `st` is being captured: a handle that
+  // is captured must have run once, eagerly, at its largest T.
+  moe_status reserve(int T, hipStream_t st) {
     if (T <= ws_tokens) return MOE_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    MOE_HIP(hipStreamIsCapturing(st, &cs), "MoELayer scratch resize");
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(MOE_ERR_WORKSPACE,
+                  "MoELayer: scratch for T=%d (reserved for %d) cannot grow under stream capture; "
+                  "run the handle once at its largest T before capturing",
+                  T, ws_tokens);
     const size_t need = moe_layer_workspace_bytes(&desc, T);
     if (ws) {
-      // A previous call may still be reading the old scratch on its stream.
       MOE_HIP(hipDeviceSynchronize(), "MoELayer scratch resize");
-      MOE_HIP(hipFree(ws), "MoELayer scratch free");
+      const hipError_t e = hipFree(ws);
       ws = nullptr;
+      ws_bytes = 0;
+      ws_tokens = 0;
+      MOE_HIP(e, "MoELayer scratch free");
     }
     MOE_HIP(hipMalloc(&ws, need), "MoELayer scratch allocation");
     ws_bytes = need;
@@ -1389,7 +1603,7 @@ struct moe_layer {
 
   moe_status decode_many(const void* h, int T, void* out, hipStream_t st) {
     if (T <= 0) return fail(MOE_ERR_INVALID, "MoELayer.decodeMany: T must be positive");
-    MOE_TRY(reserve(T));
+    MOE_TRY(reserve(T, st));
     return layer_forward(&desc, h, h, T, out, ws, ws_bytes, nullptr, st);
   }
 };

@@ -132,6 +132,13 @@ hipError_t launch_router_logits_norm(const void* h, const void* m, const void* n
                                      int E, void* logits, void* res_out, void* xn_out,
                                      hipStream_t st);
 
+// Router logits with an affine-quantised weight W (one stacked projection
+// [1, E, H], codes of `bits`, scales in sbdt, log2(group size / 32) = gsh):
+// 16-bit x / bias / logits of type xdt, H % 32 == 0, H <= 8192.
+hipError_t launch_router_q(int bits, const void* x, int xdt, int T, int H, const GemvProj& W,
+                           int sbdt, int gsh, const void* bias, int E, void* logits,
+                           hipStream_t st);
+
 // ------------------------------------------------------------- dispatch --
 // Writes counts, offsets, perm, inv_perm and the used-expert list.
 // launch_router_topk + launch_dispatch_plan in one workgroup for T <= 8

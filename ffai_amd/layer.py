@@ -100,9 +100,13 @@ class StackedExperts:
 class MoELayer:
     """MoE feed-forward layer (router -> dispatch -> grouped expert products
     -> combine [+ shared expert]) on one GPU. With MOE_ACT_RELU2 the experts
-    have no gate projection: pass gate=None (and None as the shared gate)."""
+    have no gate projection: pass gate=None (and None as the shared gate).
+    The router weight and the shared expert's sigmoid gate are either dense
+    tensors ([E, hidden], [1, hidden]) or, as loadLinear returns them for a
+    quantised checkpoint (Layers.swift:371-400), one-expert StackedExperts
+    ([1, E, hidden], [1, 1, hidden])."""
 
-    def __init__(self, *, router_weight: torch.Tensor, router: MoERouter,
+    def __init__(self, *, router_weight, router: MoERouter,
                  gate: Optional[StackedExperts], up: StackedExperts, down: StackedExperts,
                  hidden: int, act_dtype: torch.dtype,
                  router_bias: Optional[torch.Tensor] = None,
@@ -122,8 +126,12 @@ class MoELayer:
         d.hidden, d.n_experts, d.top_k = self.hidden, self.router.nExperts, self.router.topK
         d.intermediate = self.up.n
         d.act_dtype = moe_dtype(self.act_dtype)
-        d.router_weight = self.router_weight.data_ptr()
-        d.router_dtype = moe_dtype(self.router_weight.dtype)
+        if isinstance(self.router_weight, StackedExperts):
+            d.router_q = self.router_weight.struct()
+            d.router_dtype = d.act_dtype
+        else:
+            d.router_weight = self.router_weight.data_ptr()
+            d.router_dtype = moe_dtype(self.router_weight.dtype)
         d.router_bias = None if self.router_bias is None else self.router_bias.data_ptr()
         d.gating, d.norm_topk_prob = self.router.gatingMode, int(bool(self.router.normTopKProb))
         d.expert_bias = None if self.router.expertBias is None else self.router.expertBias.data_ptr()
@@ -134,8 +142,11 @@ class MoELayer:
             d.has_shared = 1
             d.shared_gate, d.shared_up, d.shared_down = (
                 QProj() if p is None else p.struct() for p in self.shared)
-            d.shared_gate_weight = (None if self.shared_gate_weight is None
-                                    else self.shared_gate_weight.data_ptr())
+            sgw = self.shared_gate_weight
+            if isinstance(sgw, StackedExperts):
+                d.shared_gate_q = sgw.struct()
+            else:
+                d.shared_gate_weight = None if sgw is None else sgw.data_ptr()
         r = self.router
         d.logit_scale, d.routed_scale = r.logitScale, r.routedScale
         d.expert_scale = None if r.expertScale is None else r.expertScale.data_ptr()
@@ -145,13 +156,82 @@ class MoELayer:
     def desc(self) -> LayerDesc:
         return self._desc
 
+    @property
+    def device(self) -> torch.device:
+        return self.up.weight.device
+
+    def parameters(self):
+        """(name, tensor) pairs in the order and with the names of
+        MoELayer.parameters() (MoELayer.swift:500-522): the router, then each
+        expert's projections as views of the stacked tensors, then the
+        shared expert; plus the sigmoid gate of the shared expert under its
+        checkpoint name (Qwen3xText.swift:660-661)."""
+        out = []
+
+        def linear(prefix, w):  # a dense weight or a one-expert quantised stack
+            if isinstance(w, StackedExperts):
+                return [(f"{prefix}.weight", w.weight[0]), (f"{prefix}.scales", w.scales[0]),
+                        (f"{prefix}.biases", w.biases[0])]
+            return [(f"{prefix}.weight", w)]
+
+        out += linear("gate", self.router_weight)
+        if self.router_bias is not None:
+            out.append(("gate.bias", self.router_bias))
+
+        def proj(prefix, p):
+            if p is None:
+                return []
+            items = [(f"{prefix}.weight", p.weight), (f"{prefix}.scales", p.scales),
+                     (f"{prefix}.biases", p.biases)]
+            if p.out_bias is not None:
+                items.append((f"{prefix}.bias", p.out_bias))
+            return items
+
+        for name, p in (("gate_proj", self.gate), ("up_proj", self.up), ("down_proj", self.down)):
+            if p is None:
+                continue
+            for e in range(p.n_experts):
+                for n, t in proj(f"experts.{e}.{name}", p):
+                    out.append((n, t[e]))
+        if self.shared is not None:
+            for name, p in zip(("gate_proj", "up_proj", "down_proj"), self.shared):
+                if p is not None:
+                    out += [(n, t[0]) for n, t in proj(f"shared_expert.{name}", p)]
+            if self.shared_gate_weight is not None:
+                out += linear("shared_expert_gate", self.shared_gate_weight)
+        return out
+
+    def paths(self, T: int) -> dict:
+        """The kernels a call of T rows runs per stage (moe_layer_path):
+        'decode1', 'gemv', 'gemv_mma', 'gemm' or 'none'."""
+        p = _lib.LayerPaths()
+        check(_lib.load().moe_layer_path(C.byref(self._desc), T, C.byref(p)))
+        return p.names()
+
+    def _check_rows(self, name: str, t: Optional[torch.Tensor], T: Optional[int] = None):
+        """Rows handed to the C ABI: [T, hidden], the layer's activation dtype,
+        contiguous, on the layer's device (the kernels read and write them
+        through raw pointers)."""
+        if t is None:
+            return
+        dev = self.device
+        if t.dim() != 2 or t.shape[1] != self.hidden or (T is not None and t.shape[0] != T):
+            want = f"[{'T' if T is None else T}, {self.hidden}]"
+            raise ValueError(f"MoELayer: {name} must be {want}, got {list(t.shape)}")
+        if t.dtype != self.act_dtype:
+            raise ValueError(f"MoELayer: {name} dtype {t.dtype} is not the layer's {self.act_dtype}")
+        if not t.is_contiguous():
+            raise ValueError(f"MoELayer: {name} must be contiguous")
+        if t.device != dev:
+            raise ValueError(f"MoELayer: {name} is on {t.device}, the layer on {dev}")
+
     def workspace_bytes(self, T: int) -> int:
         return _lib.load().moe_layer_workspace_bytes(C.byref(self._desc), T)
 
     def workspace(self, T: int) -> torch.Tensor:
         need = self.workspace_bytes(T)
         if self._ws is None or self._ws.numel() < need:
-            self._ws = torch.empty(need, dtype=torch.uint8, device=self.router_weight.device)
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
         return self._ws
 
     def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, trace: bool = False,
@@ -160,11 +240,14 @@ class MoELayer:
         the router's input, for Gemma 4 whose router and experts read
         differently normalised rows. With trace=True also returns the
         routing (logits, topk_idx, topk_weight, perm, offsets)."""
-        if router_x is not None and (router_x.shape != x.shape or router_x.dtype != x.dtype):
-            raise ValueError("MoELayer: router_x must match x in shape and dtype")
+        self._check_rows("x", x)
         T = x.shape[0]
+        if T <= 0:
+            raise ValueError("MoELayer.decodeMany: T must be positive")
+        self._check_rows("router_x", router_x, T)
         if out is None:
             out = torch.empty_like(x)
+        self._check_rows("out", out, T)
         ws = self.workspace(T)
         tr = None
         tensors = None
@@ -191,11 +274,20 @@ class MoELayer:
         """The block between the decoder steps (Qwen3xText.swift:2640-2670,
         1015-1035): r = h + mixer_out, y = r + MoE(rmsnorm(r) * norm_weight).
         Returns y; residual_out (optional) receives r."""
-        if mixer_out.shape != h.shape or norm_weight.numel() != self.hidden:
-            raise ValueError("MoELayer.forward_residual: shape mismatch")
+        self._check_rows("h", h)
         T = h.shape[0]
+        if T <= 0:
+            raise ValueError("MoELayer.decodeMany: T must be positive")
+        self._check_rows("mixer_out", mixer_out, T)
+        if (norm_weight.dim() != 1 or norm_weight.numel() != self.hidden
+                or norm_weight.dtype != self.act_dtype or not norm_weight.is_contiguous()
+                or norm_weight.device != h.device):
+            raise ValueError("MoELayer.forward_residual: norm_weight must be a contiguous "
+                             f"[{self.hidden}] vector of the layer's dtype on its device")
         if out is None:
             out = torch.empty_like(h)
+        self._check_rows("out", out, T)
+        self._check_rows("residual_out", residual_out, T)
         ws = self.workspace(T)
         check(_lib.load().moe_layer_forward_residual(
             C.byref(self._desc), _ptr(h), _ptr(mixer_out), _ptr(norm_weight), float(eps), T,

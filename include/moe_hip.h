@@ -133,6 +133,17 @@ typedef struct moe_layer_desc {
                                       weight * expert_scale[e] (Gemma 4
                                       per_expert_scale,
                                       Gemma4Text.swift:945-950) */
+    /* Affine-quantised router and shared-expert gate: the mlx
+     * QuantizedLinear that loadLinear returns for a quantised checkpoint
+     * (Layers.swift:371-400; Qwen3xText.swift:605-606, 660-661). When
+     * router_q.weight is non-NULL the router projection is this one-expert
+     * stack [1, n_experts, hidden] (n = n_experts, k = hidden, n_experts =
+     * 1, out_bias NULL) and router_weight must be NULL; router_bias still
+     * applies. Likewise shared_gate_q ([1, 1, hidden]) replaces
+     * shared_gate_weight. Dequantised inside the router kernels (the weights
+     * are never rounded); 16-bit activations only. */
+    moe_qproj router_q;
+    moe_qproj shared_gate_q;
 } moe_layer_desc;
 
 /* Optional device outputs of a layer call, for callers and tests that need
@@ -176,6 +187,14 @@ moe_status moe_derive_bits(int64_t packed_cols, int64_t scale_cols,
 moe_status moe_router_logits(const void* x, int32_t x_dtype, int32_t T, int32_t hidden,
                              const void* weight, int32_t w_dtype, const void* bias,
                              int32_t n_experts, void* logits, hipStream_t stream);
+
+/* moe_router_logits with an affine-quantised weight (QuantizedLinear,
+ * Layers.swift:371-400): w is a one-expert stack [1, n_experts, hidden]
+ * (w->n = n_experts, w->k = hidden, w->n_experts = 1). x, bias and logits
+ * in x_dtype (f16 or bf16). */
+moe_status moe_router_logits_q(const void* x, int32_t x_dtype, int32_t T, int32_t hidden,
+                               const moe_qproj* w, const void* bias, int32_t n_experts,
+                               void* logits, hipStream_t stream);
 
 /* MoERouter.route on the GPU for every token row: Ops.moeRouterTopKMany
  * (Ops.swift:2589-2662) generalised to all gating modes of
@@ -303,6 +322,23 @@ moe_status moe_layer_forward_residual(const moe_layer_desc* d, const void* h,
                                       int32_t T, void* y, void* residual_out, void* workspace,
                                       size_t workspace_bytes, const moe_layer_trace* trace,
                                       hipStream_t stream);
+
+/* The kernels a layer call of T rows runs, per stage, for 16-byte aligned
+ * activation rows. No reference counterpart: the reference picks its tile
+ * kernels internally (MoELayer.swift:855-882); callers and tests use this
+ * to know which kernel a configuration exercises. 0 = stage absent. */
+typedef enum moe_path {
+    MOE_PATH_NONE = 0,
+    MOE_PATH_DECODE1 = 1,   /* one token: gate/up with in-kernel routing,
+                               fused down + combine */
+    MOE_PATH_GEMV = 2,      /* HBM-streaming grouped GEMV (VALU dot2) */
+    MOE_PATH_GEMV_MMA = 3,  /* batched grouped GEMV on the matrix cores */
+    MOE_PATH_GEMM = 4       /* grouped GEMM on the matrix cores */
+} moe_path;
+typedef struct moe_layer_paths {
+    int32_t gate_up, down, shared_gate_up, shared_down; /* moe_path */
+} moe_layer_paths;
+moe_status moe_layer_path(const moe_layer_desc* d, int32_t T, moe_layer_paths* out);
 
 /* ---- MoELayer handle (owns its workspace like the reference instance) -- */
 typedef struct moe_layer* moe_layer_t;

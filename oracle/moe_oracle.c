@@ -256,6 +256,46 @@ void or_router_logits(const void* x, int x_dt, int T, int H,
     free(wr);
 }
 
+/* Dequantised row r of a stacked projection: w = s * q + b in fp32
+ * (QuantizedOps.swift:33-45), the form or_qgemm_rows multiplies. */
+static void dequant_row(const or_qproj* p, size_t r, float* wrow) {
+    int K = p->k, gs = p->group_size, bits = p->bits, groups = K / gs;
+    const uint32_t* wr = p->weight + r * ((size_t)K * bits / 32);
+    for (int g = 0; g < groups; g++) {
+        float s = load1(p->scales, p->sb_dt, r * groups + g);
+        float b = load1(p->biases, p->sb_dt, r * groups + g);
+        for (int j = 0; j < gs; j++) {
+            float q = (float)get_code(wr, bits, (size_t)g * gs + j);
+            float sq = s * q;
+            wrow[g * gs + j] = sq + b;
+        }
+    }
+}
+
+int or_router_logits_q(const void* x, int x_dt, int T, int H, const or_qproj* W,
+                       const void* bias, int E, float* logits) {
+    if (!W || !bits_ok(W->bits) || W->k != H || W->n != E || W->group_size <= 0 ||
+        H % W->group_size || ((long)H * W->bits) % 32)
+        return -1;
+    float* xr = (float*)malloc(sizeof(float) * (size_t)H);
+    float* wr = (float*)malloc(sizeof(float) * (size_t)H * (size_t)E);
+    for (int e = 0; e < E; e++) dequant_row(W, (size_t)e, wr + (size_t)e * H);
+    for (int t = 0; t < T; t++) {
+        or_load((const char*)x + (size_t)t * H * (x_dt == OR_F32 ? 4 : 2), x_dt, (size_t)H, xr);
+        for (int e = 0; e < E; e++) {
+            double acc = 0.0;
+            const float* w = wr + (size_t)e * H;
+            for (int h = 0; h < H; h++) acc += (double)w[h] * (double)xr[h];
+            float l = or_round_dt((float)acc, x_dt);
+            if (bias) l = or_round_dt(l + load1(bias, x_dt, (size_t)e), x_dt);
+            logits[(size_t)t * E + e] = l;
+        }
+    }
+    free(xr);
+    free(wr);
+    return 0;
+}
+
 /* Numerically-stable softmax with the uniform fallback
  * (MoELayer.swift:210-219); the sum runs in index order. */
 void or_softmax(const float* x, int n, float* out) {
@@ -466,8 +506,6 @@ int or_qgemm_rows(const or_qproj* p, const float* a, int M,
                   const uint32_t* row_expert, float* out) {
     int N = p->n, K = p->k, gs = p->group_size, bits = p->bits;
     if (!bits_ok(bits) || gs <= 0 || K % gs || (K * bits) % 32 || M < 0) return -1;
-    size_t row_words = (size_t)K * bits / 32;
-    int groups = K / gs;
     int E = 0;
     for (int m = 0; m < M; m++)
         if ((int)row_expert[m] + 1 > E) E = (int)row_expert[m] + 1;
@@ -482,17 +520,7 @@ int or_qgemm_rows(const or_qproj* p, const float* a, int M,
     for (int e = 0; e < E; e++) {
         if (start[e + 1] == start[e]) continue;
         for (int n = 0; n < N; n++) {
-            size_t r = (size_t)e * N + n;
-            const uint32_t* wr = p->weight + r * row_words;
-            for (int g = 0; g < groups; g++) {
-                float s = load1(p->scales, p->sb_dt, r * groups + g);
-                float b = load1(p->biases, p->sb_dt, r * groups + g);
-                for (int j = 0; j < gs; j++) {
-                    float q = (float)get_code(wr, bits, (size_t)g * gs + j);
-                    float sq = s * q;
-                    wrow[g * gs + j] = sq + b;
-                }
-            }
+            dequant_row(p, (size_t)e * N + n, wrow);
             for (int i = start[e]; i < start[e + 1]; i++) {
                 int m = rows[i];
                 const float* x = a + (size_t)m * K;
@@ -700,6 +728,8 @@ static int layer_impl(const or_layer* L, const void* x, const void* router_x, in
     /* 1. router projection */
     float* logits = (float*)malloc(sizeof(float) * (size_t)T * E);
     if (given_logits) memcpy(logits, given_logits, sizeof(float) * (size_t)T * E);
+    else if (L->router_q.weight)
+        or_router_logits_q(router_x, dt, T, H, &L->router_q, L->router_bias, E, logits);
     else or_router_logits(router_x, dt, T, H, L->router_weight, L->router_dt, L->router_bias, E,
                           logits);
 
@@ -754,7 +784,10 @@ static int layer_impl(const or_layer* L, const void* x, const void* router_x, in
         or_qgemm_rows(&L->shared_down, sg, T, zero, so);
         finish_proj(&L->shared_down, so, T, zero, dt);
         float* gl = NULL;
-        if (L->shared_gate_weight) {
+        if (L->shared_gate_q.weight) {
+            gl = (float*)malloc(sizeof(float) * (size_t)T);
+            or_router_logits_q(x, dt, T, H, &L->shared_gate_q, NULL, 1, gl);
+        } else if (L->shared_gate_weight) {
             gl = (float*)malloc(sizeof(float) * (size_t)T);
             or_router_logits(x, dt, T, H, L->shared_gate_weight, L->router_dt, NULL, 1, gl);
         }

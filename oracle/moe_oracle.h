@@ -86,6 +86,13 @@ typedef struct or_qproj {
     int bits, group_size, sb_dt, n, k;
 } or_qproj;
 
+/* The router projection with an affine-quantised weight (QuantizedLinear,
+ * Layers.swift:371-400): row e of W dequantised as or_qgemm_rows does
+ * (w = s*q + b in fp32), dot products in double, then rounded as
+ * or_router_logits rounds. W is a one-expert stack with W->n = E. */
+int or_router_logits_q(const void* x, int x_dt, int T, int H, const or_qproj* W,
+                       const void* bias, int E, float* logits);
+
 /* out[m, :] = W[row_expert[m]] · a[m, :]  (fp32 dequant, double accumulate) */
 int or_qgemm_rows(const or_qproj* p, const float* a, int M,
                   const uint32_t* row_expert, float* out);
@@ -116,6 +123,10 @@ typedef struct or_layer {
     const void* shared_gate_weight;   /* nullable [H] in router_dt */
     float logit_scale, routed_scale;  /* 0 reads as 1 */
     const float* expert_scale;        /* nullable [E] */
+    /* quantised router / shared gate (QuantizedLinear, Layers.swift:371-400):
+     * used instead of router_weight / shared_gate_weight when .weight is
+     * non-NULL; one-expert stacks [1, E, H] and [1, 1, H] */
+    or_qproj router_q, shared_gate_q;
 } or_layer;
 
 /* If given_logits is non-NULL it replaces the router projection (used to

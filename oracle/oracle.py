@@ -62,6 +62,7 @@ class OrLayer(C.Structure):
         ("shared_gate", OrQProj), ("shared_up", OrQProj), ("shared_down", OrQProj),
         ("shared_gate_weight", C.c_void_p),
         ("logit_scale", C.c_float), ("routed_scale", C.c_float), ("expert_scale", C.c_void_p),
+        ("router_q", OrQProj), ("shared_gate_q", OrQProj),
     ]
 
 
@@ -83,6 +84,8 @@ def _declare(L):
     L.or_dequantize_affine.restype = i
     L.or_router_logits.argtypes = [vp, i, i, i, vp, i, vp, i, vp]
     L.or_router_logits.restype = None
+    L.or_router_logits_q.argtypes = [vp, i, i, i, C.POINTER(OrQProj), vp, i, vp]
+    L.or_router_logits_q.restype = i
     L.or_topk_indices.argtypes = [vp, i, i, vp]; L.or_topk_indices.restype = i
     L.or_softmax.argtypes = [vp, i, vp]; L.or_softmax.restype = None
     L.or_route.argtypes = [vp, i, i, i, i, i, vp, vp, vp]; L.or_route.restype = i
@@ -197,6 +200,20 @@ def router_logits(x, x_dt, W, w_dt, bias=None):
     out = np.zeros((T, E), dtype=np.float32)
     b = None if bias is None else np.ascontiguousarray(bias)
     lib().or_router_logits(_p(x), x_dt, T, H, _p(W), w_dt, _p(b), E, _p(out))
+    return out
+
+
+def router_logits_q(x, x_dt, q, bias=None):
+    """Router logits with an affine-quantised weight: q is a QProj holding one
+    expert [1, E, H]."""
+    x = np.ascontiguousarray(x)
+    T, H = x.shape
+    E = q.n
+    out = np.zeros((T, E), dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias)
+    qc = q.c()
+    if lib().or_router_logits_q(_p(x), x_dt, T, H, C.byref(qc), _p(b), E, _p(out)) != 0:
+        raise ValueError("invalid quantised router")
     return out
 
 

@@ -37,6 +37,41 @@ def gen_qproj(rng, E, N, K, bits, gs, sb_dt, s_range=(0.005, 0.02), b_range=(-0.
     return orc.QProj(w, s, b, bits, gs, sb_dt, out_bias=ob)
 
 
+def affine_quantize(W, bits, gs, sb_dt):
+    """mlx's affine quantiser on a dense [N, K] float matrix, per group of gs
+    values: scale = (max - min) / (2^bits - 1), bias = min, code = round((w -
+    bias) / scale) clamped to the code range; scale and bias stored in sb_dt.
+    Returns a one-expert QProj [1, N, K] (the layout loadLinear gives a
+    quantised router or shared-expert gate)."""
+    W = np.asarray(W, dtype=np.float64)
+    N, K = W.shape
+    g = W.reshape(N, K // gs, gs)
+    lo, hi = g.min(axis=2), g.max(axis=2)
+    scale = (hi - lo) / (2 ** bits - 1)
+    scale = np.where(scale == 0, 1.0, scale)
+    s_st, b_st = store(scale, sb_dt), store(lo, sb_dt)
+    s_f, b_f = load(s_st, sb_dt).astype(np.float64), load(b_st, sb_dt).astype(np.float64)
+    q = np.clip(np.rint((g - b_f[..., None]) / s_f[..., None]), 0, 2 ** bits - 1).astype(np.uint8)
+    w = orc.pack_codes(q.reshape(N, K), bits).reshape(1, N, K * bits // 32)
+    return orc.QProj(w, s_st.reshape(1, N, K // gs), b_st.reshape(1, N, K // gs), bits, gs, sb_dt)
+
+
+def with_quantised_router(spec, bits=None, shared_gate_bits=None, gs=64, sb_dt=None):
+    """spec with its dense router (and/or shared-expert gate) replaced by the
+    mlx affine quantisation of the same weights."""
+    import copy
+    out = copy.copy(spec)
+    sb = spec.act_dt if sb_dt is None else sb_dt
+    if bits is not None:
+        out.router_weight = affine_quantize(load(spec.router_weight, spec.router_dt), bits, gs, sb)
+        out.name = f"{spec.name}+router{bits}b"
+    if shared_gate_bits is not None:
+        out.shared_gate_weight = affine_quantize(load(spec.shared_gate_weight, spec.router_dt),
+                                                 shared_gate_bits, gs, sb)
+        out.name = f"{out.name}+sgate{shared_gate_bits}b"
+    return out
+
+
 @dataclass
 class LayerSpec:
     hidden: int
@@ -70,7 +105,10 @@ class LayerSpec:
         L = orc.OrLayer()
         L.hidden, L.n_experts, L.top_k = self.hidden, self.n_experts, self.top_k
         L.intermediate, L.act_dt = self.intermediate, self.act_dt
-        L.router_weight = self.router_weight.ctypes.data
+        if isinstance(self.router_weight, orc.QProj):
+            L.router_q = self.router_weight.c()
+        else:
+            L.router_weight = self.router_weight.ctypes.data
         L.router_dt = self.router_dt
         L.router_bias = None if self.router_bias is None else self.router_bias.ctypes.data
         L.gating, L.norm_topk = self.gating, int(self.norm_topk)
@@ -82,8 +120,11 @@ class LayerSpec:
             L.has_shared = 1
             L.shared_gate, L.shared_up, L.shared_down = (
                 orc.OrQProj() if p is None else p.c() for p in self.shared)
-            L.shared_gate_weight = (None if self.shared_gate_weight is None
-                                    else self.shared_gate_weight.ctypes.data)
+            sgw = self.shared_gate_weight
+            if isinstance(sgw, orc.QProj):
+                L.shared_gate_q = sgw.c()
+            else:
+                L.shared_gate_weight = None if sgw is None else sgw.ctypes.data
         L.logit_scale, L.routed_scale = self.logit_scale, self.routed_scale
         L.expert_scale = None if self.expert_scale is None else self.expert_scale.ctypes.data
         self._keep = L
@@ -109,16 +150,38 @@ class LayerSpec:
             return fl.StackedExperts(T(q.weight), T(q.scales), T(q.biases), q.bits, q.gs,
                                      out_bias=T(q.out_bias))
 
+        def W(a):  # dense router / gate weight or a one-expert quantised stack
+            return P(a) if isinstance(a, orc.QProj) else T(a)
+
         act = {F32: torch.float32, F16: torch.float16, BF16: torch.bfloat16}[self.act_dt]
         router = fl.MoERouter(self.n_experts, self.top_k, self.gating, self.norm_topk,
                               T(self.expert_bias), self.logit_scale, self.routed_scale,
                               T(self.expert_scale))
         shared = None if self.shared is None else tuple(P(q) for q in self.shared)
-        return fl.MoELayer(router_weight=T(self.router_weight), router=router, gate=P(self.gate),
+        return fl.MoELayer(router_weight=W(self.router_weight), router=router, gate=P(self.gate),
                            up=P(self.up), down=P(self.down), hidden=self.hidden, act_dtype=act,
                            router_bias=T(self.router_bias), activation=self.activation,
                            alpha=self.alpha, limit=self.limit, shared=shared,
-                           shared_gate_weight=T(self.shared_gate_weight))
+                           shared_gate_weight=W(self.shared_gate_weight))
+
+    def oracle_logits(self, rx):
+        """The router logits the oracle computes for router input rows rx."""
+        if isinstance(self.router_weight, orc.QProj):
+            return orc.router_logits_q(rx, self.act_dt, self.router_weight, self.router_bias)
+        return orc.router_logits(rx, self.act_dt, self.router_weight, self.router_dt,
+                                 self.router_bias)
+
+    def logits_tolerance(self, ref):
+        """Allowed |GPU - oracle| per logit: two storage ulps (a bias add rounds
+        twice); a quantised router also differs in fp32 summation order over
+        terms much larger than a small logit, so it gets 1e-4 of its row's
+        largest logit on top."""
+        ulp = np.abs(ref) * (2.0 ** -7 if self.act_dt == BF16 else 2.0 ** -10 if self.act_dt == F16
+                             else 2.0 ** -20) + 1e-6
+        tol = 2.02 * ulp
+        if isinstance(self.router_weight, orc.QProj):
+            tol = tol + 1e-4 * (1.0 + np.abs(ref).max(axis=1, keepdims=True))
+        return tol
 
     def x(self, T, seed=0):
         rng = np.random.default_rng(seed + 1000)
@@ -183,7 +246,14 @@ def cfg_qwen3(seed=0, n_experts=128, hidden=2048, inter=768, router_bias=None):
                      down=gen_qproj(rng, E, H, I, 4, 64, F16), name="qwen3")
 
 
-def zipf_router_bias(E, s=1.1, beta=1.0, seed=0):
+# Router-bias strength for configs[3]: beta * log p with p Zipf(1.1) gives a
+# hottest-expert load of about 10x the median at 0.33 (4096 tokens, 128
+# experts, top-8: max / median 9.9-10.0 over two seeds; beta = 1.0 gives
+# about 230x, nearly every token on the hottest expert).
+ZIPF_BETA = 0.33
+
+
+def zipf_router_bias(E, s=1.1, beta=ZIPF_BETA, seed=0):
     """beta * log p_e with p Zipf(s) over a random permutation of ranks."""
     rng = np.random.default_rng(seed + 7)
     ranks = rng.permutation(E) + 1

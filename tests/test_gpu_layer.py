@@ -12,8 +12,9 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from moe_spec import (BF16, F16, F32, cfg_bits, cfg_gemma4, cfg_gptoss, cfg_mixed, cfg_nemotron, cfg_qwen3,
-                      cfg_tiny, check_close, load, store, to_numpy_f32, to_torch, zipf_router_bias)
+from moe_spec import (BF16, F16, F32, affine_quantize, cfg_bits, cfg_gemma4, cfg_gptoss, cfg_mixed,
+                      cfg_nemotron, cfg_qwen3, cfg_tiny, check_close, load, store, to_numpy_f32,
+                      to_torch, with_quantised_router, zipf_router_bias)
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -125,6 +126,63 @@ def test_router_logits_within_one_ulp(dt, wdt, E, H, T):
 
 
 # ------------------------------------------------------------------- plan --
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("T,E,H,gs,dt,bias", [
+    (1, 32, 2880, 64, BF16, True),     # one token: one wave per expert
+    (7, 40, 1024, 32, F16, False),     # a few tokens, E not a multiple of 32
+    (64, 128, 2048, 64, BF16, False),  # many tokens: the matrix-core kernel
+    (96, 64, 768, 128, F16, True),
+    (40, 40, 512, 64, BF16, True),     # many tokens, E % 32 != 0: the row kernel
+])
+def test_router_logits_q(bits, T, E, H, gs, dt, bias):
+    """moe_router_logits_q (an mlx QuantizedLinear router) against the oracle's
+    quantised router: codes exact, per-group scale and bias in fp32."""
+    rng = np.random.default_rng(bits * 1000 + T)
+    sb = BF16 if dt == F16 else F16
+    q = affine_quantize(rng.normal(0, 1 / np.sqrt(H), size=(E, H)), bits, gs, sb)
+    x = store(rng.normal(0, 1, size=(T, H)), dt)
+    b = store(rng.normal(0, 0.1, size=E), dt) if bias else None
+    ref = orc.router_logits_q(x, dt, q, b)
+    P = lambda a: to_torch(a) if a.dtype != np.uint32 else torch.from_numpy(a.view(np.int32)).cuda()  # noqa: E731
+    w, sc, bi = P(q.weight), to_torch(q.scales), to_torch(q.biases)
+    qp = _lib.QProj(w.data_ptr(), sc.data_ptr(), bi.data_ptr(), None, bits, gs, sb, E, H, 1)
+    xt = to_torch(x)
+    bt = None if b is None else to_torch(b)
+    out = torch.empty(T, E, dtype=xt.dtype, device="cuda")
+    check(_lib.load().moe_router_logits_q(_p(xt), dt, T, H, C.byref(qp),
+                                          None if bt is None else _p(bt), E, _p(out), _stream()))
+    torch.cuda.synchronize()
+    got = to_numpy_f32(out)
+    ulp = np.abs(ref) * (2.0 ** -7 if dt == BF16 else 2.0 ** -10) + 1e-6
+    tol = 2.02 * ulp + 1e-4 * (1.0 + np.abs(ref).max(axis=1, keepdims=True))
+    assert np.all(np.abs(got - ref) <= tol), float(np.abs(got - ref).max())
+    # most logits round to the oracle's value exactly (f16 rows carry three
+    # more mantissa bits, and its magic offset 1024 cancels more than bf16's
+    # 128, so fewer of them do)
+    assert np.mean(got == ref) > (0.9 if dt == BF16 else 0.6)
+
+
+@pytest.mark.parametrize("T", [1, 64, 256])
+def test_layer_quantised_router_qwen3(T):
+    """A 4-bit mlx router on the Qwen3 shape: one token (row kernel), 64 rows
+    (matrix-core GEMV experts) and 256 rows (grouped GEMM experts)."""
+    run_layer(with_quantised_router(cfg_qwen3(), bits=4), T, seed=T)
+
+
+@pytest.mark.parametrize("T", [1, 48])
+def test_layer_quantised_router_gptoss(gptoss, T):
+    """An 8-bit router with GPT-OSS's bias (double rounding after the
+    quantised product)."""
+    run_layer(with_quantised_router(gptoss, bits=8), T, seed=T)
+
+
+@pytest.mark.parametrize("T", [1, 64])
+def test_layer_quantised_shared_gate(mixed, T):
+    """A 4-bit router and a 4-bit shared_expert_gate (Qwen3xText.swift:660-661,
+    947-951) on the mixed-bit layer."""
+    run_layer(with_quantised_router(mixed, bits=4, shared_gate_bits=4), T, seed=T + 1)
+
 
 @pytest.mark.parametrize("T,k,E", [(1, 8, 128), (1, 4, 32), (16, 2, 8), (64, 8, 128), (512, 8, 128),
                                    (4096, 8, 128), (2048, 8, 256), (777, 3, 1000)])
@@ -307,12 +365,9 @@ def run_layer(spec, T, seed=0):
     y, tr = dev.forward(to_torch(x), trace=True, router_x=None if rx is None else to_torch(rx))
     torch.cuda.synchronize()
     logits_gpu = to_numpy_f32(tr["logits"])
-    logits_cpu = orc.router_logits(x if rx is None else rx, spec.act_dt, spec.router_weight,
-                                   spec.router_dt, spec.router_bias)
-    ulp = np.abs(logits_cpu) * (2.0 ** -7 if spec.act_dt == BF16 else 2.0 ** -10 if spec.act_dt == F16
-                                else 2.0 ** -20) + 1e-6
-    # a bias add rounds twice, so allow two storage ulps
-    assert np.all(np.abs(logits_gpu - logits_cpu) <= 2.02 * ulp), "router logits"
+    logits_cpu = spec.oracle_logits(x if rx is None else rx)
+    assert np.all(np.abs(logits_gpu - logits_cpu) <= spec.logits_tolerance(logits_cpu)), \
+        "router logits"
     y_ref, _, idx_ref, w_ref = orc.moe_layer(spec, x, given_logits=logits_gpu, router_x=rx)
     assert np.array_equal(_u32(tr["topk_idx"]), idx_ref), "expert ids"
     assert np.array_equal(tr["topk_weight"].cpu().numpy().view(np.uint32), w_ref.view(np.uint32)), \

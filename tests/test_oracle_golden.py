@@ -407,6 +407,56 @@ def test_gemv_reference_cells(cell):
     assert np.allclose(got, ref, rtol=1e-5, atol=1e-4)
 
 
+@pytest.mark.parametrize("cell", GOLD["gemv_cells"], ids=lambda c: f"bits{c['bits']}")
+def test_router_logits_q_reference_cells(cell):
+    """The quantised router (QuantizedLinear, Layers.swift:371-400) on the
+    reference's per-bit GEMV cells (QuantizedOpsTests.swift:126-438): same
+    products as or_qgemm_rows, one row per expert, f32 rows so nothing rounds
+    after the dot product."""
+    bits, OUT, IN, gs = cell["bits"], cell["out"], cell["in"], cell["gs"]
+    q = np.array([[_expr(cell["q"], j=j, r=r) for j in range(IN)] for r in range(OUT)], np.uint8)
+    ng = IN // gs
+    n_sb = OUT * ng if "i" in cell["scale"] else OUT
+    sc = np.array([_expr(cell["scale"], i=i, r=i) for i in range(n_sb)], np.float32)
+    bi = np.array([_expr(cell["bias"], i=i, r=i) for i in range(n_sb)], np.float32)
+    x = np.array([_expr(cell["x"], j=j) for j in range(IN)], np.float32)
+    if cell["sb"] == "bf16_trunc":
+        sc, bi, x = _bf_trunc(sc), _bf_trunc(bi), _bf_trunc(x)
+    sc2, bi2 = sc.reshape(OUT, -1), bi.reshape(OUT, -1)
+    if sc2.shape[1] == 1 and ng > 1:
+        sc2, bi2 = np.repeat(sc2, ng, 1), np.repeat(bi2, ng, 1)
+    w = orc.pack_codes(q, bits).reshape(1, OUT, IN * bits // 32)
+    p = orc.QProj(w, np.ascontiguousarray(sc2.reshape(1, OUT, ng)),
+                  np.ascontiguousarray(bi2.reshape(1, OUT, ng)), bits, gs, orc.F32)
+    got = orc.router_logits_q(x.reshape(1, IN), orc.F32, p)[0]
+    ref = np.array([sum((float(q[r, j]) * float(sc2[r, j // gs]) + float(bi2[r, j // gs])) * float(x[j])
+                        for j in range(IN)) for r in range(OUT)])
+    assert np.allclose(got, ref, rtol=1e-5, atol=1e-4)
+    assert np.array_equal(got, orc.qgemm_rows(p, x.reshape(1, IN), np.zeros(1, np.uint32))[0])
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+def test_router_logits_q_equals_dense_restatement(bits):
+    """The quantised router equals the dense router run on the stream's own
+    dequantisation (or_dequantize_affine, an independent unpack of the bit
+    stream) bit for bit, bias double rounding included; a router whose groups
+    are read with the wrong group size does not."""
+    from moe_spec import affine_quantize
+    rng = np.random.default_rng(bits)
+    E, H, gs = 24, 256, 64
+    q = affine_quantize(rng.normal(0, 1 / 16, size=(E, H)), bits, gs, orc.BF16)
+    x = orc.from_f32(rng.normal(0, 1, size=(5, H)).astype(np.float32), orc.BF16)
+    b = orc.from_f32(rng.normal(0, 0.1, size=E).astype(np.float32), orc.BF16)
+    dense = orc.dequantize_affine(q.weight, q.scales, q.biases, q.sb_dt, bits, gs, E * H)
+    ref = orc.router_logits(x, orc.BF16, np.ascontiguousarray(dense, np.float32).reshape(E, H),
+                            orc.F32, b)
+    got = orc.router_logits_q(x, orc.BF16, q, b)
+    assert np.array_equal(got, ref)
+    wrong = orc.QProj(q.weight, q.scales.reshape(1, E, -1)[:, :, : H // 128].copy(),
+                      q.biases.reshape(1, E, -1)[:, :, : H // 128].copy(), bits, 128, q.sb_dt)
+    assert not np.array_equal(orc.router_logits_q(x, orc.BF16, wrong, b), ref)
+
+
 # ------------------------------------------------ activations / combine ----
 
 def test_swiglu_kat():

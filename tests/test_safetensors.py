@@ -431,7 +431,9 @@ def _checkpoint_spec(seed=0):
                      router_weight=store(rng.normal(0, 1 / np.sqrt(H), size=(E, H)), BF16),
                      router_dt=BF16,
                      gate=gen_qproj(rng, E, I, H, 3, 64, BF16), up=gen_qproj(rng, E, I, H, 3, 64, BF16),
-                     down=gen_qproj(rng, E, H, I, 6, 64, BF16), shared=shared, name="ckpt")
+                     down=gen_qproj(rng, E, H, I, 6, 64, BF16), shared=shared,
+                     shared_gate_weight=store(rng.normal(0, 1 / np.sqrt(H), size=(1, H)), BF16),
+                     name="ckpt")
 
 
 @pytest.mark.gpu
@@ -443,8 +445,10 @@ def test_checkpoint_experts_drive_the_layer(tmp_path, T):
     torch = _torch()
     from ffai_amd import layer as fl
     from ffai_amd.safetensors import SafeTensorsBundle
-    from moe_spec import check_close, load, to_numpy_f32, to_torch
-    spec = _checkpoint_spec()
+    from moe_spec import check_close, load, to_numpy_f32, to_torch, with_quantised_router
+    # the router (mlp.gate) and the shared expert's sigmoid gate are quantised
+    # linears in an mlx checkpoint (loadLinear, Qwen3xText.swift:605-606, 660-661)
+    spec = with_quantised_router(_checkpoint_spec(), bits=4, shared_gate_bits=4)
     p = "model.layers.7.mlp"
 
     def trip(base, q, two_d=False):
@@ -456,7 +460,9 @@ def test_checkpoint_experts_drive_the_layer(tmp_path, T):
     shard2 = {**trip(f"{p}.switch_mlp.down_proj", spec.down),
               **trip(f"{p}.shared_expert.gate_proj", spec.shared[0], True),
               **trip(f"{p}.shared_expert.up_proj", spec.shared[1], True),
-              **trip(f"{p}.shared_expert.down_proj", spec.shared[2], True)}
+              **trip(f"{p}.shared_expert.down_proj", spec.shared[2], True),
+              **trip(f"{p}.gate", spec.router_weight, True),
+              **trip(f"{p}.shared_expert_gate", spec.shared_gate_weight, True)}
     write_st(tmp_path / "model-00001-of-00002.safetensors", shard1)
     write_st(tmp_path / "model-00002-of-00002.safetensors", shard2)
     wm = {n: "model-00001-of-00002.safetensors" for n in shard1}
@@ -469,12 +475,16 @@ def test_checkpoint_experts_drive_the_layer(tmp_path, T):
         u, d = b.stackedExpertsMany([f"{p}.switch_mlp.up_proj", f"{p}.switch_mlp.down_proj"], 64)
         sh = tuple(b.stackedExpertsMany([f"{p}.shared_expert.{n}_proj" for n in ("gate", "up", "down")],
                                         64))
-    assert (g.bits, u.bits, d.bits, sh[2].bits) == (3, 3, 6, 8)
+        assert b.isQuantized(f"{p}.gate") and b.isQuantized(f"{p}.shared_expert_gate")
+        rq, sgq = b.stackedExpertsMany([f"{p}.gate", f"{p}.shared_expert_gate"], 64)
+    assert (g.bits, u.bits, d.bits, sh[2].bits, rq.bits, sgq.bits) == (3, 3, 6, 8, 4, 4)
     assert g.weight.shape == (16, 256, 512 * 3 // 32) and sh[0].weight.shape == (1, 384, 64)
+    assert rq.weight.shape == (1, 16, 64) and sgq.weight.shape == (1, 1, 64)
     mem = spec.device()
     router = fl.MoERouter(spec.n_experts, spec.top_k)
-    ck = fl.MoELayer(router_weight=mem.router_weight, router=router, gate=g, up=u, down=d,
-                     hidden=spec.hidden, act_dtype=torch.bfloat16, shared=sh)
+    ck = fl.MoELayer(router_weight=rq, router=router, gate=g, up=u, down=d,
+                     hidden=spec.hidden, act_dtype=torch.bfloat16, shared=sh,
+                     shared_gate_weight=sgq)
     xn = spec.x(T, seed=T)
     x = to_torch(xn)
     y_ck, tr = ck.forward(x, trace=True)
