@@ -32,7 +32,7 @@ EXPORTS = [
     "moe_dispatch_plan", "moe_dequantize_affine", "moe_expert_matmul_workspace_bytes",
     "moe_expert_matmul", "moe_activation_apply", "moe_unpermute", "moe_layer_workspace_bytes",
     "moe_layer_forward", "moe_layer_forward_routed", "moe_layer_forward_residual",
-    "moe_layer_path", "moe_add_rmsnorm", "moe_mxfp4_to_affine", "moe_layer_create", "moe_layer_destroy",
+    "moe_layer_path", "moe_layer_forward_noalloc", "moe_layer_noalloc_max_bytes", "moe_add_rmsnorm", "moe_mxfp4_to_affine", "moe_layer_create", "moe_layer_destroy",
     "moe_layer_decode", "moe_layer_decode_many",
     "moe_st_open", "moe_st_close", "moe_st_count", "moe_st_name", "moe_st_info", "moe_st_read_host",
     "moe_st_upload", "moe_st_is_quantized", "moe_st_stacked_bytes", "moe_st_load_stacked",
@@ -127,6 +127,10 @@ def load():
     lib.moe_layer_forward_residual.argtypes = [C.POINTER(LayerDesc), vp, vp, vp, C.c_float, i32,
                                                vp, vp, vp, sz, C.POINTER(LayerTrace), st]
     lib.moe_layer_path.argtypes = [C.POINTER(LayerDesc), i32, C.POINTER(LayerPaths)]
+    lib.moe_layer_forward_noalloc.argtypes = [C.POINTER(LayerDesc), vp, i32, vp,
+                                              C.POINTER(LayerTrace), st]
+    lib.moe_layer_noalloc_max_bytes.argtypes = []
+    lib.moe_layer_noalloc_max_bytes.restype = sz
     lib.moe_add_rmsnorm.argtypes = [vp, vp, vp, C.c_float, i32, i32, i32, vp, vp, st]
     lib.moe_mxfp4_to_affine.argtypes = [vp, vp, C.c_int64, vp, vp, vp, i32, st]
     lib.moe_layer_create.argtypes = [C.POINTER(LayerDesc), C.POINTER(vp)]
@@ -157,7 +161,7 @@ def load():
                  "moe_router_logits_q", "moe_router_topk", "moe_router_topk_scaled", "moe_dispatch_plan",
                  "moe_dequantize_affine", "moe_expert_matmul", "moe_activation_apply",
                  "moe_unpermute", "moe_layer_forward", "moe_layer_forward_routed",
-                 "moe_layer_forward_residual", "moe_layer_path",
+                 "moe_layer_forward_residual", "moe_layer_path", "moe_layer_forward_noalloc",
                  "moe_add_rmsnorm", "moe_mxfp4_to_affine",
                  "moe_layer_create", "moe_layer_decode",
                  "moe_layer_decode_many", "moe_st_open", "moe_st_info", "moe_st_read_host",

@@ -305,6 +305,20 @@ moe_status moe_layer_forward_routed(const moe_layer_desc* d, const void* x,
                                     size_t workspace_bytes, const moe_layer_trace* trace,
                                     hipStream_t stream);
 
+/* moe_layer_forward for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference: the workspace is a static
+ * device array of moe_layer_noalloc_max_bytes() bytes (16 MiB) that each GPU
+ * holds for the life of the process, instead of a caller buffer; a call
+ * whose workspace (moe_layer_workspace_bytes) would exceed it returns
+ * MOE_ERR_WORKSPACE before any launch. Every launch stays on `stream` (no
+ * side stream). All calls on one GPU share the array: calls that overlap on
+ * a GPU (other streams, other host threads) race and must be serialised by
+ * the caller. */
+moe_status moe_layer_forward_noalloc(const moe_layer_desc* d, const void* x, int32_t T, void* y,
+                                     const moe_layer_trace* trace, hipStream_t stream);
+size_t moe_layer_noalloc_max_bytes(void);
+
 /* The MoE block with the decoder steps on either side folded in: the
  * post-attention residual add + RMSNorm before it (Ops.addAndRmsNorm,
  * Qwen3xText.swift:2640-2660) and the residual add after it
