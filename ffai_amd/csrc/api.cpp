@@ -94,22 +94,25 @@ hipError_t launch_router_q(int bits, const void* x, int xdt, int T, int H, const
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemm_b2(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
-hipError_t launch_gemm_b3(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
-hipError_t launch_gemm_b4(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
-hipError_t launch_gemm_b5(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
-hipError_t launch_gemm_b6(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
-hipError_t launch_gemm_b8(int, int, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b2(int, bool, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b3(int, bool, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b4(int, bool, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b5(int, bool, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b6(int, bool, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b8(int, bool, bool, const GemmArgs&, int, hipStream_t, KEvents);
 
-hipError_t launch_gemm(int bits, int xdt, int sbdt, bool gateup, const GemmArgs& a, int grid,
-                       hipStream_t st, KEvents ev) {
+hipError_t launch_gemm(int bits, int xdt, int sbdt, bool gateup, bool a_bf16, const GemmArgs& a0,
+                       int grid, hipStream_t st, KEvents ev) {
+  if (sbdt != DT_BF16 && sbdt != DT_F16) return hipErrorInvalidValue;
+  GemmArgs a = a0;
+  a.sb_bf16 = sbdt == DT_BF16;
   switch (bits) {
-    case 2: return launch_gemm_b2(xdt, sbdt, gateup, a, grid, st, ev);
-    case 3: return launch_gemm_b3(xdt, sbdt, gateup, a, grid, st, ev);
-    case 4: return launch_gemm_b4(xdt, sbdt, gateup, a, grid, st, ev);
-    case 5: return launch_gemm_b5(xdt, sbdt, gateup, a, grid, st, ev);
-    case 6: return launch_gemm_b6(xdt, sbdt, gateup, a, grid, st, ev);
-    case 8: return launch_gemm_b8(xdt, sbdt, gateup, a, grid, st, ev);
+    case 2: return launch_gemm_b2(xdt, gateup, a_bf16, a, grid, st, ev);
+    case 3: return launch_gemm_b3(xdt, gateup, a_bf16, a, grid, st, ev);
+    case 4: return launch_gemm_b4(xdt, gateup, a_bf16, a, grid, st, ev);
+    case 5: return launch_gemm_b5(xdt, gateup, a_bf16, a, grid, st, ev);
+    case 6: return launch_gemm_b6(xdt, gateup, a_bf16, a, grid, st, ev);
+    case 8: return launch_gemm_b8(xdt, gateup, a_bf16, a, grid, st, ev);
   }
   return hipErrorInvalidValue;
 }
@@ -460,9 +463,10 @@ int group_shift(int gs) { return gs == 128 ? 2 : (gs == 64 ? 1 : 0); }
 // ---------------------------------------------------------------------------
 
 struct Workspace {
-  size_t logits, idx, w, counts, offsets, used, perm, inv, act, Y, plan_scratch, tiles;
-  size_t r_plan, r_tiles;  // router projection on the matrix cores
-  size_t s_off, s_used, s_act, s_out, s_logit, s_tiles;
+  size_t logits, idx, w, counts, offsets, used, perm, inv, act, Y, plan_scratch;
+  size_t items_gu, items_dn;  // grouped-GEMM work items of the routed experts
+  size_t x16;                 // the layer input as the GEMMs' f16 operand
+  size_t s_off, s_used, s_act, s_out, s_logit, s_items_gu, s_items_dn;
   size_t xn, res;  // decoder step before the block: normalised rows, residual
   size_t total;
 };
@@ -489,9 +493,9 @@ Workspace layout(const moe_layer_desc* d, int T) {
   w.act = take(M * I * ds);
   w.Y = take(M * H * ds);
   w.plan_scratch = take(dispatch_scratch_bytes(T, (int)k, (int)E));
-  w.tiles = take((1 + 2 * (size_t)gemm_max_tiles((int)M, (int)E)) * 4);
-  w.r_plan = take(4 * 4);  // offsets {0, T} and the used list of a one-expert plan
-  w.r_tiles = take((1 + 2 * (size_t)gemm_max_tiles(T, 1)) * 4);
+  w.items_gu = take(gemm_items_bytes((int)M, (int)E, (int)I, true));
+  w.items_dn = take(gemm_items_bytes((int)M, (int)E, (int)H, false));
+  w.x16 = take((size_t)T * H * 2);
   if (d->has_shared) {
     const size_t SI = (size_t)d->shared_up.n;
     w.s_off = take(2 * 4);
@@ -499,7 +503,8 @@ Workspace layout(const moe_layer_desc* d, int T) {
     w.s_act = take((size_t)T * SI * ds);
     w.s_out = take((size_t)T * H * ds);
     w.s_logit = take((size_t)T * ds);
-    w.s_tiles = take((1 + 2 * (size_t)gemm_max_tiles(T, 1)) * 4);
+    w.s_items_gu = take(gemm_items_bytes(T, 1, (int)SI, true));
+    w.s_items_dn = take(gemm_items_bytes(T, 1, (int)H, false));
   }
   w.xn = take((size_t)T * H * ds);
   w.res = take((size_t)T * H * ds);
@@ -715,46 +720,33 @@ bool gemm_ok(const moe_qproj& p, int xdt, int M, const void* out = nullptr) {
          M >= kGemmMinRows * slots && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
 }
 
-// Router logits on the matrix cores for many tokens when the expert count is
-// not a multiple of 32: a one-expert plan over the T rows with the dense
-// router weight through the grouped GEMM; the bias rounds after the product
-// as in router_logits_kernel. Multiples of 32 take router_gemm_kernel inside
-// launch_router_logits instead (no plan, every CU busy).
-bool router_gemm_ok(const moe_layer_desc* d, int T) {
-  return T >= kGemmMinRows && d->act_dtype != MOE_F32 && d->router_dtype == d->act_dtype &&
-         d->hidden % 64 == 0 && d->n_experts % 8 == 0 && d->n_experts % 32 != 0 &&
-         (size_t)T * d->hidden * 2 < (1ull << 32);
-}
-
-moe_status run_router_gemm(const moe_layer_desc* d, const void* x, int T, void* logits,
-                           uint32_t* plan, uint32_t* tiles, hipStream_t st) {
-  MOE_HIP(launch_identity_plan(plan, plan + 2, T, st), "router plan launch");
-  MOE_HIP(launch_gemm_tiles(plan, 1, kGemmRows, tiles, st), "router tile list launch");
-  GemmArgs a{};
-  a.p0 = GemvProj{reinterpret_cast<const uint32_t*>(d->router_weight), nullptr, nullptr,
-                  d->router_bias};
-  a.x = x;
-  a.x_rows = T;
-  a.topk = 1;
-  a.offsets = plan;
-  a.tiles = tiles;
-  a.out = logits;
-  a.N = d->n_experts;
-  a.K = d->hidden;
-  const long items = (long)gemm_max_tiles(T, 1) * ((d->n_experts + 255) / 256);
-  const int grid = (int)((items + 7) / 8 * 8);
-  MOE_HIP(launch_gemm_dense(d->act_dtype, a, grid, st), "router GEMM launch");
-  return MOE_OK;
-}
-
 // out[p] = W[e(p)] . a[row(p)] (or the gate/up pair with the activation)
-// over the row tiles of a plan, on the matrix cores. `tiles` must hold the
-// list written by launch_gemm_tiles for the same offsets.
-moe_status run_gemm(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
-                    const uint32_t* perm, int topk, const uint32_t* offsets,
-                    const uint32_t* tiles, int M, void* out, int act, float alpha, float limit,
+// over a plan, on the matrix cores. `items` must hold the work list written by
+// launch_gemm_items for the same offsets and (N, gate/up). The A rows x are
+// f16 A operands (kA16Shift), or bf16 rows converted while staging (a_bf16,
+// single projections only); a gate/up pair writes its activation as A rows.
+// The routed experts / the shared expert of a layer call of T rows take the
+// grouped GEMM (gate/up and down together: the gate/up epilogue writes the
+// down GEMM's f16 operand).
+bool routed_gemm(const moe_layer_desc* d, int T) {
+  const moe_qproj& p0 = d->activation == MOE_ACT_RELU2 ? d->up : d->gate;
+  const int M = T * d->top_k;
+  return gemm_ok(p0, d->act_dtype, M) && gemm_ok(d->down, d->act_dtype, M);
+}
+bool shared_gemm(const moe_layer_desc* d, int T) {
+  if (!d->has_shared) return false;
+  const moe_qproj& p0 = d->activation == MOE_ACT_RELU2 ? d->shared_up : d->shared_gate;
+  return gemm_ok(p0, d->act_dtype, T) && gemm_ok(d->shared_down, d->act_dtype, T);
+}
+
+// out_a16: a single projection writes A rows for a following GEMM (the
+// first stage of squared-ReLU experts).
+moe_status run_gemm(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt, bool a_bf16,
+                    bool out_a16, const uint32_t* perm, int topk, const uint32_t* offsets,
+                    const uint32_t* items, int M, void* out, int act, float alpha, float limit,
                     hipStream_t st, KEvents ev = {}) {
   GemmArgs a{};
+  a.out_a16 = out_a16;
   a.p0 = to_proj(p0);
   if (p1) a.p1 = to_proj(*p1);
   a.x = x;
@@ -762,7 +754,7 @@ moe_status run_gemm(const moe_qproj& p0, const moe_qproj* p1, const void* x, int
   a.perm = perm;
   a.topk = topk;
   a.offsets = offsets;
-  a.tiles = tiles;
+  a.items = items;
   a.out = out;
   a.N = p0.n;
   a.K = p0.k;
@@ -771,10 +763,10 @@ moe_status run_gemm(const moe_qproj& p0, const moe_qproj* p1, const void* x, int
   a.alpha = alpha;
   a.limit = limit;
   const bool gu = p1 != nullptr;
-  const int cols = gemm_block_cols(gu);
-  const long items = (long)gemm_max_tiles(M, p0.n_experts) * ((p0.n + cols - 1) / cols);
-  const int grid = (int)((items + 7) / 8 * 8);  // a multiple of the 8 XCDs
-  MOE_HIP(launch_gemm(p0.bits, xdt, p0.sb_dtype, gu, a, grid, st, ev), "grouped GEMM launch");
+  const long items_max = gemm_max_items(M, p0.n_experts, p0.n, gu);
+  const int grid = (int)((items_max + 7) / 8 * 8);  // a multiple of the 8 XCDs
+  MOE_HIP(launch_gemm(p0.bits, xdt, p0.sb_dtype, gu, a_bf16, a, grid, st, ev),
+          "grouped GEMM launch");
   return MOE_OK;
 }
 
@@ -927,10 +919,10 @@ extern "C" moe_status moe_mxfp4_to_affine(const uint32_t* packed, const uint8_t*
   return ok();
 }
 
-extern "C" size_t moe_expert_matmul_workspace_bytes(int32_t n_experts, int32_t M) {
-  if (n_experts <= 0 || M <= 0) return 0;
+extern "C" size_t moe_expert_matmul_workspace_bytes(int32_t n_experts, int32_t M, int32_t n) {
+  if (n_experts <= 0 || M <= 0 || n <= 0) return 0;
   return align_up((size_t)(n_experts + 1) * 4, 256) +
-         align_up((1 + 2 * (size_t)gemm_max_tiles(M, n_experts)) * 4, 256);
+         align_up(gemm_items_bytes(M, n_experts, n, false), 256);
 }
 
 extern "C" moe_status moe_expert_matmul(const moe_qproj* p, const void* a, int32_t a_dtype,
@@ -944,15 +936,17 @@ extern "C" moe_status moe_expert_matmul(const moe_qproj* p, const void* a, int32
   if (!dt_ok(a_dtype) || !pair_ok(a_dtype, p->sb_dtype))
     return fail(MOE_ERR_UNSUPPORTED, "expert_matmul: activation/scale dtype pair not built");
   if (p->n_experts > 1024) return fail(MOE_ERR_UNSUPPORTED, "expert_matmul: n_experts above 1024");
-  const size_t need = moe_expert_matmul_workspace_bytes(p->n_experts, M);
+  const size_t need = moe_expert_matmul_workspace_bytes(p->n_experts, M, p->n);
   if (!workspace || workspace_bytes < need)
     return fail(MOE_ERR_WORKSPACE, "expert_matmul: workspace of %zu bytes needed", need);
   if (gemm_ok(*p, a_dtype, M, out)) {
-    uint32_t* tiles = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(workspace) +
+    uint32_t* items = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(workspace) +
                                                   align_up((size_t)(p->n_experts + 1) * 4, 256));
-    MOE_HIP(launch_gemm_tiles(offsets, p->n_experts, kGemmRows, tiles, stream), "tile list launch");
-    MOE_TRY(run_gemm(*p, nullptr, a, a_dtype, perm, top_k, offsets, tiles, M, out, 0, 0.f, 0.f,
-                     stream));
+    MOE_HIP(launch_gemm_items(offsets, p->n_experts, p->n, false, items, 0, false, nullptr, stream),
+            "GEMM work list launch");
+    // bf16 rows are converted to the f16 operand while staging
+    MOE_TRY(run_gemm(*p, nullptr, a, a_dtype, a_dtype == MOE_BF16, false, perm, top_k, offsets,
+                     items, M, out, 0, 0.f, 0.f, stream));
     return ok();
   }
   uint32_t* used = reinterpret_cast<uint32_t*>(workspace);
@@ -1143,7 +1137,9 @@ class SideFork {
   moe_status status_ = MOE_OK;
 };
 
-moe_status shared_expert(const moe_layer_desc* d, const void* x, int T, void* ws,
+// x16: the layer input as the GEMMs' f16 operand (written before the fork
+// when the grouped GEMM runs for the shared expert).
+moe_status shared_expert(const moe_layer_desc* d, const void* x, const void* x16, int T, void* ws,
                          const Workspace& w, hipStream_t st, int* smode) {
   *smode = 0;
   if (!d->has_shared) return MOE_OK;
@@ -1155,16 +1151,17 @@ moe_status shared_expert(const moe_layer_desc* d, const void* x, int T, void* ws
   const bool gated = d->activation != MOE_ACT_RELU2;
   const moe_qproj& p0 = gated ? d->shared_gate : d->shared_up;
   const moe_qproj* p1 = gated ? &d->shared_up : nullptr;
-  if (gemm_ok(p0, xdt, T) && gemm_ok(d->shared_down, xdt, T)) {
+  if (shared_gemm(d, T)) {
     // many tokens through one expert: the matrix-core path
-    MOE_HIP(launch_gemm_tiles(at<uint32_t>(ws, w.s_off), 1, kGemmRows, at<uint32_t>(ws, w.s_tiles),
-                              st),
-            "shared tile list launch");
-    MOE_TRY(run_gemm(p0, p1, x, xdt, nullptr, 1, at<uint32_t>(ws, w.s_off),
-                     at<uint32_t>(ws, w.s_tiles), T, at<void>(ws, w.s_act), d->activation,
+    MOE_HIP(launch_gemm_items(at<uint32_t>(ws, w.s_off), 1, p0.n, p1 != nullptr,
+                              at<uint32_t>(ws, w.s_items_gu), d->hidden, false,
+                              at<uint32_t>(ws, w.s_items_dn), st),
+            "shared GEMM work list launch");
+    MOE_TRY(run_gemm(p0, p1, x16, xdt, false, true, nullptr, 1, at<uint32_t>(ws, w.s_off),
+                     at<uint32_t>(ws, w.s_items_gu), T, at<void>(ws, w.s_act), d->activation,
                      d->act_alpha, d->act_limit, st));
-    MOE_TRY(run_gemm(d->shared_down, nullptr, at<void>(ws, w.s_act), xdt, nullptr, 1,
-                     at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_tiles), T,
+    MOE_TRY(run_gemm(d->shared_down, nullptr, at<void>(ws, w.s_act), xdt, false, false, nullptr, 1,
+                     at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_items_dn), T,
                      at<void>(ws, w.s_out), 0, 0.f, 0.f, st));
   } else {
     MOE_TRY(run_gemv(p0, p1, x, xdt, nullptr, 1, at<uint32_t>(ws, w.s_off),
@@ -1341,13 +1338,19 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     MOE_HIP(launch_router_q(q.bits, rx, xdt, T, H, to_proj(q), q.sb_dtype, group_shift(q.group_size),
                             d->router_bias, E, at<void>(ws, w.logits), st),
             "quantised router launch");
-  } else if (router_gemm_ok(d, T)) {
-    MOE_TRY(run_router_gemm(d, rx, T, at<void>(ws, w.logits), at<uint32_t>(ws, w.r_plan),
-                            at<uint32_t>(ws, w.r_tiles), st));
   } else {
     MOE_HIP(launch_router_logits(rx, xdt, T, H, d->router_weight, d->router_dtype, d->router_bias,
                                  E, at<void>(ws, w.logits), st),
             "router logits launch");
+  }
+
+  // the grouped GEMMs read the layer input as f16 operands: a bf16 input is
+  // scaled into f16 range once here, for the routed and the shared expert
+  const bool gemm = !(T == 1 && dec1_supported(d)) && routed_gemm(d, T);
+  const void* x16 = x;
+  if ((gemm || shared_gemm(d, T)) && xdt == MOE_BF16) {
+    MOE_HIP(launch_to_a16(x, at<void>(ws, w.x16), (int64_t)T * H, st), "f16 operand launch");
+    x16 = at<void>(ws, w.x16);
   }
 
   const bool dec1 = (T == 1 && dec1_supported(d));
@@ -1358,7 +1361,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
   // layer 3.5 us more than they saved)
   SideFork side(allow_side && d->has_shared && T >= kGemmMinRows, st);
   MOE_TRY(side.status());
-  MOE_TRY(shared_expert(d, x, T, ws, w, side.stream(), &smode));
+  MOE_TRY(shared_expert(d, x, x16, T, ws, w, side.stream(), &smode));
   MOE_TRY(side.mark());
   if (dec1) {
     // 2. one token: routing inside the gate/up kernel (MoELayer.swift:1167-1282
@@ -1421,14 +1424,14 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     const bool gated = d->activation != MOE_ACT_RELU2;
     const moe_qproj& p0 = gated ? d->gate : d->up;
     const moe_qproj* p1 = gated ? &d->up : nullptr;
-    const bool gemm = gemm_ok(p0, xdt, M) && gemm_ok(d->down, xdt, M);
     // 3. gate/up + activation over the plan (MoELayer.swift:883-893)
     if (gemm) {
-      MOE_HIP(launch_gemm_tiles(at<uint32_t>(ws, w.offsets), E, kGemmRows, at<uint32_t>(ws, w.tiles),
+      MOE_HIP(launch_gemm_items(at<uint32_t>(ws, w.offsets), E, p0.n, p1 != nullptr,
+                                at<uint32_t>(ws, w.items_gu), H, false, at<uint32_t>(ws, w.items_dn),
                                 st),
-              "tile list launch");
-      MOE_TRY(run_gemm(p0, p1, x, xdt, at<uint32_t>(ws, w.perm), k,
-                       at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.tiles), M,
+              "GEMM work list launch");
+      MOE_TRY(run_gemm(p0, p1, x16, xdt, false, true, at<uint32_t>(ws, w.perm), k,
+                       at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.items_gu), M,
                        at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st, kev(0)));
     } else {
       MOE_TRY(run_gemv(p0, p1, x, xdt, at<uint32_t>(ws, w.perm), k,
@@ -1438,9 +1441,9 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     }
     // 4. down projection, then the weighted combine (MoELayer.swift:899-939)
     if (gemm) {
-      MOE_TRY(run_gemm(d->down, nullptr, at<void>(ws, w.act), xdt, nullptr, 1,
-                       at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.tiles), M, at<void>(ws, w.Y),
-                       0, 0.f, 0.f, st, kev(1)));
+      MOE_TRY(run_gemm(d->down, nullptr, at<void>(ws, w.act), xdt, false, false, nullptr, 1,
+                       at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.items_dn), M,
+                       at<void>(ws, w.Y), 0, 0.f, 0.f, st, kev(1)));
     } else {
       MOE_TRY(run_gemv(d->down, nullptr, at<void>(ws, w.act), xdt, nullptr, 1,
                        at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, T == 1,
@@ -1466,7 +1469,7 @@ moe_layer_paths layer_paths(const moe_layer_desc* d, int T, bool x_aligned) {
   const moe_qproj* p1 = gated ? &d->up : nullptr;
   if (T == 1 && dec1_supported(d)) {
     p.gate_up = p.down = MOE_PATH_DECODE1;
-  } else if (gemm_ok(p0, xdt, M) && gemm_ok(d->down, xdt, M)) {
+  } else if (routed_gemm(d, T)) {
     p.gate_up = p.down = MOE_PATH_GEMM;
   } else {
     const int slots = std::min(E, M);
@@ -1476,7 +1479,7 @@ moe_layer_paths layer_paths(const moe_layer_desc* d, int T, bool x_aligned) {
   if (d->has_shared) {
     const moe_qproj& s0 = gated ? d->shared_gate : d->shared_up;
     const moe_qproj* s1 = gated ? &d->shared_up : nullptr;
-    if (gemm_ok(s0, xdt, T) && gemm_ok(d->shared_down, xdt, T)) {
+    if (shared_gemm(d, T)) {
       p.shared_gate_up = p.shared_down = MOE_PATH_GEMM;
     } else {
       p.shared_gate_up = gk(gemv_kind(s0, s1, x_aligned, xdt, 1, T, T == 1, 1 << 30));

@@ -320,54 +320,91 @@ hipError_t launch_dispatch_plan(const uint32_t* idx, int T, int k, int E, uint32
   return hipGetLastError();
 }
 
-// Row tiles of an expert-sorted plan for the grouped GEMM: tiles[0] = count,
-// then (expert, first sorted position) pairs, experts ascending, tiles of
-// bm positions (the last tile of an expert may be partial).
-__global__ __launch_bounds__(kPlanThreads) void gemm_tiles_kernel(const uint32_t* __restrict__ offsets,
-                                                                  int E, int bm,
-                                                                  uint32_t* __restrict__ tiles) {
-  // An expert's rows are covered by bm-row tiles; a last partial tile of at
-  // most bm / 2 rows is a half tile (its expert id carries kHalfTile), so
-  // the kernel spreads it over all its waves instead of leaving half idle.
-  __shared__ uint32_t scan[kPlanThreads];
+// Work items of the grouped GEMM over an expert-sorted plan (the list format
+// is described at launch_gemm_items). Thread t takes experts t * EPT .. + EPT;
+// one block scan gives each thread's first item.
+struct ItemCols {
+  int nb[2][3];  // column blocks per tile shape, for each of the two lists
+};
+
+__global__ __launch_bounds__(kPlanThreads) void gemm_items_kernel(
+    const uint32_t* __restrict__ offsets, int E, const ItemCols ic, uint32_t* __restrict__ items0,
+    uint32_t* __restrict__ items1) {
+  __shared__ uint32_t scan[2][kPlanThreads];
   constexpr int EPT = kPlanMaxE / kPlanThreads;  // experts per thread
   const int t = threadIdx.x;
-  const uint32_t hb = (uint32_t)bm / 2u;
-  uint32_t n[EPT], tot = 0;
+  uint32_t rows[EPT], first[EPT], tot0 = 0, tot1 = 0;
 #pragma unroll
   for (int j = 0; j < EPT; j++) {
     const int e = t * EPT + j;
-    n[j] = 0;
-    if (e < E) n[j] = (offsets[e + 1] - offsets[e] + (uint32_t)bm - 1) / (uint32_t)bm;
-    tot += n[j];
+    rows[j] = 0;
+    first[j] = 0;
+    if (e < E) {
+      first[j] = offsets[e];
+      rows[j] = offsets[e + 1] - first[j];
+    }
+    const uint32_t full = rows[j] / 256u, rem = rows[j] % 256u;
+    // the remainder takes the smallest shape that holds it
+    const int rs = rem > 128u ? 0 : (rem > 64u ? 1 : 2);
+    tot0 += full * (uint32_t)ic.nb[0][0] + (rem ? (uint32_t)ic.nb[0][rs] : 0u);
+    tot1 += full * (uint32_t)ic.nb[1][0] + (rem ? (uint32_t)ic.nb[1][rs] : 0u);
   }
-  scan[t] = tot;
+  scan[0][t] = tot0;
+  scan[1][t] = tot1;
   __syncthreads();
   for (int off = 1; off < kPlanThreads; off <<= 1) {
-    const uint32_t v = t >= off ? scan[t - off] : 0u;
+    const uint32_t v0 = t >= off ? scan[0][t - off] : 0u;
+    const uint32_t v1 = t >= off ? scan[1][t - off] : 0u;
     __syncthreads();
-    scan[t] += v;
+    scan[0][t] += v0;
+    scan[1][t] += v1;
     __syncthreads();
   }
-  uint32_t base = scan[t] - tot;
+  uint32_t base0 = scan[0][t] - tot0, base1 = scan[1][t] - tot1;
 #pragma unroll
   for (int j = 0; j < EPT; j++) {
-    const int e = t * EPT + j;
-    const uint32_t rows = e < E ? offsets[e + 1] - offsets[e] : 0u;
-    for (uint32_t i = 0; i < n[j]; i++) {
-      const uint32_t left = rows - i * (uint32_t)bm;
-      tiles[1 + 2 * (base + i)] = (uint32_t)e | (left <= hb ? kHalfTile : 0u);
-      tiles[2 + 2 * (base + i)] = offsets[e] + i * (uint32_t)bm;
+    const uint32_t e = (uint32_t)(t * EPT + j);
+    for (uint32_t r0 = 0; r0 < rows[j]; r0 += 256u) {
+      const uint32_t left = rows[j] - r0;
+      const uint32_t shape = left > 128u ? 0u : (left > 64u ? 1u : 2u);
+      const uint32_t tag = e | (shape << 30);
+      const uint32_t nb0 = (uint32_t)ic.nb[0][shape];
+      for (uint32_t b = 0; b < nb0; b++) {
+        uint32_t* it = items0 + 1 + 3 * (base0 + b);
+        it[0] = tag;
+        it[1] = first[j] + r0;
+        it[2] = b;
+      }
+      base0 += nb0;
+      if (items1) {
+        const uint32_t nb1 = (uint32_t)ic.nb[1][shape];
+        for (uint32_t b = 0; b < nb1; b++) {
+          uint32_t* it = items1 + 1 + 3 * (base1 + b);
+          it[0] = tag;
+          it[1] = first[j] + r0;
+          it[2] = b;
+        }
+        base1 += nb1;
+      }
     }
-    base += n[j];
   }
-  if (t == kPlanThreads - 1) tiles[0] = scan[t];
+  if (t == kPlanThreads - 1) {
+    items0[0] = scan[0][t];
+    if (items1) items1[0] = scan[1][t];
+  }
 }
 
-hipError_t launch_gemm_tiles(const uint32_t* offsets, int E, int bm, uint32_t* tiles,
+hipError_t launch_gemm_items(const uint32_t* offsets, int E, int N0, bool gateup0,
+                             uint32_t* items0, int N1, bool gateup1, uint32_t* items1,
                              hipStream_t st) {
   if (E > kPlanMaxE) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(gemm_tiles_kernel, dim3(1), dim3(kPlanThreads), 0, st, offsets, E, bm, tiles);
+  ItemCols ic{};
+  for (int sh = 0; sh < 3; sh++) {
+    ic.nb[0][sh] = (N0 + gemm_cols(sh, gateup0) - 1) / gemm_cols(sh, gateup0);
+    ic.nb[1][sh] = items1 ? (N1 + gemm_cols(sh, gateup1) - 1) / gemm_cols(sh, gateup1) : 0;
+  }
+  hipLaunchKernelGGL(gemm_items_kernel, dim3(1), dim3(kPlanThreads), 0, st, offsets, E, ic, items0,
+                     items1);
   return hipGetLastError();
 }
 

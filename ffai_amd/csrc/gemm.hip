@@ -2,26 +2,42 @@
 //
 // Replaces Ops.moeGatherDequantGemmInt4 bm8/bm16/bm64/m1
 // (Sources/FFAI/Ops/Ops.swift:4553-5201, 6499-6585) with the tile choice of
-// MoELayer.swift:855-882, generalised to 2/3/4/5/6/8-bit weights, any
-// group size in {32, 64, 128} and scale dtypes independent of the
-// activation dtype:
+// MoELayer.swift:855-882, generalised to 2/3/4/5/6/8-bit weights, group sizes
+// 32/64/128 and scale dtypes independent of the activation dtype:
 //   gate/up:  act[p, n] = act_fn(round(Wg[e(p)][n] . x[row(p)]),
 //                                round(Wu[e(p)][n] . x[row(p)]))
 //   single:   out[p, n] = round(W[e(p)][n] . a[p])
 // over the expert-sorted positions p of a dispatch plan.
 //
-// Work: a tile list of (expert, up to 256 consecutive sorted positions; the
-// last tile of an expert with at most 128 rows is a half tile); block = one
-// tile x one column slice (256 weight rows). Per 64-value chunk of K the
-// block stages the tile's activation rows and the slice's weights,
-// dequantised once per block to the MFMA operand type, in double-buffered
-// LDS; 8 waves multiply with v_mfma_f32_32x32x16 (see the kernel comment).
-// Dequantisation: codes -> fp32 (exact) -> s*q + b (fp32) -> bf16 / f16.
+// Operands are f16 on v_mfma_f32_32x32x16_f16:
+//  - weights are dequantised exactly to s * q + b rounded once to f16
+//    (2^-12 relative; bf16 operands would round them to 2^-9): codes enter
+//    as 1024 + q (exact in f16), one packed subtraction gives q, one packed
+//    fma s * q + b;
+//  - activations of an f16 layer are used as they are; those of a bf16 layer
+//    are scaled by 2^-8 into f16 range (exact for magnitudes 2^-6 .. 1.6e7,
+//    saturating beyond), either beforehand (launch_to_a16, and the gate/up
+//    epilogue writes its activation in that form for the down GEMM) or while
+//    staging (a_bf16); the epilogue multiplies the fp32 sums by 2^8.
 //
-// K order inside a 64-value chunk: lane half h of the wave takes values
-// [32h, 32h + 32) — one whole 32-value unit — and step s (0..3) of the
-// 16-deep MFMA reduction feeds values 16 s + 8 h + e, e < 8 (LDS chunk
-// 2 s + h of the row); A and B fragments are read in the same order.
+// Work: a list of items (expert, first sorted position, column block) built
+// on the device from the CSR offsets (launch_gemm_items). An expert's rows go
+// in tiles of 256, and its last tile takes the smallest block shape that holds
+// the rest, so the matrix cores see few padded rows:
+//   shape 0: 256 rows x 256 weight rows, waves 4 x 2, 64 x 128 per wave;
+//   shape 1: 128 rows x 256 weight rows, waves 2 x 4, 64 x 64 per wave;
+//   shape 2:  64 rows x 512 weight rows, waves 1 x 8, 64 x 64 per wave.
+// A wave owns 64 rows x NJ * 32 weight rows (gate/up: half gate, half up, so
+// the epilogue pairs them in one lane). (128 x 512 with 64 x 128 per wave
+// would match shape 0's MFMA work per block but needs two weight units per
+// thread next to 128 accumulators and spills registers.) Blocks b, b + 8, ...
+// run on one XCD: the items are split into 8 contiguous ranges at run time,
+// one per XCD, so neighbouring column blocks of a row tile share its L2.
+//
+// Per 64-value chunk of K the block stages the tile's activation rows and its
+// weight rows (dequantised once per block) in double-buffered LDS; global loads
+// run two chunks ahead in registers, the next chunk's weights are dequantised
+// between the MFMA steps, and block barriers order LDS only.
 #include <hip/hip_ext.h>
 
 #include <type_traits>
@@ -35,282 +51,308 @@
 
 namespace moe {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-struct ProjViewG {
-  rsrc_t w, s, b;
-};
-
-constexpr int kGBK = 64;  // values per K chunk
-
-template <typename XT> struct MfmaOp;
-template <> struct MfmaOp<bf16_t> {
-  typedef bf16x8_t V;
-  static __device__ __forceinline__ f32x16_t mma(V a, V b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-  }
-};
-template <> struct MfmaOp<f16_t> {
-  typedef f16x8_t V;
-  static __device__ __forceinline__ f32x16_t mma(V a, V b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-  }
-};
-
-// Code e (0..7) of step s (0..3) of a 32-value unit, as an exact float.
-template <int BITS>
-__device__ __forceinline__ float unit_code(const uint32_t (&w)[BITS], int s, int e) {
-  const int bit = (8 * s + e) * BITS;
-  const int lo = bit >> 5, sh = bit & 31;
-  uint32_t v = w[lo] >> sh;
-  if (sh + BITS > 32) v |= w[lo + 1] << (32 - sh);
-  return (float)(v & ((1u << BITS) - 1u));
+__device__ __forceinline__ f32x16_t mma_f16(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
-// Eight dequantised weights of step s: w = s * q + b rounded to the MFMA
-// operand type. 4-bit codes are split into byte lanes first so every code
-// converts with one v_cvt_f32_ubyte.
-template <int BITS, typename XT>
-__device__ __forceinline__ typename MfmaOp<XT>::V dequant8(const uint32_t (&w)[BITS], int s,
-                                                          float sc, float bi) {
-  if constexpr (BITS == 16) {
-    // plain weights already in the operand type
-    (void)sc;
-    (void)bi;
-    return __builtin_bit_cast(typename MfmaOp<XT>::V, u32x4_t{w[4 * s], w[4 * s + 1], w[4 * s + 2], w[4 * s + 3]});
-  }
-  float q[8];
-  if constexpr (BITS == 4) {
-    const uint32_t lo = w[s] & 0x0F0F0F0Fu, hi = (w[s] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      q[2 * j] = (float)((lo >> (8 * j)) & 0xFFu);
-      q[2 * j + 1] = (float)((hi >> (8 * j)) & 0xFFu);
-    }
-  } else if constexpr (BITS == 8) {
-#pragma unroll
-    for (int e = 0; e < 8; e++) q[e] = (float)((w[2 * s + (e >> 2)] >> (8 * (e & 3))) & 0xFFu);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; e++) q[e] = unit_code<BITS>(w, s, e);
-  }
-  typename MfmaOp<XT>::V r;
-#pragma unroll
-  for (int e = 0; e < 8; e++) r[e] = from_f<XT>(__builtin_fmaf(sc, q[e], bi));
-  return r;
-}
+constexpr int kGBK = 64;  // values per K chunk (128 bytes of an LDS row)
 
-template <int BITS, typename ST>
-__device__ __forceinline__ ProjViewG proj_view_g(const GemvProj& p, uint32_t e, int N,
-                                                 int row_words, int groups) {
-  const size_t rows = (size_t)e * (size_t)N;
-  ProjViewG v;
-  v.w = make_rsrc(p.w + rows * row_words, (uint32_t)N * (uint32_t)row_words * 4u);
-  v.s = make_rsrc(reinterpret_cast<const ST*>(p.s) + rows * groups,
-                  (uint32_t)N * (uint32_t)groups * (uint32_t)sizeof(ST));
-  v.b = make_rsrc(reinterpret_cast<const ST*>(p.b) + rows * groups,
-                  (uint32_t)N * (uint32_t)groups * (uint32_t)sizeof(ST));
-  return v;
-}
-
-// LDS tile of 256 rows x 64 values (16-bit), 128 B per row. The banks
-// repeat every 256 B (two rows) and a 16-byte read serves 16 lanes per
-// cycle, so the 16-byte chunk c of row r sits at slot c ^ ((r >> 1) & 7):
-// 16 consecutive rows reading the same chunk then cover every bank once.
-constexpr int kTR = 256;
+// LDS tiles are 128 B per row. The banks repeat every 256 B (two rows) and a
+// 16-byte read serves 16 lanes per cycle, so the 16-byte chunk c of row r
+// sits at slot c ^ ((r >> 1) & 7): 16 consecutive rows reading the same
+// chunk then cover every bank once.
 __device__ __forceinline__ int tile_swz(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ uint32_t tile_off(int r, int c) {
   return (uint32_t)(r * 128 + ((c ^ tile_swz(r)) << 4));
 }
 
-// Block tile: 256 rows x 256 weight rows (gate/up: 128 output columns of
-// gate and of up; otherwise 256 output columns), 8 waves in a 4 x 2 grid:
-// wave (wm, wn) owns rows [64 wm, +64) as 2 MFMA row tiles and 4 MFMA column
-// tiles (gate/up: gate columns [64 wn, +64) and the matching up columns), so
-// its accumulators fit 128 registers and two waves share each SIMD. Row
-// tiles past the expert's last position skip their MFMAs. A half tile (the
-// last tile of an expert, at most 128 rows) gives each wave the 32-row band
-// [32 wm, +32) instead, so its rows are spread over all four SIMDs.
-//
-// Per 64-value chunk: every thread copies 64 bytes of activation rows and
-// dequantises one 32-value unit of one weight row into LDS, once for the
-// whole block, and each wave runs 4 steps x 8 v_mfma_f32_32x32x16. Global
-// loads run two chunks ahead of the MFMAs; chunk c + 1 is written to LDS
-// (its weights dequantised between the MFMA steps) while chunk c is
-// multiplied.
-// All operand rows of a lane are congruent mod 16, so one swizzled chunk
-// offset per step serves every LDS read (immediate row offsets).
-template <int BITS, typename XT, typename ST, bool GATEUP>
-__global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
-  __shared__ __align__(16) unsigned char As[2][kTR * 128];
-  __shared__ __align__(16) unsigned char Bs[2][kTR * 128];
-  typedef typename MfmaOp<XT>::V V;
+template <int S> struct GShape;
+template <> struct GShape<0> { static constexpr int MR = 256, NR = 256, WMN = 4, NJ = 4; };
+template <> struct GShape<1> { static constexpr int MR = 128, NR = 256, WMN = 2, NJ = 2; };
+template <> struct GShape<2> { static constexpr int MR = 64, NR = 512, WMN = 1, NJ = 2; };
+
+struct ProjViewG {
+  rsrc_t w, s, b;
+};
+template <int BITS>
+__device__ __forceinline__ ProjViewG proj_view_g(const GemvProj& p, uint32_t e, int N, int row_words,
+                                                 int groups) {
+  const size_t rows = (size_t)e * (size_t)N;
+  ProjViewG v;
+  v.w = make_rsrc(p.w + rows * row_words, (uint32_t)N * (uint32_t)row_words * 4u);
+  v.s = make_rsrc(reinterpret_cast<const uint16_t*>(p.s) + rows * groups, (uint32_t)N * (uint32_t)groups * 2u);
+  v.b = make_rsrc(reinterpret_cast<const uint16_t*>(p.b) + rows * groups, (uint32_t)N * (uint32_t)groups * 2u);
+  return v;
+}
+
+// Values 8 s + 2 p and 8 s + 2 p + 1 (p < 4) of a 32-value unit as 16-bit
+// pairs 0x6400 | q, i.e. 1024 + q in f16 (exact for q < 1024).
+template <int BITS>
+__device__ __forceinline__ void quarter_pairs(const uint32_t (&w)[BITS], int s, uint32_t (&pr)[4]) {
+  const uint32_t M = opaque_vgpr(0x64006400u);
+  if constexpr (BITS == 4) {
+    // word s holds the quarter: nibbles 0, 2, 4, 6 in the bytes of t, 1, 3, 5, 7 in u
+    const uint32_t t = w[s] & 0x0F0F0F0Fu, u = (w[s] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+    for (int p = 0; p < 4; p++)  // bytes [t.p, 0, u.p, 0]
+      pr[p] = __builtin_amdgcn_perm(u, t, (uint32_t)p | 0x0C00u | ((uint32_t)(4 + p) << 16) | 0x0C000000u) | M;
+  } else if constexpr (BITS == 8) {
+#pragma unroll
+    for (int p = 0; p < 4; p++) {  // bytes [b(2p), 0, b(2p+1), 0] of word 2 s + p / 2
+      const int bb = 2 * (p & 1);
+      pr[p] = __builtin_amdgcn_perm(0u, w[2 * s + (p >> 1)],
+                                    (uint32_t)bb | 0x0C00u | ((uint32_t)(bb + 1) << 16) | 0x0C000000u) | M;
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      uint32_t c[2];
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        const int bit = (8 * s + 2 * p + k) * BITS, lo = bit >> 5, sh = bit & 31;
+        uint32_t v = w[lo] >> sh;
+        if (sh + BITS > 32) v |= w[lo + 1] << (32 - sh);
+        c[k] = v & ((1u << BITS) - 1u);
+      }
+      pr[p] = (c[0] | (c[1] << 16)) | M;
+    }
+  }
+}
+
+// A 16-bit scale or bias (bf16 or f16 storage) as an f16 pair.
+__device__ __forceinline__ h2_t sb_h2(uint32_t raw16, bool bf16) {
+  _Float16 h;
+  if (bf16) h = (_Float16)__uint_as_float(raw16 << 16);  // exact inside f16's range
+  else h = __builtin_bit_cast(_Float16, (uint16_t)raw16);
+  return h2_t{h, h};
+}
+
+// Two bf16 values -> f16 * 2^-8 (round toward zero, so finite values saturate
+// instead of overflowing; exact wherever the result is a normal f16).
+__device__ __forceinline__ uint32_t bf2_to_a16(uint32_t u) {
+  const float lo = __builtin_ldexpf(__uint_as_float(u << 16), -kA16Shift);
+  const float hi = __builtin_ldexpf(__uint_as_float(u & 0xFFFF0000u), -kA16Shift);
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+}
+
+// One stored output value (fp32, already in the output's units) as the f16 A
+// operand of the next GEMM: round to the layer dtype first (the reference
+// stores the activation in it), then scale into f16 range, saturating.
+template <typename XT>
+__device__ __forceinline__ _Float16 to_a16(float v) {
+  v = round_to<XT>(v);
+  if constexpr (__is_same(XT, bf16_t)) {
+    v = __builtin_ldexpf(v, -kA16Shift);
+    v = fminf(fmaxf(v, -65504.0f), 65504.0f);
+  }
+  return (_Float16)v;
+}
+
+// One block's tile: rows [m0, m0 + MR) of expert e (positions below pend),
+// weight rows of column block bn.
+template <int S, int BITS, typename XT, bool GATEUP, bool ABF16>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds, uint32_t e,
+                                          uint32_t m0, int bn) {
+  typedef GShape<S> G;
+  constexpr int MR = G::MR, NR = G::NR, WMN = G::WMN, WN = 8 / WMN, NJ = G::NJ;
+  constexpr int ABUF = MR * 128, BBUF = NR * 128;
+  constexpr int AI = MR / 64;       // activation copies of 16 B per thread per chunk
+  constexpr int BI = NR * 2 / 512;  // weight units per thread per chunk
+  constexpr float OSCALE = __is_same(XT, bf16_t) ? (float)(1 << kA16Shift) : 1.0f;
+  unsigned char* As = lds;
+  unsigned char* Bs = lds + 2 * ABUF;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  const int ncols = GATEUP ? 128 : 256;  // output columns per block
-  const int n_tiles = (a.N + ncols - 1) / ncols;
-
-  // blocks b, b + 8, b + 16, ... share an XCD (and its L2): give them
-  // consecutive work items, column slices of one row tile first
-  const uint32_t per = gridDim.x >> 3;
-  const uint32_t wi = (blockIdx.x & 7u) * per + (blockIdx.x >> 3);
-  const uint32_t ntile = a.tiles[0];
-  if (wi >= ntile * (uint32_t)n_tiles) return;
-  const uint32_t tile = wi / (uint32_t)n_tiles;
-  const int bn = (int)(wi - tile * (uint32_t)n_tiles);
-  // tile fields are block-uniform; readfirstlane keeps the buffer resources
-  // built from them scalar
-  const uint32_t ef = __builtin_amdgcn_readfirstlane(a.tiles[1 + 2 * tile]);
-  const uint32_t e = ef & ~kHalfTile;
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(a.tiles[2 + 2 * tile]);
-  // rows per wave band: 64 (two MFMA row tiles) in a full 256-row tile, 32
-  // (one) in a half tile, so that all four SIMDs share a short tile's rows
-  const int band = (ef & kHalfTile) ? 32 : 64;
+  const int wm = wave / WN, wn = wave % WN;
   const uint32_t pend = __builtin_amdgcn_readfirstlane(a.offsets[e + 1]);
-
   const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
   const int nchunks = K / kGBK;
+  const bool sb_bf16 = a.sb_bf16 != 0;
 
-  // ---- activation rows: thread (wave, lane) copies, for i < 4, 16 bytes
-  // of LDS row 32 wave + 8 i + lane / 8, slot lane % 8 (logical chunk
-  // (lane % 8) ^ tile_swz(row)); two register sets keep chunk c + 2 in flight
-  // one wave-uniform buffer resource over all activation rows; per-lane
-  // 32-bit byte offsets of the four rows this lane copies
-  const rsrc_t xr = make_rsrc(a.x, (uint32_t)min((size_t)a.x_rows * K * sizeof(XT), (size_t)0xFFFFFFFFu));
-  uint32_t xoff[4];
+  // ---- activation rows: thread t copies, for i < AI, the 16 bytes of LDS
+  // row t / 8 + 64 i in slot t % 8 (logical chunk (t % 8) ^ tile_swz(row))
+  const rsrc_t xr = make_rsrc(a.x, (uint32_t)min((size_t)a.x_rows * K * 2u, (size_t)0xFFFFFFFFu));
+  uint32_t xoff[AI];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int r = 32 * wave + 8 * i + (lane >> 3);
+  for (int i = 0; i < AI; i++) {
+    const int r = (threadIdx.x >> 3) + 64 * i;
     const uint32_t p = min(m0 + (uint32_t)r, pend - 1);
     const uint32_t xrow = a.perm ? a.perm[p] / (uint32_t)a.topk : p;
-    const int c = (lane & 7) ^ tile_swz(r);
-    xoff[i] = (xrow * (uint32_t)K + (uint32_t)(8 * c)) * (uint32_t)sizeof(XT);
+    const int c = (threadIdx.x & 7) ^ tile_swz(r);
+    xoff[i] = (xrow * (uint32_t)K + (uint32_t)(8 * c)) * 2u;
   }
-  // LDS byte offset of load i: row 32 wave + 8 i + lane / 8, slot lane % 8
-  const uint32_t aoff0 = (uint32_t)((32 * wave + (lane >> 3)) * 128 + ((lane & 7) << 4));
+  const uint32_t aoff0 = (uint32_t)((threadIdx.x >> 3) * 128 + ((threadIdx.x & 7) << 4));
   struct ARegs {
-    u32x4_t v[4];
+    u32x4_t v[AI];
   };
   auto load_a = [&](int chunk, ARegs& ar) {
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      ar.v[i] = bload128(xr, xoff[i] + (uint32_t)(chunk * kGBK * (int)sizeof(XT)));
+    for (int i = 0; i < AI; i++) ar.v[i] = bload128(xr, xoff[i] + (uint32_t)(chunk * kGBK * 2));
   };
   auto store_a = [&](const ARegs& ar, int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4_t*>(&As[buf][aoff0 + 1024 * i]) = ar.v[i];
-  };
-
-  // ---- weights: thread t dequantises unit t % 2 (values [32 (t % 2), +32)
-  // of the chunk) of LDS weight row t / 2
-  const int brl = threadIdx.x >> 1, bu = threadIdx.x & 1;
-  const bool upper = GATEUP && wave >= 4;  // LDS rows 128..255 hold up (wave-uniform)
-  const int wrow = GATEUP ? bn * 128 + (brl & 127) : bn * 256 + brl;
-  const uint32_t brow = (uint32_t)min(wrow, N - 1);
-  const ProjViewG PB = proj_view_g<BITS, ST>(upper ? a.p1 : a.p0, e, N, row_words, groups);
-  // packed codes, scale and bias of one unit: two register sets so that
-  // chunk c + 2 is in flight while chunk c + 1 is dequantised
-  struct BUnit {
-    uint32_t w[BITS];
-    ST s, b;
-  };
-  auto load_b = [&](int chunk, BUnit& u) {
-    const int unit = 2 * chunk + bu;
-    bload_unit<BITS>(PB.w, (brow * (uint32_t)row_words + (uint32_t)(unit * BITS)) * 4u, u.w);
-    if constexpr (BITS != 16) {
-      const uint32_t gi = brow * (uint32_t)groups + (uint32_t)(unit >> a.gsh);
-      u.s = __builtin_bit_cast(ST, bload16(PB.s, gi * (uint32_t)sizeof(ST)));
-      u.b = __builtin_bit_cast(ST, bload16(PB.b, gi * (uint32_t)sizeof(ST)));
+    for (int i = 0; i < AI; i++) {
+      u32x4_t v = ar.v[i];
+      if constexpr (ABF16) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) v[q] = bf2_to_a16(v[q]);
+      }
+      *reinterpret_cast<u32x4_t*>(As + buf * ABUF + aoff0 + 64 * 128 * i) = v;
     }
   };
-  // 8 values [8 s, 8 s + 8) of the unit -> LDS chunk 4 bu + s
-  auto store_b = [&](const BUnit& u, int s, int buf) {
-    const V v = BITS == 16 ? dequant8<BITS, XT>(u.w, s, 0.f, 0.f)
-                           : dequant8<BITS, XT>(u.w, s, to_f<ST>(u.s), to_f<ST>(u.b));
-    *reinterpret_cast<V*>(&Bs[buf][tile_off(brl, 4 * bu + s)]) = v;
+
+  // ---- weights: thread t dequantises, for i < BI, unit t % 2 (values
+  // [32 (t % 2), +32) of the chunk) of LDS weight row t / 2 + 256 i. Gate/up:
+  // LDS rows below NR / 2 hold gate rows, the rest up rows (for shape 0 that
+  // splits at wave 4, for the others at i = 1: wave-uniform either way).
+  const int bu = threadIdx.x & 1;
+  int brl[BI];
+  uint32_t brow[BI];
+  ProjViewG PB[BI];
+#pragma unroll
+  for (int i = 0; i < BI; i++) {
+    brl[i] = (threadIdx.x >> 1) + 256 * i;
+    int wrow;
+    bool upper = false;
+    if constexpr (GATEUP) {
+      upper = brl[i] >= NR / 2;
+      wrow = bn * (NR / 2) + (brl[i] & (NR / 2 - 1));
+    } else {
+      wrow = bn * NR + brl[i];
+    }
+    brow[i] = (uint32_t)min(wrow, N - 1);
+    // upper is wave-uniform (see above); the branch keeps the views scalar
+    if (GATEUP && __builtin_amdgcn_readfirstlane((int)upper))
+      PB[i] = proj_view_g<BITS>(a.p1, e, N, row_words, groups);
+    else
+      PB[i] = proj_view_g<BITS>(a.p0, e, N, row_words, groups);
+  }
+  // packed codes, scale and bias of a thread's units: two register sets, so
+  // chunk c + 2 is in flight while chunk c + 1 is dequantised
+  struct BUnits {
+    uint32_t w[BI][BITS];
+    uint32_t sb[BI];  // scale | bias << 16, raw 16-bit storage
+  };
+  auto load_b = [&](int chunk, BUnits& u) {
+    const int unit = 2 * chunk + bu;
+#pragma unroll
+    for (int i = 0; i < BI; i++) {
+      bload_unit<BITS>(PB[i].w, (brow[i] * (uint32_t)row_words + (uint32_t)(unit * BITS)) * 4u, u.w[i]);
+      const uint32_t gi = (brow[i] * (uint32_t)groups + (uint32_t)(unit >> a.gsh)) * 2u;
+      u.sb[i] = (uint32_t)bload16(PB[i].s, gi) | ((uint32_t)bload16(PB[i].b, gi) << 16);
+    }
+  };
+  // values [8 s, 8 s + 8) of each unit -> LDS chunk 4 bu + s of its row
+  auto store_b = [&](const BUnits& u, const h2_t (&s2)[BI], const h2_t (&b2)[BI], int s, int buf) {
+#pragma unroll
+    for (int i = 0; i < BI; i++) {
+      uint32_t pr[4];
+      quarter_pairs<BITS>(u.w[i], s, pr);
+      u32x4_t v;
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const h2_t q = __builtin_bit_cast(h2_t, pr[p]) - h2_t{(_Float16)1024.0f, (_Float16)1024.0f};
+        v[p] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2[i], b2[i]));
+      }
+      *reinterpret_cast<u32x4_t*>(Bs + buf * BBUF + tile_off(brl[i], 4 * bu + s)) = v;
+    }
+  };
+  auto sb_pairs = [&](const BUnits& u, h2_t (&s2)[BI], h2_t (&b2)[BI]) {
+#pragma unroll
+    for (int i = 0; i < BI; i++) {
+      s2[i] = sb_h2(u.sb[i] & 0xFFFFu, sb_bf16);
+      b2[i] = sb_h2(u.sb[i] >> 16, sb_bf16);
+    }
   };
 
-  f32x16_t acc[2][4];
+  f32x16_t acc[2][NJ];
 #pragma unroll
   for (int i = 0; i < 2; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = f32x16_t{};
+    for (int j = 0; j < NJ; j++) acc[i][j] = f32x16_t{};
 
-  // row tiles of this wave's band that hold positions of the expert
-  const uint32_t bstart = m0 + (uint32_t)(band * wm);
-  const int mvalid = (bstart >= pend) ? 0 : (band == 32 || bstart + 32u >= pend) ? 1 : 2;
+  // row tiles of this wave's 64-row band that hold positions of the expert
+  const uint32_t bstart = m0 + 64u * (uint32_t)wm;
+  const int mvalid = (bstart >= pend) ? 0 : (bstart + 32u >= pend ? 1 : 2);
 
-  // MFMA operand rows of this lane: A rows band wm + 32 i + col, B rows
-  // (gate/up) 64 wn + 32 j + col and 128 + 64 wn + 32 (j - 2) + col, or
-  // 128 wn + 32 j + col; all congruent to col mod 16, so they share
-  // tile_swz(col)
+  // MFMA operand rows of this lane: A rows 64 wm + 32 i + col, B rows (LDS)
+  // 32 j + col within the wave's weight rows; all congruent to col mod 32, so
+  // they share tile_swz(col)
   const int col = lane & 31, h = lane >> 5;
-  const uint32_t arow0 = (uint32_t)(band * wm + col) * 128u;
-  const uint32_t brow0 = (uint32_t)((GATEUP ? 64 * wn : 128 * wn) + col) * 128u;
+  const uint32_t arow0 = (uint32_t)(64 * wm + col) * 128u;
   auto boff = [&](int j) -> uint32_t {
-    return GATEUP ? (uint32_t)((j < 2 ? 32 * j : 128 + 32 * (j - 2)) * 128) : (uint32_t)(32 * j * 128);
+    int r;
+    if constexpr (GATEUP) {
+      constexpr int HJ = NJ / 2;  // gate tiles, then the matching up tiles
+      r = (j < HJ ? 0 : NR / 2) + 32 * HJ * wn + 32 * (j % HJ);
+    } else {
+      r = 32 * NJ * wn + 32 * j;
+    }
+    return (uint32_t)(r + col) * 128u;
   };
 
   // One chunk: MFMAs on LDS buffer `buf`. First chunk c + 1's activations
-  // (loaded during chunk c - 1) go from `ar` to the other buffer, which
-  // chunk c - 1's closing barrier freed, and `ar` takes chunk c + 2's loads;
-  // chunk c + 1's weights (set nb) are dequantised into the other buffer
-  // between the MFMA steps, and chunk c + 2's weights load into the set cb
-  // that chunk c used. One activation register set suffices.
-  // Loads and LDS writes are unconditional (past the end they repeat the
-  // last chunk, in bounds and never read) so that the compiler can count
-  // outstanding loads exactly and never waits for the newest ones.
-  // MV: row tiles of this wave with positions of the expert (0..2), a
-  // compile-time constant so that each version of the loop is straight-line
-  // code the compiler can schedule across steps (a branch per row tile split
-  // every step into blocks that serialised LDS reads and MFMAs)
-  auto chunk_step = [&](auto mv, int c, int buf, ARegs& ar, BUnit& cb, const BUnit& nb) {
+  // (loaded during chunk c - 1) go from `ar` to the other buffer, which chunk
+  // c - 1's closing barrier freed, and `ar` takes chunk c + 2's loads; chunk
+  // c + 1's weights (set nb) are dequantised into the other buffer between
+  // the MFMA steps, and chunk c + 2's weights load into the set cb that chunk
+  // c used. Loads and LDS writes are unconditional (past the end they repeat
+  // the last chunk, in bounds and never read) so that the compiler can count
+  // outstanding loads exactly. MV: row tiles of this wave with positions of
+  // the expert (0..2), a compile-time constant, so each version of the loop
+  // is straight-line code.
+  auto chunk_step = [&](auto mv, int c, int buf, ARegs& ar, BUnits& cb, const BUnits& nb) {
     constexpr int MV = decltype(mv)::value;
     const int cp = min(c + 2, nchunks - 1);
     store_a(ar, buf ^ 1);
     load_a(cp, ar);
     load_b(cp, cb);
-    // keep chunk c + 2's loads issued here: sunk below the first weight
-    // dequantisation they turned its wait for chunk c + 1's weights into a
-    // wait for every load in flight
+    // keep chunk c + 2's loads issued here (sunk below the first weight
+    // dequantisation they would turn its wait into a wait for every load)
     __builtin_amdgcn_sched_barrier(0);
-    const unsigned char* Ab = &As[buf][0];
-    const unsigned char* Bb = &Bs[buf][0];
-    // operand fragments of step s + 1 are read while step s multiplies
-    V bf[2][4], af[2][2];
-    auto read_frags = [&](int s, V (&b)[4], V (&a2)[2]) {
+    h2_t s2[BI], b2[BI];
+    sb_pairs(nb, s2, b2);
+    const unsigned char* Ab = As + buf * ABUF;
+    const unsigned char* Bb = Bs + buf * BBUF;
+    u32x4_t bf[2][NJ], af[2][2];
+    auto read_frags = [&](int s, u32x4_t (&b)[NJ], u32x4_t (&a2)[2]) {
       const uint32_t sw = (uint32_t)(((2 * s + h) ^ tile_swz(col)) << 4);
 #pragma unroll
-      for (int j = 0; j < 4; j++) b[j] = *reinterpret_cast<const V*>(Bb + brow0 + boff(j) + sw);
+      for (int j = 0; j < NJ; j++) b[j] = *reinterpret_cast<const u32x4_t*>(Bb + boff(j) + sw);
 #pragma unroll
-      for (int i = 0; i < 2; i++) a2[i] = *reinterpret_cast<const V*>(Ab + arow0 + 32 * 128 * i + sw);
+      for (int i = 0; i < 2; i++) a2[i] = *reinterpret_cast<const u32x4_t*>(Ab + arow0 + 32 * 128 * i + sw);
     };
     read_frags(0, bf[0], af[0]);
 #pragma unroll
     for (int s = 0; s < 4; s++) {
       if (s < 3) read_frags(s + 1, bf[(s + 1) & 1], af[(s + 1) & 1]);
 #pragma unroll
-      for (int i = 0; i < MV; i++) {
+      for (int i = 0; i < MV; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = MfmaOp<XT>::mma(af[s & 1][i], bf[s & 1][j], acc[i][j]);
-      }
-      store_b(nb, s, buf ^ 1);
+        for (int j = 0; j < NJ; j++) acc[i][j] = mma_f16(af[s & 1][i], bf[s & 1][j], acc[i][j]);
+      store_b(nb, s2, b2, s, buf ^ 1);
     }
     lds_barrier();
   };
 
   ARegs ar;
-  BUnit u0, u1;
+  BUnits u0, u1;
   load_a(0, ar);
   load_b(0, u0);
   load_b(min(1, nchunks - 1), u1);
   store_a(ar, 0);
   load_a(min(1, nchunks - 1), ar);
+  {
+    h2_t s2[BI], b2[BI];
+    sb_pairs(u0, s2, b2);
 #pragma unroll
-  for (int s = 0; s < 4; s++) store_b(u0, s, 0);
+    for (int s = 0; s < 4; s++) store_b(u0, s2, b2, s, 0);
+  }
   lds_barrier();
 
   auto run = [&](auto mv) {
@@ -325,19 +367,17 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
   else run(std::integral_constant<int, 0>{});
 
   // epilogue: lane holds column col, rows 8 (r / 4) + 4 h + r % 4 of each
-  // 32 x 32 tile. The wave's finished outputs (64 rows x OC columns) go
+  // 32 x 32 tile. The wave's outputs (64 rows x OC columns, 16-bit) go
   // through LDS (free after the last barrier) so that the global stores are
-  // 16 contiguous bytes of one output row per lane instead of 2-byte stores.
-  XT* out = reinterpret_cast<XT*>(a.out);
+  // 16 contiguous bytes of one output row per lane.
+  constexpr int OC = GATEUP ? NJ * 16 : NJ * 32;  // output columns per wave
+  constexpr int HJ = GATEUP ? NJ / 2 : NJ;
+  const int cbase = GATEUP ? bn * (NR / 2) + wn * OC : bn * NR + wn * OC;
   const XT* ob0 = reinterpret_cast<const XT*>(a.p0.ob);
   const XT* ob1 = reinterpret_cast<const XT*>(GATEUP ? a.p1.ob : a.p0.ob);
-  constexpr int OC = GATEUP ? 64 : 128;  // output columns per wave
-  const int cbase = GATEUP ? bn * 128 + 64 * wn : bn * 256 + 128 * wn;
-  const uint32_t prow0 = bstart;
-  // 8 waves x 64 x OC 16-bit values: As holds waves 0-3, Bs waves 4-7
-  XT* wt = reinterpret_cast<XT*>(wave < 4 ? &As[0][0] : &Bs[0][0]) + (wave & 3) * 64 * OC;
+  uint16_t* wt = reinterpret_cast<uint16_t*>(lds) + wave * 64 * OC;
 #pragma unroll
-  for (int j = 0; j < (GATEUP ? 2 : 4); j++) {
+  for (int j = 0; j < HJ; j++) {
     const int cn = cbase + 32 * j + col;
     const float obg = (ob0 && cn < N) ? to_f<XT>(ob0[(size_t)e * N + cn]) : 0.f;
     const float obu = (GATEUP && ob1 && cn < N) ? to_f<XT>(ob1[(size_t)e * N + cn]) : 0.f;
@@ -346,73 +386,85 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         const int row = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-        float v = round_to<XT>(acc[i][j][r]);
+        float v = round_to<XT>(acc[i][j][r] * OSCALE);
         if (ob0) v = round_to<XT>(v + obg);
+        uint16_t bits;
         if constexpr (GATEUP) {
-          float u = round_to<XT>(acc[i][j + 2][r]);
+          float u = round_to<XT>(acc[i][j + HJ][r] * OSCALE);
           if (ob1) u = round_to<XT>(u + obu);
-          v = apply_act<XT>(v, u, a.act, a.alpha, a.limit);
-        } else if (a.act == ACT_RELU2) {  // single projection: ReLU^2 only
-          v = apply_act<XT>(0.f, v, ACT_RELU2, 0.f, 0.f);
+          bits = __builtin_bit_cast(uint16_t, to_a16<XT>(apply_act<XT>(v, u, a.act, a.alpha, a.limit)));
+        } else {
+          if (a.act == ACT_RELU2) v = apply_act<XT>(0.f, v, ACT_RELU2, 0.f, 0.f);  // single: ReLU^2 only
+          bits = a.out_a16 ? __builtin_bit_cast(uint16_t, to_a16<XT>(v))
+                           : __builtin_bit_cast(uint16_t, from_f<XT>(v));
         }
-        wt[row * OC + 32 * j + col] = from_f<XT>(v);
+        wt[row * OC + 32 * j + col] = bits;
       }
     }
   }
   // each lane: 16 bytes (8 columns) of one row per step; the wave reads only
   // its own region, so no block barrier is needed
+  uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
   constexpr int C8 = OC / 8;
 #pragma unroll
-  for (int t = 0; t < 64 * C8 / 64; t++) {
+  for (int t = 0; t < C8; t++) {
     const int q = 64 * t + lane;
     const int row = q / C8, c8 = q - row * C8;
-    const uint32_t p = prow0 + (uint32_t)row;
+    const uint32_t p = bstart + (uint32_t)row;
     const int cn0 = cbase + 8 * c8;
     const u32x4_t v = *reinterpret_cast<const u32x4_t*>(wt + row * OC + 8 * c8);
-    // rows past the band belong to the next wave (half tiles)
-    if (row < band && p < pend && cn0 < N)  // N % 8 == 0 (host check): whole 16-byte groups
+    if (p < pend && cn0 < N)  // N % 8 == 0 (host check): whole 16-byte groups
       *reinterpret_cast<u32x4_t*>(out + (size_t)p * N + cn0) = v;
   }
 }
 
-template <int BITS, typename XT, typename ST>
-static hipError_t launch_gemm_t(bool gateup, const GemmArgs& a, int grid, hipStream_t st,
-                                KEvents ev) {
-  if (gateup)
-    hipExtLaunchKernelGGL((gemm_grouped_kernel<BITS, XT, ST, true>), dim3(grid), dim3(512), 0, st,
-                          ev.start, ev.stop, 0, a);
-  else
-    hipExtLaunchKernelGGL((gemm_grouped_kernel<BITS, XT, ST, false>), dim3(grid), dim3(512), 0, st,
-                          ev.start, ev.stop, 0, a);
+template <int BITS, typename XT, bool GATEUP, bool ABF16>
+__global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
+  // the largest shape: shape 2's two buffers of 64 activation rows and 512
+  // weight rows (144 KB); shapes 0 and 1 use 128 and 96 KB
+  __shared__ __align__(16) unsigned char lds[2 * (64 + 512) * 128];
+  // the items split into 8 contiguous ranges, one per XCD (blocks b, b + 8,
+  // ... share an XCD)
+  const uint32_t n = __builtin_amdgcn_readfirstlane(a.items[0]);
+  const uint32_t per = (n + 7u) >> 3;
+  const uint32_t j = blockIdx.x >> 3;
+  if (j >= per) return;
+  const uint32_t wi = (blockIdx.x & 7u) * per + j;
+  if (wi >= n) return;
+  const uint32_t tag = __builtin_amdgcn_readfirstlane(a.items[1 + 3 * wi]);
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(a.items[2 + 3 * wi]);
+  const int bn = (int)__builtin_amdgcn_readfirstlane(a.items[3 + 3 * wi]);
+  const uint32_t e = tag & 0x3FFFFFFFu, shape = tag >> 30;
+  if (shape == 0) gemm_tile<0, BITS, XT, GATEUP, ABF16>(a, lds, e, m0, bn);
+  else if (shape == 1) gemm_tile<1, BITS, XT, GATEUP, ABF16>(a, lds, e, m0, bn);
+  else gemm_tile<2, BITS, XT, GATEUP, ABF16>(a, lds, e, m0, bn);
+}
+
+template <int BITS, typename XT, bool GATEUP, bool ABF16>
+static hipError_t launch_gemm_v(const GemmArgs& a, int grid, hipStream_t st, KEvents ev) {
+  hipExtLaunchKernelGGL((gemm_grouped_kernel<BITS, XT, GATEUP, ABF16>), dim3(grid), dim3(512), 0, st,
+                        ev.start, ev.stop, 0, a);
   return hipGetLastError();
 }
 
 #define MOE_CAT2(a, b) a##b
 #define MOE_CAT(a, b) MOE_CAT2(a, b)
 
-hipError_t MOE_CAT(launch_gemm_b, MOE_BITS)(int xdt, int sbdt, bool gateup, const GemmArgs& a,
+// Gate/up pairs read A16 rows (the layer converts its input first); single
+// projections read A16 rows, or bf16 rows converted while staging (a_bf16).
+hipError_t MOE_CAT(launch_gemm_b, MOE_BITS)(int xdt, bool gateup, bool a_bf16, const GemmArgs& a,
                                              int grid, hipStream_t st, KEvents ev) {
-  if (xdt == DT_BF16 && sbdt == DT_BF16) return launch_gemm_t<MOE_BITS, bf16_t, bf16_t>(gateup, a, grid, st, ev);
-  if (xdt == DT_BF16 && sbdt == DT_F16) return launch_gemm_t<MOE_BITS, bf16_t, f16_t>(gateup, a, grid, st, ev);
-  if (xdt == DT_F16 && sbdt == DT_F16) return launch_gemm_t<MOE_BITS, f16_t, f16_t>(gateup, a, grid, st, ev);
-  if (xdt == DT_F16 && sbdt == DT_BF16) return launch_gemm_t<MOE_BITS, f16_t, bf16_t>(gateup, a, grid, st, ev);
+  if (xdt == DT_BF16) {
+    if (gateup) return a_bf16 ? hipErrorInvalidValue : launch_gemm_v<MOE_BITS, bf16_t, true, false>(a, grid, st, ev);
+    return a_bf16 ? launch_gemm_v<MOE_BITS, bf16_t, false, true>(a, grid, st, ev)
+                  : launch_gemm_v<MOE_BITS, bf16_t, false, false>(a, grid, st, ev);
+  }
+  if (xdt == DT_F16) {
+    if (a_bf16) return hipErrorInvalidValue;
+    return gateup ? launch_gemm_v<MOE_BITS, f16_t, true, false>(a, grid, st, ev)
+                  : launch_gemm_v<MOE_BITS, f16_t, false, false>(a, grid, st, ev);
+  }
   return hipErrorInvalidValue;
 }
-
-#if MOE_BITS == 4
-// Dense 16-bit weights of the activation type (the router projection over
-// many tokens): the same kernel with the dequantisation replaced by a copy.
-hipError_t launch_gemm_dense(int xdt, const GemmArgs& a, int grid, hipStream_t st) {
-  if (xdt == DT_BF16)
-    hipLaunchKernelGGL((gemm_grouped_kernel<16, bf16_t, bf16_t, false>), dim3(grid), dim3(512), 0,
-                       st, a);
-  else if (xdt == DT_F16)
-    hipLaunchKernelGGL((gemm_grouped_kernel<16, f16_t, f16_t, false>), dim3(grid), dim3(512), 0,
-                       st, a);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
-}
-#endif
 
 }  // namespace moe

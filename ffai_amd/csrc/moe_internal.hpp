@@ -185,7 +185,13 @@ hipError_t launch_convert(const void* src, int sdt, void* dst, int ddt, int64_t 
                           hipStream_t st);
 
 // ----------------------------------------------------------------- GEMM --
-// Grouped dequant GEMM over row tiles of a dispatch plan (MFMA).
+// Grouped dequant GEMM over a dispatch plan on the matrix cores, f16
+// operands. The A rows are f16: activations of an f16 layer as they are, or
+// of a bf16 layer scaled by 2^-8 (kA16Shift) into f16 range; with a_bf16 the
+// kernel reads bf16 rows and converts them itself. Gate/up pairs write their
+// activation in that same f16 form (the down GEMM's A rows); a single
+// projection writes out_dtype rows.
+constexpr int kA16Shift = 8;
 struct GemmArgs {
   GemvProj p0, p1;           // gate/up pair (p1 = up) or a single projection
   const void* x;             // activation rows [x_rows, K]
@@ -193,25 +199,48 @@ struct GemmArgs {
   const uint32_t* perm;      // nullable: row(p) = perm[p] / topk, else p
   int topk;
   const uint32_t* offsets;   // [E+1] CSR over sorted positions
-  const uint32_t* tiles;     // [1 + 2 * max_tiles]: count, (expert | kHalfTile?, first position)
+  const uint32_t* items;     // work items (launch_gemm_items)
   void* out;                 // [M, N]
   int N, K, gsh;
+  int sb_bf16;               // scales / biases stored as bf16 (else f16)
+  int out_a16;               // a single projection writes f16 A rows (the first
+                             // stage of squared-ReLU experts), else its dtype
   int act;
   float alpha, limit;
 };
-constexpr int kGemmRows = 256;  // rows per tile
-// Expert-id flag of a tile list entry: a half tile (at most kGemmRows / 2
-// rows, the last of its expert).
-constexpr uint32_t kHalfTile = 0x80000000u;
-// Output columns per block: 128 (gate/up pairs) or 256 (single projection).
-inline int gemm_block_cols(bool gateup) { return gateup ? 128 : 256; }
-inline int gemm_max_tiles(int M, int E) { return (M + kGemmRows - 1) / kGemmRows + E; }
-hipError_t launch_gemm_tiles(const uint32_t* offsets, int E, int bm, uint32_t* tiles,
+// Block shapes (activation rows x weight rows per block; 8 waves of 64 rows
+// each): an expert's rows go in 256-row tiles, and its last tile is the
+// smallest shape that holds what is left.
+constexpr int kGemmShapeRows[3] = {256, 128, 64};
+constexpr int kGemmShapeWRows[3] = {256, 256, 512};
+inline int gemm_shape_for(int rows) { return rows > 128 ? 0 : (rows > 64 ? 1 : 2); }
+// Output columns per block: half the weight rows for a gate/up pair.
+inline int gemm_cols(int shape, bool gateup) {
+  return gateup ? kGemmShapeWRows[shape] / 2 : kGemmShapeWRows[shape];
+}
+// Upper bound on the work items of a plan of M rows over E experts (shapes
+// 0 and 1 have the most column blocks).
+inline long gemm_max_items(int M, int E, int N, bool gateup) {
+  const long tiles = (M + 255) / 256 + (long)E;
+  return tiles * ((N + gemm_cols(0, gateup) - 1) / gemm_cols(0, gateup));
+}
+inline size_t gemm_items_bytes(int M, int E, int N, bool gateup) {
+  return (size_t)(1 + 3 * gemm_max_items(M, E, N, gateup)) * 4;
+}
+// items[0] = count, then per item {expert | shape << 30, first sorted
+// position, column block}: experts ascending, an expert's row tiles in order,
+// a tile's column blocks in order (neighbouring items share activation rows).
+// Writes the list for (N0, gateup0) into items0 and, when items1 is
+// non-NULL, the list for (N1, gateup1) over the same tiles into items1.
+hipError_t launch_gemm_items(const uint32_t* offsets, int E, int N0, bool gateup0,
+                             uint32_t* items0, int N1, bool gateup1, uint32_t* items1,
                              hipStream_t st);
-hipError_t launch_gemm(int bits, int xdt, int sbdt, bool gateup, const GemmArgs& a, int grid,
-                       hipStream_t st, KEvents ev = {});
-// p0.w holds dense [N, K] weights of the activation type; p0.ob an optional
-// bias added after rounding (round(round(W x) + b)).
-hipError_t launch_gemm_dense(int xdt, const GemmArgs& a, int grid, hipStream_t st);
+// grid: 8 * ceil(gemm_max_items / 8) blocks (items are split evenly over the
+// XCDs at run time; blocks without an item return at once).
+hipError_t launch_gemm(int bits, int xdt, int sbdt, bool gateup, bool a_bf16, const GemmArgs& a,
+                       int grid, hipStream_t st, KEvents ev = {});
+// Elementwise bf16 -> f16 * 2^-kA16Shift (saturating), n a multiple of 8,
+// 16-byte aligned buffers.
+hipError_t launch_to_a16(const void* x, void* y, int64_t n, hipStream_t st);
 
 }  // namespace moe

@@ -237,8 +237,9 @@ __global__ __launch_bounds__(256) void router_logits_row_kernel(const XT* __rest
 // token row c (A) and of expert row c (B), 16 contiguous bytes each, so no
 // LDS staging is needed; loads run two groups ahead of the MFMAs. The four
 // partial tiles are added in wave order through LDS, then rounded as
-// router_logits_kernel rounds (product, then + bias). Needs H % 64 == 0,
-// E % 32 == 0 and T * H, E * H below 2^31 elements (32-bit byte offsets).
+// router_logits_kernel rounds (product, then + bias). Needs H % 64 == 0 and
+// T * H, E * H below 2^31 elements (32-bit byte offsets); the last expert
+// tile repeats expert E - 1 past E and stores nothing there.
 // Four waves per tile measured faster than eight or sixteen on the Qwen3 and
 // GPT-OSS prefill shapes (18 against 22 and 25 us for 4096 tokens, 128
 // experts).
@@ -273,7 +274,7 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
   const int t0 = blockIdx.x * 32, e0 = blockIdx.y * 32;
   // rows past T repeat the last token; their outputs are not stored
   const uint32_t row = (uint32_t)min(t0 + col, T - 1);
-  const uint32_t ex = (uint32_t)(e0 + col);
+  const uint32_t ex = (uint32_t)min(e0 + col, E - 1);  // experts past E repeat the last one
   const rsrc_t xr = make_rsrc(x, (uint32_t)((size_t)T * H * sizeof(XT)));
   const rsrc_t wr = make_rsrc(W, (uint32_t)((size_t)E * H * sizeof(XT)));
   const uint32_t xo = (row * (uint32_t)H + 8u * (uint32_t)h) * 2u;
@@ -324,7 +325,7 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
     float s = part[0][r * 33 + c];
 #pragma unroll
     for (int w = 1; w < kRgWaves; w++) s += part[w][r * 33 + c];
-    if (t0 + r < T) {
+    if (t0 + r < T && e0 + c < E) {
       float l = round_to<XT>(s);
       if (bias) l = round_to<XT>(l + to_f<XT>(bias[e0 + c]));
       logits[(size_t)(t0 + r) * E + e0 + c] = from_f<XT>(l);
@@ -355,9 +356,8 @@ template <typename XT, typename WT>
 static hipError_t launch_rl(const void* x, int T, int H, const void* W, const void* bias, int E,
                             void* logits, hipStream_t st) {
   if constexpr (__is_same(XT, WT) && !__is_same(XT, float)) {
-    if (T >= 32 && H % 64 == 0 && E % 32 == 0 && (size_t)T * H < (1ull << 31) &&
-        (size_t)E * H < (1ull << 31)) {
-      hipLaunchKernelGGL((router_gemm_kernel<XT>), dim3((T + 31) / 32, E / 32), dim3(64 * kRgWaves),
+    if (T >= 32 && H % 64 == 0 && (size_t)T * H < (1ull << 31) && (size_t)E * H < (1ull << 31)) {
+      hipLaunchKernelGGL((router_gemm_kernel<XT>), dim3((T + 31) / 32, (E + 31) / 32), dim3(64 * kRgWaves),
                          0, st, (const XT*)x, (const XT*)W, (const XT*)bias, (XT*)logits, T, H, E);
       return hipGetLastError();
     }

@@ -150,7 +150,7 @@ __global__ __launch_bounds__(64 * kRqWaves) void router_qgemm_kernel(const XT* _
   const int col = lane & 31, h = lane >> 5;
   const int t0 = blockIdx.x * 32, e0 = blockIdx.y * 32;
   const uint32_t row = (uint32_t)min(t0 + col, T - 1);  // rows past T repeat the last token
-  const uint32_t ex = (uint32_t)(e0 + col);
+  const uint32_t ex = (uint32_t)min(e0 + col, E - 1);  // experts past E repeat the last one
   const int CU = H >> 5, groups = CU >> gsh, row_words = CU * BITS;
   const rsrc_t xr = make_rsrc(x, (uint32_t)((size_t)T * H * sizeof(XT)));
   const rsrc_t wr = make_rsrc(W.w, (uint32_t)((size_t)E * row_words * 4));
@@ -222,7 +222,7 @@ __global__ __launch_bounds__(64 * kRqWaves) void router_qgemm_kernel(const XT* _
     float v = part[0][r * 33 + c];
 #pragma unroll
     for (int w = 1; w < kRqWaves; w++) v += part[w][r * 33 + c];
-    if (t0 + r < T) {
+    if (t0 + r < T && e0 + c < E) {
       float l = round_to<XT>(v);
       if (bias) l = round_to<XT>(l + to_f<XT>(bias[e0 + c]));
       logits[(size_t)(t0 + r) * E + e0 + c] = from_f<XT>(l);
@@ -234,8 +234,8 @@ __global__ __launch_bounds__(64 * kRqWaves) void router_qgemm_kernel(const XT* _
 template <int BITS, typename XT, typename ST>
 static hipError_t launch_rq_t(const void* x, int T, int H, const GemvProj& W, int gsh,
                               const void* bias, int E, void* logits, hipStream_t st) {
-  if (T >= 32 && H % 64 == 0 && E % 32 == 0) {
-    hipLaunchKernelGGL((router_qgemm_kernel<BITS, XT, ST>), dim3((T + 31) / 32, E / 32),
+  if (T >= 32 && H % 64 == 0) {
+    hipLaunchKernelGGL((router_qgemm_kernel<BITS, XT, ST>), dim3((T + 31) / 32, (E + 31) / 32),
                        dim3(64 * kRqWaves), 0, st, (const XT*)x, W, (const XT*)bias, (XT*)logits,
                        T, H, E, gsh);
     return hipGetLastError();

@@ -171,18 +171,15 @@ def literal_bar(got, ref, label):
     assert mean_rel <= 1e-3, f"{label}: mean relative error {mean_rel:.3e} > 1e-3"
 
 
-_GEMM_BF16_WEIGHTS = pytest.mark.xfail(
-    strict=True, reason="the grouped GEMM rounds dequantised weights to bf16: mean relative "
-                        "error 4.6e-3 measured on these layers")
-
-
 @pytest.mark.parametrize("T,path,E,k,bits", [
     (1, "decode1", 128, 8, (4, 4)),      # one token, fused kernels
     (1, "decode1", 256, 8, (3, 6)),
     (64, "gemv_mma", 128, 8, (4, 4)),    # 4 rows per used expert on the matrix cores
     (64, "gemv_mma", 256, 8, (3, 6)),
-    pytest.param(1024, "gemm", 32, 4, (4, 4), marks=_GEMM_BF16_WEIGHTS),  # grouped GEMM, 128 rows
-    pytest.param(1024, "gemm", 32, 4, (3, 6), marks=_GEMM_BF16_WEIGHTS),  # per expert
+    (1024, "gemm", 32, 4, (4, 4)),       # grouped GEMM, 128 rows per expert
+    (1024, "gemm", 32, 4, (3, 6)),
+    (256, "gemm", 16, 4, (4, 4)),        # 64 rows per expert: the 64-row tile shape
+    (320, "gemm", 16, 4, (3, 6)),        # 80 rows per expert: the 128-row tile shape
 ])
 def test_literal_tolerance_centred(T, path, E, k, bits):
     spec = cfg_centred(seed=T + E, E=E, H=2048, I=768, k=k, bits_gu=bits[0], bits_d=bits[1])

@@ -230,7 +230,7 @@ def test_expert_matmul_all_widths(bits, dt, sb):
     q.weight, q.scales, q.biases = wt.data_ptr(), st.data_ptr(), bt.data_ptr()
     at = to_torch(a)
     out = torch.empty(M, N, dtype=at.dtype, device="cuda")
-    wsb = lib.moe_expert_matmul_workspace_bytes(E, M)
+    wsb = lib.moe_expert_matmul_workspace_bytes(E, M, N)
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
     offt = to_torch(offsets.view(np.int32))
     check(lib.moe_expert_matmul(C.byref(q), _p(at), dt, None, 1, M, _p(offt), _p(out), _p(ws), wsb,
@@ -272,7 +272,7 @@ def test_expert_matmul_mfma(bits, dt, sb, gs, gather):
     q.weight, q.scales, q.biases = wt.data_ptr(), st.data_ptr(), bt.data_ptr()
     at = to_torch(a)
     out = torch.empty(M, N, dtype=at.dtype, device="cuda")
-    wsb = lib.moe_expert_matmul_workspace_bytes(E, M)
+    wsb = lib.moe_expert_matmul_workspace_bytes(E, M, N)
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
     offt = to_torch(offsets.view(np.int32))
     pt = to_torch(perm.view(np.int32)) if gather else None
@@ -280,14 +280,12 @@ def test_expert_matmul_mfma(bits, dt, sb, gs, gather):
                                 _p(out), _p(ws), wsb, _stream()))
     torch.cuda.synchronize()
     ref = orc.round_dt(orc.qgemm_rows(p, src, experts), dt)
-    # The matrix-core path rounds every dequantised weight to the MFMA operand
-    # type (bf16: 2^-9, f16: 2^-12 relative), as the reference's simdgroup
-    # matrix kernels do in the input dtype (Ops.swift:4553-4600); the
-    # reference tests those kernels at cosine >= 0.99
-    # (MoEBgemmBm64MppTests.swift:82-114). One product is held to one bf16 ulp
-    # (2^-8) of mean relative error; whole layers keep the 1e-3 bar.
-    check_close(to_numpy_f32(out), ref, dt, f"mfma expert_matmul bits={bits} gs={gs}",
-                mean_tol=2.0 ** -8 if dt == BF16 else 1e-3)
+    # The matrix-core path rounds every dequantised weight once to f16 (2^-12
+    # relative) and scales bf16 activations exactly into f16 range, so a single
+    # product meets the layer bar (the reference tests its simdgroup-matrix
+    # kernels, which round weights to the input dtype, at cosine >= 0.99:
+    # MoEBgemmBm64MppTests.swift:82-114).
+    check_close(to_numpy_f32(out), ref, dt, f"mfma expert_matmul bits={bits} gs={gs}")
 
 
 # ------------------------------------------------------------ whole layer --
