@@ -320,34 +320,41 @@ hipError_t launch_dispatch_plan(const uint32_t* idx, int T, int k, int E, uint32
   return hipGetLastError();
 }
 
-// Work items of the grouped GEMM over an expert-sorted plan (the list format
-// is described at launch_gemm_items). Thread t takes experts t * EPT .. + EPT;
-// one block scan gives each thread's first item.
 struct ItemCols {
   int nb[2][3];  // column blocks per tile shape, for each of the two lists
 };
 
+// Work items of the grouped GEMM over an expert-sorted plan (the list format
+// is described at launch_gemm_items). Thread t counts the items of experts
+// t * EPT .. + EPT; a block scan gives every expert's first item (in LDS);
+// then all threads write items in a strided loop, each finding its expert by
+// a binary search over those starts.
 __global__ __launch_bounds__(kPlanThreads) void gemm_items_kernel(
     const uint32_t* __restrict__ offsets, int E, const ItemCols ic, uint32_t* __restrict__ items0,
     uint32_t* __restrict__ items1) {
   __shared__ uint32_t scan[2][kPlanThreads];
+  __shared__ uint32_t start[2][kPlanMaxE + 1];  // first item of each expert, per list
+  __shared__ uint32_t first_pos[kPlanMaxE], rows_of[kPlanMaxE];
   constexpr int EPT = kPlanMaxE / kPlanThreads;  // experts per thread
   const int t = threadIdx.x;
-  uint32_t rows[EPT], first[EPT], tot0 = 0, tot1 = 0;
+  uint32_t cnt[2][EPT], tot0 = 0, tot1 = 0;
 #pragma unroll
   for (int j = 0; j < EPT; j++) {
     const int e = t * EPT + j;
-    rows[j] = 0;
-    first[j] = 0;
+    uint32_t rows = 0, first = 0;
     if (e < E) {
-      first[j] = offsets[e];
-      rows[j] = offsets[e + 1] - first[j];
+      first = offsets[e];
+      rows = offsets[e + 1] - first;
+      first_pos[e] = first;
+      rows_of[e] = rows;
     }
-    const uint32_t full = rows[j] / 256u, rem = rows[j] % 256u;
+    const uint32_t full = rows / 256u, rem = rows % 256u;
     // the remainder takes the smallest shape that holds it
     const int rs = rem > 128u ? 0 : (rem > 64u ? 1 : 2);
-    tot0 += full * (uint32_t)ic.nb[0][0] + (rem ? (uint32_t)ic.nb[0][rs] : 0u);
-    tot1 += full * (uint32_t)ic.nb[1][0] + (rem ? (uint32_t)ic.nb[1][rs] : 0u);
+    cnt[0][j] = full * (uint32_t)ic.nb[0][0] + (rem ? (uint32_t)ic.nb[0][rs] : 0u);
+    cnt[1][j] = full * (uint32_t)ic.nb[1][0] + (rem ? (uint32_t)ic.nb[1][rs] : 0u);
+    tot0 += cnt[0][j];
+    tot1 += cnt[1][j];
   }
   scan[0][t] = tot0;
   scan[1][t] = tot1;
@@ -360,37 +367,57 @@ __global__ __launch_bounds__(kPlanThreads) void gemm_items_kernel(
     scan[1][t] += v1;
     __syncthreads();
   }
-  uint32_t base0 = scan[0][t] - tot0, base1 = scan[1][t] - tot1;
+  uint32_t b0 = scan[0][t] - tot0, b1 = scan[1][t] - tot1;
 #pragma unroll
   for (int j = 0; j < EPT; j++) {
-    const uint32_t e = (uint32_t)(t * EPT + j);
-    for (uint32_t r0 = 0; r0 < rows[j]; r0 += 256u) {
-      const uint32_t left = rows[j] - r0;
-      const uint32_t shape = left > 128u ? 0u : (left > 64u ? 1u : 2u);
-      const uint32_t tag = e | (shape << 30);
-      const uint32_t nb0 = (uint32_t)ic.nb[0][shape];
-      for (uint32_t b = 0; b < nb0; b++) {
-        uint32_t* it = items0 + 1 + 3 * (base0 + b);
-        it[0] = tag;
-        it[1] = first[j] + r0;
-        it[2] = b;
-      }
-      base0 += nb0;
-      if (items1) {
-        const uint32_t nb1 = (uint32_t)ic.nb[1][shape];
-        for (uint32_t b = 0; b < nb1; b++) {
-          uint32_t* it = items1 + 1 + 3 * (base1 + b);
-          it[0] = tag;
-          it[1] = first[j] + r0;
-          it[2] = b;
-        }
-        base1 += nb1;
-      }
+    const int e = t * EPT + j;
+    if (e < E) {
+      start[0][e] = b0;
+      start[1][e] = b1;
     }
+    b0 += cnt[0][j];
+    b1 += cnt[1][j];
   }
-  if (t == kPlanThreads - 1) {
-    items0[0] = scan[0][t];
-    if (items1) items1[0] = scan[1][t];
+  const uint32_t n[2] = {scan[0][kPlanThreads - 1], scan[1][kPlanThreads - 1]};
+  if (t == 0) {
+    start[0][E] = n[0];
+    start[1][E] = n[1];
+    items0[0] = n[0];
+    if (items1) items1[0] = n[1];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int l = 0; l < 2; l++) {
+    uint32_t* items = l ? items1 : items0;
+    if (!items) continue;
+    const uint32_t nb0 = (uint32_t)ic.nb[l][0];
+    for (uint32_t i = (uint32_t)t; i < n[l]; i += kPlanThreads) {
+      // the last expert whose first item is at or before i (experts without
+      // items share their start with the next one)
+      int lo = 0, hi = E - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (start[l][mid] <= i) lo = mid;
+        else hi = mid - 1;
+      }
+      const uint32_t e = (uint32_t)lo, k = i - start[l][lo];
+      const uint32_t rows = rows_of[e], full = rows / 256u;
+      uint32_t tile, b, shape;
+      if (k < full * nb0) {
+        tile = k / nb0;
+        b = k - tile * nb0;
+        shape = 0u;
+      } else {
+        const uint32_t rem = rows % 256u;
+        tile = full;
+        b = k - full * nb0;
+        shape = rem > 128u ? 0u : (rem > 64u ? 1u : 2u);
+      }
+      uint32_t* it = items + 1 + 3 * i;
+      it[0] = e | (shape << 30);
+      it[1] = first_pos[e] + tile * 256u;
+      it[2] = b;
+    }
   }
 }
 

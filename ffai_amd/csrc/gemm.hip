@@ -124,12 +124,13 @@ __device__ __forceinline__ void quarter_pairs(const uint32_t (&w)[BITS], int s, 
   }
 }
 
-// A 16-bit scale or bias (bf16 or f16 storage) as an f16 pair.
+// A 16-bit scale or bias (bf16 or f16 storage) as an f16 pair. Both
+// conversions are computed and one is selected (a branch on the storage type
+// here split every chunk of the main loop into a dozen basic blocks).
 __device__ __forceinline__ h2_t sb_h2(uint32_t raw16, bool bf16) {
-  _Float16 h;
-  if (bf16) h = (_Float16)__uint_as_float(raw16 << 16);  // exact inside f16's range
-  else h = __builtin_bit_cast(_Float16, (uint16_t)raw16);
-  return h2_t{h, h};
+  const uint16_t from_bf = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float(raw16 << 16));
+  const uint32_t h = bf16 ? (uint32_t)from_bf : raw16;  // bf16: exact inside f16's range
+  return __builtin_bit_cast(h2_t, h | (h << 16));
 }
 
 // Two bf16 values -> f16 * 2^-8 (round toward zero, so finite values saturate
