@@ -124,6 +124,30 @@ __device__ __forceinline__ void quarter_pairs(const uint32_t (&w)[BITS], int s, 
   }
 }
 
+// Codes of values 8 s + 2 p and 8 s + 2 p + 1 (p < 4) of a 32-value unit as
+// f16 pairs. 4-bit: the nibbles are spread one per byte, and a byte q < 16 is
+// the OCP e4m3 number q * 2^-9 (subnormal below 8), so the scaled fp8
+// conversion at 2^9 gives q exactly, two values per instruction. Other widths:
+// 1024 + q pairs less 1024.
+template <int BITS>
+__device__ __forceinline__ void quarter_codes(const uint32_t (&w)[BITS], int s, h2_t (&q)[4]) {
+  if constexpr (BITS == 4) {
+    const uint32_t t = w[s] & 0x0F0F0F0Fu, u = (w[s] >> 4) & 0x0F0F0F0Fu;
+    const uint32_t z0 = __builtin_amdgcn_perm(u, t, 0x05010400u);  // bytes [t0, u0, t1, u1]
+    const uint32_t z1 = __builtin_amdgcn_perm(u, t, 0x07030602u);  // bytes [t2, u2, t3, u3]
+    q[0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(z0, 512.0f, false);
+    q[1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(z0, 512.0f, true);
+    q[2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(z1, 512.0f, false);
+    q[3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(z1, 512.0f, true);
+  } else {
+    uint32_t pr[4];
+    quarter_pairs<BITS>(w, s, pr);
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+      q[p] = __builtin_bit_cast(h2_t, pr[p]) - h2_t{(_Float16)1024.0f, (_Float16)1024.0f};
+  }
+}
+
 // A 16-bit scale or bias (bf16 or f16 storage) as an f16 pair. Both
 // conversions are computed and one is selected (a branch on the storage type
 // here split every chunk of the main loop into a dozen basic blocks).
@@ -237,37 +261,45 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds,
   // chunk c + 2 is in flight while chunk c + 1 is dequantised
   struct BUnits {
     uint32_t w[BI][BITS];
-    uint32_t sb[BI];  // scale | bias << 16, raw 16-bit storage
+    uint32_t s[BI], b[BI];  // raw 16-bit scale and bias (kept apart: combining them
+                            // where they load would wait for both loads right there)
   };
-  auto load_b = [&](int chunk, BUnits& u) {
+  // scales and biases load apart from the codes: a chunk issues them first,
+  // so that they have landed by the time the chunk's activations (issued
+  // next, and waited for first thing in the following chunk) have
+  auto load_sb = [&](int chunk, BUnits& u) {
     const int unit = 2 * chunk + bu;
 #pragma unroll
     for (int i = 0; i < BI; i++) {
-      bload_unit<BITS>(PB[i].w, (brow[i] * (uint32_t)row_words + (uint32_t)(unit * BITS)) * 4u, u.w[i]);
       const uint32_t gi = (brow[i] * (uint32_t)groups + (uint32_t)(unit >> a.gsh)) * 2u;
-      u.sb[i] = (uint32_t)bload16(PB[i].s, gi) | ((uint32_t)bload16(PB[i].b, gi) << 16);
+      u.s[i] = bload16(PB[i].s, gi);
+      u.b[i] = bload16(PB[i].b, gi);
     }
+  };
+  auto load_w = [&](int chunk, BUnits& u) {
+    const int unit = 2 * chunk + bu;
+#pragma unroll
+    for (int i = 0; i < BI; i++)
+      bload_unit<BITS>(PB[i].w, (brow[i] * (uint32_t)row_words + (uint32_t)(unit * BITS)) * 4u, u.w[i]);
   };
   // values [8 s, 8 s + 8) of each unit -> LDS chunk 4 bu + s of its row
   auto store_b = [&](const BUnits& u, const h2_t (&s2)[BI], const h2_t (&b2)[BI], int s, int buf) {
 #pragma unroll
     for (int i = 0; i < BI; i++) {
-      uint32_t pr[4];
-      quarter_pairs<BITS>(u.w[i], s, pr);
+      h2_t q[4];
+      quarter_codes<BITS>(u.w[i], s, q);
       u32x4_t v;
 #pragma unroll
-      for (int p = 0; p < 4; p++) {
-        const h2_t q = __builtin_bit_cast(h2_t, pr[p]) - h2_t{(_Float16)1024.0f, (_Float16)1024.0f};
-        v[p] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2[i], b2[i]));
-      }
+      for (int p = 0; p < 4; p++)
+        v[p] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q[p], s2[i], b2[i]));
       *reinterpret_cast<u32x4_t*>(Bs + buf * BBUF + tile_off(brl[i], 4 * bu + s)) = v;
     }
   };
   auto sb_pairs = [&](const BUnits& u, h2_t (&s2)[BI], h2_t (&b2)[BI]) {
 #pragma unroll
     for (int i = 0; i < BI; i++) {
-      s2[i] = sb_h2(u.sb[i] & 0xFFFFu, sb_bf16);
-      b2[i] = sb_h2(u.sb[i] >> 16, sb_bf16);
+      s2[i] = sb_h2(u.s[i], sb_bf16);
+      b2[i] = sb_h2(u.b[i], sb_bf16);
     }
   };
 
@@ -311,8 +343,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds,
     constexpr int MV = decltype(mv)::value;
     const int cp = min(c + 2, nchunks - 1);
     store_a(ar, buf ^ 1);
+    load_sb(cp, cb);
     load_a(cp, ar);
-    load_b(cp, cb);
+    load_w(cp, cb);
     // keep chunk c + 2's loads issued here (sunk below the first weight
     // dequantisation they would turn its wait into a wait for every load)
     __builtin_amdgcn_sched_barrier(0);
@@ -343,9 +376,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds,
 
   ARegs ar;
   BUnits u0, u1;
+  load_sb(0, u0);
   load_a(0, ar);
-  load_b(0, u0);
-  load_b(min(1, nchunks - 1), u1);
+  load_w(0, u0);
+  load_sb(min(1, nchunks - 1), u1);
+  load_w(min(1, nchunks - 1), u1);
   store_a(ar, 0);
   load_a(min(1, nchunks - 1), ar);
   {
@@ -356,11 +391,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds,
   }
   lds_barrier();
 
+  // Two chunks per trip and the odd chunk after the loop: with the second
+  // step conditional inside the loop, the path that skips it would make the
+  // compiler's load-counter state at the loop header that of the first step's
+  // last loads, and every chunk would then start by waiting for all of the
+  // previous chunk's loads.
   auto run = [&](auto mv) {
-    for (int c = 0; c < nchunks; c += 2) {
+    int c = 0;
+    for (; c + 1 < nchunks; c += 2) {
       chunk_step(mv, c, 0, ar, u0, u1);
-      if (c + 1 < nchunks) chunk_step(mv, c + 1, 1, ar, u1, u0);
+      chunk_step(mv, c + 1, 1, ar, u1, u0);
     }
+    if (c < nchunks) chunk_step(mv, c, 0, ar, u0, u1);
   };
   // mvalid is wave-uniform: one scalar branch picks the loop
   if (mvalid == 2) run(std::integral_constant<int, 2>{});
