@@ -329,19 +329,46 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds,
     return (uint32_t)(r + col) * 128u;
   };
 
-  // One chunk: MFMAs on LDS buffer `buf`. First chunk c + 1's activations
-  // (loaded during chunk c - 1) go from `ar` to the other buffer, which chunk
-  // c - 1's closing barrier freed, and `ar` takes chunk c + 2's loads; chunk
-  // c + 1's weights (set nb) are dequantised into the other buffer between
-  // the MFMA steps, and chunk c + 2's weights load into the set cb that chunk
-  // c used. Loads and LDS writes are unconditional (past the end they repeat
+  // the operand fragments of one 16-value step of the chunk in LDS buffer buf
+  struct Frags {
+    u32x4_t b[NJ], a[2];
+  };
+  auto read_frags = [&](int buf, int s, Frags& f) {
+    const unsigned char* Ab = As + buf * ABUF;
+    const unsigned char* Bb = Bs + buf * BBUF;
+    const uint32_t sw = (uint32_t)(((2 * s + h) ^ tile_swz(col)) << 4);
+#pragma unroll
+    for (int j = 0; j < NJ; j++) f.b[j] = *reinterpret_cast<const u32x4_t*>(Bb + boff(j) + sw);
+#pragma unroll
+    for (int i = 0; i < 2; i++) f.a[i] = *reinterpret_cast<const u32x4_t*>(Ab + arow0 + 32 * 128 * i + sw);
+  };
+  auto mma_step = [&](auto mv, const Frags& f) {
+    constexpr int MV = decltype(mv)::value;
+#pragma unroll
+    for (int i = 0; i < MV; i++)
+#pragma unroll
+      for (int j = 0; j < NJ; j++) acc[i][j] = mma_f16(f.a[i], f.b[j], acc[i][j]);
+  };
+  // Chunk c on buffer buf. Its first fragments are read as soon as the
+  // previous chunk's barrier has passed, and the previous chunk's last MFMA
+  // step (operands already in registers, `last`) is issued behind those
+  // reads, so the matrix cores work while this chunk's first operands arrive
+  // and while the activations of chunk c + 1 (loaded during chunk c - 1) go
+  // from `ar` to the other buffer, which that barrier freed. `ar` then takes
+  // chunk c + 2's loads; chunk c + 1's weights (set nb) are dequantised into
+  // the other buffer between the MFMA steps, and chunk c + 2's weights load
+  // into the set cb that chunk c used. This chunk's own last step is left in
+  // `last`. Loads and LDS writes are unconditional (past the end they repeat
   // the last chunk, in bounds and never read) so that the compiler can count
   // outstanding loads exactly. MV: row tiles of this wave with positions of
   // the expert (0..2), a compile-time constant, so each version of the loop
   // is straight-line code.
-  auto chunk_step = [&](auto mv, int c, int buf, ARegs& ar, BUnits& cb, const BUnits& nb) {
-    constexpr int MV = decltype(mv)::value;
+  auto chunk_step = [&](auto mv, auto pending, int c, int buf, ARegs& ar, BUnits& cb, const BUnits& nb,
+                        Frags& last) {
     const int cp = min(c + 2, nchunks - 1);
+    Frags f0, f1;
+    read_frags(buf, 0, f0);
+    if constexpr (decltype(pending)::value) mma_step(mv, last);
     store_a(ar, buf ^ 1);
     load_sb(cp, cb);
     load_a(cp, ar);
@@ -351,26 +378,16 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds,
     __builtin_amdgcn_sched_barrier(0);
     h2_t s2[BI], b2[BI];
     sb_pairs(nb, s2, b2);
-    const unsigned char* Ab = As + buf * ABUF;
-    const unsigned char* Bb = Bs + buf * BBUF;
-    u32x4_t bf[2][NJ], af[2][2];
-    auto read_frags = [&](int s, u32x4_t (&b)[NJ], u32x4_t (&a2)[2]) {
-      const uint32_t sw = (uint32_t)(((2 * s + h) ^ tile_swz(col)) << 4);
-#pragma unroll
-      for (int j = 0; j < NJ; j++) b[j] = *reinterpret_cast<const u32x4_t*>(Bb + boff(j) + sw);
-#pragma unroll
-      for (int i = 0; i < 2; i++) a2[i] = *reinterpret_cast<const u32x4_t*>(Ab + arow0 + 32 * 128 * i + sw);
-    };
-    read_frags(0, bf[0], af[0]);
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-      if (s < 3) read_frags(s + 1, bf[(s + 1) & 1], af[(s + 1) & 1]);
-#pragma unroll
-      for (int i = 0; i < MV; i++)
-#pragma unroll
-        for (int j = 0; j < NJ; j++) acc[i][j] = mma_f16(af[s & 1][i], bf[s & 1][j], acc[i][j]);
-      store_b(nb, s2, b2, s, buf ^ 1);
-    }
+    read_frags(buf, 1, f1);
+    mma_step(mv, f0);
+    store_b(nb, s2, b2, 0, buf ^ 1);
+    read_frags(buf, 2, f0);
+    mma_step(mv, f1);
+    store_b(nb, s2, b2, 1, buf ^ 1);
+    read_frags(buf, 3, last);
+    mma_step(mv, f0);
+    store_b(nb, s2, b2, 2, buf ^ 1);
+    store_b(nb, s2, b2, 3, buf ^ 1);
     lds_barrier();
   };
 
@@ -397,12 +414,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds,
   // last loads, and every chunk would then start by waiting for all of the
   // previous chunk's loads.
   auto run = [&](auto mv) {
-    int c = 0;
+    Frags last;
+    chunk_step(mv, std::false_type{}, 0, 0, ar, u0, u1, last);
+    int c = 1;
     for (; c + 1 < nchunks; c += 2) {
-      chunk_step(mv, c, 0, ar, u0, u1);
-      chunk_step(mv, c + 1, 1, ar, u1, u0);
+      chunk_step(mv, std::true_type{}, c, 1, ar, u1, u0, last);
+      chunk_step(mv, std::true_type{}, c + 1, 0, ar, u0, u1, last);
     }
-    if (c < nchunks) chunk_step(mv, c, 0, ar, u0, u1);
+    if (c < nchunks) chunk_step(mv, std::true_type{}, c, 1, ar, u1, u0, last);
+    mma_step(mv, last);
   };
   // mvalid is wave-uniform: one scalar branch picks the loop
   if (mvalid == 2) run(std::integral_constant<int, 2>{});
