@@ -113,8 +113,12 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 }
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
 __device__ __forceinline__ u32x4_t bload128(rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ u32x3_t bload96(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b96(r, off, 0, 0);
 }
 __device__ __forceinline__ u32x2_t bload64(rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
@@ -475,22 +479,30 @@ __device__ __forceinline__ void load_unit(const uint32_t* __restrict__ p, uint32
   }
 }
 
-// Buffer form of load_unit: byte offset `off` of a raw buffer view.
+// Buffer form of load_unit: byte offset `off` of a raw buffer view. Units of
+// 3, 5 and 6 bits are 12, 20 and 24 bytes, 4- or 8-byte aligned; buffer
+// loads of several dwords need only dword alignment, so each unit takes one
+// or two loads (a 96-bit load, or a 128-bit load and the rest) instead of one
+// per word.
 template <int BITS>
 __device__ __forceinline__ void bload_unit(rsrc_t r, uint32_t off, uint32_t (&w)[BITS]) {
   if constexpr (BITS == 2) {
     const u32x2_t v = bload64(r, off);
     w[0] = v[0]; w[1] = v[1];
-  } else if constexpr (BITS == 3 || BITS == 5) {
-    // 12- and 20-byte units are only 4-byte aligned
-#pragma unroll
-    for (int i = 0; i < BITS; i++) w[i] = bload32(r, off + 4u * i);
+  } else if constexpr (BITS == 3) {
+    const u32x3_t v = bload96(r, off);
+    w[0] = v[0]; w[1] = v[1]; w[2] = v[2];
   } else if constexpr (BITS == 4) {
     const u32x4_t v = bload128(r, off);
     w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+  } else if constexpr (BITS == 5) {
+    const u32x4_t a = bload128(r, off);
+    w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
+    w[4] = bload32(r, off + 16);
   } else if constexpr (BITS == 6) {
-    const u32x2_t a = bload64(r, off), b = bload64(r, off + 8), c = bload64(r, off + 16);
-    w[0] = a[0]; w[1] = a[1]; w[2] = b[0]; w[3] = b[1]; w[4] = c[0]; w[5] = c[1];
+    const u32x4_t a = bload128(r, off);
+    const u32x2_t b = bload64(r, off + 16);
+    w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3]; w[4] = b[0]; w[5] = b[1];
   } else if constexpr (BITS == 8) {
     const u32x4_t a = bload128(r, off), b = bload128(r, off + 16);
     w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
