@@ -113,7 +113,7 @@ def load():
     lib.moe_dispatch_workspace_bytes.restype = sz
     lib.moe_dispatch_plan.argtypes = [vp, i32, i32, i32, vp, vp, vp, vp, vp, sz, st]
     lib.moe_dequantize_affine.argtypes = [vp, vp, vp, i32, i32, i32, C.c_int64, vp, i32, st]
-    lib.moe_expert_matmul_workspace_bytes.argtypes = [i32, i32, i32]
+    lib.moe_expert_matmul_workspace_bytes.argtypes = [C.POINTER(QProj), i32, i32]
     lib.moe_expert_matmul_workspace_bytes.restype = sz
     lib.moe_expert_matmul.argtypes = [C.POINTER(QProj), vp, i32, vp, i32, i32, vp, vp, vp, sz, st]
     lib.moe_activation_apply.argtypes = [vp, vp, vp, C.c_int64, i32, i32, C.c_float, C.c_float, st]

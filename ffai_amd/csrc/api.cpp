@@ -94,25 +94,25 @@ hipError_t launch_router_q(int bits, const void* x, int xdt, int T, int H, const
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemm_b2(int, bool, bool, const GemmArgs&, int, hipStream_t, KEvents);
-hipError_t launch_gemm_b3(int, bool, bool, const GemmArgs&, int, hipStream_t, KEvents);
-hipError_t launch_gemm_b4(int, bool, bool, const GemmArgs&, int, hipStream_t, KEvents);
-hipError_t launch_gemm_b5(int, bool, bool, const GemmArgs&, int, hipStream_t, KEvents);
-hipError_t launch_gemm_b6(int, bool, bool, const GemmArgs&, int, hipStream_t, KEvents);
-hipError_t launch_gemm_b8(int, bool, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b2(int, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b3(int, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b4(int, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b5(int, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b6(int, bool, const GemmArgs&, int, hipStream_t, KEvents);
+hipError_t launch_gemm_b8(int, bool, const GemmArgs&, int, hipStream_t, KEvents);
 
-hipError_t launch_gemm(int bits, int xdt, int sbdt, bool gateup, bool a_bf16, const GemmArgs& a0,
-                       int grid, hipStream_t st, KEvents ev) {
+hipError_t launch_gemm(int bits, int xdt, int sbdt, bool gateup, const GemmArgs& a0, int grid,
+                       hipStream_t st, KEvents ev) {
   if (sbdt != DT_BF16 && sbdt != DT_F16) return hipErrorInvalidValue;
   GemmArgs a = a0;
   a.sb_bf16 = sbdt == DT_BF16;
   switch (bits) {
-    case 2: return launch_gemm_b2(xdt, gateup, a_bf16, a, grid, st, ev);
-    case 3: return launch_gemm_b3(xdt, gateup, a_bf16, a, grid, st, ev);
-    case 4: return launch_gemm_b4(xdt, gateup, a_bf16, a, grid, st, ev);
-    case 5: return launch_gemm_b5(xdt, gateup, a_bf16, a, grid, st, ev);
-    case 6: return launch_gemm_b6(xdt, gateup, a_bf16, a, grid, st, ev);
-    case 8: return launch_gemm_b8(xdt, gateup, a_bf16, a, grid, st, ev);
+    case 2: return launch_gemm_b2(xdt, gateup, a, grid, st, ev);
+    case 3: return launch_gemm_b3(xdt, gateup, a, grid, st, ev);
+    case 4: return launch_gemm_b4(xdt, gateup, a, grid, st, ev);
+    case 5: return launch_gemm_b5(xdt, gateup, a, grid, st, ev);
+    case 6: return launch_gemm_b6(xdt, gateup, a, grid, st, ev);
+    case 8: return launch_gemm_b8(xdt, gateup, a, grid, st, ev);
   }
   return hipErrorInvalidValue;
 }
@@ -723,8 +723,8 @@ bool gemm_ok(const moe_qproj& p, int xdt, int M, const void* out = nullptr) {
 // out[p] = W[e(p)] . a[row(p)] (or the gate/up pair with the activation)
 // over a plan, on the matrix cores. `items` must hold the work list written by
 // launch_gemm_items for the same offsets and (N, gate/up). The A rows x are
-// f16 A operands (kA16Shift), or bf16 rows converted while staging (a_bf16,
-// single projections only); a gate/up pair writes its activation as A rows.
+// f16 A operands (kA16Shift); a gate/up pair writes its activation as A
+// rows.
 // The routed experts / the shared expert of a layer call of T rows take the
 // grouped GEMM (gate/up and down together: the gate/up epilogue writes the
 // down GEMM's f16 operand).
@@ -741,8 +741,7 @@ bool shared_gemm(const moe_layer_desc* d, int T) {
 
 // out_a16: a single projection writes A rows for a following GEMM (the
 // first stage of squared-ReLU experts).
-moe_status run_gemm(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt, bool a_bf16,
-                    bool out_a16, const uint32_t* perm, int topk, const uint32_t* offsets,
+moe_status run_gemm(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt, bool out_a16, const uint32_t* perm, int topk, const uint32_t* offsets,
                     const uint32_t* items, int M, void* out, int act, float alpha, float limit,
                     hipStream_t st, KEvents ev = {}) {
   GemmArgs a{};
@@ -765,7 +764,7 @@ moe_status run_gemm(const moe_qproj& p0, const moe_qproj* p1, const void* x, int
   const bool gu = p1 != nullptr;
   const long items_max = gemm_max_items(M, p0.n_experts, p0.n, gu);
   const int grid = (int)((items_max + 7) / 8 * 8);  // a multiple of the 8 XCDs
-  MOE_HIP(launch_gemm(p0.bits, xdt, p0.sb_dtype, gu, a_bf16, a, grid, st, ev),
+  MOE_HIP(launch_gemm(p0.bits, xdt, p0.sb_dtype, gu, a, grid, st, ev),
           "grouped GEMM launch");
   return MOE_OK;
 }
@@ -919,10 +918,13 @@ extern "C" moe_status moe_mxfp4_to_affine(const uint32_t* packed, const uint8_t*
   return ok();
 }
 
-extern "C" size_t moe_expert_matmul_workspace_bytes(int32_t n_experts, int32_t M, int32_t n) {
-  if (n_experts <= 0 || M <= 0 || n <= 0) return 0;
-  return align_up((size_t)(n_experts + 1) * 4, 256) +
-         align_up(gemm_items_bytes(M, n_experts, n, false), 256);
+// [used list / CSR copy][GEMM work list][bf16 rows as f16 operands]
+extern "C" size_t moe_expert_matmul_workspace_bytes(const moe_qproj* p, int32_t a_dtype, int32_t M) {
+  if (!p || M <= 0 || validate_qproj_named(p, "expert_matmul") != MOE_OK || !dt_ok(a_dtype)) return 0;
+  size_t bytes = align_up((size_t)(p->n_experts + 1) * 4, 256) +
+                 align_up(gemm_items_bytes(M, p->n_experts, p->n, false), 256);
+  if (a_dtype == MOE_BF16) bytes += align_up((size_t)M * p->k * 2, 256);
+  return bytes;
 }
 
 extern "C" moe_status moe_expert_matmul(const moe_qproj* p, const void* a, int32_t a_dtype,
@@ -936,17 +938,24 @@ extern "C" moe_status moe_expert_matmul(const moe_qproj* p, const void* a, int32
   if (!dt_ok(a_dtype) || !pair_ok(a_dtype, p->sb_dtype))
     return fail(MOE_ERR_UNSUPPORTED, "expert_matmul: activation/scale dtype pair not built");
   if (p->n_experts > 1024) return fail(MOE_ERR_UNSUPPORTED, "expert_matmul: n_experts above 1024");
-  const size_t need = moe_expert_matmul_workspace_bytes(p->n_experts, M, p->n);
+  const size_t need = moe_expert_matmul_workspace_bytes(p, a_dtype, M);
   if (!workspace || workspace_bytes < need)
     return fail(MOE_ERR_WORKSPACE, "expert_matmul: workspace of %zu bytes needed", need);
   if (gemm_ok(*p, a_dtype, M, out)) {
-    uint32_t* items = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(workspace) +
-                                                  align_up((size_t)(p->n_experts + 1) * 4, 256));
+    char* wsc = reinterpret_cast<char*>(workspace);
+    const size_t items_at = align_up((size_t)(p->n_experts + 1) * 4, 256);
+    uint32_t* items = reinterpret_cast<uint32_t*>(wsc + items_at);
     MOE_HIP(launch_gemm_items(offsets, p->n_experts, p->n, false, items, 0, false, nullptr, stream),
             "GEMM work list launch");
-    // bf16 rows are converted to the f16 operand while staging
-    MOE_TRY(run_gemm(*p, nullptr, a, a_dtype, a_dtype == MOE_BF16, false, perm, top_k, offsets,
-                     items, M, out, 0, 0.f, 0.f, stream));
+    const void* a16 = a;
+    if (a_dtype == MOE_BF16) {  // the GEMM's f16 operand: bf16 rows scaled by 2^-kA16Shift
+      void* x16 = wsc + items_at + align_up(gemm_items_bytes(M, p->n_experts, p->n, false), 256);
+      const int64_t rows = perm ? (M + top_k - 1) / top_k : M;
+      MOE_HIP(launch_to_a16(a, x16, rows * p->k, stream), "f16 operand launch");
+      a16 = x16;
+    }
+    MOE_TRY(run_gemm(*p, nullptr, a16, a_dtype, false, perm, top_k, offsets, items, M, out, 0, 0.f,
+                     0.f, stream));
     return ok();
   }
   uint32_t* used = reinterpret_cast<uint32_t*>(workspace);
@@ -1157,10 +1166,10 @@ moe_status shared_expert(const moe_layer_desc* d, const void* x, const void* x16
                               at<uint32_t>(ws, w.s_items_gu), d->hidden, false,
                               at<uint32_t>(ws, w.s_items_dn), st),
             "shared GEMM work list launch");
-    MOE_TRY(run_gemm(p0, p1, x16, xdt, false, true, nullptr, 1, at<uint32_t>(ws, w.s_off),
+    MOE_TRY(run_gemm(p0, p1, x16, xdt, true, nullptr, 1, at<uint32_t>(ws, w.s_off),
                      at<uint32_t>(ws, w.s_items_gu), T, at<void>(ws, w.s_act), d->activation,
                      d->act_alpha, d->act_limit, st));
-    MOE_TRY(run_gemm(d->shared_down, nullptr, at<void>(ws, w.s_act), xdt, false, false, nullptr, 1,
+    MOE_TRY(run_gemm(d->shared_down, nullptr, at<void>(ws, w.s_act), xdt, false, nullptr, 1,
                      at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_items_dn), T,
                      at<void>(ws, w.s_out), 0, 0.f, 0.f, st));
   } else {
@@ -1430,7 +1439,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
                                 at<uint32_t>(ws, w.items_gu), H, false, at<uint32_t>(ws, w.items_dn),
                                 st),
               "GEMM work list launch");
-      MOE_TRY(run_gemm(p0, p1, x16, xdt, false, true, at<uint32_t>(ws, w.perm), k,
+      MOE_TRY(run_gemm(p0, p1, x16, xdt, true, at<uint32_t>(ws, w.perm), k,
                        at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.items_gu), M,
                        at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st, kev(0)));
     } else {
@@ -1441,7 +1450,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     }
     // 4. down projection, then the weighted combine (MoELayer.swift:899-939)
     if (gemm) {
-      MOE_TRY(run_gemm(d->down, nullptr, at<void>(ws, w.act), xdt, false, false, nullptr, 1,
+      MOE_TRY(run_gemm(d->down, nullptr, at<void>(ws, w.act), xdt, false, nullptr, 1,
                        at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.items_dn), M,
                        at<void>(ws, w.Y), 0, 0.f, 0.f, st, kev(1)));
     } else {

@@ -321,7 +321,7 @@ hipError_t launch_dispatch_plan(const uint32_t* idx, int T, int k, int E, uint32
 }
 
 struct ItemCols {
-  int nb[2][3];  // column blocks per tile shape, for each of the two lists
+  int nb[2][kGemmShapes];  // column blocks per tile shape, for each of the two lists
 };
 
 // Work items of the grouped GEMM over an expert-sorted plan (the list format
@@ -350,7 +350,7 @@ __global__ __launch_bounds__(kPlanThreads) void gemm_items_kernel(
     }
     const uint32_t full = rows / 256u, rem = rows % 256u;
     // the remainder takes the smallest shape that holds it
-    const int rs = rem > 128u ? 0 : (rem > 64u ? 1 : 2);
+    const int rs = gemm_shape_for((int)rem);
     cnt[0][j] = full * (uint32_t)ic.nb[0][0] + (rem ? (uint32_t)ic.nb[0][rs] : 0u);
     cnt[1][j] = full * (uint32_t)ic.nb[1][0] + (rem ? (uint32_t)ic.nb[1][rs] : 0u);
     tot0 += cnt[0][j];
@@ -411,7 +411,7 @@ __global__ __launch_bounds__(kPlanThreads) void gemm_items_kernel(
         const uint32_t rem = rows % 256u;
         tile = full;
         b = k - full * nb0;
-        shape = rem > 128u ? 0u : (rem > 64u ? 1u : 2u);
+        shape = (uint32_t)gemm_shape_for((int)rem);
       }
       uint32_t* it = items + 1 + 3 * i;
       it[0] = e | (shape << 30);
@@ -426,7 +426,7 @@ hipError_t launch_gemm_items(const uint32_t* offsets, int E, int N0, bool gateup
                              hipStream_t st) {
   if (E > kPlanMaxE) return hipErrorInvalidValue;
   ItemCols ic{};
-  for (int sh = 0; sh < 3; sh++) {
+  for (int sh = 0; sh < kGemmShapes; sh++) {
     ic.nb[0][sh] = (N0 + gemm_cols(sh, gateup0) - 1) / gemm_cols(sh, gateup0);
     ic.nb[1][sh] = items1 ? (N1 + gemm_cols(sh, gateup1) - 1) / gemm_cols(sh, gateup1) : 0;
   }

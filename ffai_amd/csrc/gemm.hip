@@ -11,33 +11,34 @@
 //
 // Operands are f16 on v_mfma_f32_32x32x16_f16:
 //  - weights are dequantised exactly to s * q + b rounded once to f16
-//    (2^-12 relative; bf16 operands would round them to 2^-9): codes enter
-//    as 1024 + q (exact in f16), one packed subtraction gives q, one packed
-//    fma s * q + b;
+//    (2^-12 relative; bf16 operands would round them to 2^-9): 4-bit codes
+//    become f16 q through the scaled fp8 conversion, other widths enter as
+//    1024 + q (exact in f16) less 1024; one packed fma gives s * q + b;
 //  - activations of an f16 layer are used as they are; those of a bf16 layer
 //    are scaled by 2^-8 into f16 range (exact for magnitudes 2^-6 .. 1.6e7,
-//    saturating beyond), either beforehand (launch_to_a16, and the gate/up
-//    epilogue writes its activation in that form for the down GEMM) or while
-//    staging (a_bf16); the epilogue multiplies the fp32 sums by 2^8.
+//    saturating beyond) beforehand (launch_to_a16, and the gate/up epilogue
+//    writes its activation in that form for the down GEMM); the epilogue
+//    multiplies the fp32 sums by 2^8.
 //
 // Work: a list of items (expert, first sorted position, column block) built
 // on the device from the CSR offsets (launch_gemm_items). An expert's rows go
-// in tiles of 256, and its last tile takes the smallest block shape that holds
-// the rest, so the matrix cores see few padded rows:
+// in tiles of 256, and a last tile of at most 128 rows takes the half shape:
 //   shape 0: 256 rows x 256 weight rows, waves 4 x 2, 64 x 128 per wave;
-//   shape 1: 128 rows x 256 weight rows, waves 2 x 4, 64 x 64 per wave;
-//   shape 2:  64 rows x 512 weight rows, waves 1 x 8, 64 x 64 per wave.
+//   shape 1: 128 rows x 256 weight rows, waves 2 x 4, 64 x 64 per wave.
 // A wave owns 64 rows x NJ * 32 weight rows (gate/up: half gate, half up, so
-// the epilogue pairs them in one lane). (128 x 512 with 64 x 128 per wave
-// would match shape 0's MFMA work per block but needs two weight units per
-// thread next to 128 accumulators and spills registers.) Blocks b, b + 8, ...
+// the epilogue pairs them in one lane); a wave whose rows hold no position of
+// the expert skips its MFMAs. Both shapes dequantise 256 weight rows per
+// chunk, one unit per thread, so a block's cost is set mostly by K; a
+// 64-row shape over 512 weight rows would need LDS for two more weight rows
+// per thread than the three activation stages leave. Blocks b, b + 8, ...
 // run on one XCD: the items are split into 8 contiguous ranges at run time,
 // one per XCD, so neighbouring column blocks of a row tile share its L2.
 //
-// Per 64-value chunk of K the block stages the tile's activation rows and its
-// weight rows (dequantised once per block) in double-buffered LDS; global loads
-// run two chunks ahead in registers, the next chunk's weights are dequantised
-// between the MFMA steps, and block barriers order LDS only.
+// Per 64-value chunk of K the block holds the tile's activation rows (copied
+// from memory straight into a ring of three LDS stages, two chunks ahead) and
+// its weight rows (codes, scales and biases loaded three chunks ahead into
+// registers, dequantised once per block into two LDS buffers between the MFMA
+// steps of the chunk before). One block barrier per chunk.
 #include <hip/hip_ext.h>
 
 #include <type_traits>
@@ -62,6 +63,33 @@ __device__ __forceinline__ f32x16_t mma_f16(u32x4_t a, u32x4_t b, f32x16_t c) {
 
 constexpr int kGBK = 64;  // values per K chunk (128 bytes of an LDS row)
 
+// vector-memory instructions of one bload_unit
+template <int BITS>
+constexpr int kUnitLoads = (BITS == 5 || BITS == 6 || BITS == 8) ? 2 : 1;
+
+// s_waitcnt for at most N outstanding vector-memory operations (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14; expcnt 6:4 and lgkmcnt 11:8 left
+// at their maxima)
+template <int N>
+__device__ __forceinline__ void vmcnt_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Block barrier for LDS written by this block's LDS stores and by its
+// memory-to-LDS copies of earlier chunks: waits for the wave's own LDS
+// operations (lgkmcnt 0) only. A release fence on LDS would also wait for
+// every memory-to-LDS copy in flight, including the ones issued for chunks
+// two ahead; the callers wait for the copies that must have landed
+// (vmcnt_wait) themselves. The signal fences keep the compiler from moving
+// memory operations across the barrier.
+__device__ __forceinline__ void lds_barrier_copies_in_flight() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt at their maxima
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // LDS tiles are 128 B per row. The banks repeat every 256 B (two rows) and a
 // 16-byte read serves 16 lanes per cycle, so the 16-byte chunk c of row r
 // sits at slot c ^ ((r >> 1) & 7): 16 consecutive rows reading the same
@@ -74,7 +102,14 @@ __device__ __forceinline__ uint32_t tile_off(int r, int c) {
 template <int S> struct GShape;
 template <> struct GShape<0> { static constexpr int MR = 256, NR = 256, WMN = 4, NJ = 4; };
 template <> struct GShape<1> { static constexpr int MR = 128, NR = 256, WMN = 2, NJ = 2; };
-template <> struct GShape<2> { static constexpr int MR = 64, NR = 512, WMN = 1, NJ = 2; };
+
+// LDS: three activation stages (one object each, so that the compiler tracks
+// the memory-to-LDS copies into each stage on their own and waits for only
+// the stage a read needs) and the two weight buffers.
+constexpr int kAStageBytes = 256 * 128, kBBufBytes = 256 * 128;
+struct GemmLds {
+  unsigned char *a0, *a1, *a2, *b;
+};
 
 struct ProjViewG {
   rsrc_t w, s, b;
@@ -157,14 +192,6 @@ __device__ __forceinline__ h2_t sb_h2(uint32_t raw16, bool bf16) {
   return __builtin_bit_cast(h2_t, h | (h << 16));
 }
 
-// Two bf16 values -> f16 * 2^-8 (round toward zero, so finite values saturate
-// instead of overflowing; exact wherever the result is a normal f16).
-__device__ __forceinline__ uint32_t bf2_to_a16(uint32_t u) {
-  const float lo = __builtin_ldexpf(__uint_as_float(u << 16), -kA16Shift);
-  const float hi = __builtin_ldexpf(__uint_as_float(u & 0xFFFF0000u), -kA16Shift);
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
-}
-
 // One stored output value (fp32, already in the output's units) as the f16 A
 // operand of the next GEMM: round to the layer dtype first (the reference
 // stores the activation in it), then scale into f16 range, saturating.
@@ -180,17 +207,22 @@ __device__ __forceinline__ _Float16 to_a16(float v) {
 
 // One block's tile: rows [m0, m0 + MR) of expert e (positions below pend),
 // weight rows of column block bn.
-template <int S, int BITS, typename XT, bool GATEUP, bool ABF16>
-__device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds, uint32_t e,
-                                          uint32_t m0, int bn) {
+template <int S, int BITS, typename XT, bool GATEUP>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, uint32_t e, uint32_t m0,
+                                          int bn) {
   typedef GShape<S> G;
   constexpr int MR = G::MR, NR = G::NR, WMN = G::WMN, WN = 8 / WMN, NJ = G::NJ;
-  constexpr int ABUF = MR * 128, BBUF = NR * 128;
+  constexpr int BBUF = NR * 128;
   constexpr int AI = MR / 64;       // activation copies of 16 B per thread per chunk
   constexpr int BI = NR * 2 / 512;  // weight units per thread per chunk
+  static_assert(MR * 128 <= kAStageBytes && 2 * BBUF <= kBBufBytes * 2, "LDS layout");
   constexpr float OSCALE = __is_same(XT, bf16_t) ? (float)(1 << kA16Shift) : 1.0f;
-  unsigned char* As = lds;
-  unsigned char* Bs = lds + 2 * ABUF;
+  unsigned char* Bs = L.b;  // two weight buffers of BBUF bytes
+  // activation stage ST (compile time: each stage is its own LDS object)
+  auto stage = [&](auto st) -> unsigned char* {
+    constexpr int ST = decltype(st)::value;
+    return ST == 0 ? L.a0 : (ST == 1 ? L.a1 : L.a2);
+  };
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
@@ -199,8 +231,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds,
   const int nchunks = K / kGBK;
   const bool sb_bf16 = a.sb_bf16 != 0;
 
-  // ---- activation rows: thread t copies, for i < AI, the 16 bytes of LDS
-  // row t / 8 + 64 i in slot t % 8 (logical chunk (t % 8) ^ tile_swz(row))
+  // ---- activation rows go from memory straight to LDS (buffer loads with
+  // the LDS flag: lane l of a wave writes the 16 bytes at M0 + 16 l). Thread
+  // t fills, for i < AI, slot t % 8 of LDS row t / 8 + 64 i with the row's
+  // logical 16-byte chunk (t % 8) ^ tile_swz(row); a wave's 64 lanes cover 8
+  // consecutive rows, one contiguous KB of LDS.
   const rsrc_t xr = make_rsrc(a.x, (uint32_t)min((size_t)a.x_rows * K * 2u, (size_t)0xFFFFFFFFu));
   uint32_t xoff[AI];
 #pragma unroll
@@ -211,23 +246,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds,
     const int c = (threadIdx.x & 7) ^ tile_swz(r);
     xoff[i] = (xrow * (uint32_t)K + (uint32_t)(8 * c)) * 2u;
   }
-  const uint32_t aoff0 = (uint32_t)((threadIdx.x >> 3) * 128 + ((threadIdx.x & 7) << 4));
-  struct ARegs {
-    u32x4_t v[AI];
-  };
-  auto load_a = [&](int chunk, ARegs& ar) {
-#pragma unroll
-    for (int i = 0; i < AI; i++) ar.v[i] = bload128(xr, xoff[i] + (uint32_t)(chunk * kGBK * 2));
-  };
-  auto store_a = [&](const ARegs& ar, int buf) {
+  auto dma_a = [&](int chunk, auto st) {
 #pragma unroll
     for (int i = 0; i < AI; i++) {
-      u32x4_t v = ar.v[i];
-      if constexpr (ABF16) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) v[q] = bf2_to_a16(v[q]);
-      }
-      *reinterpret_cast<u32x4_t*>(As + buf * ABUF + aoff0 + 64 * 128 * i) = v;
+      unsigned char* dst = stage(st) + (64 * i + 8 * wave) * 128;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)dst, 16,
+                                               xoff[i] + (uint32_t)(chunk * kGBK * 2), 0, 0, 0);
     }
   };
 
@@ -257,16 +281,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds,
     else
       PB[i] = proj_view_g<BITS>(a.p0, e, N, row_words, groups);
   }
-  // packed codes, scale and bias of a thread's units: two register sets, so
-  // chunk c + 2 is in flight while chunk c + 1 is dequantised
+  // packed codes, scale and bias of a thread's units: three register sets,
+  // so chunks c + 2 and c + 3 are in flight while chunk c + 1 is dequantised
   struct BUnits {
     uint32_t w[BI][BITS];
     uint32_t s[BI], b[BI];  // raw 16-bit scale and bias (kept apart: combining them
                             // where they load would wait for both loads right there)
   };
-  // scales and biases load apart from the codes: a chunk issues them first,
-  // so that they have landed by the time the chunk's activations (issued
-  // next, and waited for first thing in the following chunk) have
   auto load_sb = [&](int chunk, BUnits& u) {
     const int unit = 2 * chunk + bu;
 #pragma unroll
@@ -329,12 +350,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds,
     return (uint32_t)(r + col) * 128u;
   };
 
-  // the operand fragments of one 16-value step of the chunk in LDS buffer buf
+  // the operand fragments of one 16-value step of a chunk: activations from
+  // stage st, weights from buffer buf
   struct Frags {
     u32x4_t b[NJ], a[2];
   };
-  auto read_frags = [&](int buf, int s, Frags& f) {
-    const unsigned char* Ab = As + buf * ABUF;
+  auto read_frags = [&](auto st, int buf, int s, Frags& f) {
+    const unsigned char* Ab = stage(st);
     const unsigned char* Bb = Bs + buf * BBUF;
     const uint32_t sw = (uint32_t)(((2 * s + h) ^ tile_swz(col)) << 4);
 #pragma unroll
@@ -349,85 +371,113 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds,
 #pragma unroll
       for (int j = 0; j < NJ; j++) acc[i][j] = mma_f16(f.a[i], f.b[j], acc[i][j]);
   };
-  // Chunk c on buffer buf. Its first fragments are read as soon as the
-  // previous chunk's barrier has passed, and the previous chunk's last MFMA
-  // step (operands already in registers, `last`) is issued behind those
-  // reads, so the matrix cores work while this chunk's first operands arrive
-  // and while the activations of chunk c + 1 (loaded during chunk c - 1) go
-  // from `ar` to the other buffer, which that barrier freed. `ar` then takes
-  // chunk c + 2's loads; chunk c + 1's weights (set nb) are dequantised into
-  // the other buffer between the MFMA steps, and chunk c + 2's weights load
-  // into the set cb that chunk c used. This chunk's own last step is left in
-  // `last`. Loads and LDS writes are unconditional (past the end they repeat
-  // the last chunk, in bounds and never read) so that the compiler can count
+  // vector-memory instructions per thread: a chunk's activation copies, and
+  // one chunk's scales, biases and codes
+  constexpr int kCopyLoads = AI, kUnitSetLoads = BI * (2 + kUnitLoads<BITS>);
+  // A chunk's activations were issued one chunk before its barrier, ahead of
+  // that chunk's weight loads (in the program, and sched_barriers keep them
+  // there); at most the weight loads of that chunk plus everything the next
+  // chunk issued may then be outstanding.
+  constexpr int kCopyWait = kCopyLoads + 2 * kUnitSetLoads;
+  // Chunk c: activations in stage ST = c % 3, weights in buffer buf = c % 2.
+  // Its first fragments are read as soon as the previous chunk's barrier has
+  // passed, and the previous chunk's last MFMA step (operands already in
+  // registers, `last`) is issued behind those reads, so the matrix cores work
+  // while this chunk's first operands arrive. Then chunk c + 2's activations
+  // go to stage (c + 2) % 3, which held chunk c - 1 (free since that
+  // barrier), and chunk c + 3's scales, biases and codes to the register set
+  // cb that chunk c used; chunk c + 1's weights (set nb) are dequantised into
+  // the other buffer between the MFMA steps. This chunk's own last step is
+  // left in `last`. Loads are unconditional (past the end they repeat the
+  // last chunk, in bounds and never read) so that the compiler can count
   // outstanding loads exactly. MV: row tiles of this wave with positions of
   // the expert (0..2), a compile-time constant, so each version of the loop
   // is straight-line code.
-  auto chunk_step = [&](auto mv, auto pending, int c, int buf, ARegs& ar, BUnits& cb, const BUnits& nb,
+  auto chunk_step = [&](auto mv, auto pending, auto st, int c, BUnits& cb, const BUnits& nb,
                         Frags& last) {
-    const int cp = min(c + 2, nchunks - 1);
+    constexpr int ST = decltype(st)::value;
+    const int buf = c & 1;
     Frags f0, f1;
-    read_frags(buf, 0, f0);
+    read_frags(st, buf, 0, f0);
     if constexpr (decltype(pending)::value) mma_step(mv, last);
-    store_a(ar, buf ^ 1);
-    load_sb(cp, cb);
-    load_a(cp, ar);
-    load_w(cp, cb);
-    // keep chunk c + 2's loads issued here (sunk below the first weight
+    dma_a(min(c + 2, nchunks - 1), std::integral_constant<int, (ST + 2) % 3>{});
+    __builtin_amdgcn_sched_barrier(0);
+    load_sb(min(c + 3, nchunks - 1), cb);
+    load_w(min(c + 3, nchunks - 1), cb);
+    // keep chunk c + 3's loads issued here (sunk below the first weight
     // dequantisation they would turn its wait into a wait for every load)
     __builtin_amdgcn_sched_barrier(0);
     h2_t s2[BI], b2[BI];
     sb_pairs(nb, s2, b2);
-    read_frags(buf, 1, f1);
+    read_frags(st, buf, 1, f1);
     mma_step(mv, f0);
     store_b(nb, s2, b2, 0, buf ^ 1);
-    read_frags(buf, 2, f0);
+    read_frags(st, buf, 2, f0);
     mma_step(mv, f1);
     store_b(nb, s2, b2, 1, buf ^ 1);
-    read_frags(buf, 3, last);
+    read_frags(st, buf, 3, last);
     mma_step(mv, f0);
     store_b(nb, s2, b2, 2, buf ^ 1);
     store_b(nb, s2, b2, 3, buf ^ 1);
-    lds_barrier();
+    // this wave's copies of chunk c + 1's activations have landed; the
+    // barrier then publishes every wave's
+    vmcnt_wait<kCopyWait>();
+    lds_barrier_copies_in_flight();
   };
 
-  ARegs ar;
-  BUnits u0, u1;
+  using S0_ = std::integral_constant<int, 0>;
+  using S1_ = std::integral_constant<int, 1>;
+  using S2_ = std::integral_constant<int, 2>;
+  BUnits u0, u1, u2;
+  dma_a(0, S0_{});
+  __builtin_amdgcn_sched_barrier(0);
   load_sb(0, u0);
-  load_a(0, ar);
   load_w(0, u0);
+  __builtin_amdgcn_sched_barrier(0);
+  dma_a(min(1, nchunks - 1), S1_{});
+  __builtin_amdgcn_sched_barrier(0);
   load_sb(min(1, nchunks - 1), u1);
   load_w(min(1, nchunks - 1), u1);
-  store_a(ar, 0);
-  load_a(min(1, nchunks - 1), ar);
+  load_sb(min(2, nchunks - 1), u2);
+  load_w(min(2, nchunks - 1), u2);
+  __builtin_amdgcn_sched_barrier(0);
   {
     h2_t s2[BI], b2[BI];
     sb_pairs(u0, s2, b2);
 #pragma unroll
     for (int s = 0; s < 4; s++) store_b(u0, s2, b2, s, 0);
   }
-  lds_barrier();
+  vmcnt_wait<kCopyLoads + 3 * kUnitSetLoads>();  // chunk 0's activations
+  lds_barrier_copies_in_flight();
 
-  // Two chunks per trip and the odd chunk after the loop: with the second
-  // step conditional inside the loop, the path that skips it would make the
-  // compiler's load-counter state at the loop header that of the first step's
-  // last loads, and every chunk would then start by waiting for all of the
-  // previous chunk's loads.
+  // Three chunks per trip (the stage and register-set rotation), the rest
+  // after the loop: with steps conditional inside the loop, a path skipping
+  // them would leave the compiler's load-counter state at the loop header
+  // that of an earlier step, and every chunk would then start by waiting for
+  // all of the previous chunk's loads.
   auto run = [&](auto mv) {
     Frags last;
-    chunk_step(mv, std::false_type{}, 0, 0, ar, u0, u1, last);
+    chunk_step(mv, std::false_type{}, S0_{}, 0, u0, u1, last);
     int c = 1;
-    for (; c + 1 < nchunks; c += 2) {
-      chunk_step(mv, std::true_type{}, c, 1, ar, u1, u0, last);
-      chunk_step(mv, std::true_type{}, c + 1, 0, ar, u0, u1, last);
+    for (; c + 2 < nchunks; c += 3) {
+      chunk_step(mv, std::true_type{}, S1_{}, c, u1, u2, last);
+      chunk_step(mv, std::true_type{}, S2_{}, c + 1, u2, u0, last);
+      chunk_step(mv, std::true_type{}, S0_{}, c + 2, u0, u1, last);
     }
-    if (c < nchunks) chunk_step(mv, std::true_type{}, c, 1, ar, u1, u0, last);
+    if (c < nchunks) {
+      chunk_step(mv, std::true_type{}, S1_{}, c, u1, u2, last);
+      if (c + 1 < nchunks) chunk_step(mv, std::true_type{}, S2_{}, c + 1, u2, u0, last);
+    }
     mma_step(mv, last);
   };
   // mvalid is wave-uniform: one scalar branch picks the loop
   if (mvalid == 2) run(std::integral_constant<int, 2>{});
   else if (mvalid == 1) run(std::integral_constant<int, 1>{});
   else run(std::integral_constant<int, 0>{});
+  // the repeated last-chunk copies may still be landing in LDS, which the
+  // epilogue reuses
+  vmcnt_wait<0>();
+  lds_barrier();
 
   // epilogue: lane holds column col, rows 8 (r / 4) + 4 h + r % 4 of each
   // 32 x 32 tile. The wave's outputs (64 rows x OC columns, 16-bit) go
@@ -438,7 +488,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds,
   const int cbase = GATEUP ? bn * (NR / 2) + wn * OC : bn * NR + wn * OC;
   const XT* ob0 = reinterpret_cast<const XT*>(a.p0.ob);
   const XT* ob1 = reinterpret_cast<const XT*>(GATEUP ? a.p1.ob : a.p0.ob);
-  uint16_t* wt = reinterpret_cast<uint16_t*>(lds) + wave * 64 * OC;
+  uint16_t* wt = reinterpret_cast<uint16_t*>(L.b) + wave * 64 * OC;  // 64 KB at most
 #pragma unroll
   for (int j = 0; j < HJ; j++) {
     const int cn = cbase + 32 * j + col;
@@ -481,11 +531,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, unsigned char* lds,
   }
 }
 
-template <int BITS, typename XT, bool GATEUP, bool ABF16>
+template <int BITS, typename XT, bool GATEUP>
 __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
-  // the largest shape: shape 2's two buffers of 64 activation rows and 512
-  // weight rows (144 KB); shapes 0 and 1 use 128 and 96 KB
-  __shared__ __align__(16) unsigned char lds[2 * (64 + 512) * 128];
+  __shared__ __align__(16) unsigned char a0[kAStageBytes], a1[kAStageBytes], a2[kAStageBytes];
+  __shared__ __align__(16) unsigned char b[2 * kBBufBytes];
   // the items split into 8 contiguous ranges, one per XCD (blocks b, b + 8,
   // ... share an XCD)
   const uint32_t n = __builtin_amdgcn_readfirstlane(a.items[0]);
@@ -498,14 +547,14 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(a.items[2 + 3 * wi]);
   const int bn = (int)__builtin_amdgcn_readfirstlane(a.items[3 + 3 * wi]);
   const uint32_t e = tag & 0x3FFFFFFFu, shape = tag >> 30;
-  if (shape == 0) gemm_tile<0, BITS, XT, GATEUP, ABF16>(a, lds, e, m0, bn);
-  else if (shape == 1) gemm_tile<1, BITS, XT, GATEUP, ABF16>(a, lds, e, m0, bn);
-  else gemm_tile<2, BITS, XT, GATEUP, ABF16>(a, lds, e, m0, bn);
+  const GemmLds L{a0, a1, a2, b};
+  if (shape == 0) gemm_tile<0, BITS, XT, GATEUP>(a, L, e, m0, bn);
+  else gemm_tile<1, BITS, XT, GATEUP>(a, L, e, m0, bn);
 }
 
-template <int BITS, typename XT, bool GATEUP, bool ABF16>
+template <int BITS, typename XT, bool GATEUP>
 static hipError_t launch_gemm_v(const GemmArgs& a, int grid, hipStream_t st, KEvents ev) {
-  hipExtLaunchKernelGGL((gemm_grouped_kernel<BITS, XT, GATEUP, ABF16>), dim3(grid), dim3(512), 0, st,
+  hipExtLaunchKernelGGL((gemm_grouped_kernel<BITS, XT, GATEUP>), dim3(grid), dim3(512), 0, st,
                         ev.start, ev.stop, 0, a);
   return hipGetLastError();
 }
@@ -513,20 +562,15 @@ static hipError_t launch_gemm_v(const GemmArgs& a, int grid, hipStream_t st, KEv
 #define MOE_CAT2(a, b) a##b
 #define MOE_CAT(a, b) MOE_CAT2(a, b)
 
-// Gate/up pairs read A16 rows (the layer converts its input first); single
-// projections read A16 rows, or bf16 rows converted while staging (a_bf16).
-hipError_t MOE_CAT(launch_gemm_b, MOE_BITS)(int xdt, bool gateup, bool a_bf16, const GemmArgs& a,
-                                             int grid, hipStream_t st, KEvents ev) {
-  if (xdt == DT_BF16) {
-    if (gateup) return a_bf16 ? hipErrorInvalidValue : launch_gemm_v<MOE_BITS, bf16_t, true, false>(a, grid, st, ev);
-    return a_bf16 ? launch_gemm_v<MOE_BITS, bf16_t, false, true>(a, grid, st, ev)
-                  : launch_gemm_v<MOE_BITS, bf16_t, false, false>(a, grid, st, ev);
-  }
-  if (xdt == DT_F16) {
-    if (a_bf16) return hipErrorInvalidValue;
-    return gateup ? launch_gemm_v<MOE_BITS, f16_t, true, false>(a, grid, st, ev)
-                  : launch_gemm_v<MOE_BITS, f16_t, false, false>(a, grid, st, ev);
-  }
+// A rows are f16 operands (A16 for a bf16 layer) in every case.
+hipError_t MOE_CAT(launch_gemm_b, MOE_BITS)(int xdt, bool gateup, const GemmArgs& a, int grid,
+                                             hipStream_t st, KEvents ev) {
+  if (xdt == DT_BF16)
+    return gateup ? launch_gemm_v<MOE_BITS, bf16_t, true>(a, grid, st, ev)
+                  : launch_gemm_v<MOE_BITS, bf16_t, false>(a, grid, st, ev);
+  if (xdt == DT_F16)
+    return gateup ? launch_gemm_v<MOE_BITS, f16_t, true>(a, grid, st, ev)
+                  : launch_gemm_v<MOE_BITS, f16_t, false>(a, grid, st, ev);
   return hipErrorInvalidValue;
 }
 

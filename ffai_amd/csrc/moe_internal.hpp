@@ -187,8 +187,8 @@ hipError_t launch_convert(const void* src, int sdt, void* dst, int ddt, int64_t 
 // ----------------------------------------------------------------- GEMM --
 // Grouped dequant GEMM over a dispatch plan on the matrix cores, f16
 // operands. The A rows are f16: activations of an f16 layer as they are, or
-// of a bf16 layer scaled by 2^-8 (kA16Shift) into f16 range; with a_bf16 the
-// kernel reads bf16 rows and converts them itself. Gate/up pairs write their
+// of a bf16 layer scaled by 2^-8 (kA16Shift) into f16 range (launch_to_a16),
+// which the kernel copies into LDS as they are. Gate/up pairs write their
 // activation in that same f16 form (the down GEMM's A rows); a single
 // projection writes out_dtype rows.
 constexpr int kA16Shift = 8;
@@ -211,9 +211,10 @@ struct GemmArgs {
 // Block shapes (activation rows x weight rows per block; 8 waves of 64 rows
 // each): an expert's rows go in 256-row tiles, and its last tile is the
 // smallest shape that holds what is left.
-constexpr int kGemmShapeRows[3] = {256, 128, 64};
-constexpr int kGemmShapeWRows[3] = {256, 256, 512};
-inline int gemm_shape_for(int rows) { return rows > 128 ? 0 : (rows > 64 ? 1 : 2); }
+constexpr int kGemmShapes = 2;
+constexpr int kGemmShapeRows[kGemmShapes] = {256, 128};
+constexpr int kGemmShapeWRows[kGemmShapes] = {256, 256};
+__host__ __device__ inline int gemm_shape_for(int rows) { return rows > 128 ? 0 : 1; }
 // Output columns per block: half the weight rows for a gate/up pair.
 inline int gemm_cols(int shape, bool gateup) {
   return gateup ? kGemmShapeWRows[shape] / 2 : kGemmShapeWRows[shape];
@@ -237,8 +238,8 @@ hipError_t launch_gemm_items(const uint32_t* offsets, int E, int N0, bool gateup
                              hipStream_t st);
 // grid: 8 * ceil(gemm_max_items / 8) blocks (items are split evenly over the
 // XCDs at run time; blocks without an item return at once).
-hipError_t launch_gemm(int bits, int xdt, int sbdt, bool gateup, bool a_bf16, const GemmArgs& a,
-                       int grid, hipStream_t st, KEvents ev = {});
+hipError_t launch_gemm(int bits, int xdt, int sbdt, bool gateup, const GemmArgs& a, int grid,
+                       hipStream_t st, KEvents ev = {});
 // Elementwise bf16 -> f16 * 2^-kA16Shift (saturating), n a multiple of 8,
 // 16-byte aligned buffers.
 hipError_t launch_to_a16(const void* x, void* y, int64_t n, hipStream_t st);

@@ -239,9 +239,10 @@ moe_status moe_dequantize_affine(const uint32_t* weight, const void* scales, con
  * p. Replaces Ops.dequantGemvInt4ExpertIndexed(Many) (Ops.swift:2444-2587)
  * and Ops.moeGatherDequantGemmInt4 bm8/bm16/bm64/m1 (Ops.swift:4553-5201,
  * 6499-6585). Picks the HBM-streaming GEMV or the MFMA GEMM by rows per
- * expert. out and a are in a_dtype; n is the projection's output width
- * (p->n), which sizes the GEMM's work list in the workspace. */
-size_t moe_expert_matmul_workspace_bytes(int32_t n_experts, int32_t M, int32_t n);
+ * expert. out and a are in a_dtype. The workspace holds the GEMM's work list
+ * and, for bf16 rows, their f16 operand copy; its size depends on the
+ * projection, the activation dtype and M (0 for invalid arguments). */
+size_t moe_expert_matmul_workspace_bytes(const moe_qproj* p, int32_t a_dtype, int32_t M);
 moe_status moe_expert_matmul(const moe_qproj* p, const void* a, int32_t a_dtype,
                              const uint32_t* perm, int32_t top_k, int32_t M,
                              const uint32_t* offsets, void* out, void* workspace,

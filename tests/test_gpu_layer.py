@@ -230,7 +230,7 @@ def test_expert_matmul_all_widths(bits, dt, sb):
     q.weight, q.scales, q.biases = wt.data_ptr(), st.data_ptr(), bt.data_ptr()
     at = to_torch(a)
     out = torch.empty(M, N, dtype=at.dtype, device="cuda")
-    wsb = lib.moe_expert_matmul_workspace_bytes(E, M, N)
+    wsb = lib.moe_expert_matmul_workspace_bytes(C.byref(q), dt, M)
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
     offt = to_torch(offsets.view(np.int32))
     check(lib.moe_expert_matmul(C.byref(q), _p(at), dt, None, 1, M, _p(offt), _p(out), _p(ws), wsb,
@@ -272,7 +272,7 @@ def test_expert_matmul_mfma(bits, dt, sb, gs, gather):
     q.weight, q.scales, q.biases = wt.data_ptr(), st.data_ptr(), bt.data_ptr()
     at = to_torch(a)
     out = torch.empty(M, N, dtype=at.dtype, device="cuda")
-    wsb = lib.moe_expert_matmul_workspace_bytes(E, M, N)
+    wsb = lib.moe_expert_matmul_workspace_bytes(C.byref(q), dt, M)
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
     offt = to_torch(offsets.view(np.int32))
     pt = to_torch(perm.view(np.int32)) if gather else None
