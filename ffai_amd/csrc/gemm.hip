@@ -393,17 +393,23 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
   // outstanding loads exactly. MV: row tiles of this wave with positions of
   // the expert (0..2), a compile-time constant, so each version of the loop
   // is straight-line code.
-  auto chunk_step = [&](auto mv, auto pending, auto st, int c, BUnits& cb, const BUnits& nb,
-                        Frags& last) {
+  // TAIL: one of the last chunks, which issues only the loads of chunks that
+  // exist and drains all loads before its barrier.
+  auto chunk_step = [&](auto mv, auto pending, auto st, auto tail, int c, BUnits& cb,
+                        const BUnits& nb, Frags& last) {
     constexpr int ST = decltype(st)::value;
+    constexpr bool TAIL = decltype(tail)::value;
     const int buf = c & 1;
     Frags f0, f1;
     read_frags(st, buf, 0, f0);
     if constexpr (decltype(pending)::value) mma_step(mv, last);
-    dma_a(min(c + 2, nchunks - 1), std::integral_constant<int, (ST + 2) % 3>{});
+    if (!TAIL || c + 2 < nchunks)
+      dma_a(min(c + 2, nchunks - 1), std::integral_constant<int, (ST + 2) % 3>{});
     __builtin_amdgcn_sched_barrier(0);
-    load_sb(min(c + 3, nchunks - 1), cb);
-    load_w(min(c + 3, nchunks - 1), cb);
+    if (!TAIL || c + 3 < nchunks) {
+      load_sb(min(c + 3, nchunks - 1), cb);
+      load_w(min(c + 3, nchunks - 1), cb);
+    }
     // keep chunk c + 3's loads issued here (sunk below the first weight
     // dequantisation they would turn its wait into a wait for every load)
     __builtin_amdgcn_sched_barrier(0);
@@ -421,7 +427,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
     store_b(nb, s2, b2, 3, buf ^ 1);
     // this wave's copies of chunk c + 1's activations have landed; the
     // barrier then publishes every wave's
-    vmcnt_wait<kCopyWait>();
+    if constexpr (TAIL) vmcnt_wait<0>();
+    else vmcnt_wait<kCopyWait>();
     lds_barrier_copies_in_flight();
   };
 
@@ -455,29 +462,36 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
   // them would leave the compiler's load-counter state at the loop header
   // that of an earlier step, and every chunk would then start by waiting for
   // all of the previous chunk's loads.
+  // The trips of the loop issue every load unconditionally (each loads
+  // chunks that exist); the last up to five chunks run as tail steps, which
+  // issue no loads past the end, so that no load is still in flight when the
+  // epilogue starts.
   auto run = [&](auto mv) {
+    using Y = std::true_type;
+    using F = std::false_type;
     Frags last;
-    chunk_step(mv, std::false_type{}, S0_{}, 0, u0, u1, last);
+    chunk_step(mv, F{}, S0_{}, F{}, 0, u0, u1, last);
     int c = 1;
-    for (; c + 2 < nchunks; c += 3) {
-      chunk_step(mv, std::true_type{}, S1_{}, c, u1, u2, last);
-      chunk_step(mv, std::true_type{}, S2_{}, c + 1, u2, u0, last);
-      chunk_step(mv, std::true_type{}, S0_{}, c + 2, u0, u1, last);
+    for (; c + 5 < nchunks; c += 3) {
+      chunk_step(mv, Y{}, S1_{}, F{}, c, u1, u2, last);
+      chunk_step(mv, Y{}, S2_{}, F{}, c + 1, u2, u0, last);
+      chunk_step(mv, Y{}, S0_{}, F{}, c + 2, u0, u1, last);
     }
-    if (c < nchunks) {
-      chunk_step(mv, std::true_type{}, S1_{}, c, u1, u2, last);
-      if (c + 1 < nchunks) chunk_step(mv, std::true_type{}, S2_{}, c + 1, u2, u0, last);
-    }
+    if (c < nchunks) chunk_step(mv, Y{}, S1_{}, Y{}, c, u1, u2, last);
+    if (c + 1 < nchunks) chunk_step(mv, Y{}, S2_{}, Y{}, c + 1, u2, u0, last);
+    if (c + 2 < nchunks) chunk_step(mv, Y{}, S0_{}, Y{}, c + 2, u0, u1, last);
+    if (c + 3 < nchunks) chunk_step(mv, Y{}, S1_{}, Y{}, c + 3, u1, u2, last);
+    if (c + 4 < nchunks) chunk_step(mv, Y{}, S2_{}, Y{}, c + 4, u2, u0, last);
     mma_step(mv, last);
   };
   // mvalid is wave-uniform: one scalar branch picks the loop
   if (mvalid == 2) run(std::integral_constant<int, 2>{});
   else if (mvalid == 1) run(std::integral_constant<int, 1>{});
   else run(std::integral_constant<int, 0>{});
-  // the repeated last-chunk copies may still be landing in LDS, which the
-  // epilogue reuses
+  // No load is in flight here unless K is a single chunk (the first step's
+  // clamped copies), and the epilogue reuses LDS: drain them (the last
+  // step's barrier already ordered every wave's reads of the staging areas)
   vmcnt_wait<0>();
-  lds_barrier();
 
   // epilogue: lane holds column col, rows 8 (r / 4) + 4 h + r % 4 of each
   // 32 x 32 tile. The wave's outputs (64 rows x OC columns, 16-bit) go
@@ -488,32 +502,51 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
   const int cbase = GATEUP ? bn * (NR / 2) + wn * OC : bn * NR + wn * OC;
   const XT* ob0 = reinterpret_cast<const XT*>(a.p0.ob);
   const XT* ob1 = reinterpret_cast<const XT*>(GATEUP ? a.p1.ob : a.p0.ob);
-  uint16_t* wt = reinterpret_cast<uint16_t*>(L.b) + wave * 64 * OC;  // 64 KB at most
+  // a wave's 64 x OC outputs take at most 16 KB: waves 0-3 stage them in the
+  // weight buffers, waves 4-7 in the first two activation stages (each LDS
+  // object holds only its own bytes)
+  static_assert(64 * OC * 2 <= 16384, "epilogue staging");
+  unsigned char* wreg = wave < 4 ? L.b + wave * 16384 : (wave < 6 ? L.a0 : L.a1) + (wave & 1) * 16384;
+  uint16_t* wt = reinterpret_cast<uint16_t*>(wreg);
+  // Straight-line per activation kind (a runtime switch inside the loop left
+  // a branch per output). Without an output bias the bias term is -0, the
+  // identity of addition (so the second rounding changes nothing, -0 kept).
+  auto epilogue = [&](auto actc) {
+    constexpr int ACT = decltype(actc)::value;
 #pragma unroll
-  for (int j = 0; j < HJ; j++) {
-    const int cn = cbase + 32 * j + col;
-    const float obg = (ob0 && cn < N) ? to_f<XT>(ob0[(size_t)e * N + cn]) : 0.f;
-    const float obu = (GATEUP && ob1 && cn < N) ? to_f<XT>(ob1[(size_t)e * N + cn]) : 0.f;
+    for (int j = 0; j < HJ; j++) {
+      const int cn = cbase + 32 * j + col;
+      const float obg = (ob0 && cn < N) ? to_f<XT>(ob0[(size_t)e * N + cn]) : -0.0f;
+      const float obu = (GATEUP && ob1 && cn < N) ? to_f<XT>(ob1[(size_t)e * N + cn]) : -0.0f;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+      for (int i = 0; i < 2; i++) {
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-        float v = round_to<XT>(acc[i][j][r] * OSCALE);
-        if (ob0) v = round_to<XT>(v + obg);
-        uint16_t bits;
-        if constexpr (GATEUP) {
-          float u = round_to<XT>(acc[i][j + HJ][r] * OSCALE);
-          if (ob1) u = round_to<XT>(u + obu);
-          bits = __builtin_bit_cast(uint16_t, to_a16<XT>(apply_act<XT>(v, u, a.act, a.alpha, a.limit)));
-        } else {
-          if (a.act == ACT_RELU2) v = apply_act<XT>(0.f, v, ACT_RELU2, 0.f, 0.f);  // single: ReLU^2 only
-          bits = a.out_a16 ? __builtin_bit_cast(uint16_t, to_a16<XT>(v))
-                           : __builtin_bit_cast(uint16_t, from_f<XT>(v));
+        for (int r = 0; r < 16; r++) {
+          const int row = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+          const float v = round_to<XT>(round_to<XT>(acc[i][j][r] * OSCALE) + obg);
+          uint16_t bits;
+          if constexpr (GATEUP) {
+            const float u = round_to<XT>(round_to<XT>(acc[i][j + HJ][r] * OSCALE) + obu);
+            bits = __builtin_bit_cast(uint16_t, to_a16<XT>(apply_act<XT>(v, u, ACT, a.alpha, a.limit)));
+          } else {
+            // single projections: squared ReLU only
+            const float y = ACT == ACT_RELU2 ? apply_act<XT>(0.f, v, ACT_RELU2, 0.f, 0.f) : v;
+            const uint16_t as_a16 = __builtin_bit_cast(uint16_t, to_a16<XT>(y));
+            const uint16_t as_xt = __builtin_bit_cast(uint16_t, from_f<XT>(y));
+            bits = a.out_a16 ? as_a16 : as_xt;
+          }
+          wt[row * OC + 32 * j + col] = bits;
         }
-        wt[row * OC + 32 * j + col] = bits;
       }
     }
+  };
+  if constexpr (GATEUP) {
+    if (a.act == ACT_GPTOSS) epilogue(std::integral_constant<int, ACT_GPTOSS>{});
+    else if (a.act == ACT_GEGLU) epilogue(std::integral_constant<int, ACT_GEGLU>{});
+    else epilogue(std::integral_constant<int, ACT_SWIGLU>{});
+  } else {
+    if (a.act == ACT_RELU2) epilogue(std::integral_constant<int, ACT_RELU2>{});
+    else epilogue(std::integral_constant<int, ACT_SWIGLU>{});
   }
   // each lane: 16 bytes (8 columns) of one row per step; the wave reads only
   // its own region, so no block barrier is needed
