@@ -413,10 +413,11 @@ __global__ __launch_bounds__(kPlanThreads) void gemm_items_kernel(
         b = k - full * nb0;
         shape = (uint32_t)gemm_shape_for((int)rem);
       }
-      uint32_t* it = items + 1 + 3 * i;
+      uint32_t* it = items + 4 + 4 * i;
       it[0] = e | (shape << 30);
       it[1] = first_pos[e] + tile * 256u;
       it[2] = b;
+      it[3] = first_pos[e] + rows;
     }
   }
 }

@@ -209,7 +209,7 @@ __device__ __forceinline__ _Float16 to_a16(float v) {
 // weight rows of column block bn.
 template <int S, int BITS, typename XT, bool GATEUP>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, uint32_t e, uint32_t m0,
-                                          int bn) {
+                                          int bn, uint32_t pend) {
   typedef GShape<S> G;
   constexpr int MR = G::MR, NR = G::NR, WMN = G::WMN, WN = 8 / WMN, NJ = G::NJ;
   constexpr int BBUF = NR * 128;
@@ -226,7 +226,6 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
-  const uint32_t pend = __builtin_amdgcn_readfirstlane(a.offsets[e + 1]);
   const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
   const int nchunks = K / kGBK;
   const bool sb_bf16 = a.sb_bf16 != 0;
@@ -237,15 +236,26 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
   // logical 16-byte chunk (t % 8) ^ tile_swz(row); a wave's 64 lanes cover 8
   // consecutive rows, one contiguous KB of LDS.
   const rsrc_t xr = make_rsrc(a.x, (uint32_t)min((size_t)a.x_rows * K * 2u, (size_t)0xFFFFFFFFu));
-  uint32_t xoff[AI];
+  // the rows' plan entries, loaded without a branch (a view of zero bytes
+  // when there is no gather: loads return 0) and first of all, since the
+  // copies wait for them; turned into row offsets once the weights' first
+  // loads are out (set_xoff)
+  const rsrc_t permv = make_rsrc(a.perm, (uint32_t)__builtin_amdgcn_readfirstlane(a.perm ? -1 : 0));
+  uint32_t xpos[AI], praw[AI], xoff[AI];
 #pragma unroll
   for (int i = 0; i < AI; i++) {
-    const int r = (threadIdx.x >> 3) + 64 * i;
-    const uint32_t p = min(m0 + (uint32_t)r, pend - 1);
-    const uint32_t xrow = a.perm ? a.perm[p] / (uint32_t)a.topk : p;
-    const int c = (threadIdx.x & 7) ^ tile_swz(r);
-    xoff[i] = (xrow * (uint32_t)K + (uint32_t)(8 * c)) * 2u;
+    xpos[i] = min(m0 + (uint32_t)((threadIdx.x >> 3) + 64 * i), pend - 1);
+    praw[i] = bload32(permv, xpos[i] * 4u);
   }
+  auto set_xoff = [&]() {
+#pragma unroll
+    for (int i = 0; i < AI; i++) {
+      const int r = (threadIdx.x >> 3) + 64 * i;
+      const uint32_t xrow = a.perm ? praw[i] / (uint32_t)a.topk : xpos[i];
+      const int c = (threadIdx.x & 7) ^ tile_swz(r);
+      xoff[i] = (xrow * (uint32_t)K + (uint32_t)(8 * c)) * 2u;
+    }
+  };
   auto dma_a = [&](int chunk, auto st) {
 #pragma unroll
     for (int i = 0; i < AI; i++) {
@@ -426,8 +436,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
     store_b(nb, s2, b2, 2, buf ^ 1);
     store_b(nb, s2, b2, 3, buf ^ 1);
     // this wave's copies of chunk c + 1's activations have landed; the
-    // barrier then publishes every wave's
+    // barrier then publishes every wave's (the first chunk's follow only
+    // its own loads: the prologue issued the copies last)
     if constexpr (TAIL) vmcnt_wait<0>();
+    else if constexpr (!decltype(pending)::value) vmcnt_wait<kCopyLoads + kUnitSetLoads>();
     else vmcnt_wait<kCopyWait>();
     lds_barrier_copies_in_flight();
   };
@@ -435,18 +447,19 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
   using S0_ = std::integral_constant<int, 0>;
   using S1_ = std::integral_constant<int, 1>;
   using S2_ = std::integral_constant<int, 2>;
+  // The weights of chunks 0-2 need only the item; the activation copies
+  // wait for the rows' positions (perm): weights first, copies last.
   BUnits u0, u1, u2;
-  dma_a(0, S0_{});
-  __builtin_amdgcn_sched_barrier(0);
   load_sb(0, u0);
   load_w(0, u0);
-  __builtin_amdgcn_sched_barrier(0);
-  dma_a(min(1, nchunks - 1), S1_{});
-  __builtin_amdgcn_sched_barrier(0);
   load_sb(min(1, nchunks - 1), u1);
   load_w(min(1, nchunks - 1), u1);
   load_sb(min(2, nchunks - 1), u2);
   load_w(min(2, nchunks - 1), u2);
+  __builtin_amdgcn_sched_barrier(0);
+  set_xoff();
+  dma_a(0, S0_{});
+  dma_a(min(1, nchunks - 1), S1_{});
   __builtin_amdgcn_sched_barrier(0);
   {
     h2_t s2[BI], b2[BI];
@@ -454,14 +467,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
 #pragma unroll
     for (int s = 0; s < 4; s++) store_b(u0, s2, b2, s, 0);
   }
-  vmcnt_wait<kCopyLoads + 3 * kUnitSetLoads>();  // chunk 0's activations
+  vmcnt_wait<kCopyLoads>();  // chunk 0's activations (only chunk 1's copies may remain)
   lds_barrier_copies_in_flight();
 
-  // Three chunks per trip (the stage and register-set rotation), the rest
-  // after the loop: with steps conditional inside the loop, a path skipping
-  // them would leave the compiler's load-counter state at the loop header
-  // that of an earlier step, and every chunk would then start by waiting for
-  // all of the previous chunk's loads.
   // The trips of the loop issue every load unconditionally (each loads
   // chunks that exist); the last up to five chunks run as tail steps, which
   // issue no loads past the end, so that no load is still in flight when the
@@ -576,13 +584,14 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
   if (j >= per) return;
   const uint32_t wi = (blockIdx.x & 7u) * per + j;
   if (wi >= n) return;
-  const uint32_t tag = __builtin_amdgcn_readfirstlane(a.items[1 + 3 * wi]);
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(a.items[2 + 3 * wi]);
-  const int bn = (int)__builtin_amdgcn_readfirstlane(a.items[3 + 3 * wi]);
+  const uint32_t tag = __builtin_amdgcn_readfirstlane(a.items[4 + 4 * wi]);
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(a.items[5 + 4 * wi]);
+  const int bn = (int)__builtin_amdgcn_readfirstlane(a.items[6 + 4 * wi]);
+  const uint32_t pend = __builtin_amdgcn_readfirstlane(a.items[7 + 4 * wi]);
   const uint32_t e = tag & 0x3FFFFFFFu, shape = tag >> 30;
   const GemmLds L{a0, a1, a2, b};
-  if (shape == 0) gemm_tile<0, BITS, XT, GATEUP>(a, L, e, m0, bn);
-  else gemm_tile<1, BITS, XT, GATEUP>(a, L, e, m0, bn);
+  if (shape == 0) gemm_tile<0, BITS, XT, GATEUP>(a, L, e, m0, bn, pend);
+  else gemm_tile<1, BITS, XT, GATEUP>(a, L, e, m0, bn, pend);
 }
 
 template <int BITS, typename XT, bool GATEUP>

@@ -226,11 +226,12 @@ inline long gemm_max_items(int M, int E, int N, bool gateup) {
   return tiles * ((N + gemm_cols(0, gateup) - 1) / gemm_cols(0, gateup));
 }
 inline size_t gemm_items_bytes(int M, int E, int N, bool gateup) {
-  return (size_t)(1 + 3 * gemm_max_items(M, E, N, gateup)) * 4;
+  return (size_t)(4 + 4 * gemm_max_items(M, E, N, gateup)) * 4;
 }
-// items[0] = count, then per item {expert | shape << 30, first sorted
-// position, column block}: experts ascending, an expert's row tiles in order,
-// a tile's column blocks in order (neighbouring items share activation rows).
+// items[0] = count (items[1..3] unused), then per item, 16-byte aligned,
+// {expert | shape << 30, first sorted position, column block, end of the
+// expert's positions}: experts ascending, an expert's row tiles in order, a
+// tile's column blocks in order (neighbouring items share activation rows).
 // Writes the list for (N0, gateup0) into items0 and, when items1 is
 // non-NULL, the list for (N1, gateup1) over the same tiles into items1.
 hipError_t launch_gemm_items(const uint32_t* offsets, int E, int N0, bool gateup0,
