@@ -50,6 +50,10 @@ CONFIGS = {
     "mixed": dict(H=2048, E=256, k=8, I=512, bits_gu=3, bits_d=6, sb="bf16", act="swiglu",
                   gating="softmax_topk", router_bias=False, T=2048, SI=512,
                   workload="mixed_3b6b_shared_prefill_2048"),
+    # configs[4]'s layer at one token: the 3/6-bit one-token kernels
+    "mixed1": dict(H=2048, E=256, k=8, I=512, bits_gu=3, bits_d=6, sb="bf16", act="swiglu",
+                   gating="softmax_topk", router_bias=False, T=1, SI=512,
+                   workload="mixed_3b6b_shared_decode_b1"),
 }
 
 
@@ -592,11 +596,12 @@ def main():
     if args.config == "gptoss" and not args.batch and not args.no_extra:
         # the metric's other two parts, on the prefill configs (configs[3],
         # configs[4]): fixed counts, independent of --steps / --warmup
-        for name in ("prefill", "mixed"):
+        # plus the one-token 3/6-bit row (configs[4]'s layer at T = 1)
+        for name, st2, wu2, L2 in (("prefill", 60, 6, 4), ("mixed", 60, 6, 4), ("mixed1", 480, 48, 24)):
             c2 = dict(CONFIGS[name])
-            r2, _ = run_config(c2, torch, fl, lib, steps=60, warmup=6, L=4)
+            r2, _ = run_config(c2, torch, fl, lib, steps=st2, warmup=wu2, L=L2)
             out[name] = {"workload": c2["workload"], "tokens_per_s": r2["tokens_per_s"],
-                         "ms_per_step": r2["ms_per_step"], "steps": 60, "warmup": 6,
+                         "ms_per_step": r2["ms_per_step"], "steps": st2, "warmup": wu2,
                          "timing": r2["timing"], "roofline": r2["roofline"],
                          "layer_roofline": r2["layer_roofline"], "paths": r2["config"]["paths"]}
     cpu = None
