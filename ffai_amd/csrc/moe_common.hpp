@@ -383,8 +383,11 @@ template <int BITS> __host__ __device__ __forceinline__ int pair_pos(int v) {
   return blk * P + (i < H ? 2 * i : 2 * (i - H) + 1);
 }
 
+// (hi:lo) >> sh for sh in [0, 32), one v_alignbit_b32. (A 64-bit shift here
+// let the compiler merge neighbouring words of a unit into 64-bit loads from
+// the unit array, which then stayed a memory array instead of registers.)
 __device__ __forceinline__ uint32_t funnel(uint32_t hi, uint32_t lo, int sh) {
-  return sh == 0 ? lo : (uint32_t)((((uint64_t)hi << 32) | lo) >> sh);
+  return __builtin_amdgcn_alignbit(hi, lo, (uint32_t)sh);
 }
 
 // A VGPR copy of c that the compiler cannot fold back into a literal: GFX9
