@@ -141,18 +141,16 @@ def proj_bytes(p, experts):
     return experts * (n * k * p.bits // 8 + 2 * n * (k // p.group_size) * sb)
 
 
-def measured_traffic(workload, T):
-    """HBM bytes per launch of the dominant kernel from the committed FETCH_SIZE
-    / WRITE_SIZE passes (the profiles/*_traffic.json whose "workload" is this
-    one), or None."""
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` (the gate/up launch) from the committed
+    FETCH_SIZE / WRITE_SIZE passes (the profiles/*_traffic.json whose
+    "workload" is this one), or None."""
     import glob
-    if T != 1:
-        return None
     for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_traffic.json"))):
         with open(path) as f:
             data = json.load(f)
         if data.get("workload") == workload:
-            k = data.get("kernels", {}).get("gateup1_kernel")
+            k = data.get("kernels", {}).get(kernel)
             return None if k is None else k["hbm_bytes"]
     return None
 
@@ -724,7 +722,8 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L):
                           peak=HBM_PEAK_GBS, unit="GB/s")
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
     layer_roof["frac"] = round(layer_roof["achieved"] / layer_roof["peak"], 4)
-    roof["traffic"] = measured_traffic(cfg["workload"], T)
+    roof["traffic"] = measured_traffic(cfg["workload"], {
+        "decode1": "gateup1_kernel", "gemm": "gemm_grouped_gateup"}.get(paths["gate_up"], ""))
     roof["kernel"] = {"decode1": "gateup1_kernel (one-token gate/up with routing)",
                       "gemm": "gemm_grouped_kernel (MFMA gate/up over the expert row tiles)",
                       "gemv_mma": "gemv_mma_kernel (MFMA gate/up over the dispatch plan)",
