@@ -698,6 +698,17 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L):
     H, I, k = cfg["H"], cfg["I"], cfg["k"]
     gu_bytes = proj_bytes(lay0.gate, U) + proj_bytes(lay0.up, U) + T * H * 2 + T * k * I * 2
     dn_bytes = proj_bytes(lay0.down, U) + T * k * I * 2 + T * H * 2
+    sh_gu_bytes = sh_dn_bytes = 0
+    if lay0.shared is not None:
+        sg, su, sd = lay0.shared
+        sh_gu_bytes = (0 if sg is None else proj_bytes(sg, 1)) + proj_bytes(su, 1)
+        sh_dn_bytes = proj_bytes(sd, 1)
+    if paths["shared_gate_up"] == "decode1":
+        # the one-token launches also stream the shared expert
+        gu_bytes += sh_gu_bytes + T * su.n * 2
+        dn_bytes += sh_dn_bytes + T * su.n * 2
+        # its activation row is written and read inside the layer: not layer traffic
+        sh_gu_bytes, sh_dn_bytes = -T * su.n * 4, 0
     M = T * k
     gu_flops = 2.0 * M * 2 * H * I
     dn_flops = 2.0 * M * H * I
@@ -705,7 +716,7 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L):
     if cfg["SI"]:
         sh_flops = 2.0 * T * 3 * H * cfg["SI"]
     router_bytes = cfg["E"] * H * 2
-    layer_bytes = gu_bytes + dn_bytes - T * k * I * 4 + router_bytes
+    layer_bytes = gu_bytes + dn_bytes - T * k * I * 4 + router_bytes + sh_gu_bytes + sh_dn_bytes
     if paths["gate_up"] == "gemm":
         roof = dict(bound="mfma", achieved=round(gu_flops / (gu_us * 1e-6) / 1e12, 2),
                     peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s")

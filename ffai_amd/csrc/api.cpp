@@ -1146,6 +1146,23 @@ class SideFork {
   moe_status status_ = MOE_OK;
 };
 
+// The shared expert's sigmoid gate logits (Qwen3xText.swift:947-951) into
+// the workspace, from a dense or a quantised gate row; none without a gate.
+moe_status shared_gate_logits(const moe_layer_desc* d, const void* x, int T, void* ws,
+                              const Workspace& w, hipStream_t st) {
+  const int xdt = d->act_dtype;
+  if (d->shared_gate_q.weight)
+    MOE_HIP(launch_router_q(d->shared_gate_q.bits, x, xdt, T, d->hidden, to_proj(d->shared_gate_q),
+                            d->shared_gate_q.sb_dtype, group_shift(d->shared_gate_q.group_size),
+                            nullptr, 1, at<void>(ws, w.s_logit), st),
+            "shared gate launch");
+  else if (d->shared_gate_weight)
+    MOE_HIP(launch_router_logits(x, xdt, T, d->hidden, d->shared_gate_weight, d->router_dtype,
+                                 nullptr, 1, at<void>(ws, w.s_logit), st),
+            "shared gate launch");
+  return MOE_OK;
+}
+
 // x16: the layer input as the GEMMs' f16 operand (written before the fork
 // when the grouped GEMM runs for the shared expert).
 moe_status shared_expert(const moe_layer_desc* d, const void* x, const void* x16, int T, void* ws,
@@ -1180,16 +1197,7 @@ moe_status shared_expert(const moe_layer_desc* d, const void* x, const void* x16
                      at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), 1, T, single,
                      at<void>(ws, w.s_out), 0, 0.f, 0.f, st));
   }
-  if (d->shared_gate_q.weight)
-    MOE_HIP(launch_router_q(d->shared_gate_q.bits, x, xdt, T, d->hidden, to_proj(d->shared_gate_q),
-                            d->shared_gate_q.sb_dtype, group_shift(d->shared_gate_q.group_size),
-                            nullptr, 1, at<void>(ws, w.s_logit), st),
-            "shared gate launch");
-  else if (d->shared_gate_weight)
-    MOE_HIP(launch_router_logits(x, xdt, T, d->hidden, d->shared_gate_weight, d->router_dtype,
-                                 nullptr, 1, at<void>(ws, w.s_logit), st),
-            "shared gate launch");
-  return MOE_OK;
+  return shared_gate_logits(d, x, T, ws, w, st);
 }
 
 // Decode (T = 1) launch geometry. Lanes per row: the best unit utilisation
@@ -1249,12 +1257,60 @@ bool dec1_supported(const moe_layer_desc* d) {
   return true;
 }
 
-// down projection + weighted combine of one token (down1_kernel).
+// The shared expert of a one-token call inside the two one-token launches
+// (its gate/up rows as more gate/up blocks, its down rows as m = SI / I more
+// waves of each down block, the gated add in the down kernel's combine)
+// instead of five launches of its own: when each shared projection has the
+// bits, group size and scale dtype of its routed counterpart, SI is a
+// multiple of I and k + m waves fit a block. in_kernel_gate: the sigmoid
+// gate's logit comes from one more gate/up block (a dense gate row in the
+// activation dtype, 16-byte aligned); otherwise its own launch writes it.
+struct Dec1Shared {
+  bool on = false, in_kernel_gate = false;
+  int m = 0;
+};
+
+Dec1Shared dec1_shared(const moe_layer_desc* d) {
+  Dec1Shared r;
+  if (!d->has_shared) return r;
+  const bool gated = d->activation != MOE_ACT_RELU2;
+  auto same = [](const moe_qproj& a, const moe_qproj& b) {
+    return a.bits == b.bits && a.group_size == b.group_size && a.sb_dtype == b.sb_dtype;
+  };
+  if ((gated && !same(d->gate, d->shared_gate)) || !same(d->up, d->shared_up) ||
+      !same(d->down, d->shared_down))
+    return r;
+  const int I = d->intermediate, SI = d->shared_up.n;
+  if (SI <= 0 || SI % I != 0 || SI > 8192 || d->top_k + SI / I > kDec1MaxWaves) return r;
+  // shared byte offsets below 2^31, as for the routed stacks
+  const size_t up_row = (size_t)d->shared_up.k * d->shared_up.bits / 8;
+  const size_t dn_row = (size_t)d->shared_down.k * d->shared_down.bits / 8;
+  if (((size_t)SI + 256) * up_row >= (1ull << 31) ||
+      ((size_t)d->hidden + 256) * dn_row >= (1ull << 31))
+    return r;
+  r.on = true;
+  r.m = SI / I;
+  r.in_kernel_gate = d->shared_gate_weight && !d->shared_gate_q.weight &&
+                     d->router_dtype == d->act_dtype &&
+                     reinterpret_cast<uintptr_t>(d->shared_gate_weight) % 16 == 0;
+  return r;
+}
+
+// down projection + weighted combine of one token (down1_kernel), with the
+// shared expert's down rows and gated add when fs.on.
 moe_status run_down1(const moe_layer_desc* d, void* y, const uint32_t* idx, const float* w,
-                     const void* act, hipStream_t st, KEvents ev, const void* res = nullptr) {
+                     const void* act, hipStream_t st, KEvents ev, const void* res = nullptr,
+                     const Dec1Shared& fs = Dec1Shared{}, const void* s_act = nullptr,
+                     const void* s_logit = nullptr) {
   const int k = d->top_k, H = d->hidden, I = d->intermediate;
   const Dec1Geom dg = dec1_geom(H, I, group_shift(d->down.group_size), k, true);
   Down1Args dn{};
+  if (fs.on) {
+    dn.sp = to_proj(d->shared_down);
+    dn.s_act = s_act;
+    dn.s_logit = s_logit;
+    dn.m = fs.m;
+  }
   dn.idx = idx;
   dn.w = w;
   dn.act = act;
@@ -1370,7 +1426,14 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
   // layer 3.5 us more than they saved)
   SideFork side(allow_side && d->has_shared && T >= kGemmMinRows, st);
   MOE_TRY(side.status());
-  MOE_TRY(shared_expert(d, x, x16, T, ws, w, side.stream(), &smode));
+  // one token: the shared expert inside the two one-token launches when its
+  // formats allow (its gate logit from its own launch unless dense)
+  const Dec1Shared fs = dec1 ? dec1_shared(d) : Dec1Shared{};
+  if (fs.on) {
+    if (!fs.in_kernel_gate) MOE_TRY(shared_gate_logits(d, x, T, ws, w, st));
+  } else {
+    MOE_TRY(shared_expert(d, x, x16, T, ws, w, side.stream(), &smode));
+  }
   MOE_TRY(side.mark());
   if (dec1) {
     // 2. one token: routing inside the gate/up kernel (MoELayer.swift:1167-1282
@@ -1401,10 +1464,24 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     g.act_kind = d->activation;
     g.alpha = d->act_alpha;
     g.limit = d->act_limit;
-    MOE_HIP(launch_gateup1(gu.bits, xdt, gu.sb_dtype, g, gg.rm, gg.grid, st, kev(0)),
+    int grid = gg.grid;
+    const bool sgate = fs.on && (d->shared_gate_weight || d->shared_gate_q.weight);
+    if (fs.on) {
+      g.sg = to_proj(d->shared_gate);
+      g.su = to_proj(d->shared_up);
+      g.s_act = at<void>(ws, w.s_act);
+      g.SN = d->shared_up.n;
+      g.s_blocks = (g.SN + gg.rows_per_block - 1) / gg.rows_per_block;
+      g.s_logit = at<void>(ws, w.s_logit);
+      g.sgw = fs.in_kernel_gate ? d->shared_gate_weight : nullptr;
+      grid += g.s_blocks + (fs.in_kernel_gate ? 1 : 0);
+    }
+    MOE_HIP(launch_gateup1(gu.bits, xdt, gu.sb_dtype, g, gg.rm, grid, st, kev(0)),
             "gate/up decode launch");
-    // the residual goes into the last store: down1's without a shared expert
-    MOE_TRY(run_down1(d, y, g.idx, g.w, g.act, st, kev(1), smode ? nullptr : res));
+    // the residual goes into the last store: down1's without a separate
+    // shared expert
+    MOE_TRY(run_down1(d, y, g.idx, g.w, g.act, st, kev(1), smode ? nullptr : res, fs,
+                      at<void>(ws, w.s_act), sgate ? at<void>(ws, w.s_logit) : nullptr));
     MOE_TRY(side.join());
     if (smode)
       MOE_HIP(launch_add_shared(y, at<void>(ws, w.s_out), at<void>(ws, w.s_logit), smode, T, H, xdt,
@@ -1476,7 +1553,8 @@ moe_layer_paths layer_paths(const moe_layer_desc* d, int T, bool x_aligned) {
   auto gk = [](GemvKind kd) { return (int32_t)(kd == kGemvMma ? MOE_PATH_GEMV_MMA : MOE_PATH_GEMV); };
   const moe_qproj& p0 = gated ? d->gate : d->up;
   const moe_qproj* p1 = gated ? &d->up : nullptr;
-  if (T == 1 && dec1_supported(d)) {
+  const bool dec1 = T == 1 && dec1_supported(d);
+  if (dec1) {
     p.gate_up = p.down = MOE_PATH_DECODE1;
   } else if (routed_gemm(d, T)) {
     p.gate_up = p.down = MOE_PATH_GEMM;
@@ -1488,7 +1566,9 @@ moe_layer_paths layer_paths(const moe_layer_desc* d, int T, bool x_aligned) {
   if (d->has_shared) {
     const moe_qproj& s0 = gated ? d->shared_gate : d->shared_up;
     const moe_qproj* s1 = gated ? &d->shared_up : nullptr;
-    if (shared_gemm(d, T)) {
+    if (dec1 && dec1_shared(d).on) {
+      p.shared_gate_up = p.shared_down = MOE_PATH_DECODE1;
+    } else if (shared_gemm(d, T)) {
       p.shared_gate_up = p.shared_down = MOE_PATH_GEMM;
     } else {
       p.shared_gate_up = gk(gemv_kind(s0, s1, x_aligned, xdt, 1, T, T == 1, 1 << 30));

@@ -717,28 +717,76 @@ __global__ __launch_bounds__(256) void gemv_single_kernel(const GemvArgs a) {
 // activation row into LDS once; each lane reads its units from there after
 // its weight loads are in flight (per-lane global loads of the same row
 // would occupy the CU's load path for about a microsecond before routing).
-template <int BITS, typename XT, typename ST, int UR, int RM, int EPL>
+// The shared expert's sigmoid gate logit, round(x . w) over one dense row in
+// the activation dtype: each thread takes 8-value pieces in index order,
+// then the sums go through a fixed DPP tree and the four waves in order.
+template <typename XT>
+__device__ void shared_gate_logit(const XT* x, const XT* w, int K, XT* out) {
+  __shared__ float part[4];
+  const rsrc_t xr = make_rsrc(x, (uint32_t)(K * sizeof(XT)));
+  const rsrc_t wr = make_rsrc(w, (uint32_t)(K * sizeof(XT)));
+  float acc = 0.f;
+#pragma unroll 1
+  for (int c = threadIdx.x; c < K / 8; c += blockDim.x) {
+    const u32x4_t xv = bload128(xr, (uint32_t)c * 16u), wv = bload128(wr, (uint32_t)c * 16u);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      acc = fmaf(to_f<XT>(__builtin_bit_cast(XT, (uint16_t)(xv[q] & 0xFFFFu))),
+                 to_f<XT>(__builtin_bit_cast(XT, (uint16_t)(wv[q] & 0xFFFFu))), acc);
+      acc = fmaf(to_f<XT>(__builtin_bit_cast(XT, (uint16_t)(xv[q] >> 16))),
+                 to_f<XT>(__builtin_bit_cast(XT, (uint16_t)(wv[q] >> 16))), acc);
+    }
+  }
+  acc = group_sum(acc, 6);
+  if ((threadIdx.x & 63) == 63) part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) t += part[i];
+    out[0] = from_f<XT>(t);
+  }
+}
+
+template <int BITS, typename XT, typename ST, int UR, int RM, int EPL, bool SH>
 __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
   __shared__ float sc[kTopkMaxE];
   __shared__ int route[2];
   __shared__ __align__(16) uint32_t xl[kDec1MaxHidden / 2];
+  const int routed_blocks = a.k * a.row_blocks;
+  // the shared expert's gate logit block (the last, with a dense gate row)
+  if (SH && a.sgw && (int)blockIdx.x == routed_blocks + a.s_blocks) {
+    shared_gate_logit<XT>(reinterpret_cast<const XT*>(a.x), reinterpret_cast<const XT*>(a.sgw),
+                          a.K, reinterpret_cast<XT*>(a.s_logit));
+    return;
+  }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar branches below
-  const int slot = blockIdx.x / a.row_blocks, rb = blockIdx.x - slot * a.row_blocks;
-  const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
+  // blocks from routed_blocks on hold rows of the shared expert (expert 0 of
+  // its one-expert projections); the rest a slot of the routed experts
+  const bool shb = SH && (int)blockIdx.x >= routed_blocks;
+  const int slot = shb ? 0 : (int)blockIdx.x / a.row_blocks;
+  const int rb = shb ? (int)blockIdx.x - routed_blocks : (int)blockIdx.x - slot * a.row_blocks;
+  const int N = shb ? a.SN : a.N;
+  const int K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
   const int L = 1 << a.lg, SG = 64 >> a.lg;
   const int sg = lane >> a.lg, li = lane & (L - 1);
   const int r_begin = rb * a.rows_per_block;
   const int r_end = min(N, r_begin + a.rows_per_block);
   const int r0 = r_begin + wave * SG + sg, stride = 4 * SG;
-  const XT* ob_g = reinterpret_cast<const XT*>(a.g.ob);
-  const XT* ob_u = reinterpret_cast<const XT*>(a.u.ob);
+  const GemvProj pg = shb ? a.sg : a.g, pu = shb ? a.su : a.u;
+  const XT* ob_g = reinterpret_cast<const XT*>(pg.ob);
+  const XT* ob_u = reinterpret_cast<const XT*>(pu.ob);
 
   // wave 0 routes the token (every block computes identical, deterministic
   // results); block 0 publishes the routing
   if (wave != 0) stage_x_row<XT, 6>(reinterpret_cast<const XT*>(a.x), K, xl, threadIdx.x - 64,
                                  blockDim.x - 64);
-  if (wave == 0) {
+  if (wave == 0 && shb) {
+    if (lane == 0) {
+      route[0] = 0;
+      route[1] = 0;
+    }
+  } else if (wave == 0) {
     const bool writer = blockIdx.x == 0;
     int sel;
     float wgt = 0.f;
@@ -776,10 +824,10 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
   // squared-ReLU experts have no gate projection (g.w null): the gate reads
   // go to empty buffer views, which return zeros without touching memory
   // (no branch around the loads), and the activation reads u only
-  const ProjView U = proj_view<BITS, ST>(a.u, (uint32_t)e, N, row_words, groups);
-  const rsrc_t none = make_rsrc(a.u.w, 0u);
-  const ProjView G = a.g.w ? proj_view<BITS, ST>(a.g, (uint32_t)e, N, row_words, groups)
-                           : ProjView{none, none, none};
+  const ProjView U = proj_view<BITS, ST>(pu, (uint32_t)e, N, row_words, groups);
+  const rsrc_t none = make_rsrc(pu.w, 0u);
+  const ProjView G = pg.w ? proj_view<BITS, ST>(pg, (uint32_t)e, N, row_words, groups)
+                          : ProjView{none, none, none};
   const uint32_t wstep = (uint32_t)(L * BITS * 4), sstep = (uint32_t)((L >> a.gsh) * sizeof(ST));
   WUnit<BITS, ST> gw[RM][UR], uw[RM][UR];
 #pragma unroll
@@ -796,7 +844,7 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
   float xs[UR];
   lds_x_units_nat<BITS, XT, UR>(xl, li, L, CU, xu, xs);
 
-  XT* act = reinterpret_cast<XT*>(a.act) + (size_t)rank * N;
+  XT* act = shb ? reinterpret_cast<XT*>(a.s_act) : reinterpret_cast<XT*>(a.act) + (size_t)rank * N;
 #pragma unroll
   for (int it = 0; it < RM; it++) {
     float g = group_sum(dot_units<BITS, XT, ST, UR>(gw[it], xu, xs, li, L, CU), a.lg);
@@ -812,16 +860,20 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
   }
 }
 
-// down projection + weighted combine for one token. Block = k waves; wave q
-// takes the rank-q expert and its activation row (registers, pair order),
-// and all waves share the block's rows: sub-group sg owns rows
-// r_begin + sg + it SG for it < RM. Each expert's output is rounded to the
-// activation dtype (then its output bias added and rounded) before it is
-// weighted, as the unfused path stores it (MoELayer.swift:895-939); the
-// weighted outputs are added in rank order.
-template <int BITS, typename XT, typename ST, int UR, int RM>
-__global__ __launch_bounds__(512) void down1_kernel(const Down1Args a) {
-  __shared__ float ys[kDec1MaxK * kDec1MaxRows * 64];
+// down projection + weighted combine for one token. Block = k waves (SH:
+// k + m); wave q < k takes the rank-q expert and its activation row
+// (registers, pair order), wave k + j the j-th column slice of the shared
+// expert, and all waves share the block's rows: sub-group sg owns rows
+// r_begin + sg + it SG for it < RM. Each routed expert's output is rounded
+// to the activation dtype (then its output bias added and rounded) before it
+// is weighted, as the unfused path stores it (MoELayer.swift:895-939); the
+// weighted outputs are added in rank order. The shared expert's slices are
+// summed in fp32 and rounded once, then added to the rounded routed sum with
+// its gate weight, as the shared add does after a separate shared expert.
+template <int BITS, typename XT, typename ST, int UR, int RM, bool SH>
+__global__ __launch_bounds__(SH ? 64 * kDec1MaxWaves : 64 * kDec1MaxK) void down1_kernel(
+    const Down1Args a) {
+  __shared__ float ys[(SH ? kDec1MaxWaves : kDec1MaxK) * kDec1MaxRows * 64];
   __shared__ float wr[kDec1MaxK];
   // wave-uniform by construction; readfirstlane tells the compiler, so the
   // buffer resources built from it stay scalar
@@ -831,59 +883,95 @@ __global__ __launch_bounds__(512) void down1_kernel(const Down1Args a) {
   const int sg = lane >> a.lg, li = lane & (L - 1);
   const int rpb = a.rows_per_block;  // RM * SG
   const int r_begin = blockIdx.x * rpb;
+  const bool shw = SH && q >= a.k;  // a shared-expert wave
+  const int j = q - a.k;            // its column slice
   const XT* ob = reinterpret_cast<const XT*>(a.p.ob);
 
-  const uint32_t e = __builtin_amdgcn_readfirstlane(a.idx[q]);
-  if (lane == 0) wr[q] = round_to<XT>(a.w[q]);
+  uint32_t e = 0;
+  ProjView P;
+  UnitAddr base{0u, 0u};
+  int rw = row_words, grp = groups;
+  const XT* act;
   float obv[RM];
+  if (shw) {
+    rw = a.m * row_words;
+    grp = a.m * groups;
+    P = proj_view<BITS, ST>(a.sp, 0u, N, rw, grp);
+    base.w0 = (uint32_t)(j * row_words * 4);
+    base.s0 = (uint32_t)(j * groups * (int)sizeof(ST));
+    act = reinterpret_cast<const XT*>(a.s_act) + (size_t)j * K;
 #pragma unroll
-  for (int it = 0; it < RM; it++)
-    obv[it] = ob ? to_f<XT>(ob[(size_t)e * N + min(r_begin + sg + it * SG, N - 1)]) : 0.f;
-  const ProjView P = proj_view<BITS, ST>(a.p, e, N, row_words, groups);
+    for (int it = 0; it < RM; it++) obv[it] = 0.f;
+  } else {
+    e = __builtin_amdgcn_readfirstlane(a.idx[q]);
+    if (lane == 0) wr[q] = round_to<XT>(a.w[q]);
+#pragma unroll
+    for (int it = 0; it < RM; it++)
+      obv[it] = ob ? to_f<XT>(ob[(size_t)e * N + min(r_begin + sg + it * SG, N - 1)]) : 0.f;
+    P = proj_view<BITS, ST>(a.p, e, N, row_words, groups);
+    act = reinterpret_cast<const XT*>(a.act) + (size_t)q * K;
+  }
   const uint32_t wstep = (uint32_t)(L * BITS * 4), sstep = (uint32_t)((L >> a.gsh) * sizeof(ST));
   WUnit<BITS, ST> w[RM][UR];
 #pragma unroll
   for (int it = 0; it < RM; it++) {
-    const UnitAddr ad = unit_addr<BITS, ST>((uint32_t)(r_begin + sg + it * SG), row_words, groups, li, a.gsh);
+    UnitAddr ad = unit_addr<BITS, ST>((uint32_t)(r_begin + sg + it * SG), rw, grp, li, a.gsh);
+    ad.w0 += base.w0;
+    ad.s0 += base.s0;
     bload_units<BITS, ST, UR>(P, ad, wstep, sstep, w[it]);
   }
   XUnit<XT> xu[UR];
   float xs[UR];
-  const XT* act = reinterpret_cast<const XT*>(a.act) + (size_t)q * K;
   bload_x_units<BITS, XT, UR>(make_rsrc(act, (uint32_t)(K * sizeof(XT))), li, L, xu, xs);
   __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the math
 
 #pragma unroll
   for (int it = 0; it < RM; it++) {
     float y = group_sum(dot_units<BITS, XT, ST, UR>(w[it], xu, xs, li, L, CU), a.lg);
-    y = round_to<XT>(y);
-    if (ob) y = round_to<XT>(y + obv[it]);
+    if (!shw) {
+      y = round_to<XT>(y);
+      if (ob) y = round_to<XT>(y + obv[it]);
+    }
     if (li == L - 1) ys[q * rpb + sg + it * SG] = y;
   }
   __syncthreads();
   XT* out = reinterpret_cast<XT*>(a.out);
+  const XT* sob = reinterpret_cast<const XT*>(a.sp.ob);
+  const float gate = (SH && a.s_logit)
+                         ? 1.0f / (1.0f + __expf(-to_f<XT>(reinterpret_cast<const XT*>(a.s_logit)[0])))
+                         : 1.0f;
   for (int t = threadIdx.x; t < rpb; t += blockDim.x) {
     const int row = r_begin + t;
     if (row >= N) break;
     float acc = 0.f;
     for (int qq = 0; qq < a.k; qq++) acc += wr[qq] * ys[qq * rpb + t];
-    if (a.res) acc = to_f<XT>(reinterpret_cast<const XT*>(a.res)[row]) + round_to<XT>(acc);
+    if constexpr (SH) {
+      float sv = 0.f;
+      for (int jj = 0; jj < a.m; jj++) sv += ys[(a.k + jj) * rpb + t];
+      sv = round_to<XT>(sv);
+      if (sob) sv = round_to<XT>(sv + to_f<XT>(sob[row]));
+      acc = round_to<XT>(acc);
+      if (a.res) acc = to_f<XT>(reinterpret_cast<const XT*>(a.res)[row]) + acc;
+      acc = acc + gate * sv;
+    } else {
+      if (a.res) acc = to_f<XT>(reinterpret_cast<const XT*>(a.res)[row]) + round_to<XT>(acc);
+    }
     out[row] = from_f<XT>(acc);
   }
 }
 
-template <int BITS, typename XT, typename ST, int UR, int RM>
+template <int BITS, typename XT, typename ST, int UR, int RM, bool SH>
 static hipError_t launch_gateup1_e(int E, const Decode1Args& a, int grid, hipStream_t st,
                                    KEvents ev) {
   if (E <= 64)
-    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, 1>), dim3(grid), dim3(256), 0, st,
-                          ev.start, ev.stop, 0, a);
-  else if (E <= 128)
-    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, 2>), dim3(grid), dim3(256), 0, st,
-                          ev.start, ev.stop, 0, a);
-  else
-    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, kTopkEPL>), dim3(grid), dim3(256), 0,
+    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, 1, SH>), dim3(grid), dim3(256), 0,
                           st, ev.start, ev.stop, 0, a);
+  else if (E <= 128)
+    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, 2, SH>), dim3(grid), dim3(256), 0,
+                          st, ev.start, ev.stop, 0, a);
+  else
+    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, kTopkEPL, SH>), dim3(grid),
+                          dim3(256), 0, st, ev.start, ev.stop, 0, a);
   return hipGetLastError();
 }
 
@@ -893,19 +981,31 @@ static hipError_t launch_dec1_u(bool down, int var, const void* args, int grid, 
   (void)smem;
   if (!down) {
     const Decode1Args& a = *reinterpret_cast<const Decode1Args*>(args);
+    const bool sh = a.s_blocks > 0;
     switch (var) {
-      case 1: return launch_gateup1_e<BITS, XT, ST, UR, 1>(a.E, a, grid, st, ev);
-      case 2: return launch_gateup1_e<BITS, XT, ST, UR, 2>(a.E, a, grid, st, ev);
+      case 1: return sh ? launch_gateup1_e<BITS, XT, ST, UR, 1, true>(a.E, a, grid, st, ev)
+                        : launch_gateup1_e<BITS, XT, ST, UR, 1, false>(a.E, a, grid, st, ev);
+      case 2: return sh ? launch_gateup1_e<BITS, XT, ST, UR, 2, true>(a.E, a, grid, st, ev)
+                        : launch_gateup1_e<BITS, XT, ST, UR, 2, false>(a.E, a, grid, st, ev);
       default: return hipErrorInvalidValue;
     }
   }
   const Down1Args& a = *reinterpret_cast<const Down1Args*>(args);
-  const dim3 block(64 * a.k);
+  const bool sh = a.m > 0;
+  const dim3 block(64 * (a.k + a.m));
+#define MOE_DN(RM)                                                                           \
+  if (sh)                                                                                    \
+    hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, RM, true>), dim3(grid), block, 0,  \
+                          st, ev.start, ev.stop, 0, a);                                      \
+  else                                                                                       \
+    hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, RM, false>), dim3(grid), block, 0, \
+                          st, ev.start, ev.stop, 0, a);
   switch (var) {
-    case 1: hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, 1>), dim3(grid), block, 0, st, ev.start, ev.stop, 0, a); break;
-    case 2: hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, 2>), dim3(grid), block, 0, st, ev.start, ev.stop, 0, a); break;
+    case 1: MOE_DN(1) break;
+    case 2: MOE_DN(2) break;
     default: return hipErrorInvalidValue;
   }
+#undef MOE_DN
   return hipGetLastError();
 }
 

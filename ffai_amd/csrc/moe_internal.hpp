@@ -85,6 +85,16 @@ struct Decode1Args {
   int N, K, gsh, row_blocks, rows_per_block, lg;
   int act_kind;
   float alpha, limit;
+  // A shared expert in the same launch (s_blocks > 0): blocks k * row_blocks
+  // onwards compute its SN gate/up rows (one-expert projections sg / su,
+  // same bits, group size and scale dtype as g / u) into s_act; with sgw (a
+  // dense gate row [K] in the activation dtype) one more block computes the
+  // sigmoid gate's logit into s_logit[0].
+  GemvProj sg, su;
+  void* s_act;               // [SN]
+  int SN, s_blocks;
+  const void* sgw;           // nullable
+  void* s_logit;             // [1]
 };
 
 struct Down1Args {
@@ -95,12 +105,24 @@ struct Down1Args {
   void* out;                 // [N]
   const void* res;           // nullable [N]: residual added before the final rounding
   int k, N, K, gsh, rows_per_block, lg;
+  // A shared expert as m more waves (m > 0): wave k + j reads columns
+  // [j K, (j + 1) K) of the rows of sp (one expert, m K columns, same bits,
+  // group size and scale dtype as p) against s_act[j K, ...); the waves'
+  // sum is rounded (then its output bias added and rounded) and added to
+  // the rounded routed combine with the weight sigmoid(s_logit[0]) (1 when
+  // s_logit is null), as the separate shared-expert path adds it.
+  GemvProj sp;
+  const void* s_act;         // [m K]
+  const void* s_logit;       // nullable [1]
+  int m;
 };
 
 // Launch limits of the decode kernels: a block has one wave per selected
 // expert (down) and each lane holds at most kDec1MaxRows rows of at most 4
 // units each.
 constexpr int kDec1MaxK = 8;
+// Waves of a down1_kernel block with a shared expert: k routed + m shared.
+constexpr int kDec1MaxWaves = 12;
 constexpr int kDec1MaxRows = 2;
 constexpr int kDec1MaxHidden = 8192;  // activation row staged in LDS
 // Weight rows per lane of gemv_multi_kernel: one for a gate/up pair (two

@@ -346,7 +346,9 @@ moe_status moe_layer_forward_residual(const moe_layer_desc* d, const void* h,
 typedef enum moe_path {
     MOE_PATH_NONE = 0,
     MOE_PATH_DECODE1 = 1,   /* one token: gate/up with in-kernel routing,
-                               fused down + combine */
+                               fused down + combine (for the shared stages:
+                               the shared expert runs inside those two
+                               launches) */
     MOE_PATH_GEMV = 2,      /* HBM-streaming grouped GEMV (VALU dot2) */
     MOE_PATH_GEMV_MMA = 3,  /* batched grouped GEMV on the matrix cores */
     MOE_PATH_GEMM = 4       /* grouped GEMM on the matrix cores */

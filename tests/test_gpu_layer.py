@@ -13,8 +13,8 @@ import pytest
 
 import oracle as orc
 from moe_spec import (BF16, F16, F32, affine_quantize, cfg_bits, cfg_gemma4, cfg_gptoss, cfg_mixed,
-                      cfg_nemotron, cfg_qwen3, cfg_tiny, check_close, load, store, to_numpy_f32,
-                      to_torch, with_quantised_router, zipf_router_bias)
+                      cfg_nemotron, cfg_qwen3, cfg_tiny, check_close, gen_qproj, load, store,
+                      to_numpy_f32, to_torch, with_quantised_router, zipf_router_bias)
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -548,6 +548,48 @@ def mixed():
 @pytest.mark.parametrize("T", [1, 24, 64])
 def test_layer_mixed_bits_shared(mixed, T):
     run_layer(mixed, T)
+
+
+def _shared_variant(kind):
+    """One-token shared-expert layers on either side of the limits of the
+    fused path (the shared expert inside the two one-token launches)."""
+    if kind == "m2":        # SI = 2 I: two column slices per down block
+        return cfg_mixed(n_experts=64, shared_inter=1024)
+    if kind == "m5":        # k + m = 13 waves: more than a down block takes
+        return cfg_mixed(n_experts=64, shared_inter=2560)
+    spec = cfg_mixed(n_experts=64)
+    rng = np.random.default_rng(11)
+    H, SI = spec.hidden, 512
+    if kind == "other_bits":  # shared gate/up 4-bit against routed 3-bit
+        spec.shared = (gen_qproj(rng, 1, SI, H, 4, 64, BF16), gen_qproj(rng, 1, SI, H, 4, 64, BF16),
+                       spec.shared[2])
+    elif kind == "f32_gate":  # router and shared gate rows in f32: the gate's own launch
+        spec.router_weight = load(spec.router_weight, BF16)
+        spec.shared_gate_weight = load(spec.shared_gate_weight, BF16)
+        spec.router_dt = F32
+    elif kind == "out_bias":  # output biases on every shared projection
+        spec.shared = (gen_qproj(rng, 1, SI, H, 3, 64, BF16, out_bias_dt=BF16),
+                       gen_qproj(rng, 1, SI, H, 3, 64, BF16, out_bias_dt=BF16),
+                       gen_qproj(rng, 1, H, SI, 6, 64, BF16, out_bias_dt=BF16))
+    return spec
+
+
+@pytest.mark.parametrize("kind,fused", [("m1", True), ("m2", True), ("m5", False),
+                                        ("other_bits", False), ("f32_gate", True),
+                                        ("out_bias", True)])
+def test_one_token_shared_expert(kind, fused):
+    """At one token a shared expert whose projections have the routed ones'
+    formats runs inside gateup1_kernel / down1_kernel (moe_layer_path reports
+    decode1 for its stages), otherwise on its own launches; both match the
+    oracle."""
+    spec = cfg_mixed(n_experts=64) if kind == "m1" else _shared_variant(kind)
+    p = _lib.LayerPaths()
+    check(_lib.load().moe_layer_path(C.byref(spec.device().desc), 1, C.byref(p)))
+    names = p.names()
+    assert names["gate_up"] == names["down"] == "decode1"
+    want = "decode1" if fused else "gemv"
+    assert names["shared_gate_up"] == names["shared_down"] == want, names
+    run_layer(spec, 1, seed=3)
 
 
 BITS_CASES = [(2, 8, 64, F16, BF16), (5, 2, 32, BF16, F16), (8, 5, 128, F16, F16),
