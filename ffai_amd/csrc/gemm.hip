@@ -102,6 +102,10 @@ __device__ __forceinline__ uint32_t tile_off(int r, int c) {
 template <int S> struct GShape;
 template <> struct GShape<0> { static constexpr int MR = 256, NR = 256, WMN = 4, NJ = 4; };
 template <> struct GShape<1> { static constexpr int MR = 128, NR = 256, WMN = 2, NJ = 2; };
+// 64 rows: the waves split the weight rows only (32 each; for a gate/up pair
+// waves 0-3 hold gate rows and 4-7 the matching up rows, paired through LDS
+// in the epilogue), so every wave has MFMA work.
+template <> struct GShape<2> { static constexpr int MR = 64, NR = 256, WMN = 1, NJ = 1; };
 
 // LDS: three activation stages (one object each, so that the compiler tracks
 // the memory-to-LDS copies into each stage on their own and waits for only
@@ -203,6 +207,64 @@ __device__ __forceinline__ _Float16 to_a16(float v) {
     v = fminf(fmaxf(v, -65504.0f), 65504.0f);
   }
   return (_Float16)v;
+}
+
+// Gate/up epilogue of the 64-row shape: wave w < 4 holds gate columns
+// 32 w + col of the block, wave w + 4 the matching up columns. Each wave
+// stores its projections, rounded as the other shapes round them, into a
+// [64 rows][256] 16-bit table in the weight buffers (free after the last
+// barrier); after a block barrier every thread pairs gate and up for 8
+// consecutive output columns of a row and stores them as 16 bytes.
+template <typename XT>
+__device__ __forceinline__ void gateup_epilogue_split(const GemmArgs& a, const GemmLds L,
+                                                      const f32x16_t (&acc)[2][1], uint32_t e,
+                                                      uint32_t m0, int bn, uint32_t pend, int wn,
+                                                      int col, int h, float oscale) {
+  const int N = a.N;
+  uint16_t* tb = reinterpret_cast<uint16_t*>(L.b);
+  const int cn = bn * 128 + 32 * (wn & 3) + col;  // output column of this lane
+  const XT* ob = reinterpret_cast<const XT*>(wn < 4 ? a.p0.ob : a.p1.ob);
+  const float obv = (ob && cn < N) ? to_f<XT>(ob[(size_t)e * N + cn]) : -0.0f;
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int row = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+      const float v = round_to<XT>(round_to<XT>(acc[i][0][r] * oscale) + obv);
+      tb[row * 256 + 32 * wn + col] = __builtin_bit_cast(uint16_t, from_f<XT>(v));
+    }
+  __syncthreads();
+  uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
+  auto finish = [&](auto actc) {
+    constexpr int ACT = decltype(actc)::value;
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      const int q = (int)threadIdx.x + 512 * t;  // 64 rows x 16 pieces of 8 columns
+      const int row = q >> 4, c8 = q & 15;
+      const u32x4_t gv = *reinterpret_cast<const u32x4_t*>(tb + row * 256 + 8 * c8);
+      const u32x4_t uv = *reinterpret_cast<const u32x4_t*>(tb + row * 256 + 128 + 8 * c8);
+      u32x4_t o;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        uint32_t pk = 0;
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+          const float g = to_f<XT>(__builtin_bit_cast(XT, (uint16_t)(gv[k] >> (16 * half))));
+          const float u = to_f<XT>(__builtin_bit_cast(XT, (uint16_t)(uv[k] >> (16 * half))));
+          const uint16_t bits = __builtin_bit_cast(uint16_t, to_a16<XT>(apply_act<XT>(g, u, ACT, a.alpha, a.limit)));
+          pk |= (uint32_t)bits << (16 * half);
+        }
+        o[k] = pk;
+      }
+      const uint32_t p = m0 + (uint32_t)row;
+      const int cn0 = bn * 128 + 8 * c8;
+      if (p < pend && cn0 < N)  // N % 8 == 0 (host check): whole 16-byte groups
+        *reinterpret_cast<u32x4_t*>(out + (size_t)p * N + cn0) = o;
+    }
+  };
+  if (a.act == ACT_GPTOSS) finish(std::integral_constant<int, ACT_GPTOSS>{});
+  else if (a.act == ACT_GEGLU) finish(std::integral_constant<int, ACT_GEGLU>{});
+  else finish(std::integral_constant<int, ACT_SWIGLU>{});
 }
 
 // One block's tile: rows [m0, m0 + MR) of expert e (positions below pend),
@@ -351,7 +413,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
   const uint32_t arow0 = (uint32_t)(64 * wm + col) * 128u;
   auto boff = [&](int j) -> uint32_t {
     int r;
-    if constexpr (GATEUP) {
+    if constexpr (S == 2) {
+      r = 32 * wn + 32 * j;  // gate rows below NR / 2: waves 0-3 gate, 4-7 up
+    } else if constexpr (GATEUP) {
       constexpr int HJ = NJ / 2;  // gate tiles, then the matching up tiles
       r = (j < HJ ? 0 : NR / 2) + 32 * HJ * wn + 32 * (j % HJ);
     } else {
@@ -501,6 +565,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
   // step's barrier already ordered every wave's reads of the staging areas)
   vmcnt_wait<0>();
 
+  if constexpr (GATEUP && S == 2) {
+    gateup_epilogue_split<XT>(a, L, acc, e, m0, bn, pend, wn, col, h, OSCALE);
+    return;
+  }
   // epilogue: lane holds column col, rows 8 (r / 4) + 4 h + r % 4 of each
   // 32 x 32 tile. The wave's outputs (64 rows x OC columns, 16-bit) go
   // through LDS (free after the last barrier) so that the global stores are
@@ -591,7 +659,8 @@ __global__ __launch_bounds__(512) void gemm_grouped_kernel(const GemmArgs a) {
   const uint32_t e = tag & 0x3FFFFFFFu, shape = tag >> 30;
   const GemmLds L{a0, a1, a2, b};
   if (shape == 0) gemm_tile<0, BITS, XT, GATEUP>(a, L, e, m0, bn, pend);
-  else gemm_tile<1, BITS, XT, GATEUP>(a, L, e, m0, bn, pend);
+  else if (shape == 1) gemm_tile<1, BITS, XT, GATEUP>(a, L, e, m0, bn, pend);
+  else gemm_tile<2, BITS, XT, GATEUP>(a, L, e, m0, bn, pend);
 }
 
 template <int BITS, typename XT, bool GATEUP>

@@ -230,13 +230,15 @@ struct GemmArgs {
   int act;
   float alpha, limit;
 };
-// Block shapes (activation rows x weight rows per block; 8 waves of 64 rows
-// each): an expert's rows go in 256-row tiles, and its last tile is the
-// smallest shape that holds what is left.
-constexpr int kGemmShapes = 2;
-constexpr int kGemmShapeRows[kGemmShapes] = {256, 128};
-constexpr int kGemmShapeWRows[kGemmShapes] = {256, 256};
-__host__ __device__ inline int gemm_shape_for(int rows) { return rows > 128 ? 0 : 1; }
+// Block shapes (activation rows x weight rows per block, 8 waves): an
+// expert's rows go in 256-row tiles, and its last tile is the smallest shape
+// that holds what is left.
+constexpr int kGemmShapes = 3;
+constexpr int kGemmShapeRows[kGemmShapes] = {256, 128, 64};
+constexpr int kGemmShapeWRows[kGemmShapes] = {256, 256, 256};
+__host__ __device__ inline int gemm_shape_for(int rows) {
+  return rows > 128 ? 0 : (rows > 64 ? 1 : 2);
+}
 // Output columns per block: half the weight rows for a gate/up pair.
 inline int gemm_cols(int shape, bool gateup) {
   return gateup ? kGemmShapeWRows[shape] / 2 : kGemmShapeWRows[shape];
