@@ -602,12 +602,40 @@ def main():
                          "ms_per_step": r2["ms_per_step"], "steps": st2, "warmup": wu2,
                          "timing": r2["timing"], "roofline": r2["roofline"],
                          "layer_roofline": r2["layer_roofline"], "paths": r2["config"]["paths"]}
+    copy = copy_bandwidth(torch)
+    out["hbm_copy"] = {"GBps": copy, "method": "1 GiB device-to-device copy x 10, read + write "
+                       "bytes over the event time"}
+    for r in [out["roofline"]] + [out[n]["roofline"] for n in ("prefill", "mixed", "mixed1")
+                                  if n in out]:
+        if r["bound"] == "hbm":
+            r["frac_of_copy"] = round(r["achieved"] / copy, 4)
+    log(f"device copy {copy:.1f} GB/s")
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU oracle ...")
         cpu = cpu_baseline(layer0, cfg, torch)
     out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)
+
+
+def copy_bandwidth(torch, nbytes=1 << 30, reps=10):
+    """Measured device-copy bandwidth (bytes read + bytes written per second)
+    of a plain 1 GiB device-to-device copy, timed with events: the practical
+    HBM ceiling next to the 8 TB/s vendor peak."""
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    b.synchronize()
+    gbps = 2.0 * nbytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9
+    del src, dst
+    return round(gbps, 1)
 
 
 def run_config(cfg, torch, fl, lib, steps, warmup, L):

@@ -189,14 +189,14 @@ __device__ __forceinline__ UnitAddr unit_addr(uint32_t row, int row_words, int g
   return a;
 }
 
-template <int BITS, typename ST, int UR>
+template <int BITS, typename ST, int UR, int AUX = 0>
 __device__ __forceinline__ void bload_units(const ProjView& v, UnitAddr ad, uint32_t wstep,
                                             uint32_t sstep, WUnit<BITS, ST> (&u)[UR]) {
 #pragma unroll
   for (int j = 0; j < UR; j++) {
-    bload_unit<BITS>(v.w, ad.w0 + (uint32_t)j * wstep, u[j].w);
-    u[j].s_raw = __builtin_bit_cast(ST, bload16(v.s, ad.s0 + (uint32_t)j * sstep));
-    u[j].b_raw = __builtin_bit_cast(ST, bload16(v.b, ad.s0 + (uint32_t)j * sstep));
+    bload_unit<BITS, AUX>(v.w, ad.w0 + (uint32_t)j * wstep, u[j].w);
+    u[j].s_raw = __builtin_bit_cast(ST, bload16<AUX>(v.s, ad.s0 + (uint32_t)j * sstep));
+    u[j].b_raw = __builtin_bit_cast(ST, bload16<AUX>(v.b, ad.s0 + (uint32_t)j * sstep));
   }
 }
 

@@ -258,8 +258,8 @@ __global__ __launch_bounds__(256, 2) void gemv_multi_kernel(const GemvArgs a) {
       ws.ob0[it] = a.p0.ob ? to_f<XT>(reinterpret_cast<const XT*>(a.p0.ob)[ebase + row]) : 0.f;
       ws.ob1[it] = (GATEUP && a.p1.ob) ? to_f<XT>(reinterpret_cast<const XT*>(a.p1.ob)[ebase + row]) : 0.f;
       const UnitAddr ad = unit_addr<BITS, ST>((uint32_t)row, row_words, groups, li, a.gsh);
-      bload_units<BITS, ST, UR>(P0, ad, wstep, sstep, ws.w0[it]);
-      if constexpr (GATEUP) bload_units<BITS, ST, UR>(P1, ad, wstep, sstep, ws.w1[it]);
+      bload_units<BITS, ST, UR, kStream>(P0, ad, wstep, sstep, ws.w0[it]);
+      if constexpr (GATEUP) bload_units<BITS, ST, UR, kStream>(P1, ad, wstep, sstep, ws.w1[it]);
     }
   };
   // iteration i's rows against the nt staged activation rows of pass pc
@@ -833,8 +833,8 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
 #pragma unroll
   for (int it = 0; it < RM; it++) {
     const UnitAddr ad = unit_addr<BITS, ST>((uint32_t)(r0 + it * stride), row_words, groups, li, a.gsh);
-    bload_units<BITS, ST, UR>(G, ad, wstep, sstep, gw[it]);
-    bload_units<BITS, ST, UR>(U, ad, wstep, sstep, uw[it]);
+    bload_units<BITS, ST, UR, kStream>(G, ad, wstep, sstep, gw[it]);
+    bload_units<BITS, ST, UR, kStream>(U, ad, wstep, sstep, uw[it]);
   }
   // every weight load is issued before the first dot product: without the
   // fence the scheduler interleaves loads with math to save registers, and
@@ -918,7 +918,7 @@ __global__ __launch_bounds__(SH ? 64 * kDec1MaxWaves : 64 * kDec1MaxK) void down
     UnitAddr ad = unit_addr<BITS, ST>((uint32_t)(r_begin + sg + it * SG), rw, grp, li, a.gsh);
     ad.w0 += base.w0;
     ad.s0 += base.s0;
-    bload_units<BITS, ST, UR>(P, ad, wstep, sstep, w[it]);
+    bload_units<BITS, ST, UR, kStream>(P, ad, wstep, sstep, w[it]);
   }
   XUnit<XT> xu[UR];
   float xs[UR];

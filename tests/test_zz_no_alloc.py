@@ -46,7 +46,7 @@ def _same(a, b):
     return torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8))
 
 
-@pytest.mark.parametrize("cfg,Ts", [("qwen3", (64, 8)), ("gptoss", (4, 1)), ("mixed", (48, 2))])
+@pytest.mark.parametrize("cfg,Ts", [("qwen3", (64, 8)), ("gptoss", (4, 1)), ("mixed", (48, 2, 1))])
 def test_noalloc_matches_forward(cfg, Ts):
     spec = {"qwen3": cfg_qwen3, "gptoss": cfg_gptoss, "mixed": cfg_mixed}[cfg]()
     dev = spec.device()
