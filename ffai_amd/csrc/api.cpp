@@ -1395,6 +1395,13 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     x = rx = xn;
   }
 
+  // the grouped GEMMs read the layer input as f16 operands: a bf16 input is
+  // scaled into f16 range once, for the routed and the shared expert (by the
+  // router's matrix-core kernel when it reads the same rows, else on its own)
+  const bool gemm = !(T == 1 && dec1_supported(d)) && routed_gemm(d, T);
+  const bool want_x16 = (gemm || shared_gemm(d, T)) && xdt == MOE_BF16;
+  bool x16_done = false;
+
   // 1. router projection (MoELayer.swift:540 / 689-690)
   if (logits_done) {
     // done above
@@ -1405,16 +1412,15 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
             "quantised router launch");
   } else {
     MOE_HIP(launch_router_logits(rx, xdt, T, H, d->router_weight, d->router_dtype, d->router_bias,
-                                 E, at<void>(ws, w.logits), st),
+                                 E, at<void>(ws, w.logits), st,
+                                 want_x16 && rx == x ? at<void>(ws, w.x16) : nullptr, &x16_done),
             "router logits launch");
   }
 
-  // the grouped GEMMs read the layer input as f16 operands: a bf16 input is
-  // scaled into f16 range once here, for the routed and the shared expert
-  const bool gemm = !(T == 1 && dec1_supported(d)) && routed_gemm(d, T);
   const void* x16 = x;
-  if ((gemm || shared_gemm(d, T)) && xdt == MOE_BF16) {
-    MOE_HIP(launch_to_a16(x, at<void>(ws, w.x16), (int64_t)T * H, st), "f16 operand launch");
+  if (want_x16) {
+    if (!x16_done)
+      MOE_HIP(launch_to_a16(x, at<void>(ws, w.x16), (int64_t)T * H, st), "f16 operand launch");
     x16 = at<void>(ws, w.x16);
   }
 

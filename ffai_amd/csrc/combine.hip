@@ -140,24 +140,13 @@ __global__ __launch_bounds__(256) void activation_kernel(const XT* __restrict__ 
   }
 }
 
-// bf16 rows -> the f16 A operand of the grouped GEMM: value * 2^-8, rounded
-// toward zero (exact for results in f16's normal range; finite inputs
-// saturate instead of overflowing). 8 values per thread and step.
+// bf16 rows -> the f16 A operand of the grouped GEMM (bf16x8_to_a16), 8
+// values per thread and step.
 __global__ __launch_bounds__(256) void to_a16_kernel(const uint4* __restrict__ x,
                                                      uint4* __restrict__ y, int64_t n8) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const uint4 v = x[i];
-    const uint32_t in[4] = {v.x, v.y, v.z, v.w};
-    uint32_t o[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const float lo = __builtin_ldexpf(__uint_as_float(in[q] << 16), -kA16Shift);
-      const float hi = __builtin_ldexpf(__uint_as_float(in[q] & 0xFFFF0000u), -kA16Shift);
-      o[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
-    }
-    y[i] = make_uint4(o[0], o[1], o[2], o[3]);
-  }
+       i += (int64_t)gridDim.x * blockDim.x)
+    y[i] = bf16x8_to_a16<kA16Shift>(x[i]);
 }
 
 hipError_t launch_to_a16(const void* x, void* y, int64_t n, hipStream_t st) {

@@ -320,15 +320,17 @@ hipError_t launch_dispatch_plan(const uint32_t* idx, int T, int k, int E, uint32
   return hipGetLastError();
 }
 
+constexpr int kItemBlocks = 8;  // blocks writing the GEMM work items
+
 struct ItemCols {
   int nb[2][kGemmShapes];  // column blocks per tile shape, for each of the two lists
 };
 
 // Work items of the grouped GEMM over an expert-sorted plan (the list format
 // is described at launch_gemm_items). Thread t counts the items of experts
-// t * EPT .. + EPT; a block scan gives every expert's first item (in LDS);
-// then all threads write items in a strided loop, each finding its expert by
-// a binary search over those starts.
+// t * EPT .. + EPT; a block scan gives every expert's first item (in LDS),
+// the same in every block; then the threads of all blocks write items in a
+// strided loop, each finding its expert by a binary search over those starts.
 __global__ __launch_bounds__(kPlanThreads) void gemm_items_kernel(
     const uint32_t* __restrict__ offsets, int E, const ItemCols ic, uint32_t* __restrict__ items0,
     uint32_t* __restrict__ items1) {
@@ -382,8 +384,10 @@ __global__ __launch_bounds__(kPlanThreads) void gemm_items_kernel(
   if (t == 0) {
     start[0][E] = n[0];
     start[1][E] = n[1];
-    items0[0] = n[0];
-    if (items1) items1[0] = n[1];
+    if (blockIdx.x == 0) {
+      items0[0] = n[0];
+      if (items1) items1[0] = n[1];
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -391,7 +395,8 @@ __global__ __launch_bounds__(kPlanThreads) void gemm_items_kernel(
     uint32_t* items = l ? items1 : items0;
     if (!items) continue;
     const uint32_t nb0 = (uint32_t)ic.nb[l][0];
-    for (uint32_t i = (uint32_t)t; i < n[l]; i += kPlanThreads) {
+    for (uint32_t i = blockIdx.x * kPlanThreads + (uint32_t)t; i < n[l];
+         i += gridDim.x * kPlanThreads) {
       // the last expert whose first item is at or before i (experts without
       // items share their start with the next one)
       int lo = 0, hi = E - 1;
@@ -431,7 +436,9 @@ hipError_t launch_gemm_items(const uint32_t* offsets, int E, int N0, bool gateup
     ic.nb[0][sh] = (N0 + gemm_cols(sh, gateup0) - 1) / gemm_cols(sh, gateup0);
     ic.nb[1][sh] = items1 ? (N1 + gemm_cols(sh, gateup1) - 1) / gemm_cols(sh, gateup1) : 0;
   }
-  hipLaunchKernelGGL(gemm_items_kernel, dim3(1), dim3(kPlanThreads), 0, st, offsets, E, ic, items0,
+  // every block scans the experts' item counts (cheap) and writes a strided
+  // share of the items
+  hipLaunchKernelGGL(gemm_items_kernel, dim3(kItemBlocks), dim3(kPlanThreads), 0, st, offsets, E, ic, items0,
                      items1);
   return hipGetLastError();
 }

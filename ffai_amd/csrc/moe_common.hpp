@@ -143,6 +143,22 @@ __device__ __forceinline__ uint16_t bload16(rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, AUX);
 }
 
+// Eight bf16 values (16 bytes) -> f16 * 2^-SHIFT, rounded toward zero: the
+// grouped GEMM's A operand of a bf16 layer (exact for results in f16's
+// normal range; finite inputs saturate instead of overflowing).
+template <int SHIFT>
+__device__ __forceinline__ uint4 bf16x8_to_a16(uint4 v) {
+  const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const float lo = __builtin_ldexpf(__uint_as_float(in[q] << 16), -SHIFT);
+    const float hi = __builtin_ldexpf(__uint_as_float(in[q] & 0xFFFF0000u), -SHIFT);
+    o[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 // ------------------------------------------------------ deterministic exp --
 // Cody-Waite reduction by ln2 plus Moshier's degree-5 polynomial (Cephes
 // expf), written as explicit fused/unfused fp32 operations so that the CPU

@@ -142,8 +142,12 @@ hipError_t launch_gemv(int bits, int xdt, int sbdt, bool gateup, int tokmax, con
 size_t gemv_smem_bytes(int xdt, int K, int tok_chunk);
 
 // ---------------------------------------------------------------- router --
+// x16 (nullable): where the many-token matrix-core kernel, for bf16 rows,
+// also writes the rows as the expert GEMMs' f16 operand (launch_to_a16's
+// values); *x16_done tells whether it did.
 hipError_t launch_router_logits(const void* x, int xdt, int T, int H, const void* W, int wdt,
-                                const void* bias, int E, void* logits, hipStream_t st);
+                                const void* bias, int E, void* logits, hipStream_t st,
+                                void* x16 = nullptr, bool* x16_done = nullptr);
 hipError_t launch_router_topk(const void* logits, int dt, int T, int E, int k,
                               const RouteOpts& ro, uint32_t* idx, float* w, hipStream_t st);
 // One token: res = round(h + m), xn = round(rmsnorm(res) * nw), then the

@@ -265,9 +265,23 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
                                                                     const XT* __restrict__ W,
                                                                     const XT* __restrict__ bias,
                                                                     XT* __restrict__ logits, int T,
-                                                                    int H, int E) {
+                                                                    int H, int E,
+                                                                    uint4* __restrict__ x16) {
   // partial tiles, rows padded to 33 floats
   __shared__ float part[kRgWaves][32 * 33];
+  if (x16) {
+    // the f16 A operand of the expert GEMMs (bf16 rows only), as a by-product:
+    // the expert tiles of a token tile convert a share of its rows each
+    const int per = (32 + (int)gridDim.y - 1) / (int)gridDim.y;
+    const int r0 = (int)blockIdx.x * 32 + (int)blockIdx.y * per;
+    const int r1 = min(min((int)blockIdx.x * 32 + 32, r0 + per), T);
+    const int n8 = H / 8;  // 16-byte pieces per row
+    const uint4* xs = reinterpret_cast<const uint4*>(x);
+    for (int p = threadIdx.x; p < (r1 - r0) * n8; p += blockDim.x) {
+      const size_t i = (size_t)r0 * n8 + p;
+      x16[i] = bf16x8_to_a16<kA16Shift>(xs[i]);
+    }
+  }
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 31, h = lane >> 5;
@@ -354,11 +368,14 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const XT* __restrict__
 
 template <typename XT, typename WT>
 static hipError_t launch_rl(const void* x, int T, int H, const void* W, const void* bias, int E,
-                            void* logits, hipStream_t st) {
+                            void* logits, hipStream_t st, void* x16, bool* x16_done) {
   if constexpr (__is_same(XT, WT) && !__is_same(XT, float)) {
     if (T >= 32 && H % 64 == 0 && (size_t)T * H < (1ull << 31) && (size_t)E * H < (1ull << 31)) {
+      const bool conv = x16 && __is_same(XT, bf16_t);
       hipLaunchKernelGGL((router_gemm_kernel<XT>), dim3((T + 31) / 32, (E + 31) / 32), dim3(64 * kRgWaves),
-                         0, st, (const XT*)x, (const XT*)W, (const XT*)bias, (XT*)logits, T, H, E);
+                         0, st, (const XT*)x, (const XT*)W, (const XT*)bias, (XT*)logits, T, H, E,
+                         conv ? (uint4*)x16 : nullptr);
+      if (x16_done) *x16_done = conv;
       return hipGetLastError();
     }
     if (T == 1 && H <= 4 * 2048) {
@@ -394,8 +411,10 @@ static hipError_t launch_rl(const void* x, int T, int H, const void* W, const vo
 }
 
 hipError_t launch_router_logits(const void* x, int xdt, int T, int H, const void* W, int wdt,
-                                const void* bias, int E, void* logits, hipStream_t st) {
-#define MOE_RL2(XT, WT) return launch_rl<XT, WT>(x, T, H, W, bias, E, logits, st);
+                                const void* bias, int E, void* logits, hipStream_t st, void* x16,
+                                bool* x16_done) {
+  if (x16_done) *x16_done = false;
+#define MOE_RL2(XT, WT) return launch_rl<XT, WT>(x, T, H, W, bias, E, logits, st, x16, x16_done);
   if (xdt == DT_BF16) {
     if (wdt == DT_BF16) { MOE_RL2(bf16_t, bf16_t) }
     if (wdt == DT_F16) { MOE_RL2(bf16_t, f16_t) }
