@@ -21,7 +21,7 @@ namespace moe {
 
 constexpr int kPlanThreads = 256;
 constexpr int kPlanMaxE = 1024;
-constexpr int kChunk = 2048;             // entries per chunk in the multi-block plan
+constexpr int kChunk = 1024;             // entries per chunk in the multi-block plan
 constexpr int kSingleBlockMax = 4096;    // M at or below which one workgroup plans
 
 // Exclusive scan of cnt[0..E) over 256 threads (4 experts per thread).

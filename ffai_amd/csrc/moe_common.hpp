@@ -142,6 +142,10 @@ template <int AUX = 0>
 __device__ __forceinline__ uint16_t bload16(rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, AUX);
 }
+// A store whose lane offset is at or past the view's end is dropped.
+__device__ __forceinline__ void bstore128(rsrc_t r, uint32_t off, u32x4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0);
+}
 
 // Eight bf16 values (16 bytes) -> f16 * 2^-SHIFT, rounded toward zero: the
 // grouped GEMM's A operand of a bf16 layer (exact for results in f16's

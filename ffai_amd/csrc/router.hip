@@ -232,18 +232,25 @@ __global__ __launch_bounds__(256) void router_logits_row_kernel(const XT* __rest
 // Router logits for many tokens on the matrix cores. Block = one tile of 32
 // tokens x 32 experts; its 4 waves split the hidden dimension into 64-value
 // groups g = wave + 4 i and each accumulates its groups with
-// v_mfma_f32_32x32x16. Both operands come straight from global memory in
-// fragment order: lane (c, h) of step q holds values 16 q + 8 h .. + 8 of
-// token row c (A) and of expert row c (B), 16 contiguous bytes each, so no
-// LDS staging is needed; loads run two groups ahead of the MFMAs. The four
-// partial tiles are added in wave order through LDS, then rounded as
-// router_logits_kernel rounds (product, then + bias). Needs H % 64 == 0 and
-// T * H, E * H below 2^31 elements (32-bit byte offsets); the last expert
-// tile repeats expert E - 1 past E and stores nothing there.
-// Four waves per tile measured faster than eight or sixteen on the Qwen3 and
-// GPT-OSS prefill shapes (18 against 22 and 25 us for 4096 tokens, 128
-// experts).
+// v_mfma_f32_32x32x16 (lane (c, h) of step q holds values 16 q + 8 h .. + 8
+// of token row c (A) and of expert row c (B)). The four partial tiles are
+// added in wave order through LDS, then rounded as router_logits_kernel
+// rounds (product, then + bias). Needs H % 64 == 0 and T * H, E * H below
+// 2^31 elements (32-bit byte offsets); the last expert tile repeats expert
+// E - 1 past E and stores nothing there.
+//
+// Both tiles pass through LDS in chunks of 256 values: a wave's load
+// instruction covers two rows x 512 contiguous bytes (whole cache lines),
+// where fragment-order loads straight from memory touched 32 rows x 32 bytes
+// per instruction and ran the one-column shared gate of a 2048-token call at
+// 25 us. Chunks c + 1 and c + 2 are in registers while chunk c is multiplied
+// from LDS. Rows are stored with their 16-byte pieces XORed by the row's low
+// four bits, so the 16 rows a fragment read touches at once hit distinct
+// banks.
 constexpr int kRgWaves = 4;
+constexpr int kRgChunk = 256;                  // values of K per LDS chunk
+constexpr int kRgPieces = kRgChunk / 8;        // 16-byte pieces per row chunk
+constexpr int kRgLoads = 32 * kRgPieces / (64 * kRgWaves);  // pieces per thread per tile
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 template <typename XT> struct RgMfma;
@@ -260,6 +267,10 @@ template <> struct RgMfma<f16_t> {
   }
 };
 
+__device__ __forceinline__ int rg_slot(int row, int piece) {
+  return row * kRgPieces + (piece ^ (row & 15));
+}
+
 template <typename XT>
 __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __restrict__ x,
                                                                     const XT* __restrict__ W,
@@ -267,78 +278,126 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
                                                                     XT* __restrict__ logits, int T,
                                                                     int H, int E,
                                                                     uint4* __restrict__ x16) {
-  // partial tiles, rows padded to 33 floats
-  __shared__ float part[kRgWaves][32 * 33];
-  if (x16) {
-    // the f16 A operand of the expert GEMMs (bf16 rows only), as a by-product:
-    // the expert tiles of a token tile convert a share of its rows each
-    const int per = (32 + (int)gridDim.y - 1) / (int)gridDim.y;
-    const int r0 = (int)blockIdx.x * 32 + (int)blockIdx.y * per;
-    const int r1 = min(min((int)blockIdx.x * 32 + 32, r0 + per), T);
-    const int n8 = H / 8;  // 16-byte pieces per row
-    const uint4* xs = reinterpret_cast<const uint4*>(x);
-    for (int p = threadIdx.x; p < (r1 - r0) * n8; p += blockDim.x) {
-      const size_t i = (size_t)r0 * n8 + p;
-      x16[i] = bf16x8_to_a16<kA16Shift>(xs[i]);
-    }
-  }
-  const int lane = threadIdx.x & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // token tile and expert tile of one chunk; the partial tiles of the
+  // epilogue (rows padded to 33 floats) reuse the same bytes
+  __shared__ u32x4_t stage[2][32 * kRgPieces];
+  static_assert(sizeof(stage) >= kRgWaves * 32 * 33 * sizeof(float), "epilogue fits the stage");
+  // Blocks go to the eight XCDs round robin (block b to XCD b % 8). The nE
+  // expert tiles of one token tile take ids 8 apart inside a window of 8 nE
+  // ids, so they run close together on one XCD and read the token rows from
+  // its L2 after the first of them has fetched them.
+  const int nE = (E + 31) >> 5;
+  const int b = (int)blockIdx.x, win = b / (8 * nE), slot = b - win * 8 * nE;
+  const int tt = win * 8 + (slot & 7), et = slot >> 3;
+  if (tt * 32 >= T) return;  // padding of the last window; uniform over the block
+  const int t0 = tt * 32, e0 = et * 32;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, h = lane >> 5;
-  const int t0 = blockIdx.x * 32, e0 = blockIdx.y * 32;
-  // rows past T repeat the last token; their outputs are not stored
-  const uint32_t row = (uint32_t)min(t0 + col, T - 1);
-  const uint32_t ex = (uint32_t)min(e0 + col, E - 1);  // experts past E repeat the last one
+  const int G = H >> 6, nC = (H + kRgChunk - 1) / kRgChunk;
   const rsrc_t xr = make_rsrc(x, (uint32_t)((size_t)T * H * sizeof(XT)));
   const rsrc_t wr = make_rsrc(W, (uint32_t)((size_t)E * H * sizeof(XT)));
-  const uint32_t xo = (row * (uint32_t)H + 8u * (uint32_t)h) * 2u;
-  const uint32_t wo = (ex * (uint32_t)H + 8u * (uint32_t)h) * 2u;
-  const int G = H >> 6;
-  const int ng = (G - wv + kRgWaves - 1) / kRgWaves;  // groups wv + 4 i, i < ng (0 when wv >= G)
-
-  struct Set {
-    u32x4_t a[4], b[4];
-  };
-  // group i of this wave (clamped into the row: loads past the wave's last
-  // group are in bounds and never multiplied)
-  auto load = [&](int i, Set& s) __attribute__((always_inline)) {
-    const uint32_t kb = (uint32_t)min(wv + kRgWaves * i, G - 1) * 128u;
+  // thread piece j: row (j * 64 * kRgWaves + tid) / kRgPieces of the tile,
+  // piece (...) % kRgPieces of the chunk. Rows past T repeat the last token
+  // and experts past E the last expert (never stored); pieces past H read
+  // the next row or, for the buffer's last row, zero, and are never used.
+  uint32_t xo[kRgLoads], wo[kRgLoads];
+  int prow[kRgLoads], ppc[kRgLoads];
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      s.a[q] = bload128(xr, xo + kb + 32u * (uint32_t)q);
-      s.b[q] = bload128(wr, wo + kb + 32u * (uint32_t)q);
+  for (int j = 0; j < kRgLoads; j++) {
+    const int P = j * 64 * kRgWaves + tid;
+    prow[j] = P / kRgPieces;
+    ppc[j] = P % kRgPieces;
+    const uint32_t tr = (uint32_t)min(t0 + prow[j], T - 1), er = (uint32_t)min(e0 + prow[j], E - 1);
+    xo[j] = (tr * (uint32_t)H + 8u * (uint32_t)ppc[j]) * 2u;
+    wo[j] = (er * (uint32_t)H + 8u * (uint32_t)ppc[j]) * 2u;
+  }
+  struct Tile {
+    u32x4_t a[kRgLoads], b[kRgLoads];
+  };
+  auto load = [&](int c, Tile& s) __attribute__((always_inline)) {
+    const uint32_t kb = (uint32_t)min(c, nC - 1) * (uint32_t)(kRgChunk * 2);
+#pragma unroll
+    for (int j = 0; j < kRgLoads; j++) {
+      s.a[j] = bload128(xr, xo[j] + kb);
+      s.b[j] = bload128(wr, wo[j] + kb);
+    }
+  };
+  // the f16 A operand of the expert GEMMs (bf16 rows only), as a by-product:
+  // the nE expert tiles of a token tile convert a share of its rows each.
+  // Stores go through a buffer view of x16 with the offsets of pieces outside
+  // the share (or past H) set to the view's end, where they are dropped: no
+  // branches, so the loads of later chunks keep their exact wait counts.
+  const int per = (32 + nE - 1) / nE;
+  const int cv0 = et * per, cv1 = min(min(cv0 + per, 32), T - t0);
+  const uint32_t x16_bytes = x16 ? (uint32_t)((size_t)T * H * 2) : 0u;
+  const rsrc_t cr = make_rsrc(x16, x16_bytes);
+  auto put = [&](int c, const Tile& s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < kRgLoads; j++) {
+      stage[0][rg_slot(prow[j], ppc[j])] = s.a[j];
+      stage[1][rg_slot(prow[j], ppc[j])] = s.b[j];
+    }
+#pragma unroll
+    for (int j = 0; j < kRgLoads; j++) {
+      const int k8 = c * kRgPieces + ppc[j];  // piece of the whole row
+      const bool mine = prow[j] >= cv0 && prow[j] < cv1 && 8 * k8 < H;
+      const uint32_t off = mine ? ((uint32_t)(t0 + prow[j]) * (uint32_t)(H / 8) + (uint32_t)k8) * 16u : x16_bytes;
+      const uint4 v = bf16x8_to_a16<kA16Shift>(make_uint4(s.a[j].x, s.a[j].y, s.a[j].z, s.a[j].w));
+      bstore128(cr, off, u32x4_t{v.x, v.y, v.z, v.w});
     }
   };
   f32x16_t acc = {};
-  auto mma = [&](const Set& s) __attribute__((always_inline)) {
+  auto mma = [&](int c) __attribute__((always_inline)) {
+    if (4 * c + wv < G) {  // wave-uniform: the wave's group of chunk c
+      u32x4_t fa[4], fb[4];
 #pragma unroll
-    for (int q = 0; q < 4; q++) acc = RgMfma<XT>::mma(s.a[q], s.b[q], acc);
+      for (int q = 0; q < 4; q++) {
+        const int p = 8 * wv + 2 * q + h;
+        fa[q] = stage[0][rg_slot(col, p)];
+        fb[q] = stage[1][rg_slot(col, p)];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; q++) acc = RgMfma<XT>::mma(fa[q], fb[q], acc);
+    }
   };
-  Set s0, s1, s2;
+  // LDS-only barriers: the next chunks' loads stay in flight across them
+  // (the scheduling barrier keeps chunk 0's loads ahead of chunk 1's, so the
+  // first stores to LDS wait for chunk 0 only)
+  Tile s0, s1;
   load(0, s0);
+  __builtin_amdgcn_sched_barrier(0);
   load(1, s1);
-  for (int i = 0; i < ng; i += 3) {  // ng is wave-uniform: scalar branches
-    load(i + 2, s2);
-    mma(s0);
-    if (i + 1 >= ng) break;
-    load(i + 3, s0);
-    mma(s1);
-    if (i + 2 >= ng) break;
-    load(i + 4, s1);
-    mma(s2);
+  __builtin_amdgcn_sched_barrier(0);
+  // Chunk c from s0, chunk c + 1 from s1; each set reloads two chunks on.
+  // With nC odd the last trip's second chunk is past H: its loads repeat the
+  // last chunk, its x16 stores are dropped and no wave has a group in it (no
+  // break in the loop, which would cost the wait counts their exactness).
+  for (int c = 0; c < nC; c += 2) {  // nC is uniform: a scalar loop
+    put(c, s0);
+    lds_barrier();
+    load(c + 2, s0);
+    mma(c);
+    lds_barrier();
+    put(c + 1, s1);
+    lds_barrier();
+    load(c + 3, s1);
+    mma(c + 1);
+    lds_barrier();
   }
 
+  float* part = reinterpret_cast<float*>(&stage[0][0]);  // [kRgWaves][32 * 33]
   // lane (col, h) holds rows 8 (r / 4) + 4 h + r % 4 of column col
 #pragma unroll
-  for (int r = 0; r < 16; r++) part[wv][(8 * (r >> 2) + 4 * h + (r & 3)) * 33 + col] = acc[r];
+  for (int r = 0; r < 16; r++) part[wv * 32 * 33 + (8 * (r >> 2) + 4 * h + (r & 3)) * 33 + col] = acc[r];
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < 1024 / (64 * kRgWaves); j++) {
-    const int o = threadIdx.x + 64 * kRgWaves * j;
+    const int o = tid + 64 * kRgWaves * j;
     const int r = o >> 5, c = o & 31;
-    float s = part[0][r * 33 + c];
+    float s = part[r * 33 + c];
 #pragma unroll
-    for (int w = 1; w < kRgWaves; w++) s += part[w][r * 33 + c];
+    for (int w = 1; w < kRgWaves; w++) s += part[w * 32 * 33 + r * 33 + c];
     if (t0 + r < T && e0 + c < E) {
       float l = round_to<XT>(s);
       if (bias) l = round_to<XT>(l + to_f<XT>(bias[e0 + c]));
@@ -372,7 +431,8 @@ static hipError_t launch_rl(const void* x, int T, int H, const void* W, const vo
   if constexpr (__is_same(XT, WT) && !__is_same(XT, float)) {
     if (T >= 32 && H % 64 == 0 && (size_t)T * H < (1ull << 31) && (size_t)E * H < (1ull << 31)) {
       const bool conv = x16 && __is_same(XT, bf16_t);
-      hipLaunchKernelGGL((router_gemm_kernel<XT>), dim3((T + 31) / 32, (E + 31) / 32), dim3(64 * kRgWaves),
+      const int windows = (T + 255) / 256;  // eight token tiles each
+      hipLaunchKernelGGL((router_gemm_kernel<XT>), dim3(windows * 8 * ((E + 31) / 32)), dim3(64 * kRgWaves),
                          0, st, (const XT*)x, (const XT*)W, (const XT*)bias, (XT*)logits, T, H, E,
                          conv ? (uint4*)x16 : nullptr);
       if (x16_done) *x16_done = conv;
