@@ -356,7 +356,10 @@ __global__ __launch_bounds__(256, 2) void gemv_multi_kernel(const GemvArgs a) {
       stage_store<BITS, XT>(xn, nt, CU, q0, xl, xsl);
     }
     lds_barrier();
-    // iteration i + 1's weights load while iteration i multiplies
+    // iteration i + 1's weights load while iteration i multiplies (a form
+    // with no break and loads past the last iteration that read nothing, as
+    // in gemv_mma_kernel, measured slower here: blocks have one or two
+    // iterations, Qwen3 batch 4 43.1 -> 45.7 us per layer step)
     for (int i = 0; i < nit; i += 2) {
       if (i + 1 < nit) load_w(i + 1, wb);
       compute(i, wa, pc, nt);
@@ -439,8 +442,14 @@ __device__ __forceinline__ u32x4_t mma_codes(const uint32_t* unit, int kb, uint3
   }
 }
 
+// Four waves per SIMD where that fits in 128 VGPRs without spills (2- and
+// 4-bit, 3-bit gate/up); the compiler's own choice elsewhere.
+template <int BITS, bool GATEUP>
+constexpr int kMmaWavesPerEu = (BITS == 2 || BITS == 4 || (BITS == 3 && GATEUP)) ? 4 : 1;
+
 template <int BITS, typename XT, typename ST, bool GATEUP>
-__global__ __launch_bounds__(256) void gemv_mma_kernel(const GemvArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kMmaWavesPerEu<BITS, GATEUP>)))
+void gemv_mma_kernel(const GemvArgs a) {
   __shared__ __align__(16) uint32_t wl[2][kMmaRows * kMmaU * BITS];  // [row][unit slot][BITS words]
   __shared__ __align__(16) uint32_t sl[2][kMmaRows * kMmaU];      // [row][unit]: s | b << 16
   __shared__ __align__(16) uint32_t xl[2][kMmaU * kMmaTok * 16];  // [unit][row][quad slot][4 words]
@@ -483,16 +492,21 @@ __global__ __launch_bounds__(256) void gemv_mma_kernel(const GemvArgs a) {
     const int g = GATEUP ? r_begin + (slr & 31) : r_begin + slr;
     return (uint32_t)min(g, N - 1);
   };
+  // chunks past the last load their weights at offsets past the views' ends
+  // (2^31 and more: the views of one expert are far smaller), which read zero
+  // without touching memory, so the loop below issues the same loads on every
+  // trip. (Selecting views of zero bytes instead cost eight VGPRs.)
   auto load_stage = [&](int c, uint32_t xrow, Stage& st) __attribute__((always_inline)) {
     const int cc = min(c, nchunks - 1);
+    const uint32_t dead = c < nchunks ? 0u : 0x80000000u;  // block-uniform
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int slr = s_lr0 + 32 * j;
       const ProjView& pv = (GATEUP && j == 1) ? P1 : P0;
       const uint32_t grow = gw_row(slr);
       const uint32_t u = (uint32_t)min(kMmaU * cc + s_us, CU - 1);
-      bload_unit<BITS>(pv.w, (grow * (uint32_t)row_words + u * (uint32_t)BITS) * 4u, st.w[j]);
-      const uint32_t gi = (grow * (uint32_t)groups + (u >> a.gsh)) * (uint32_t)sizeof(ST);
+      bload_unit<BITS>(pv.w, (grow * (uint32_t)row_words + u * (uint32_t)BITS) * 4u + dead, st.w[j]);
+      const uint32_t gi = (grow * (uint32_t)groups + (u >> a.gsh)) * (uint32_t)sizeof(ST) + dead;
       st.sb[j] = (uint32_t)bload16(pv.s, gi) | ((uint32_t)bload16(pv.b, gi) << 16);
       const int ux = min(kMmaU * cc + x_us0 + 4 * j, CU - 1);
       st.x[j] = *reinterpret_cast<const u32x4_t*>(x + (size_t)xrow * K + (size_t)ux * 32 + x_kb * 8);
@@ -552,18 +566,23 @@ __global__ __launch_bounds__(256) void gemv_mma_kernel(const GemvArgs a) {
     Stage s0, s1;
     load_stage(0, xrow, s0);
     load_stage(1, xrow, s1);
-    __syncthreads();  // the last pass's LDS reads (and gl) are done
+    lds_barrier();  // the last pass's LDS reads (and gl) are done; loads stay in flight
     store_stage(s0, 0);
     load_stage(2, xrow, s0);
     lds_barrier();
     acc = f32x4_t{};
+    // No break in this loop: with one, the compiler's wait counts at the loop
+    // head took the break path's state (chunk c + 3's loads youngest) and the
+    // stores of chunk c + 1 waited for chunk c + 2's loads as well. An odd
+    // chunk count runs a last trip whose second chunk is skipped (its weight
+    // loads read nothing, its stores land in a buffer nothing reads). Peeling
+    // that chunk off the loop instead cost eight VGPRs and one wave per SIMD.
     for (int c = 0; c < nchunks; c += 2) {
       compute(c, 0);
       store_stage(s1, 1);  // chunk c + 1
       load_stage(c + 3, xrow, s1);
       lds_barrier();
-      if (c + 1 >= nchunks) break;
-      compute(c + 1, 1);
+      if (c + 1 < nchunks) compute(c + 1, 1);
       store_stage(s0, 0);  // chunk c + 2
       load_stage(c + 4, xrow, s0);
       lds_barrier();
