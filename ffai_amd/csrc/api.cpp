@@ -1494,6 +1494,14 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
                                 st, res),
               "shared add launch");
   } else {
+    // squared-ReLU experts: the single up projection (NemotronHText.swift:756-761)
+    const bool gated = d->activation != MOE_ACT_RELU2;
+    const moe_qproj& p0 = gated ? d->gate : d->up;
+    const moe_qproj* p1 = gated ? &d->up : nullptr;
+    // the GEMM work lists, written by the plan's last launch when it can
+    const GemmItemsReq ireq{p0.n, p1 != nullptr, at<uint32_t>(ws, w.items_gu),
+                            H,    false,         at<uint32_t>(ws, w.items_dn)};
+    bool items_done = false;
     // 2. selection + dispatch plan (MoELayer.swift:706-792): one launch for a
     //    small batch, else the top-k and plan kernels
     if (launch_route_plan(at<void>(ws, w.logits), xdt, T, E, k, route_opts(d),
@@ -1508,20 +1516,16 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
                                    at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.perm),
                                    at<uint32_t>(ws, w.inv), at<uint32_t>(ws, w.used),
                                    at<void>(ws, w.plan_scratch), dispatch_scratch_bytes(T, k, E),
-                                   st),
+                                   st, gemm ? &ireq : nullptr, &items_done),
               "dispatch plan launch");
     }
     const int slots = std::min(E, M);
-    // squared-ReLU experts: the single up projection (NemotronHText.swift:756-761)
-    const bool gated = d->activation != MOE_ACT_RELU2;
-    const moe_qproj& p0 = gated ? d->gate : d->up;
-    const moe_qproj* p1 = gated ? &d->up : nullptr;
     // 3. gate/up + activation over the plan (MoELayer.swift:883-893)
     if (gemm) {
-      MOE_HIP(launch_gemm_items(at<uint32_t>(ws, w.offsets), E, p0.n, p1 != nullptr,
-                                at<uint32_t>(ws, w.items_gu), H, false, at<uint32_t>(ws, w.items_dn),
-                                st),
-              "GEMM work list launch");
+      if (!items_done)
+        MOE_HIP(launch_gemm_items(at<uint32_t>(ws, w.offsets), E, ireq.N0, ireq.gateup0,
+                                  ireq.items0, ireq.N1, ireq.gateup1, ireq.items1, st),
+                "GEMM work list launch");
       MOE_TRY(run_gemm(p0, p1, x16, xdt, true, at<uint32_t>(ws, w.perm), k,
                        at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.items_gu), M,
                        at<void>(ws, w.act), d->activation, d->act_alpha, d->act_limit, st, kev(0)));

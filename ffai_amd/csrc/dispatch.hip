@@ -298,28 +298,6 @@ size_t dispatch_scratch_bytes(int T, int k, int E) {
   return (size_t)(nchunks * E * 4);
 }
 
-hipError_t launch_dispatch_plan(const uint32_t* idx, int T, int k, int E, uint32_t* counts,
-                                uint32_t* offsets, uint32_t* perm, uint32_t* inv_perm,
-                                uint32_t* used, void* scratch, size_t scratch_bytes,
-                                hipStream_t st) {
-  const int M = T * k;
-  if (E > kPlanMaxE) return hipErrorInvalidValue;
-  if (M <= kSingleBlockMax) {
-    hipLaunchKernelGGL(plan_single_kernel, dim3(1), dim3(kPlanThreads), 0, st, idx, M, E, counts,
-                       offsets, perm, inv_perm, used);
-    return hipGetLastError();
-  }
-  const int nchunks = (M + kChunk - 1) / kChunk;
-  if (scratch == nullptr || scratch_bytes < (size_t)nchunks * E * 4) return hipErrorInvalidValue;
-  uint32_t* hist = reinterpret_cast<uint32_t*>(scratch);
-  hipLaunchKernelGGL(plan_hist_kernel, dim3(nchunks), dim3(kPlanThreads), 0, st, idx, M, E, hist);
-  hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(kPlanThreads), 0, st, nchunks, E, hist,
-                     counts, offsets, used);
-  hipLaunchKernelGGL(plan_scatter_kernel, dim3(nchunks), dim3(kPlanThreads), 0, st, idx, M, E,
-                     hist, perm, inv_perm);
-  return hipGetLastError();
-}
-
 constexpr int kItemBlocks = 8;  // blocks writing the GEMM work items
 
 struct ItemCols {
@@ -331,9 +309,9 @@ struct ItemCols {
 // t * EPT .. + EPT; a block scan gives every expert's first item (in LDS),
 // the same in every block; then the threads of all blocks write items in a
 // strided loop, each finding its expert by a binary search over those starts.
-__global__ __launch_bounds__(kPlanThreads) void gemm_items_kernel(
-    const uint32_t* __restrict__ offsets, int E, const ItemCols ic, uint32_t* __restrict__ items0,
-    uint32_t* __restrict__ items1) {
+__device__ void gemm_items_body(const uint32_t* __restrict__ offsets, int E, const ItemCols& ic,
+                                uint32_t* __restrict__ items0, uint32_t* __restrict__ items1,
+                                int blk, int nblk) {
   __shared__ uint32_t scan[2][kPlanThreads];
   __shared__ uint32_t start[2][kPlanMaxE + 1];  // first item of each expert, per list
   __shared__ uint32_t first_pos[kPlanMaxE], rows_of[kPlanMaxE];
@@ -384,7 +362,7 @@ __global__ __launch_bounds__(kPlanThreads) void gemm_items_kernel(
   if (t == 0) {
     start[0][E] = n[0];
     start[1][E] = n[1];
-    if (blockIdx.x == 0) {
+    if (blk == 0) {
       items0[0] = n[0];
       if (items1) items1[0] = n[1];
     }
@@ -395,8 +373,8 @@ __global__ __launch_bounds__(kPlanThreads) void gemm_items_kernel(
     uint32_t* items = l ? items1 : items0;
     if (!items) continue;
     const uint32_t nb0 = (uint32_t)ic.nb[l][0];
-    for (uint32_t i = blockIdx.x * kPlanThreads + (uint32_t)t; i < n[l];
-         i += gridDim.x * kPlanThreads) {
+    for (uint32_t i = (uint32_t)blk * kPlanThreads + (uint32_t)t; i < n[l];
+         i += (uint32_t)nblk * kPlanThreads) {
       // the last expert whose first item is at or before i (experts without
       // items share their start with the next one)
       int lo = 0, hi = E - 1;
@@ -427,15 +405,74 @@ __global__ __launch_bounds__(kPlanThreads) void gemm_items_kernel(
   }
 }
 
+__global__ __launch_bounds__(kPlanThreads) void gemm_items_kernel(
+    const uint32_t* __restrict__ offsets, int E, const ItemCols ic, uint32_t* __restrict__ items0,
+    uint32_t* __restrict__ items1) {
+  gemm_items_body(offsets, E, ic, items0, items1, (int)blockIdx.x, (int)gridDim.x);
+}
+
+// Multi-block pass 3 with the grouped GEMM's work items: each block scatters
+// its chunk as plan_scatter_kernel does, then writes a strided share of the
+// items as gemm_items_kernel does (they need only the offsets, which the
+// scan pass wrote). One launch fewer per prefill step.
+__global__ __launch_bounds__(kPlanThreads) void plan_scatter_items_kernel(
+    const uint32_t* __restrict__ idx, int M, int E, const uint32_t* __restrict__ hist,
+    uint32_t* perm, uint32_t* inv, const uint32_t* __restrict__ offsets, const ItemCols ic,
+    uint32_t* __restrict__ items0, uint32_t* __restrict__ items1) {
+  __shared__ uint32_t cursor[kPlanMaxE];
+  const int tid = threadIdx.x, c = blockIdx.x;
+  for (int e = tid; e < E; e += kPlanThreads) cursor[e] = hist[(size_t)c * E + e];
+  __syncthreads();
+  const int begin = c * kChunk, end = min(M, begin + kChunk);
+  stable_scatter(idx, begin, end, E, id_bits(E), cursor, perm, inv);
+  gemm_items_body(offsets, E, ic, items0, items1, c, (int)gridDim.x);
+}
+
+static ItemCols item_cols(int N0, bool gateup0, int N1, bool gateup1, bool two) {
+  ItemCols ic{};
+  for (int sh = 0; sh < kGemmShapes; sh++) {
+    ic.nb[0][sh] = (N0 + gemm_cols(sh, gateup0) - 1) / gemm_cols(sh, gateup0);
+    ic.nb[1][sh] = two ? (N1 + gemm_cols(sh, gateup1) - 1) / gemm_cols(sh, gateup1) : 0;
+  }
+  return ic;
+}
+
+hipError_t launch_dispatch_plan(const uint32_t* idx, int T, int k, int E, uint32_t* counts,
+                                uint32_t* offsets, uint32_t* perm, uint32_t* inv_perm,
+                                uint32_t* used, void* scratch, size_t scratch_bytes,
+                                hipStream_t st, const GemmItemsReq* items, bool* items_done) {
+  if (items_done) *items_done = false;
+  const int M = T * k;
+  if (E > kPlanMaxE) return hipErrorInvalidValue;
+  if (M <= kSingleBlockMax) {
+    hipLaunchKernelGGL(plan_single_kernel, dim3(1), dim3(kPlanThreads), 0, st, idx, M, E, counts,
+                       offsets, perm, inv_perm, used);
+    return hipGetLastError();
+  }
+  const int nchunks = (M + kChunk - 1) / kChunk;
+  if (scratch == nullptr || scratch_bytes < (size_t)nchunks * E * 4) return hipErrorInvalidValue;
+  uint32_t* hist = reinterpret_cast<uint32_t*>(scratch);
+  hipLaunchKernelGGL(plan_hist_kernel, dim3(nchunks), dim3(kPlanThreads), 0, st, idx, M, E, hist);
+  hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(kPlanThreads), 0, st, nchunks, E, hist,
+                     counts, offsets, used);
+  if (items) {
+    const ItemCols ic = item_cols(items->N0, items->gateup0, items->N1, items->gateup1,
+                                  items->items1 != nullptr);
+    hipLaunchKernelGGL(plan_scatter_items_kernel, dim3(nchunks), dim3(kPlanThreads), 0, st, idx,
+                       M, E, hist, perm, inv_perm, offsets, ic, items->items0, items->items1);
+    if (items_done) *items_done = true;
+  } else {
+    hipLaunchKernelGGL(plan_scatter_kernel, dim3(nchunks), dim3(kPlanThreads), 0, st, idx, M, E,
+                       hist, perm, inv_perm);
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm_items(const uint32_t* offsets, int E, int N0, bool gateup0,
                              uint32_t* items0, int N1, bool gateup1, uint32_t* items1,
                              hipStream_t st) {
   if (E > kPlanMaxE) return hipErrorInvalidValue;
-  ItemCols ic{};
-  for (int sh = 0; sh < kGemmShapes; sh++) {
-    ic.nb[0][sh] = (N0 + gemm_cols(sh, gateup0) - 1) / gemm_cols(sh, gateup0);
-    ic.nb[1][sh] = items1 ? (N1 + gemm_cols(sh, gateup1) - 1) / gemm_cols(sh, gateup1) : 0;
-  }
+  const ItemCols ic = item_cols(N0, gateup0, N1, gateup1, items1 != nullptr);
   // every block scans the experts' item counts (cheap) and writes a strided
   // share of the items
   hipLaunchKernelGGL(gemm_items_kernel, dim3(kItemBlocks), dim3(kPlanThreads), 0, st, offsets, E, ic, items0,

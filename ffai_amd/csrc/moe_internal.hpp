@@ -172,10 +172,23 @@ hipError_t launch_router_q(int bits, const void* x, int xdt, int T, int H, const
 hipError_t launch_route_plan(const void* logits, int dt, int T, int E, int k, const RouteOpts& ro,
                              uint32_t* idx, float* w, uint32_t* counts, uint32_t* offsets,
                              uint32_t* perm, uint32_t* inv, uint32_t* used, hipStream_t st);
+// The grouped GEMM's work items (launch_gemm_items arguments) to be written
+// by the plan's last launch.
+struct GemmItemsReq {
+  int N0;
+  bool gateup0;
+  uint32_t* items0;
+  int N1;
+  bool gateup1;
+  uint32_t* items1;  // nullptr: one list
+};
+// With `items`, a multi-block plan also writes the GEMM work items (then
+// *items_done is set; a one-workgroup plan leaves them to launch_gemm_items).
 hipError_t launch_dispatch_plan(const uint32_t* idx, int T, int k, int E, uint32_t* counts,
                                 uint32_t* offsets, uint32_t* perm, uint32_t* inv_perm,
                                 uint32_t* used, void* scratch, size_t scratch_bytes,
-                                hipStream_t st);
+                                hipStream_t st, const GemmItemsReq* items = nullptr,
+                                bool* items_done = nullptr);
 size_t dispatch_scratch_bytes(int T, int k, int E);
 // Fills offsets {0, M}, used {1, 0} for a single-expert identity plan.
 hipError_t launch_identity_plan(uint32_t* offsets, uint32_t* used, int M, hipStream_t st);
