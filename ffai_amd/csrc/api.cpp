@@ -521,10 +521,13 @@ GemvProj to_proj(const moe_qproj& q) { return GemvProj{q.weight, q.scales, q.bia
 int pick_lg_dec1(int CU, int gsh);
 
 // Row iterations per gemv_multi_kernel block (each shares the block's staged
-// activation rows; two keep both iterations' weight loads in flight at once,
-// more measured slower) and the block count below which fewer are used.
-constexpr int kMultiIters = 2;
-constexpr int kMultiBlocks = 1024;
+// activation rows; the next iteration's weights load while one multiplies)
+// and the block count below which fewer are used. Swept over (iterations,
+// floor) = (1, 2, 4, 8) x (1024, 512), µs per layer step at 4 / 16 tokens:
+// (4, 512) GPT-OSS 72.4 / 158.7, Qwen3 41.8 / 84.0, against (2, 1024) 77.1 /
+// 169.3 and 42.9 / 84.7; one iteration or eight are slower.
+constexpr int kMultiIters = 4;
+constexpr int kMultiBlocks = 512;
 
 // Rows per used expert from which the batched GEMV runs on the matrix cores
 // (Qwen3 shape, 4 per expert: 192 -> 154 us per layer step; GPT-OSS, 8 per
