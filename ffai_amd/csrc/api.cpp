@@ -531,12 +531,18 @@ constexpr int kMultiBlocks = 512;
 
 // Rows per used expert from which the batched GEMV runs on the matrix cores
 // (Qwen3 shape, 4 per expert: 192 -> 154 us per layer step; GPT-OSS, 8 per
-// expert: 409 -> 208 us; at 1-2 per expert gemv_multi_kernel is faster).
+// expert: 409 -> 208 us; at 1 per expert gemv_multi_kernel is faster).
 // Codes of other widths cost gemv_multi_kernel more unpacking, so they move
 // from 2 rows per expert (mixed 3/6-bit layer, 64 tokens: 317 -> 231 us).
 // One expert alone (a shared expert) gets only ceil(N / 32) matrix-core
 // blocks, so it moves only once a pass fills the 16 activation rows.
-constexpr int kMmaMinRows = 4;
+// 4-bit thresholds re-measured after the matrix-core GEMV's loop and
+// occupancy changes: a gate/up pair from 2 rows per used expert (Qwen3 32
+// tokens 124.3 -> 117.6 us, GPT-OSS 16 tokens gate/up 96.8 -> 85.1 us), a
+// single projection from 3 (GPT-OSS 16 tokens, 2 per expert: down 45.5 on
+// gemv_multi_kernel against 50.0; at 24 tokens 58.8 against 52.5).
+constexpr int kMmaMinRowsPair = 2;
+constexpr int kMmaMinRowsSingle = 3;
 constexpr int kMmaMinRowsOther = 2;
 constexpr int kMmaMinRowsSingleExpert = 16;
 
@@ -576,7 +582,8 @@ GemvKind gemv_kind(const moe_qproj& p0, const moe_qproj* p1, bool x_aligned, int
   // the matrix cores once the used experts average enough rows: below that
   // the K-chunk pipeline's latency outweighs the VALU it saves
   const int min_rows = slots <= 1 ? kMmaMinRowsSingleExpert
-                                  : (p0.bits == 4 ? kMmaMinRows : kMmaMinRowsOther);
+                      : p0.bits != 4 ? kMmaMinRowsOther
+                                     : (p1 ? kMmaMinRowsPair : kMmaMinRowsSingle);
   if ((long)M >= (long)min_rows * std::max(1, slots) && mma_ok(p0, p1, x_aligned, xdt))
     return kGemvMma;
   const int tm = multi_rows_per_pass(std::min(max_rows, M), M, slots);
