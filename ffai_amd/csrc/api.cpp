@@ -716,9 +716,14 @@ moe_status run_gemv(const moe_qproj& p0, const moe_qproj* p1, const void* x, int
 }
 
 // The MFMA grouped GEMM pays off once the used experts average enough rows
-// to fill a good part of its 128-row tiles; below that the HBM-streaming
-// GEMV, which reads every weight once per 8 rows, is faster.
-constexpr int kGemmMinRows = 32;
+// to fill a good part of its 64-row tiles; below that the matrix-core GEMV,
+// which reads every weight once per 16 rows, is faster. Swept at 16 / 24 /
+// 32+ rows per expert (µs per layer step, GEMV against GEMM): 16 rows
+// Qwen3 192.8 / 184.4, GPT-OSS 254.0 / 301.9, mixed-bit 317.3 / 320.0; 24
+// rows Qwen3 242.0 / 191.8, GPT-OSS 323.9 / 305.3, mixed-bit 381.2 / 321.1.
+// The same count moves a shared expert (one expert, T rows) onto the side
+// stream and the GEMM (mixed-bit layer at 24 tokens: 147.6 -> 121.0 us).
+constexpr int kGemmMinRows = 24;
 
 // The matrix-core GEMM writes whole 16-byte groups of an output row: N is a
 // multiple of 8 and the output 16-byte aligned (workspace buffers always are).

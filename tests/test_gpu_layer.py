@@ -616,7 +616,8 @@ def test_layer_mfma_path(case):
                                   (5, 2, 64, BF16, F16)],
                          ids=lambda c: f"gu{c[0]}-d{c[1]}-gs{c[2]}-sb{c[3]}-x{c[4]}")
 def test_layer_batched_mma_path(case):
-    """4 to 31 rows per expert with 2- to 6-bit weights: the batched GEMV on
+    """Up to 23 rows per used expert on average with 2- to 6-bit weights (24
+    and more take the grouped GEMM): the batched GEMV on
     the matrix cores (codes of 3, 5 and 6 bits straddle words inside a lane's
     8-value block), with a partial last block of down rows (hidden 544 is 8.5
     blocks of 64) and passes of 16 activation rows (up to 30 rows for one
