@@ -724,6 +724,10 @@ moe_status run_gemv(const moe_qproj& p0, const moe_qproj* p1, const void* x, int
 // The same count moves a shared expert (one expert, T rows) onto the side
 // stream and the GEMM (mixed-bit layer at 24 tokens: 147.6 -> 121.0 us).
 constexpr int kGemmMinRows = 24;
+// Rows from which a shared expert forks onto the side stream, whatever
+// kernel it then runs (mixed-bit layer, µs per layer step in order / forked:
+// 8 tokens 85.8 / 79.7, 16 tokens 111.7 / 99.0; 4 tokens 58.3 either way).
+constexpr int kSideMinRows = 8;
 
 // The matrix-core GEMM writes whole 16-byte groups of an output row: N is a
 // multiple of 8 and the output 16-byte aligned (workspace buffers always are).
@@ -1441,11 +1445,11 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
 
   const bool dec1 = (T == 1 && dec1_supported(d));
   int smode = 0;
-  // a shared expert large enough for the matrix cores overlaps the routed
-  // experts (MoELayer.swift:620-624: it only joins at the combine); a small
-  // one stays in order (the fork and join cost a one-token NemotronH-shaped
-  // layer 3.5 us more than they saved)
-  SideFork side(allow_side && d->has_shared && T >= kGemmMinRows, st);
+  // a shared expert of kSideMinRows or more rows overlaps the routed experts
+  // (MoELayer.swift:620-624: it only joins at the combine); a smaller one
+  // stays in order (the fork and join cost a one-token NemotronH-shaped layer
+  // 3.5 us more than they saved)
+  SideFork side(allow_side && d->has_shared && T >= kSideMinRows, st);
   MOE_TRY(side.status());
   // one token: the shared expert inside the two one-token launches when its
   // formats allow (its gate logit from its own launch unless dense)
