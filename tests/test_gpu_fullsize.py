@@ -23,8 +23,8 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from moe_spec import (BF16, F16, LayerSpec, cfg_mixed, cfg_qwen3, check_close, gen_qproj, load,
-                      store, to_numpy_f32, to_torch, zipf_router_bias, ZIPF_BETA)
+from moe_spec import (BF16, F16, LayerSpec, cfg_gptoss, cfg_mixed, cfg_qwen3, check_close, gen_qproj,
+                      load, store, to_numpy_f32, to_torch, zipf_router_bias, ZIPF_BETA)
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -130,6 +130,17 @@ def test_mixed_2048_shared_full_size():
     the sigmoid-gated shared expert on its side stream."""
     info = run_full(cfg_mixed(), 2048, dict(gate_up="gemm", down="gemm", shared_gate_up="gemm",
                                             shared_down="gemm"))
+    assert info["hot_rows"] > 0
+
+
+def test_gptoss_256_gemm_path():
+    """GPT-OSS-20B shape (hidden = intermediate = 2880, 32 experts, top-4, the
+    biased router, per-expert output biases and the clamped SwiGLU) at 256
+    tokens: 32 rows per expert take the grouped GEMM, and the router
+    projection writes the GEMMs' f16 operand copy from its LDS chunks (2880 =
+    11.25 chunks of 256, so the last chunk's pieces past the row end are
+    dropped)."""
+    info = run_full(cfg_gptoss(seed=7, expert_bias=True), 256, dict(gate_up="gemm", down="gemm"))
     assert info["hot_rows"] > 0
 
 

@@ -103,11 +103,13 @@ def test_router_topk_bit_exact(E, k, mode):
 
 @pytest.mark.parametrize("T", [19, 77])
 @pytest.mark.parametrize("dt,wdt,E,H", [(BF16, BF16, 128, 2048), (F16, F16, 8, 256), (BF16, BF16, 32, 2880),
-                                         (F32, F32, 4, 64), (F16, F16, 64, 128)])
+                                         (F32, F32, 4, 64), (F16, F16, 64, 128), (BF16, BF16, 1, 768)])
 def test_router_logits_within_one_ulp(dt, wdt, E, H, T):
-    """T >= 32 with one 16-bit type, H % 64 == 0 and E % 32 == 0 runs on the
-    matrix cores (a partial last token tile at T = 77; H = 128 leaves half of
-    the K-split waves without a group; H = 2880 splits 45 groups unevenly)."""
+    """T >= 32 with one 16-bit type and H % 64 == 0 runs on the matrix cores
+    (a partial last token tile at T = 77; H = 128 leaves half of the K-split
+    waves without a group; H = 2880 splits 45 groups unevenly and ends in a
+    partial 256-value chunk; H = 768 is an odd count of chunks; E = 1, a
+    shared gate, repeats its one row over the expert tile)."""
     rng = np.random.default_rng(H + T)
     x = store(rng.normal(0, 1, (T, H)), dt)
     W = store(rng.normal(0, 1 / np.sqrt(H), (E, H)), wdt)
