@@ -1456,10 +1456,10 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
   const Dec1Shared fs = dec1 ? dec1_shared(d) : Dec1Shared{};
   if (fs.on) {
     if (!fs.in_kernel_gate) MOE_TRY(shared_gate_logits(d, x, T, ws, w, st));
-  } else {
+  } else if (dec1) {
     MOE_TRY(shared_expert(d, x, x16, T, ws, w, side.stream(), &smode));
   }
-  MOE_TRY(side.mark());
+  if (dec1) MOE_TRY(side.mark());
   if (dec1) {
     // 2. one token: routing inside the gate/up kernel (MoELayer.swift:1167-1282
     //    without a host round trip), then the fused down + combine
@@ -1564,6 +1564,16 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
                        at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.used), slots, M, T == 1,
                        at<void>(ws, w.Y), 0, 0.f, 0.f, st, kev(1), T));
     }
+    // The shared expert is enqueued after the routed launches (its fork point
+    // is still the router step). Replaying a HIP graph captured from this
+    // call, the runtime ran the branch captured first after the fork on the
+    // router's hardware queue and the other on a second queue (rocprofv3
+    // traces); that first branch should be the routed chain, which sets the
+    // step's length. Enqueued first, the shared branch took the router's
+    // queue and the routed chain's top-k started 11 us after the router
+    // ended (mixed-bit prefill step 373.8 -> 366.7 us with this order).
+    MOE_TRY(shared_expert(d, x, x16, T, ws, w, side.stream(), &smode));
+    MOE_TRY(side.mark());
     MOE_TRY(side.join());
     MOE_HIP(launch_unpermute(at<void>(ws, w.Y), at<uint32_t>(ws, w.inv), at<float>(ws, w.w), T, H,
                              k, y, xdt, smode ? at<void>(ws, w.s_out) : nullptr,
