@@ -1184,8 +1184,9 @@ moe_status shared_gate_logits(const moe_layer_desc* d, const void* x, int T, voi
 
 // x16: the layer input as the GEMMs' f16 operand (written before the fork
 // when the grouped GEMM runs for the shared expert).
+// gate_done: the router launch already wrote the shared gate's logits.
 moe_status shared_expert(const moe_layer_desc* d, const void* x, const void* x16, int T, void* ws,
-                         const Workspace& w, hipStream_t st, int* smode) {
+                         const Workspace& w, hipStream_t st, int* smode, bool gate_done) {
   *smode = 0;
   if (!d->has_shared) return MOE_OK;
   const int xdt = d->act_dtype;
@@ -1216,7 +1217,7 @@ moe_status shared_expert(const moe_layer_desc* d, const void* x, const void* x16
                      at<uint32_t>(ws, w.s_off), at<uint32_t>(ws, w.s_used), 1, T, single,
                      at<void>(ws, w.s_out), 0, 0.f, 0.f, st));
   }
-  return shared_gate_logits(d, x, T, ws, w, st);
+  return gate_done ? MOE_OK : shared_gate_logits(d, x, T, ws, w, st);
 }
 
 // Decode (T = 1) launch geometry. Lanes per row: the best unit utilisation
@@ -1419,7 +1420,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
   // router's matrix-core kernel when it reads the same rows, else on its own)
   const bool gemm = !(T == 1 && dec1_supported(d)) && routed_gemm(d, T);
   const bool want_x16 = (gemm || shared_gemm(d, T)) && xdt == MOE_BF16;
-  bool x16_done = false;
+  bool x16_done = false, sgate_done = false;
 
   // 1. router projection (MoELayer.swift:540 / 689-690)
   if (logits_done) {
@@ -1430,9 +1431,14 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
                             d->router_bias, E, at<void>(ws, w.logits), st),
             "quantised router launch");
   } else {
+    // a dense shared gate of the router's type, applied to the same rows, is
+    // computed by the router launch when that runs on the matrix cores
+    const bool gate2 = d->has_shared && d->shared_gate_weight && !d->shared_gate_q.weight && rx == x;
     MOE_HIP(launch_router_logits(rx, xdt, T, H, d->router_weight, d->router_dtype, d->router_bias,
                                  E, at<void>(ws, w.logits), st,
-                                 want_x16 && rx == x ? at<void>(ws, w.x16) : nullptr, &x16_done),
+                                 want_x16 && rx == x ? at<void>(ws, w.x16) : nullptr, &x16_done,
+                                 gate2 ? d->shared_gate_weight : nullptr, 1,
+                                 gate2 ? at<void>(ws, w.s_logit) : nullptr, &sgate_done),
             "router logits launch");
   }
 
@@ -1457,7 +1463,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
   if (fs.on) {
     if (!fs.in_kernel_gate) MOE_TRY(shared_gate_logits(d, x, T, ws, w, st));
   } else if (dec1) {
-    MOE_TRY(shared_expert(d, x, x16, T, ws, w, side.stream(), &smode));
+    MOE_TRY(shared_expert(d, x, x16, T, ws, w, side.stream(), &smode, sgate_done));
   }
   if (dec1) MOE_TRY(side.mark());
   if (dec1) {
@@ -1572,7 +1578,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     // step's length. Enqueued first, the shared branch took the router's
     // queue and the routed chain's top-k started 11 us after the router
     // ended (mixed-bit prefill step 373.8 -> 366.7 us with this order).
-    MOE_TRY(shared_expert(d, x, x16, T, ws, w, side.stream(), &smode));
+    MOE_TRY(shared_expert(d, x, x16, T, ws, w, side.stream(), &smode, sgate_done));
     MOE_TRY(side.mark());
     MOE_TRY(side.join());
     MOE_HIP(launch_unpermute(at<void>(ws, w.Y), at<uint32_t>(ws, w.inv), at<float>(ws, w.w), T, H,

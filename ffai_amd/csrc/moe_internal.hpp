@@ -146,10 +146,15 @@ size_t gemv_smem_bytes(int xdt, int K, int tok_chunk);
 // ---------------------------------------------------------------- router --
 // x16 (nullable): where the many-token matrix-core kernel, for bf16 rows,
 // also writes the rows as the expert GEMMs' f16 operand (launch_to_a16's
-// values); *x16_done tells whether it did.
+// values); *x16_done tells whether it did. W2 / E2 / logits2 (nullable): a
+// second projection of the same rows with weights of W's type and no bias
+// (a shared expert's gate), which that kernel computes in the same launch;
+// *second_done tells whether it did (else the caller launches it).
 hipError_t launch_router_logits(const void* x, int xdt, int T, int H, const void* W, int wdt,
                                 const void* bias, int E, void* logits, hipStream_t st,
-                                void* x16 = nullptr, bool* x16_done = nullptr);
+                                void* x16 = nullptr, bool* x16_done = nullptr,
+                                const void* W2 = nullptr, int E2 = 0, void* logits2 = nullptr,
+                                bool* second_done = nullptr);
 hipError_t launch_router_topk(const void* logits, int dt, int T, int E, int k,
                               const RouteOpts& ro, uint32_t* idx, float* w, hipStream_t st);
 // One token: res = round(h + m), xn = round(rmsnorm(res) * nw), then the

@@ -277,7 +277,9 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
                                                                     const XT* __restrict__ bias,
                                                                     XT* __restrict__ logits, int T,
                                                                     int H, int E,
-                                                                    uint4* __restrict__ x16) {
+                                                                    uint4* __restrict__ x16,
+                                                                    const XT* __restrict__ W2,
+                                                                    XT* __restrict__ logits2, int E2) {
   // token tile and expert tile of one chunk; the partial tiles of the
   // epilogue (rows padded to 33 floats) reuse the same bytes
   __shared__ u32x4_t stage[2][32 * kRgPieces];
@@ -286,17 +288,25 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
   // expert tiles of one token tile take ids 8 apart inside a window of 8 nE
   // ids, so they run close together on one XCD and read the token rows from
   // its L2 after the first of them has fetched them.
-  const int nE = (E + 31) >> 5;
+  // Expert tiles past the first ceil(E / 32) belong to a second projection
+  // of the same rows (W2: E2 rows, no bias, into logits2), such as a shared
+  // expert's gate, so that it costs no launch of its own.
+  const int nE1 = (E + 31) >> 5, nE = nE1 + ((E2 + 31) >> 5);
   const int b = (int)blockIdx.x, win = b / (8 * nE), slot = b - win * 8 * nE;
   const int tt = win * 8 + (slot & 7), et = slot >> 3;
   if (tt * 32 >= T) return;  // padding of the last window; uniform over the block
-  const int t0 = tt * 32, e0 = et * 32;
+  const bool second = et >= nE1;
+  const XT* __restrict__ Wt = second ? W2 : W;
+  const XT* __restrict__ bt = second ? nullptr : bias;
+  XT* __restrict__ out = second ? logits2 : logits;
+  const int Et = second ? E2 : E;
+  const int t0 = tt * 32, e0 = (second ? et - nE1 : et) * 32;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, h = lane >> 5;
   const int G = H >> 6, nC = (H + kRgChunk - 1) / kRgChunk;
   const rsrc_t xr = make_rsrc(x, (uint32_t)((size_t)T * H * sizeof(XT)));
-  const rsrc_t wr = make_rsrc(W, (uint32_t)((size_t)E * H * sizeof(XT)));
+  const rsrc_t wr = make_rsrc(Wt, (uint32_t)((size_t)Et * H * sizeof(XT)));
   // thread piece j: row (j * 64 * kRgWaves + tid) / kRgPieces of the tile,
   // piece (...) % kRgPieces of the chunk. Rows past T repeat the last token
   // and experts past E the last expert (never stored); pieces past H read
@@ -308,7 +318,7 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
     const int P = j * 64 * kRgWaves + tid;
     prow[j] = P / kRgPieces;
     ppc[j] = P % kRgPieces;
-    const uint32_t tr = (uint32_t)min(t0 + prow[j], T - 1), er = (uint32_t)min(e0 + prow[j], E - 1);
+    const uint32_t tr = (uint32_t)min(t0 + prow[j], T - 1), er = (uint32_t)min(e0 + prow[j], Et - 1);
     xo[j] = (tr * (uint32_t)H + 8u * (uint32_t)ppc[j]) * 2u;
     wo[j] = (er * (uint32_t)H + 8u * (uint32_t)ppc[j]) * 2u;
   }
@@ -398,10 +408,10 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
     float s = part[r * 33 + c];
 #pragma unroll
     for (int w = 1; w < kRgWaves; w++) s += part[w * 32 * 33 + r * 33 + c];
-    if (t0 + r < T && e0 + c < E) {
+    if (t0 + r < T && e0 + c < Et) {
       float l = round_to<XT>(s);
-      if (bias) l = round_to<XT>(l + to_f<XT>(bias[e0 + c]));
-      logits[(size_t)(t0 + r) * E + e0 + c] = from_f<XT>(l);
+      if (bt) l = round_to<XT>(l + to_f<XT>(bt[e0 + c]));
+      out[(size_t)(t0 + r) * Et + e0 + c] = from_f<XT>(l);
     }
   }
 }
@@ -427,15 +437,20 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const XT* __restrict__
 
 template <typename XT, typename WT>
 static hipError_t launch_rl(const void* x, int T, int H, const void* W, const void* bias, int E,
-                            void* logits, hipStream_t st, void* x16, bool* x16_done) {
+                            void* logits, hipStream_t st, void* x16, bool* x16_done,
+                            const void* W2, int E2, void* logits2, bool* second_done) {
   if constexpr (__is_same(XT, WT) && !__is_same(XT, float)) {
     if (T >= 32 && H % 64 == 0 && (size_t)T * H < (1ull << 31) && (size_t)E * H < (1ull << 31)) {
       const bool conv = x16 && __is_same(XT, bf16_t);
+      const bool two = W2 && logits2 && E2 > 0 && (size_t)E2 * H < (1ull << 31);
       const int windows = (T + 255) / 256;  // eight token tiles each
-      hipLaunchKernelGGL((router_gemm_kernel<XT>), dim3(windows * 8 * ((E + 31) / 32)), dim3(64 * kRgWaves),
+      const int tiles = (E + 31) / 32 + (two ? (E2 + 31) / 32 : 0);
+      hipLaunchKernelGGL((router_gemm_kernel<XT>), dim3(windows * 8 * tiles), dim3(64 * kRgWaves),
                          0, st, (const XT*)x, (const XT*)W, (const XT*)bias, (XT*)logits, T, H, E,
-                         conv ? (uint4*)x16 : nullptr);
+                         conv ? (uint4*)x16 : nullptr, two ? (const XT*)W2 : nullptr,
+                         two ? (XT*)logits2 : nullptr, two ? E2 : 0);
       if (x16_done) *x16_done = conv;
+      if (second_done) *second_done = two;
       return hipGetLastError();
     }
     if (T == 1 && H <= 4 * 2048) {
@@ -472,9 +487,12 @@ static hipError_t launch_rl(const void* x, int T, int H, const void* W, const vo
 
 hipError_t launch_router_logits(const void* x, int xdt, int T, int H, const void* W, int wdt,
                                 const void* bias, int E, void* logits, hipStream_t st, void* x16,
-                                bool* x16_done) {
+                                bool* x16_done, const void* W2, int E2, void* logits2,
+                                bool* second_done) {
   if (x16_done) *x16_done = false;
-#define MOE_RL2(XT, WT) return launch_rl<XT, WT>(x, T, H, W, bias, E, logits, st, x16, x16_done);
+  if (second_done) *second_done = false;
+#define MOE_RL2(XT, WT) \
+  return launch_rl<XT, WT>(x, T, H, W, bias, E, logits, st, x16, x16_done, W2, E2, logits2, second_done);
   if (xdt == DT_BF16) {
     if (wdt == DT_BF16) { MOE_RL2(bf16_t, bf16_t) }
     if (wdt == DT_F16) { MOE_RL2(bf16_t, f16_t) }
