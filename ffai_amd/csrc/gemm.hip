@@ -147,6 +147,24 @@ __device__ __forceinline__ void quarter_pairs(const uint32_t (&w)[BITS], int s, 
       pr[p] = __builtin_amdgcn_perm(0u, w[2 * s + (p >> 1)],
                                     (uint32_t)bb | 0x0C00u | ((uint32_t)(bb + 1) << 16) | 0x0C000000u) | M;
     }
+  } else if constexpr (BITS <= 3) {
+    // Two pairs per 4 * BITS-bit field y (values a, b, c, d from bit 0):
+    // m = y | y << (16 - BITS) has a at bit 0, b at bit 16, c at bit 2 * BITS
+    // and d at bit 16 + 2 * BITS, and the two copies of y do not overlap
+    // (4 * BITS <= 16 - BITS), so one mask per pair picks them out.
+    constexpr uint32_t kField = (1u << (4 * BITS)) - 1u, kPair = ((1u << BITS) - 1u) * 0x10001u;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int bit = (2 * s + h) * 4 * BITS, lo = bit >> 5, sh = bit & 31;
+      uint32_t y;
+      if (sh + 4 * BITS <= 32)
+        y = (w[lo] >> sh) & kField;
+      else
+        y = __builtin_amdgcn_alignbit(w[lo + 1], w[lo], (uint32_t)sh) & kField;
+      const uint32_t m = y | (y << (16 - BITS));
+      pr[2 * h] = (m & kPair) | M;
+      pr[2 * h + 1] = ((m >> (2 * BITS)) & kPair) | M;
+    }
   } else {
 #pragma unroll
     for (int p = 0; p < 4; p++) {

@@ -606,7 +606,8 @@ def test_layer_bit_widths(case, T):
 
 
 @pytest.mark.parametrize("case", [(4, 4, 64, BF16, BF16), (3, 6, 64, BF16, BF16),
-                                  (5, 8, 128, F16, F16), (2, 4, 32, F16, BF16)],
+                                  (5, 8, 128, F16, F16), (2, 4, 32, F16, BF16),
+                                  (6, 3, 32, BF16, F16), (8, 2, 64, F16, F16)],
                          ids=lambda c: f"gu{c[0]}-d{c[1]}-gs{c[2]}-sb{c[3]}-x{c[4]}")
 def test_layer_mfma_path(case):
     """Whole layers with enough rows per expert for the matrix-core GEMMs."""
