@@ -165,6 +165,23 @@ __device__ __forceinline__ void quarter_pairs(const uint32_t (&w)[BITS], int s, 
       pr[2 * h] = (m & kPair) | M;
       pr[2 * h + 1] = ((m >> (2 * BITS)) & kPair) | M;
     }
+  } else if constexpr (BITS == 5 || BITS == 6) {
+    // A pair's 2 * BITS bits lie inside the 16 bits from the byte holding its
+    // first bit: one byte permute puts those 16 bits in both halves, and one
+    // packed 16-bit shift right by (o, o + BITS) brings each value to the
+    // bottom of its half.
+    typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+    constexpr uint32_t kPair = ((1u << BITS) - 1u) * 0x10001u;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const int bit = (8 * s + 2 * p) * BITS, byte = bit >> 3, o = bit & 7;
+      const int wi = byte >> 2, bw = byte & 3, wj = wi + 1 < BITS ? wi + 1 : BITS - 1;
+      const uint32_t sel = (uint32_t)bw | ((uint32_t)(bw + 1) << 8) | ((uint32_t)bw << 16) |
+                           ((uint32_t)(bw + 1) << 24);
+      const u16x2_t z = __builtin_bit_cast(u16x2_t, __builtin_amdgcn_perm(w[wj], w[wi], sel));
+      const u16x2_t t = z >> u16x2_t{(unsigned short)o, (unsigned short)(o + BITS)};
+      pr[p] = (__builtin_bit_cast(uint32_t, t) & kPair) | M;
+    }
   } else {
 #pragma unroll
     for (int p = 0; p < 4; p++) {
