@@ -259,15 +259,22 @@ __device__ __forceinline__ void gateup_epilogue_split(const GemmArgs& a, const G
   uint16_t* tb = reinterpret_cast<uint16_t*>(L.b);
   const int cn = bn * 128 + 32 * (wn & 3) + col;  // output column of this lane
   const XT* ob = reinterpret_cast<const XT*>(wn < 4 ? a.p0.ob : a.p1.ob);
-  const float obv = (ob && cn < N) ? to_f<XT>(ob[(size_t)e * N + cn]) : -0.0f;
+  // without an output bias (ob is wave-uniform) the sum is rounded once
+  auto stage_out = [&](auto biasc) {
+    constexpr bool BIAS = decltype(biasc)::value;
+    const float obv = (BIAS && cn < N) ? to_f<XT>(ob[(size_t)e * N + cn]) : -0.0f;
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int row = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-      const float v = round_to<XT>(round_to<XT>(acc[i][0][r] * oscale) + obv);
-      tb[row * 256 + 32 * wn + col] = __builtin_bit_cast(uint16_t, from_f<XT>(v));
-    }
+      for (int r = 0; r < 16; r++) {
+        const int row = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+        float v = acc[i][0][r] * oscale;
+        if constexpr (BIAS) v = round_to<XT>(round_to<XT>(v) + obv);
+        tb[row * 256 + 32 * wn + col] = __builtin_bit_cast(uint16_t, from_f<XT>(v));
+      }
+  };
+  if (ob) stage_out(std::true_type{});
+  else stage_out(std::false_type{});
   __syncthreads();
   uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
   auto finish = [&](auto actc) {
@@ -620,44 +627,68 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
   unsigned char* wreg = wave < 4 ? L.b + wave * 16384 : (wave < 6 ? L.a0 : L.a1) + (wave & 1) * 16384;
   uint16_t* wt = reinterpret_cast<uint16_t*>(wreg);
   // Straight-line per activation kind (a runtime switch inside the loop left
-  // a branch per output). Without an output bias the bias term is -0, the
-  // identity of addition (so the second rounding changes nothing, -0 kept).
-  auto epilogue = [&](auto actc) {
+  // a branch per output), and per presence of an output bias: without one,
+  // the sum is rounded once (adding -0, the identity, and rounding the
+  // rounded value again would change nothing). A single projection that
+  // writes the layer dtype (the routed down GEMM) takes its own copy too,
+  // one conversion per output instead of both forms and a select.
+  auto epilogue = [&](auto actc, auto biasc, auto xtc) {
     constexpr int ACT = decltype(actc)::value;
+    constexpr bool BIAS = decltype(biasc)::value, XT_ONLY = decltype(xtc)::value;
 #pragma unroll
     for (int j = 0; j < HJ; j++) {
       const int cn = cbase + 32 * j + col;
-      const float obg = (ob0 && cn < N) ? to_f<XT>(ob0[(size_t)e * N + cn]) : -0.0f;
-      const float obu = (GATEUP && ob1 && cn < N) ? to_f<XT>(ob1[(size_t)e * N + cn]) : -0.0f;
+      float obg = -0.0f, obu = -0.0f;
+      if constexpr (BIAS) {
+        obg = (ob0 && cn < N) ? to_f<XT>(ob0[(size_t)e * N + cn]) : -0.0f;
+        obu = (GATEUP && ob1 && cn < N) ? to_f<XT>(ob1[(size_t)e * N + cn]) : -0.0f;
+      }
 #pragma unroll
       for (int i = 0; i < 2; i++) {
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const int row = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-          const float v = round_to<XT>(round_to<XT>(acc[i][j][r] * OSCALE) + obg);
+          float v = round_to<XT>(acc[i][j][r] * OSCALE);
+          if constexpr (BIAS) v = round_to<XT>(v + obg);
           uint16_t bits;
           if constexpr (GATEUP) {
-            const float u = round_to<XT>(round_to<XT>(acc[i][j + HJ][r] * OSCALE) + obu);
+            float u = round_to<XT>(acc[i][j + HJ][r] * OSCALE);
+            if constexpr (BIAS) u = round_to<XT>(u + obu);
             bits = __builtin_bit_cast(uint16_t, to_a16<XT>(apply_act<XT>(v, u, ACT, a.alpha, a.limit)));
           } else {
             // single projections: squared ReLU only
             const float y = ACT == ACT_RELU2 ? apply_act<XT>(0.f, v, ACT_RELU2, 0.f, 0.f) : v;
-            const uint16_t as_a16 = __builtin_bit_cast(uint16_t, to_a16<XT>(y));
             const uint16_t as_xt = __builtin_bit_cast(uint16_t, from_f<XT>(y));
-            bits = a.out_a16 ? as_a16 : as_xt;
+            if constexpr (XT_ONLY) {
+              bits = as_xt;
+            } else {
+              const uint16_t as_a16 = __builtin_bit_cast(uint16_t, to_a16<XT>(y));
+              bits = a.out_a16 ? as_a16 : as_xt;
+            }
           }
           wt[row * OC + 32 * j + col] = bits;
         }
       }
     }
   };
+  using kNo = std::false_type;
+  using kYes = std::true_type;
+  const bool has_bias = ob0 != nullptr || (GATEUP && ob1 != nullptr);
+  auto by_bias = [&](auto actc, auto xtc) {
+    if (has_bias) epilogue(actc, kYes{}, xtc);
+    else epilogue(actc, kNo{}, xtc);
+  };
   if constexpr (GATEUP) {
-    if (a.act == ACT_GPTOSS) epilogue(std::integral_constant<int, ACT_GPTOSS>{});
-    else if (a.act == ACT_GEGLU) epilogue(std::integral_constant<int, ACT_GEGLU>{});
-    else epilogue(std::integral_constant<int, ACT_SWIGLU>{});
+    if (a.act == ACT_GPTOSS) by_bias(std::integral_constant<int, ACT_GPTOSS>{}, kNo{});
+    else if (a.act == ACT_GEGLU) by_bias(std::integral_constant<int, ACT_GEGLU>{}, kNo{});
+    else by_bias(std::integral_constant<int, ACT_SWIGLU>{}, kNo{});
   } else {
-    if (a.act == ACT_RELU2) epilogue(std::integral_constant<int, ACT_RELU2>{});
-    else epilogue(std::integral_constant<int, ACT_SWIGLU>{});
+    auto by_out = [&](auto actc) {
+      if (a.out_a16) by_bias(actc, kNo{});
+      else by_bias(actc, kYes{});
+    };
+    if (a.act == ACT_RELU2) by_out(std::integral_constant<int, ACT_RELU2>{});
+    else by_out(std::integral_constant<int, ACT_SWIGLU>{});
   }
   // each lane: 16 bytes (8 columns) of one row per step; the wave reads only
   // its own region, so no block barrier is needed
