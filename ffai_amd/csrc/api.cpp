@@ -723,7 +723,15 @@ moe_status run_gemv(const moe_qproj& p0, const moe_qproj* p1, const void* x, int
 // rows Qwen3 242.0 / 191.8, GPT-OSS 323.9 / 305.3, mixed-bit 381.2 / 321.1.
 // The same count moves a shared expert (one expert, T rows) onto the side
 // stream and the GEMM (mixed-bit layer at 24 tokens: 147.6 -> 121.0 us).
+// With the GEMM's epilogues at one rounding per output, layers of many
+// small experts cross over at 16 rows (GEMV against GEMM: 16 rows Qwen3
+// 192.9 / 180.5, mixed-bit 309.0 / 303.9; 20 rows 221.7 / 183.9 and 345.7 /
+// 297.1; 14 rows 177.1 / 178.5 and 281.6 / 300.6; 12 rows 163.5 / 176.0 and
+// 257.3 / 297.5), while GPT-OSS's 32 large experts keep the GEMV up to 23
+// rows (16 rows 254.8 / 299.8, 20 rows 282.9 / 301.4): its GEMM blocks run
+// 45 K chunks each in few rounds over the CUs.
 constexpr int kGemmMinRows = 24;
+constexpr int kGemmMinRowsMany = 16, kGemmManyExperts = 64;
 // Rows from which a shared expert forks onto the side stream, whatever
 // kernel it then runs (mixed-bit layer, µs per layer step in order / forked:
 // 8 tokens 85.8 / 79.7, 16 tokens 111.7 / 99.0; 4 tokens 58.3 either way).
@@ -736,7 +744,8 @@ bool gemm_ok(const moe_qproj& p, int xdt, int M, const void* out = nullptr) {
   // activation rows are addressed with 32-bit byte offsets
   const bool fits = (size_t)M * (size_t)p.k * 2 < (1ull << 32);
   return xdt != MOE_F32 && p.k % 64 == 0 && p.n % 8 == 0 && p.n_experts <= 1024 && fits &&
-         M >= kGemmMinRows * slots && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+         M >= (p.n_experts >= kGemmManyExperts ? kGemmMinRowsMany : kGemmMinRows) * slots &&
+         (reinterpret_cast<uintptr_t>(out) & 15) == 0;
 }
 
 // out[p] = W[e(p)] . a[row(p)] (or the gate/up pair with the activation)
