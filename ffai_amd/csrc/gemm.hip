@@ -648,6 +648,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const int row = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+          if constexpr (!GATEUP && !BIAS && XT_ONLY && ACT != ACT_RELU2) {
+            // the stored value is the sum rounded once: one conversion
+            wt[row * OC + 32 * j + col] = __builtin_bit_cast(uint16_t, from_f<XT>(acc[i][j][r] * OSCALE));
+            continue;
+          }
           float v = round_to<XT>(acc[i][j][r] * OSCALE);
           if constexpr (BIAS) v = round_to<XT>(v + obg);
           uint16_t bits;
