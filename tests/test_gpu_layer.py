@@ -538,6 +538,9 @@ def test_layer_qwen3_decode(qwen3, B):
 
 
 def test_layer_qwen3_prefill_zipf():
+    """256 tokens on the Qwen3 shape: 16 rows per expert on average, the
+    fewest with which a layer of 64 or more experts takes the grouped GEMM,
+    with Zipf-skewed expert loads (many experts of a few rows, a few large)."""
     spec = cfg_qwen3(seed=5, router_bias=zipf_router_bias(128, 1.1, beta=1.0))
     run_layer(spec, 256)
 
