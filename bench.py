@@ -5,16 +5,22 @@ Default workload: BASELINE.json configs[1], a GPT-OSS-20B-shaped MoE decode
 layer (hidden = intermediate = 2880, 32 experts, top-4 on logits then softmax,
 clamped SwiGLU, mlx affine 4-bit gs64 with bf16 scales/biases, biased bf16
 router) on one token. 24 independent layers' weights stay resident in HBM
-(10.7 GB, beyond the 256 MB Infinity Cache) and successive steps rotate
-through them. One step = one layer call on one token; the timed region
-replays a HIP graph of the 24-layer rotation.
+(10.7 GB, beyond the 256 MB Infinity Cache) and successive calls rotate
+through them: call c (warm-up calls included) runs layer c % 24, so a layer's
+weights come back only after 23 other layers (1.3 GB) have streamed. One
+step = one layer call on one token; the timed calls are 5 HIP-graph replays,
+each of the next stretch of the rotation.
 
 Prints one JSON line:
   value       MoE-layer tokens/s (1 token per step / time per step)
   roofline    the dominant kernel (routed gate/up grouped GEMV), HBM bound:
               algorithmic bytes per launch / its average duration, timed with
-              hipEvents on the launch stream
+              hipEvents on the launch stream; `rocprof` beside it divides the
+              same bytes by the committed rocprofv3 average of that kernel
   cpu_baseline the C oracle (oracle/) on layer 0, one token at a time
+The default line also carries configs[3] (`prefill`), configs[4] (`mixed`),
+configs[4]'s layer at one token (`mixed1`) and the configs[2] sweep
+(`qwen3_decode`, 1 / 4 / 16 / 64 tokens).
 Other configs: --config qwen3 (configs[2], --batch B), prefill,
 mixed; --config ckpt_load times the checkpoint reader loading
 stacked mlx-affine experts from the page cache into HBM.
@@ -46,7 +52,7 @@ CONFIGS = {
                   workload="qwen3moe_decode"),
     "prefill": dict(H=2048, E=128, k=8, I=768, bits_gu=4, bits_d=4, sb="f16", act="swiglu",
                     gating="softmax_topk", router_bias="zipf", beta=0.33, T=4096, SI=0,
-                    workload="qwen3moe_prefill_4096_zipf1.1"),
+                    workload="qwen3moe_prefill_4096_zipf1.1_maxmed10"),
     "mixed": dict(H=2048, E=256, k=8, I=512, bits_gu=3, bits_d=6, sb="bf16", act="swiglu",
                   gating="softmax_topk", router_bias=False, T=2048, SI=512,
                   workload="mixed_3b6b_shared_prefill_2048"),
@@ -537,7 +543,16 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 10 plain device copies of BYTES each (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
+    ap.add_argument("--summarize-rocprof", metavar="CSV",
+                    help="write --out (profiles/<name>_kernel_stats.json) from a rocprofv3 "
+                         "kernel_stats.csv of --workload made by --command, then exit")
+    ap.add_argument("--workload")
+    ap.add_argument("--command")
+    ap.add_argument("--out")
     args = ap.parse_args()
+    if args.summarize_rocprof:
+        summarize_rocprof(args)
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
@@ -567,6 +582,8 @@ def main():
     cfg = dict(CONFIGS[args.config])
     if args.batch:
         cfg["T"] = args.batch
+    if args.config == "qwen3":
+        cfg["workload"] = f"qwen3moe_decode_b{cfg['T']}"
     if args.decoder_step:
         bench_decoder_step(args, torch, cfg)
         return
@@ -601,12 +618,37 @@ def main():
             out[name] = {"workload": c2["workload"], "tokens_per_s": r2["tokens_per_s"],
                          "ms_per_step": r2["ms_per_step"], "steps": st2, "warmup": wu2,
                          "timing": r2["timing"], "roofline": r2["roofline"],
-                         "layer_roofline": r2["layer_roofline"], "paths": r2["config"]["paths"]}
+                         "layer_roofline": r2["layer_roofline"], "paths": r2["config"]["paths"],
+                         "resident_layers": r2["config"]["resident_layers"],
+                         "timed_layers": r2["config"]["timed_layers"]}
+            if "zipf" in r2["config"]:
+                out[name]["zipf"] = r2["config"]["zipf"]
+        # the Qwen3-MoE-shaped decode sweep over batch sizes, on
+        # one set of 24 resident layers (8.2 GB)
+        qcfg = dict(CONFIGS["qwen3"])
+        qlayers = build_layers(qcfg, args.layers, torch, fl, lib)
+        sweep = {}
+        for B in (1, 4, 16, 64):
+            c2 = dict(qcfg, T=B, workload=f"qwen3moe_decode_b{B}")
+            r2, _ = run_config(c2, torch, fl, lib, steps=240, warmup=24, L=len(qlayers),
+                               layers=qlayers)
+            sweep[f"b{B}"] = {"workload": c2["workload"], "tokens_per_s": r2["tokens_per_s"],
+                              "ms_per_step": r2["ms_per_step"], "steps": 240, "warmup": 24,
+                              "distinct_experts": r2["expert_stream"]["distinct_experts"],
+                              "layer_roofline": r2["layer_roofline"], "roofline": r2["roofline"],
+                              "timing": r2["timing"], "paths": r2["config"]["paths"],
+                              "resident_layers": r2["config"]["resident_layers"],
+                              "timed_layers": r2["config"]["timed_layers"]}
+        del qlayers
+        out["qwen3_decode"] = sweep
     copy = copy_bandwidth(torch)
     out["hbm_copy"] = {"GBps": copy, "method": "1 GiB device-to-device copy x 10, read + write "
                        "bytes over the event time"}
-    for r in [out["roofline"]] + [out[n]["roofline"] for n in ("prefill", "mixed", "mixed1")
-                                  if n in out]:
+    roofs = [out["roofline"]] + [out[n]["roofline"] for n in ("prefill", "mixed", "mixed1")
+                                 if n in out]
+    roofs += [v[key] for v in out.get("qwen3_decode", {}).values()
+              for key in ("roofline", "layer_roofline")]
+    for r in roofs:
         if r["bound"] == "hbm":
             r["frac_of_copy"] = round(r["achieved"] / copy, 4)
     log(f"device copy {copy:.1f} GB/s")
@@ -638,16 +680,58 @@ def copy_bandwidth(torch, nbytes=1 << 30, reps=10):
     return round(gbps, 1)
 
 
-def run_config(cfg, torch, fl, lib, steps, warmup, L):
+def build_layers(cfg, L, torch, fl, lib):
+    log(f"building {L} resident layers of {cfg['workload']} ...")
+    return [make_layer(cfg, seed=100 + l, torch=torch, fl=fl, lib=lib) for l in range(L)]
+
+
+def graph_upload(g, torch):
+    """hipGraphUpload of a captured graph's executable, so that its first
+    replay does not also pay for moving the graph to the device. Best effort:
+    a torch build without the raw handle skips it."""
+    try:
+        hip = C.CDLL("libamdhip64.so")
+        hip.hipGraphUpload.argtypes = [C.c_void_p, C.c_void_p]
+        ex = g.raw_cuda_graph_exec()
+        ex = ex if isinstance(ex, int) else int(ex)
+        return hip.hipGraphUpload(C.c_void_p(ex),
+                                  C.c_void_p(torch.cuda.current_stream().cuda_stream)) == 0
+    except Exception:  # noqa: BLE001
+        return False
+
+
+def rocprof_avg_us(workload, kernel):
+    """Average duration (us) of `kernel` (a name prefix) in the committed
+    rocprofv3 --kernel-trace --stats summary of `workload`
+    (profiles/*_kernel_stats.json, written by --summarize-rocprof), with the
+    summary's file name; (None, None) when no summary covers it."""
+    import glob
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_kernel_stats.json"))):
+        with open(path) as f:
+            data = json.load(f)
+        if data.get("workload") != workload:
+            continue
+        for name, k in data.get("kernels", {}).items():
+            if name.startswith(kernel):
+                return k["avg_us"], os.path.relpath(path, ROOT)
+    return None, None
+
+
+def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
     """Times `steps` layer calls (one step = one call of the layer on cfg["T"]
-    token rows) after `warmup` untimed eager calls. Steps rotate through L
-    resident layers. The timed steps run as 5 repeats of HIP-graph replays
-    (steps // 5 calls each, the remainder spread over the first repeats), each
+    token rows) after `warmup` untimed eager calls. Calls rotate through L
+    resident layers: call c (warm-up calls first) runs layer c % L, so the
+    timed calls continue the rotation where the warm-up stopped and every
+    layer is used again only after the L - 1 others. The timed steps run as 5
+    repeats (steps // 5 calls each, the remainder spread over the first
+    repeats), each one HIP-graph replay of its own stretch of the rotation,
     bracketed by events on the launch stream; ms_per_step is the median over
     the repeats of (repeat time / its calls)."""
     T = cfg["T"]
-    log(f"building {L} resident layers of {cfg['workload']} (T={T}) ...")
-    layers = [make_layer(cfg, seed=100 + l, torch=torch, fl=fl, lib=lib) for l in range(L)]
+    if layers is None:
+        layers = build_layers(cfg, L, torch, fl, lib)
+    L = len(layers)
+    log(f"{cfg['workload']}: T={T}, {L} resident layers")
     xs = [torch.randn(T, cfg["H"], device="cuda").to(torch.bfloat16) for _ in range(L)]
     ys = [torch.empty_like(x) for x in xs]
     for l in range(L):
@@ -656,35 +740,60 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L):
     paths = layers[0].paths(T)
 
     # warm-up: exactly `warmup` eager calls
-    for i in range(warmup):
-        layers[i % L].forward(xs[i % L], out=ys[i % L])
+    last_use = {}
+    for c in range(warmup):
+        layers[c % L].forward(xs[c % L], out=ys[c % L])
+        last_use[c % L] = c
     torch.cuda.synchronize()
 
-    # the timed steps: 5 repeats, each one HIP-graph replay
+    # the timed steps: 5 repeats, each one HIP-graph replay of the next
+    # stretch of the rotation
     nrep = 5 if steps >= 5 else max(1, steps)
     sizes = [steps // nrep + (1 if r < steps % nrep else 0) for r in range(nrep)]
-    graphs = {}
-    for n in sorted(set(sizes)):
+    graphs = []
+    c = warmup
+    reuse = []
+    timed_layers = set()
+    for n in sizes:
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            for i in range(n):
-                layers[i % L].forward(xs[i % L], out=ys[i % L])
-        graphs[n] = g
+            for _ in range(n):
+                l = c % L
+                layers[l].forward(xs[l], out=ys[l])
+                if l in last_use:
+                    reuse.append(c - last_use[l])
+                last_use[l] = c
+                timed_layers.add(l)
+                c += 1
+        graphs.append(g)
+    uploaded = all([graph_upload(g, torch) for g in graphs])
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(nrep)]
+    # a short spin on the device first, so that all five repeats (events and
+    # graph launches) are enqueued before the first one starts: the repeats
+    # then run back to back, without the host's launch time between them
+    # (a repeat of a few short calls would otherwise mostly time the host)
+    spun = hasattr(torch.cuda, "_sleep")
+    if spun:
+        torch.cuda._sleep(2_000_000)
     w0 = time.perf_counter()
-    for r, n in enumerate(sizes):
+    for r in range(nrep):
         evs[r][0].record()
-        graphs[n].replay()
+        graphs[r].replay()
         evs[r][1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
-    per_step = sorted(evs[r][0].elapsed_time(evs[r][1]) / n for r, n in enumerate(sizes))
+    each = [evs[r][0].elapsed_time(evs[r][1]) / n for r, n in enumerate(sizes)]
+    span = evs[0][0].elapsed_time(evs[-1][1]) / steps
+    per_step = sorted(each)
     ms_per_step = per_step[len(per_step) // 2]
     value = T * 1000.0 / ms_per_step
+    min_reuse = min(reuse) if reuse else None
     log(f"{steps} steps in {nrep} repeats {sizes}: {ms_per_step * 1e3:.2f} us/step (median), "
-        f"repeats {[round(v * 1e3, 2) for v in per_step]} us/step; wall {wall * 1e3:.1f} ms")
+        f"repeats {[round(v * 1e3, 2) for v in each]} us/step, all {span * 1e3:.2f}; "
+        f"{len(timed_layers)} layers timed, min reuse distance {min_reuse}; "
+        f"wall {wall * 1e3:.1f} ms")
     del graphs
 
     # kernel-level timing of the routed expert kernels: start/end events
@@ -769,15 +878,28 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L):
                       "gemv": "gemv_multi_kernel (routed gate/up over the dispatch plan)"}[
                           paths["gate_up"]]
     roof["avg_us"] = round(gu_us, 3)
+    work = gu_bytes if roof["bound"] == "hbm" else gu_flops
     if roof["bound"] == "hbm":
         roof["algorithmic_bytes"] = gu_bytes
     else:
         roof["algorithmic_flops"] = gu_flops
+    roof["avg_us_method"] = ("start/stop events recorded by the kernel's own dispatch "
+                             "(dispatch included), eager pass")
+    # the same work over the committed rocprofv3 average of this kernel
+    kname = {"decode1": "gateup1_kernel", "gemm": "gemm_grouped_kernel",
+             "gemv_mma": "gemv_mma_kernel", "gemv": "gemv_multi_kernel"}[paths["gate_up"]]
+    rp_us, rp_file = rocprof_avg_us(cfg["workload"], kname)
+    if rp_us:
+        scale = 1e9 if roof["bound"] == "hbm" else 1e12
+        ach = work / (rp_us * 1e-6) / scale
+        roof["rocprof"] = {"avg_us": rp_us, "achieved": round(ach, 2),
+                           "frac": round(ach / roof["peak"], 4), "summary": rp_file}
     log(f"gate/up kernel {gu_us:.2f} us ({gu_bytes / 1e6:.2f} MB, {gu_flops / 1e9:.1f} GFLOP); "
         f"down {dn_us:.2f} us; U={U}; paths {paths}")
     config = {"workload": cfg["workload"], "hidden": H, "experts": cfg["E"], "top_k": k,
               "intermediate": I, "tokens_per_step": T, "bits": [cfg["bits_gu"], cfg["bits_d"]],
-              "group_size": 64, "resident_layers": L, "parallelism": "single-gpu",
+              "group_size": 64, "resident_layers": L, "timed_layers": len(timed_layers),
+              "min_reuse_distance_calls": min_reuse, "parallelism": "single-gpu",
               "paths": paths}
     if cfg["SI"]:
         config["shared_intermediate"] = cfg["SI"]
@@ -789,8 +911,11 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L):
         "tokens_per_s": round(value, 1),
         "ms_per_step": round(ms_per_step, 6),
         "timing": {"repeats": nrep, "calls_per_repeat": sizes,
-                   "ms_per_step_each": [round(v, 6) for v in per_step],
-                   "method": "HIP-graph replay per repeat, events on the launch stream, median"},
+                   "ms_per_step_each": [round(v, 6) for v in each],
+                   "ms_per_step_all": round(span, 6), "graphs_uploaded": uploaded,
+                   "enqueued_ahead": spun,
+                   "method": "one HIP-graph replay per repeat (each its own stretch of the "
+                             "layer rotation), events on the launch stream, median"},
         "config": config,
         "roofline": roof,
         "layer_roofline": layer_roof,
@@ -802,6 +927,39 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L):
     del layers, xs, ys
     torch.cuda.synchronize()
     return res, out_layer
+
+
+def summarize_rocprof(args):
+    """Writes profiles/<name>_kernel_stats.json from a rocprofv3
+    kernel_stats.csv: per kernel (mangled names shortened to the function
+    name) calls and average / min / max duration in us, with the workload and
+    the command that produced the CSV. bench.py reads these summaries for the
+    rocprof side of its rooflines."""
+    import csv
+    import re
+    with open(args.summarize_rocprof) as f:
+        rows = list(csv.DictReader(f))
+    kernels = {}
+    for r in rows:
+        name = r["Name"]
+        m = re.match(r"_ZN\d*moe(\d+)(\w+)", name)
+        # _ZN3moe14gateup1_kernelI... -> gateup1_kernel (template variants
+        # of one kernel get #2, #3, ... in the order of the CSV)
+        short = m.group(2)[:int(m.group(1))] if m else name
+        key = short
+        i = 2
+        while key in kernels:
+            key = f"{short}#{i}"
+            i += 1
+        kernels[key] = {"calls": int(r["Calls"]), "avg_us": round(float(r["AverageNs"]) / 1e3, 3),
+                        "min_us": round(float(r["MinNs"]) / 1e3, 3),
+                        "max_us": round(float(r["MaxNs"]) / 1e3, 3),
+                        "share_pct": round(float(r["Percentage"]), 2), "mangled": name}
+    out = {"workload": args.workload, "command": args.command, "kernels": kernels}
+    with open(args.out, "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    print(f"wrote {args.out}: {len(kernels)} kernels")
 
 if __name__ == "__main__":
     main()
