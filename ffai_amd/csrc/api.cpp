@@ -1718,11 +1718,16 @@ struct moe_layer {
   void* ws = nullptr;
   size_t ws_bytes = 0;
   int ws_tokens = 0;
+  bool ws_async = false;          // ws came from hipMallocAsync
+  hipStream_t last_st = nullptr;  // the stream of the latest call
 
-  // Grows the scratch to T rows. Growing waits for the whole device (a
-  // previous call may still read the old scratch on any stream) and
-  // allocates, so it is refused while `st` is being captured: a handle that
-  // is captured must have run once, eagerly, at its largest T.
+  // Grows the scratch to T rows, stream-ordered: the old scratch is freed on
+  // the stream of the latest call (after that call, whose side-stream work
+  // joins back into it, has finished with it) and the new one allocated on
+  // `st`, so growing stalls no other stream. A device without memory pools
+  // falls back to a device-wide wait and hipFree. Allocating is refused while
+  // `st` is being captured: a handle that is captured must have run once,
+  // eagerly, at its largest T.
   moe_status reserve(int T, hipStream_t st) {
     if (T <= ws_tokens) return MOE_OK;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -1734,14 +1739,26 @@ struct moe_layer {
                   T, ws_tokens);
     const size_t need = moe_layer_workspace_bytes(&desc, T);
     if (ws) {
-      MOE_HIP(hipDeviceSynchronize(), "MoELayer scratch resize");
-      const hipError_t e = hipFree(ws);
+      hipError_t e;
+      if (ws_async) {
+        e = hipFreeAsync(ws, last_st);
+      } else {
+        e = hipDeviceSynchronize();
+        if (e == hipSuccess) e = hipFree(ws);
+      }
       ws = nullptr;
       ws_bytes = 0;
       ws_tokens = 0;
       MOE_HIP(e, "MoELayer scratch free");
     }
-    MOE_HIP(hipMalloc(&ws, need), "MoELayer scratch allocation");
+    if (hipMallocAsync(&ws, need, st) == hipSuccess) {
+      ws_async = true;
+    } else {
+      (void)hipGetLastError();  // no memory pools: a plain allocation
+      ws = nullptr;
+      ws_async = false;
+      MOE_HIP(hipMalloc(&ws, need), "MoELayer scratch allocation");
+    }
     ws_bytes = need;
     ws_tokens = T;
     return MOE_OK;
@@ -1750,6 +1767,7 @@ struct moe_layer {
   moe_status decode_many(const void* h, int T, void* out, hipStream_t st) {
     if (T <= 0) return fail(MOE_ERR_INVALID, "MoELayer.decodeMany: T must be positive");
     MOE_TRY(reserve(T, st));
+    last_st = st;
     return layer_forward(&desc, h, h, T, out, ws, ws_bytes, nullptr, st);
   }
 };
@@ -1769,7 +1787,12 @@ extern "C" void moe_layer_destroy(moe_layer_t layer) {
   if (!layer) return;
   if (layer->ws) {
     (void)hipDeviceSynchronize();
-    (void)hipFree(layer->ws);
+    if (layer->ws_async) {
+      (void)hipFreeAsync(layer->ws, nullptr);
+      (void)hipStreamSynchronize(nullptr);
+    } else {
+      (void)hipFree(layer->ws);
+    }
   }
   delete layer;
 }

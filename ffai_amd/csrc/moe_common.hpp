@@ -147,19 +147,25 @@ __device__ __forceinline__ void bstore128(rsrc_t r, uint32_t off, u32x4_t v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0);
 }
 
-// Eight bf16 values (16 bytes) -> f16 * 2^-SHIFT, rounded toward zero: the
-// grouped GEMM's A operand of a bf16 layer (exact for results in f16's
-// normal range; finite inputs saturate instead of overflowing).
+// Eight bf16 values (16 bytes) -> f16 * 2^-SHIFT, rounded to nearest even:
+// the grouped GEMM's A operand of a bf16 layer, converted as its epilogue
+// converts the intermediate activation (to_a16 in gemm.hip). Exact for
+// magnitudes 2^(SHIFT-14) ... 65504 * 2^SHIFT (f16's normal range after the
+// scale); below, f16 subnormals round to nearest (absolute error at most
+// 2^(SHIFT-25)); finite values beyond saturate to +-65504 * 2^SHIFT;
+// infinities and NaNs pass through.
 template <int SHIFT>
 __device__ __forceinline__ uint4 bf16x8_to_a16(uint4 v) {
   const uint32_t in[4] = {v.x, v.y, v.z, v.w};
   uint32_t o[4];
+  auto cvt = [](float f) -> uint32_t {
+    f = __builtin_ldexpf(f, -SHIFT);
+    if (__builtin_fabsf(f) > 65504.0f && __builtin_isfinite(f)) f = __builtin_copysignf(65504.0f, f);
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+  };
 #pragma unroll
-  for (int q = 0; q < 4; q++) {
-    const float lo = __builtin_ldexpf(__uint_as_float(in[q] << 16), -SHIFT);
-    const float hi = __builtin_ldexpf(__uint_as_float(in[q] & 0xFFFF0000u), -SHIFT);
-    o[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
-  }
+  for (int q = 0; q < 4; q++)
+    o[q] = cvt(__uint_as_float(in[q] << 16)) | (cvt(__uint_as_float(in[q] & 0xFFFF0000u)) << 16);
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 

@@ -234,7 +234,9 @@ __global__ __launch_bounds__(64 * kRqWaves) void router_qgemm_kernel(const XT* _
 template <int BITS, typename XT, typename ST>
 static hipError_t launch_rq_t(const void* x, int T, int H, const GemvProj& W, int gsh,
                               const void* bias, int E, void* logits, hipStream_t st) {
-  if (T >= 32 && H % 64 == 0) {
+  // the matrix-core kernel views x as one buffer with 32-bit offsets: beyond
+  // 4 GiB of input rows the per-row kernel (64-bit row addresses) runs
+  if (T >= 32 && H % 64 == 0 && (size_t)T * H * sizeof(XT) < (1ull << 32)) {
     hipLaunchKernelGGL((router_qgemm_kernel<BITS, XT, ST>), dim3((T + 31) / 32, (E + 31) / 32),
                        dim3(64 * kRqWaves), 0, st, (const XT*)x, W, (const XT*)bias, (XT*)logits,
                        T, H, E, gsh);

@@ -236,7 +236,9 @@ moe_status moe_dequantize_affine(const uint32_t* weight, const void* scales, con
  *   out[p, :] = W[e(p)] . a[row(p), :]   for every sorted position p,
  * e(p) = the expert whose CSR range [offsets[e], offsets[e+1]) holds p,
  * row(p) = perm[p] / top_k when perm is non-NULL (activation gather), else
- * p. Replaces Ops.dequantGemvInt4ExpertIndexed(Many) (Ops.swift:2444-2587)
+ * p. With perm, a holds ceil(M / top_k) rows and every perm[p] < M (a plan
+ * of M = T * top_k positions over T rows, as moe_dispatch_plan writes it);
+ * without, a holds M rows. Replaces Ops.dequantGemvInt4ExpertIndexed(Many) (Ops.swift:2444-2587)
  * and Ops.moeGatherDequantGemmInt4 bm8/bm16/bm64/m1 (Ops.swift:4553-5201,
  * 6499-6585). Picks the HBM-streaming GEMV or the MFMA GEMM by rows per
  * expert. out and a are in a_dtype. The workspace holds the GEMM's work list

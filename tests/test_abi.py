@@ -194,3 +194,22 @@ def test_no_oracle_in_product():
             if f.endswith((".py", ".cpp", ".hip", ".hpp", ".h")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "moe_oracle" not in text and "import oracle" not in text, f
+
+
+def test_swift_module_map():
+    """swift/CMoEHIP: the module map names headers that resolve to include/
+    and the library that ffai_amd/ holds, and the headers compile as plain C
+    on their own (what a Swift clang importer reads)."""
+    import subprocess
+    d = os.path.join(ROOT, "swift", "CMoEHIP")
+    text = open(os.path.join(d, "module.modulemap")).read()
+    headers = re.findall(r'header\s+"([^"]+)"', text)
+    assert set(headers) == {"moe_hip.h", "moe_safetensors.h"}
+    for h in headers:
+        assert os.path.realpath(os.path.join(d, h)) == os.path.join(ROOT, "include", h)
+        subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-x", "c",
+                        os.path.join(d, h)], check=True)
+    (link,) = re.findall(r'link\s+"([^"]+)"', text)
+    assert os.path.basename(_lib.LIB_PATH) == f"lib{link}.so"
+    pkg = open(os.path.join(ROOT, "swift", "Package.swift")).read()
+    assert '.systemLibrary(name: "CMoEHIP", path: "CMoEHIP")' in pkg

@@ -290,6 +290,50 @@ def test_expert_matmul_mfma(bits, dt, sb, gs, gather):
     check_close(to_numpy_f32(out), ref, dt, f"mfma expert_matmul bits={bits} gs={gs}")
 
 
+def test_gemm_operand_range_bf16():
+    """The matrix-core path feeds a bf16 input to the matrix cores as f16
+    values x 2^-8, converted to nearest: a row element at 2^25 (beyond
+    65504 * 2^8) saturates to 65504 * 2^8, and one at 2^-20 (an f16
+    subnormal after the scale) rounds to the nearest subnormal. The product
+    equals the fp32 oracle's on the input converted that way, and differs
+    from the unconverted input's where the value saturated."""
+    rng = np.random.default_rng(77)
+    from moe_spec import gen_qproj
+    E, N, K, bits, gs, dt, sb = 2, 128, 256, 4, 64, BF16, BF16
+    counts = np.array([40, 24])
+    M = int(counts.sum())
+    p = gen_qproj(rng, E, N, K, bits, gs, sb)
+    experts = np.repeat(np.arange(E), counts).astype(np.uint32)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.uint32)
+    xf = rng.normal(0, 1, (M, K))
+    xf[3, 17] = 2.0 ** 25
+    xf[5, 9] = -(2.0 ** 25)
+    xf[7, 100] = 2.0 ** -20 * 1.37
+    a = store(xf, dt)
+    src = load(a, dt)
+    # the operand conversion, restated: scale, saturate, f16 to nearest
+    v = np.clip(src.astype(np.float32) * np.float32(2.0 ** -8), -65504, 65504)
+    conv = v.astype(np.float16).astype(np.float32) * np.float32(2.0 ** 8)
+    assert conv[3, 17] == 65504.0 * 256 and conv[5, 9] == -65504.0 * 256
+    lib = _lib.load()
+    q = _lib.QProj(0, 0, 0, None, bits, gs, sb, N, K, E)
+    wt, st, bt = to_torch(p.weight.view(np.int32)), to_torch(p.scales), to_torch(p.biases)
+    q.weight, q.scales, q.biases = wt.data_ptr(), st.data_ptr(), bt.data_ptr()
+    at = to_torch(a)
+    out = torch.empty(M, N, dtype=at.dtype, device="cuda")
+    wsb = lib.moe_expert_matmul_workspace_bytes(C.byref(q), dt, M)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    offt = to_torch(offsets.view(np.int32))
+    check(lib.moe_expert_matmul(C.byref(q), _p(at), dt, None, 1, M, _p(offt), _p(out), _p(ws), wsb,
+                                _stream()))
+    torch.cuda.synchronize()
+    got = to_numpy_f32(out)
+    ref = orc.round_dt(orc.qgemm_rows(p, conv, experts), dt)
+    check_close(got, ref, dt, "bf16 operand range on the matrix-core path")
+    raw = orc.round_dt(orc.qgemm_rows(p, src, experts), dt)
+    assert np.abs(got[3] - raw[3]).max() > 1e3, "the 2^25 element should saturate"
+
+
 # ------------------------------------------------------------ whole layer --
 
 @pytest.mark.parametrize("E,k", [(8, 1), (32, 4), (64, 6), (128, 8), (512, 16)])
@@ -649,22 +693,34 @@ def test_layer_is_deterministic(qwen3):
 
 
 def test_layer_handle_matches_forward(tiny):
-    """moe_layer_create / decode / decode_many (the MoELayer instance API)."""
+    """moe_layer_create / decode / decode_many (the MoELayer instance API).
+    The first call reserves scratch for one row; the 16-row call on another
+    stream grows it (the old scratch freed in the first stream's order, the
+    new one allocated in the second's), and a later one-row call reuses it."""
     dev = tiny.device()
     lib = _lib.load()
     h = C.c_void_p()
     check(lib.moe_layer_create(C.byref(dev.desc), C.byref(h)))
     try:
         x = to_torch(tiny.x(16))
+        x1 = x[:1].contiguous()
         ref = dev.forward(x)
+        ref1 = dev.forward(x1)
+        torch.cuda.synchronize()
+        one = torch.empty_like(x1)
+        check(lib.moe_layer_decode(h, _p(x1), _p(one), _stream()))
         out = torch.empty_like(x)
-        check(lib.moe_layer_decode_many(h, _p(x), 16, _p(out), _stream()))
-        one = torch.empty_like(x[:1])
-        check(lib.moe_layer_decode(h, _p(x[:1].contiguous()), _p(one), _stream()))
-        ref1 = dev.forward(x[:1].contiguous())
+        s2 = torch.cuda.Stream()
+        s2.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s2):
+            check(lib.moe_layer_decode_many(h, _p(x), 16, _p(out), _stream()))
+        torch.cuda.current_stream().wait_stream(s2)
+        again = torch.empty_like(x1)
+        check(lib.moe_layer_decode(h, _p(x1), _p(again), _stream()))
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
         assert torch.equal(one.view(torch.int16), ref1.view(torch.int16))
+        assert torch.equal(again.view(torch.int16), ref1.view(torch.int16))
     finally:
         lib.moe_layer_destroy(h)
 

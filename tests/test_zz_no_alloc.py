@@ -46,11 +46,17 @@ def _same(a, b):
     return torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8))
 
 
-@pytest.mark.parametrize("cfg,Ts", [("qwen3", (64, 8)), ("gptoss", (4, 1)), ("mixed", (48, 2, 1))])
+@pytest.mark.parametrize("cfg,Ts", [("qwen3", (64, 8)), ("gptoss", (4, 1)), ("mixed", (48, 2, 1)),
+                                    ("qwen3", (256, 16))])
 def test_noalloc_matches_forward(cfg, Ts):
     spec = {"qwen3": cfg_qwen3, "gptoss": cfg_gptoss, "mixed": cfg_mixed}[cfg]()
     dev = spec.device()
     lib = _lib.load()
+    if Ts[0] == 256:
+        # 16 rows per expert: the grouped GEMM, with its work items and the
+        # f16 operand copy of the input in the static scratch
+        assert dev.paths(256)["gate_up"] == "gemm", dev.paths(256)
+        assert dev.workspace_bytes(256) <= lib.moe_layer_noalloc_max_bytes()
     for T in Ts:  # the second call has fewer rows and reuses the scratch as left
         x = to_torch(spec.x(T, seed=T))
         ref, tref = dev.forward(x, trace=True)
