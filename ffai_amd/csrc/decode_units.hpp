@@ -254,6 +254,64 @@ __device__ __forceinline__ void stage_x_row(const XT* x, int K, uint32_t* xl, in
   }
 }
 
+// Cooperative copy of `rows` 16-bit activation rows of K values (row r at
+// src_r(r)) into LDS already in pair order: unit u of row r is 16 pair words
+// at xl + (r CU + u) 16 and its sum at xs[r CU + u], so that the lanes that
+// multiply the unit read it as it is. Threads t = 0..nt-1 of a block take
+// units t, t + nt, ...; each batch of up to NB units has every load issued
+// before its first conversion.
+template <int BITS, typename XT, int NB, typename SRC>
+__device__ __forceinline__ void stage_x_pairs(SRC src_r, int rows, int K, uint32_t* xl, float* xs,
+                                              int t, int nt) {
+  const int CU = K >> 5, total = rows * CU;
+  for (int base = t; base < total; base += NB * nt) {
+    u32x4_t v[NB][4];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      const int g = min(base + b * nt, total - 1), r = g / CU, u = g - r * CU;
+      const rsrc_t rr = make_rsrc(src_r(r), (uint32_t)(K * sizeof(XT)));
+#pragma unroll
+      for (int q = 0; q < 4; q++) v[b][q] = bload128(rr, (uint32_t)u * 64u + 16u * q);
+    }
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      const int g = base + b * nt;
+      if (g < total) {
+        uint32_t n[16], x16[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          n[4 * q] = v[b][q][0]; n[4 * q + 1] = v[b][q][1];
+          n[4 * q + 2] = v[b][q][2]; n[4 * q + 3] = v[b][q][3];
+        }
+        natural_to_pairs<BITS>(n, x16);
+        uint4* d = reinterpret_cast<uint4*>(xl + 16 * g);
+#pragma unroll
+        for (int q = 0; q < 4; q++) d[q] = make_uint4(x16[4 * q], x16[4 * q + 1], x16[4 * q + 2], x16[4 * q + 3]);
+        xs[g] = sum16(n, __is_same(XT, bf16_t));
+      }
+    }
+  }
+}
+
+// Units li + j L (j < UR) of row r staged by stage_x_pairs; units past CU
+// repeat the last unit (the dot products mask them out).
+template <typename XT, int UR>
+__device__ __forceinline__ void lds_x_units_pairs(const uint32_t* xl, const float* xs, int r, int li,
+                                                  int L, int CU, XUnit<XT> (&xu)[UR],
+                                                  float (&xsum)[UR]) {
+#pragma unroll
+  for (int j = 0; j < UR; j++) {
+    const int g = r * CU + min(li + j * L, CU - 1);
+    const uint4* p = reinterpret_cast<const uint4*>(xl + 16 * g);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint4 v = p[q];
+      xu[j].v[4 * q] = v.x; xu[j].v[4 * q + 1] = v.y; xu[j].v[4 * q + 2] = v.z; xu[j].v[4 * q + 3] = v.w;
+    }
+    xsum[j] = xs[g];
+  }
+}
+
 // Units li + j L (j < UR) of a 16-bit activation row staged in LDS (natural
 // order, 16 dwords per unit) into pair order with their sums. Units past CU
 // repeat the last unit; the dot products mask them out.

@@ -771,6 +771,7 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
   __shared__ float sc[kTopkMaxE];
   __shared__ int route[2];
   __shared__ __align__(16) uint32_t xl[kDec1MaxHidden / 2];
+  __shared__ float xsm[kDec1MaxHidden / 32];
   const int routed_blocks = a.k * a.row_blocks;
   // the shared expert's gate logit block (the last, with a dense gate row)
   if (SH && a.sgw && (int)blockIdx.x == routed_blocks + a.s_blocks) {
@@ -797,9 +798,12 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
   const XT* ob_u = reinterpret_cast<const XT*>(pu.ob);
 
   // wave 0 routes the token (every block computes identical, deterministic
-  // results); block 0 publishes the routing
-  if (wave != 0) stage_x_row<XT, 6>(reinterpret_cast<const XT*>(a.x), K, xl, threadIdx.x - 64,
-                                 blockDim.x - 64);
+  // results); block 0 publishes the routing. Meanwhile the other waves stage
+  // the activation row in LDS in pair order with its unit sums, so that the
+  // lanes' dot products after the weight stream read their units as they are.
+  if (wave != 0)
+    stage_x_pairs<BITS, XT, 2>([&](int) { return reinterpret_cast<const XT*>(a.x); }, 1, K, xl, xsm,
+                               threadIdx.x - 64, blockDim.x - 64);
   if (wave == 0 && shb) {
     if (lane == 0) {
       route[0] = 0;
@@ -861,7 +865,7 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
   __builtin_amdgcn_sched_barrier(0);
   XUnit<XT> xu[UR];
   float xs[UR];
-  lds_x_units_nat<BITS, XT, UR>(xl, li, L, CU, xu, xs);
+  lds_x_units_pairs<XT, UR>(xl, xsm, 0, li, L, CU, xu, xs);
 
   XT* act = shb ? reinterpret_cast<XT*>(a.s_act) : reinterpret_cast<XT*>(a.act) + (size_t)rank * N;
 #pragma unroll
@@ -906,11 +910,25 @@ __global__ __launch_bounds__(SH ? 64 * kDec1MaxWaves : 64 * kDec1MaxK) void down
   const int j = q - a.k;            // its column slice
   const XT* ob = reinterpret_cast<const XT*>(a.p.ob);
 
+  // The activation units go out first: they need no routing, and their
+  // conversion to pair order then runs while the weights stream instead of
+  // after them (loads complete in issue order).
+  const XT* act = shw ? reinterpret_cast<const XT*>(a.s_act) + (size_t)j * K
+                      : reinterpret_cast<const XT*>(a.act) + (size_t)q * K;
+  u32x4_t xraw[UR][4];
+  {
+    const rsrc_t xr = make_rsrc(act, (uint32_t)(K * sizeof(XT)));
+#pragma unroll
+    for (int jj = 0; jj < UR; jj++)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; q4++) xraw[jj][q4] = bload128(xr, (uint32_t)(li + jj * L) * 64u + 16u * q4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
   uint32_t e = 0;
   ProjView P;
   UnitAddr base{0u, 0u};
   int rw = row_words, grp = groups;
-  const XT* act;
   float obv[RM];
   if (shw) {
     rw = a.m * row_words;
@@ -918,7 +936,6 @@ __global__ __launch_bounds__(SH ? 64 * kDec1MaxWaves : 64 * kDec1MaxK) void down
     P = proj_view<BITS, ST>(a.sp, 0u, N, rw, grp);
     base.w0 = (uint32_t)(j * row_words * 4);
     base.s0 = (uint32_t)(j * groups * (int)sizeof(ST));
-    act = reinterpret_cast<const XT*>(a.s_act) + (size_t)j * K;
 #pragma unroll
     for (int it = 0; it < RM; it++) obv[it] = 0.f;
   } else {
@@ -928,7 +945,6 @@ __global__ __launch_bounds__(SH ? 64 * kDec1MaxWaves : 64 * kDec1MaxK) void down
     for (int it = 0; it < RM; it++)
       obv[it] = ob ? to_f<XT>(ob[(size_t)e * N + min(r_begin + sg + it * SG, N - 1)]) : 0.f;
     P = proj_view<BITS, ST>(a.p, e, N, row_words, groups);
-    act = reinterpret_cast<const XT*>(a.act) + (size_t)q * K;
   }
   const uint32_t wstep = (uint32_t)(L * BITS * 4), sstep = (uint32_t)((L >> a.gsh) * sizeof(ST));
   WUnit<BITS, ST> w[RM][UR];
@@ -939,10 +955,21 @@ __global__ __launch_bounds__(SH ? 64 * kDec1MaxWaves : 64 * kDec1MaxK) void down
     ad.s0 += base.s0;
     bload_units<BITS, ST, UR, kStream>(P, ad, wstep, sstep, w[it]);
   }
+  __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the conversion and the math
   XUnit<XT> xu[UR];
   float xs[UR];
-  bload_x_units<BITS, XT, UR>(make_rsrc(act, (uint32_t)(K * sizeof(XT))), li, L, xu, xs);
-  __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the math
+#pragma unroll
+  for (int jj = 0; jj < UR; jj++) {
+    uint32_t n[16];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; q4++) {
+      n[4 * q4] = xraw[jj][q4][0]; n[4 * q4 + 1] = xraw[jj][q4][1];
+      n[4 * q4 + 2] = xraw[jj][q4][2]; n[4 * q4 + 3] = xraw[jj][q4][3];
+    }
+    natural_to_pairs<BITS>(n, xu[jj].v);
+    xs[jj] = sum16(n, __is_same(XT, bf16_t));
+  }
+  __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
   for (int it = 0; it < RM; it++) {
