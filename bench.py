@@ -528,7 +528,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2400,
-                    help="timed layer calls (5 repeats of steps / 5 calls, median reported)")
+                    help="timed layer calls (up to 5 repeats of at least one layer rotation each, median reported)")
     ap.add_argument("--warmup", type=int, default=240, help="untimed eager layer calls first")
     ap.add_argument("--config", default="gptoss",
                     choices=sorted(CONFIGS) + ["ckpt_load", "mxfp4"])
@@ -545,13 +545,30 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
     ap.add_argument("--summarize-rocprof", metavar="CSV",
                     help="write --out (profiles/<name>_kernel_stats.json) from a rocprofv3 "
-                         "kernel_stats.csv of --workload made by --command, then exit")
+                         "kernel_trace.csv of --workload made by --command, then exit")
+    ap.add_argument("--summarize-traffic", action="store_true",
+                    help="write --out (profiles/<name>_traffic.json) from the FETCH_SIZE / "
+                         "WRITE_SIZE counter CSVs of --workload and of a --copy-probe run")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="CSV",
+                    help="write --out (profiles/<name>_counters.json) from rocprofv3 --pmc "
+                         "counter CSVs of --workload made by --command, then exit")
+    ap.add_argument("--fetch")
+    ap.add_argument("--write")
+    ap.add_argument("--copy-fetch")
+    ap.add_argument("--copy-write")
+    ap.add_argument("--copy-bytes", type=int, default=268435456)
     ap.add_argument("--workload")
     ap.add_argument("--command")
     ap.add_argument("--out")
     args = ap.parse_args()
     if args.summarize_rocprof:
         summarize_rocprof(args)
+        return
+    if args.summarize_traffic:
+        summarize_traffic(args)
+        return
+    if args.summarize_counters:
+        summarize_counters(args)
         return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -701,7 +718,7 @@ def graph_upload(g, torch):
 
 
 def rocprof_avg_us(workload, kernel):
-    """Average duration (us) of `kernel` (a name prefix) in the committed
+    """Average duration (us) of `kernel` (its short name) in the committed
     rocprofv3 --kernel-trace --stats summary of `workload`
     (profiles/*_kernel_stats.json, written by --summarize-rocprof), with the
     summary's file name; (None, None) when no summary covers it."""
@@ -711,9 +728,9 @@ def rocprof_avg_us(workload, kernel):
             data = json.load(f)
         if data.get("workload") != workload:
             continue
-        for name, k in data.get("kernels", {}).items():
-            if name.startswith(kernel):
-                return k["avg_us"], os.path.relpath(path, ROOT)
+        k = data.get("kernels", {}).get(kernel)
+        if k is not None:
+            return k["avg_us"], os.path.relpath(path, ROOT)
     return None, None
 
 
@@ -722,9 +739,10 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
     token rows) after `warmup` untimed eager calls. Calls rotate through L
     resident layers: call c (warm-up calls first) runs layer c % L, so the
     timed calls continue the rotation where the warm-up stopped and every
-    layer is used again only after the L - 1 others. The timed steps run as 5
-    repeats (steps // 5 calls each, the remainder spread over the first
-    repeats), each one HIP-graph replay of its own stretch of the rotation,
+    layer is used again only after the L - 1 others. The timed steps run as
+    min(5, steps // L) repeats, at least one (steps // repeats calls each, the
+    remainder spread over the first repeats), each one HIP-graph replay of its
+    own stretch of the rotation,
     bracketed by events on the launch stream; ms_per_step is the median over
     the repeats of (repeat time / its calls)."""
     T = cfg["T"]
@@ -746,9 +764,10 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
         last_use[c % L] = c
     torch.cuda.synchronize()
 
-    # the timed steps: 5 repeats, each one HIP-graph replay of the next
-    # stretch of the rotation
-    nrep = 5 if steps >= 5 else max(1, steps)
+    # the timed steps: up to 5 repeats, each one HIP-graph replay of the next
+    # stretch of the rotation and each at least one full rotation long (a
+    # repeat of a few calls would mostly time the replay's own start and end)
+    nrep = max(1, min(5, steps // L))
     sizes = [steps // nrep + (1 if r < steps % nrep else 0) for r in range(nrep)]
     graphs = []
     c = warmup
@@ -770,7 +789,7 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(nrep)]
-    # a short spin on the device first, so that all five repeats (events and
+    # a short spin on the device first, so that all the repeats (events and
     # graph launches) are enqueued before the first one starts: the repeats
     # then run back to back, without the host's launch time between them
     # (a repeat of a few short calls would otherwise mostly time the host)
@@ -854,6 +873,9 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
         sh_flops = 2.0 * T * 3 * H * cfg["SI"]
     router_bytes = cfg["E"] * H * 2
     layer_bytes = gu_bytes + dn_bytes - T * k * I * 4 + router_bytes + sh_gu_bytes + sh_dn_bytes
+    kname = {"decode1": "gateup1_kernel",
+             "gemm": "gemm_grouped_gateup", "gemv_mma": "gemv_mma_gateup",
+             "gemv": "gemv_multi_gateup"}[paths["gate_up"]]
     if paths["gate_up"] == "gemm":
         roof = dict(bound="mfma", achieved=round(gu_flops / (gu_us * 1e-6) / 1e12, 2),
                     peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s")
@@ -870,8 +892,7 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
                           peak=HBM_PEAK_GBS, unit="GB/s")
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
     layer_roof["frac"] = round(layer_roof["achieved"] / layer_roof["peak"], 4)
-    roof["traffic"] = measured_traffic(cfg["workload"], {
-        "decode1": "gateup1_kernel", "gemm": "gemm_grouped_gateup"}.get(paths["gate_up"], ""))
+    roof["traffic"] = measured_traffic(cfg["workload"], kname)
     roof["kernel"] = {"decode1": "gateup1_kernel (one-token gate/up with routing)",
                       "gemm": "gemm_grouped_kernel (MFMA gate/up over the expert row tiles)",
                       "gemv_mma": "gemv_mma_kernel (MFMA gate/up over the dispatch plan)",
@@ -886,8 +907,6 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
     roof["avg_us_method"] = ("start/stop events recorded by the kernel's own dispatch "
                              "(dispatch included), eager pass")
     # the same work over the committed rocprofv3 average of this kernel
-    kname = {"decode1": "gateup1_kernel", "gemm": "gemm_grouped_kernel",
-             "gemv_mma": "gemv_mma_kernel", "gemv": "gemv_multi_kernel"}[paths["gate_up"]]
     rp_us, rp_file = rocprof_avg_us(cfg["workload"], kname)
     if rp_us:
         scale = 1e9 if roof["bound"] == "hbm" else 1e12
@@ -929,37 +948,172 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
     return res, out_layer
 
 
+def short_kernel_name(name):
+    """A kernel's function name from its mangled name (_ZN3moe14gateup1_kernelI...
+    -> gateup1_kernel). The grouped GEMM and the grouped GEMVs, which serve
+    both a gate/up pair and a single projection, are named after their first
+    template flag: gemm_grouped_gateup / gemm_grouped_single,
+    gemv_mma_gateup, gemv_multi_single, ..."""
+    import re
+    m = re.match(r"_ZN\d*moe(\d+)(\w+)", name)
+    if not m:
+        return name
+    short = m.group(2)[:int(m.group(1))]
+    if short in ("gemm_grouped_kernel", "gemv_mma_kernel", "gemv_multi_kernel"):
+        flag = re.search(r"Lb([01])E", name)
+        short = short[: -len("_kernel")] + ("_gateup" if flag and flag.group(1) == "1" else "_single")
+    return short
+
+
+def grid_keys(groups):
+    """Names for (short kernel name, grid size) groups: one kernel launched at
+    several grid sizes (the grouped GEMM runs the routed experts and, on a
+    side stream, the shared expert) keeps its plain name for the grid with the
+    largest total and gets name@<grid threads> for the others."""
+    by_name = {}
+    for (name, grid), total in groups.items():
+        by_name.setdefault(name, []).append((total, grid))
+    keys = {}
+    for name, lst in by_name.items():
+        lst.sort(reverse=True)
+        for i, (_, grid) in enumerate(lst):
+            keys[(name, grid)] = name if i == 0 else f"{name}@{grid}"
+    return keys
+
+
 def summarize_rocprof(args):
     """Writes profiles/<name>_kernel_stats.json from a rocprofv3
-    kernel_stats.csv: per kernel (mangled names shortened to the function
-    name) calls and average / min / max duration in us, with the workload and
-    the command that produced the CSV. bench.py reads these summaries for the
-    rocprof side of its rooflines."""
+    kernel_trace.csv (--kernel-trace, one row per dispatch): per kernel
+    (mangled names shortened to the function name, split by grid size as
+    grid_keys names them) calls and average / median / min / max duration in
+    us and the share of the run's GPU time, with the workload and the command
+    that produced the CSV. Kernels outside the library (torch's set-up fills
+    and copies, the bench's device spin) are one line in total. bench.py
+    reads these summaries for the rocprof side of its rooflines."""
     import csv
-    import re
+    import statistics
+    durs, mangled = {}, {}
+    other = {"calls": 0, "total_us": 0.0}
+    total_all = 0.0
     with open(args.summarize_rocprof) as f:
-        rows = list(csv.DictReader(f))
+        for r in csv.DictReader(f):
+            us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            total_all += us
+            name = r["Kernel_Name"]
+            if not name.startswith("_ZN3moe"):
+                other["calls"] += 1
+                other["total_us"] += us
+                continue
+            grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+            key = (short_kernel_name(name), grid)
+            durs.setdefault(key, []).append(us)
+            mangled[key] = name
+    keys = grid_keys({k: sum(v) for k, v in durs.items()})
     kernels = {}
-    for r in rows:
-        name = r["Name"]
-        m = re.match(r"_ZN\d*moe(\d+)(\w+)", name)
-        # _ZN3moe14gateup1_kernelI... -> gateup1_kernel (template variants
-        # of one kernel get #2, #3, ... in the order of the CSV)
-        short = m.group(2)[:int(m.group(1))] if m else name
-        key = short
-        i = 2
-        while key in kernels:
-            key = f"{short}#{i}"
-            i += 1
-        kernels[key] = {"calls": int(r["Calls"]), "avg_us": round(float(r["AverageNs"]) / 1e3, 3),
-                        "min_us": round(float(r["MinNs"]) / 1e3, 3),
-                        "max_us": round(float(r["MaxNs"]) / 1e3, 3),
-                        "share_pct": round(float(r["Percentage"]), 2), "mangled": name}
-    out = {"workload": args.workload, "command": args.command, "kernels": kernels}
+    for k, v in sorted(durs.items(), key=lambda kv: -sum(kv[1])):
+        kernels[keys[k]] = {"calls": len(v), "grid_threads": k[1],
+                            "avg_us": round(sum(v) / len(v), 3),
+                            "median_us": round(statistics.median(v), 3),
+                            "min_us": round(min(v), 3), "max_us": round(max(v), 3),
+                            "share_pct": round(100.0 * sum(v) / total_all, 2),
+                            "mangled": mangled[k]}
+    other["total_us"] = round(other["total_us"], 1)
+    other["share_pct"] = round(100.0 * other["total_us"] / total_all, 2)
+    out = {"workload": args.workload, "command": args.command, "kernels": kernels,
+           "other_kernels": other}
     with open(args.out, "w") as f:
         json.dump(out, f, indent=1)
         f.write("\n")
     print(f"wrote {args.out}: {len(kernels)} kernels")
+
+
+def counter_means(path):
+    """Mean value per (kernel, counter) of a rocprofv3 --pmc counter CSV
+    (one row per dispatch and counter). Kernels are keyed by their short
+    name, split by grid size as grid_keys names them (the grouped GEMM's
+    routed and shared-expert launches apart)."""
+    import collections
+    import csv
+    acc = collections.defaultdict(list)
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            acc[(short_kernel_name(r["Kernel_Name"]), int(r["Grid_Size"]),
+                 r["Counter_Name"])].append(float(r["Counter_Value"]))
+    totals = collections.defaultdict(float)
+    for (k, g, c), v in acc.items():
+        totals[(k, g)] += sum(v)
+    keys = grid_keys(totals)
+    return {(keys[(k, g)], c): sum(v) / len(v) for (k, g, c), v in acc.items()}
+
+
+def summarize_traffic(args):
+    """Writes profiles/<name>_traffic.json from four rocprofv3 --pmc runs:
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) over `--copy-probe BYTES`
+    (a plain device copy of known size, which calibrates the counters) and
+    over the workload. hbm_bytes per kernel = FETCH_SIZE x 1024 x fetch_factor
+    + WRITE_SIZE x 1024 x write_factor, the factors being the copy's bytes
+    over what the counters read for it."""
+    cf, cw = counter_means(args.copy_fetch), counter_means(args.copy_write)
+    copy_f = max(v for (k, c), v in cf.items() if c == "FETCH_SIZE")
+    copy_w = max(v for (k, c), v in cw.items() if c == "WRITE_SIZE")
+    ff = args.copy_bytes / (copy_f * 1024.0)
+    fw = args.copy_bytes / (copy_w * 1024.0)
+    wf, ww = counter_means(args.fetch), counter_means(args.write)
+    kernels = {}
+    for (k, c), v in wf.items():
+        if c != "FETCH_SIZE" or not k.startswith(("gateup1", "down1", "gemm_grouped", "gemv",
+                                                  "router", "unpermute")):
+            continue
+        w = ww.get((k, "WRITE_SIZE"))
+        if w is None:
+            continue
+        kernels[k] = {"FETCH_SIZE_KiB": round(v, 1), "WRITE_SIZE_KiB": round(w, 1),
+                      "hbm_bytes": int(round(v * 1024 * ff + w * 1024 * fw))}
+    out = {"workload": args.workload, "command": args.command,
+           "calibration": {"copy_bytes": args.copy_bytes, "FETCH_SIZE_KiB": round(copy_f, 1),
+                           "WRITE_SIZE_KiB": round(copy_w, 1), "fetch_factor": round(ff, 4),
+                           "write_factor": round(fw, 4)},
+           "kernels": kernels}
+    with open(args.out, "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    print(f"wrote {args.out}: {sorted(kernels)}")
+
+def summarize_counters(args):
+    """Writes profiles/<name>_counters.json from rocprofv3 --pmc CSVs of one
+    workload (each its own pass): the mean per dispatch of every counter per
+    kernel of the library and, where the counters are there, MFMA busy per
+    SIMD (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE / 8 XCDs x 256 CUs x
+    4 SIMDs), VALU instructions per MFMA instruction (SQ_INSTS_VALU, which
+    counts the MFMAs too, over SQ_INSTS_MFMA), the share of wave cycles spent
+    waiting for an instruction's operands (SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES)
+    and LDS bank-conflict cycles per LDS-active cycle."""
+    means = {}
+    for path in args.summarize_counters:
+        for (k, c), v in counter_means(path).items():
+            if k.startswith(("gateup1", "down1", "gemm_grouped", "gemv", "router",
+                             "unpermute")):
+                means.setdefault(k, {})[c] = round(v, 1)
+    kernels = {}
+    for k, m in sorted(means.items()):
+        d = {"counters": m}
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in m and m.get("GRBM_GUI_ACTIVE"):
+            d["mfma_busy_pct"] = round(100.0 * m["SQ_VALU_MFMA_BUSY_CYCLES"]
+                                       / (m["GRBM_GUI_ACTIVE"] / 8 * 256 * 4), 1)
+        if m.get("SQ_INSTS_MFMA"):
+            d["valu_per_mfma"] = round(m["SQ_INSTS_VALU"] / m["SQ_INSTS_MFMA"], 2)
+        if m.get("SQ_WAVE_CYCLES") and "SQ_WAIT_INST_ANY" in m:
+            d["wait_inst_pct"] = round(100.0 * m["SQ_WAIT_INST_ANY"] / m["SQ_WAVE_CYCLES"], 1)
+        if m.get("SQ_ACTIVE_INST_LDS") and "SQ_LDS_BANK_CONFLICT" in m:
+            d["lds_bank_conflict_per_active"] = round(m["SQ_LDS_BANK_CONFLICT"]
+                                                      / m["SQ_ACTIVE_INST_LDS"], 3)
+        kernels[k] = d
+    out = {"workload": args.workload, "command": args.command, "kernels": kernels}
+    with open(args.out, "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    print(f"wrote {args.out}: {sorted(kernels)}")
+
 
 if __name__ == "__main__":
     main()
