@@ -737,13 +737,19 @@ constexpr int kGemmMinRowsMany = 16, kGemmManyExperts = 64;
 // 8 tokens 85.8 / 79.7, 16 tokens 111.7 / 99.0; 4 tokens 58.3 either way).
 constexpr int kSideMinRows = 8;
 
+// The matrix-core GEMM reads a weight row's scales and biases as 32-bit words
+// (two 16-bit groups each): both arrays 4-byte aligned.
+bool sb_words_ok(const moe_qproj& p) {
+  return ((reinterpret_cast<uintptr_t>(p.scales) | reinterpret_cast<uintptr_t>(p.biases)) & 3) == 0;
+}
+
 // The matrix-core GEMM writes whole 16-byte groups of an output row: N is a
 // multiple of 8 and the output 16-byte aligned (workspace buffers always are).
 bool gemm_ok(const moe_qproj& p, int xdt, int M, const void* out = nullptr) {
   const int slots = std::min(p.n_experts, M);
   // activation rows are addressed with 32-bit byte offsets
   const bool fits = (size_t)M * (size_t)p.k * 2 < (1ull << 32);
-  return xdt != MOE_F32 && p.k % 64 == 0 && p.n % 8 == 0 && p.n_experts <= 1024 && fits &&
+  return xdt != MOE_F32 && p.k % 64 == 0 && p.n % 8 == 0 && p.n_experts <= 1024 && fits && sb_words_ok(p) &&
          M >= (p.n_experts >= kGemmManyExperts ? kGemmMinRowsMany : kGemmMinRows) * slots &&
          (reinterpret_cast<uintptr_t>(out) & 15) == 0;
 }
@@ -759,12 +765,14 @@ bool gemm_ok(const moe_qproj& p, int xdt, int M, const void* out = nullptr) {
 bool routed_gemm(const moe_layer_desc* d, int T) {
   const moe_qproj& p0 = d->activation == MOE_ACT_RELU2 ? d->up : d->gate;
   const int M = T * d->top_k;
-  return gemm_ok(p0, d->act_dtype, M) && gemm_ok(d->down, d->act_dtype, M);
+  return gemm_ok(p0, d->act_dtype, M) && gemm_ok(d->down, d->act_dtype, M) &&
+         (d->activation == MOE_ACT_RELU2 || sb_words_ok(d->up));
 }
 bool shared_gemm(const moe_layer_desc* d, int T) {
   if (!d->has_shared) return false;
   const moe_qproj& p0 = d->activation == MOE_ACT_RELU2 ? d->shared_up : d->shared_gate;
-  return gemm_ok(p0, d->act_dtype, T) && gemm_ok(d->shared_down, d->act_dtype, T);
+  return gemm_ok(p0, d->act_dtype, T) && gemm_ok(d->shared_down, d->act_dtype, T) &&
+         (d->activation == MOE_ACT_RELU2 || sb_words_ok(d->shared_up));
 }
 
 // out_a16: a single projection writes A rows for a following GEMM (the

@@ -377,6 +377,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
   int brl[BI];
   uint32_t brow[BI];
   ProjViewG PB[BI];
+  const uint32_t* SB[BI];
 #pragma unroll
   for (int i = 0; i < BI; i++) {
     brl[i] = (threadIdx.x >> 1) + 256 * i;
@@ -390,26 +391,30 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
     }
     brow[i] = (uint32_t)min(wrow, N - 1);
     // upper is wave-uniform (see above); the branch keeps the views scalar
-    if (GATEUP && __builtin_amdgcn_readfirstlane((int)upper))
-      PB[i] = proj_view_g<BITS>(a.p1, e, N, row_words, groups);
-    else
-      PB[i] = proj_view_g<BITS>(a.p0, e, N, row_words, groups);
+    const GemvProj& pj = (GATEUP && __builtin_amdgcn_readfirstlane((int)upper)) ? a.p1 : a.p0;
+    PB[i] = proj_view_g<BITS>(pj, e, N, row_words, groups);
+    // the lane pair of a weight row (bu = 0, 1) loads its scales and its
+    // biases respectively (4-byte aligned arrays, host check; the expert's
+    // first group is even since N % 8 == 0)
+    SB[i] = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(bu ? pj.b : pj.s) +
+                                              (size_t)e * N * groups);
   }
-  // packed codes, scale and bias of a thread's units: three register sets,
-  // so chunks c + 2 and c + 3 are in flight while chunk c + 1 is dequantised
+  // packed codes and the scale or bias word of a thread's units: three
+  // register sets, so chunks c + 2 and c + 3 are in flight while chunk c + 1
+  // is dequantised
   struct BUnits {
     uint32_t w[BI][BITS];
-    uint32_t s[BI], b[BI];  // raw 16-bit scale and bias (kept apart: combining them
-                            // where they load would wait for both loads right there)
+    uint32_t sb[BI];  // the 32-bit word holding the unit's 16-bit scale (bu = 0) or bias (bu = 1)
+  };
+  // group element of a thread's unit in chunk `chunk` (row-major [N][groups]):
+  // for 32-value groups the pair's two groups share one word (groups is even:
+  // K % 64 == 0), for larger ones both lanes want the same group
+  auto sb_el = [&](int i, int chunk) -> uint32_t {
+    return brow[i] * (uint32_t)groups + (uint32_t)((2 * chunk + bu) >> a.gsh);
   };
   auto load_sb = [&](int chunk, BUnits& u) {
-    const int unit = 2 * chunk + bu;
 #pragma unroll
-    for (int i = 0; i < BI; i++) {
-      const uint32_t gi = (brow[i] * (uint32_t)groups + (uint32_t)(unit >> a.gsh)) * 2u;
-      u.s[i] = bload16(PB[i].s, gi);
-      u.b[i] = bload16(PB[i].b, gi);
-    }
+    for (int i = 0; i < BI; i++) u.sb[i] = SB[i][sb_el(i, chunk) >> 1];
   };
   auto load_w = [&](int chunk, BUnits& u) {
     const int unit = 2 * chunk + bu;
@@ -430,11 +435,16 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
       *reinterpret_cast<u32x4_t*>(Bs + buf * BBUF + tile_off(brl[i], 4 * bu + s)) = v;
     }
   };
-  auto sb_pairs = [&](const BUnits& u, h2_t (&s2)[BI], h2_t (&b2)[BI]) {
+  // the unit's scale and bias: the lane pair swaps its words (DPP quad_perm
+  // [1, 0, 3, 2]) and each lane takes its 16-bit half
+  auto sb_pairs = [&](const BUnits& u, int chunk, h2_t (&s2)[BI], h2_t (&b2)[BI]) {
 #pragma unroll
     for (int i = 0; i < BI; i++) {
-      s2[i] = sb_h2(u.s[i], sb_bf16);
-      b2[i] = sb_h2(u.b[i], sb_bf16);
+      const uint32_t other = (uint32_t)__builtin_amdgcn_mov_dpp((int)u.sb[i], 0xB1, 0xF, 0xF, false);
+      const uint32_t sw = bu ? other : u.sb[i], bw = bu ? u.sb[i] : other;
+      const uint32_t sh = (sb_el(i, chunk) & 1u) * 16u;
+      s2[i] = sb_h2((sw >> sh) & 0xFFFFu, sb_bf16);
+      b2[i] = sb_h2((bw >> sh) & 0xFFFFu, sb_bf16);
     }
   };
 
@@ -489,7 +499,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
   };
   // vector-memory instructions per thread: a chunk's activation copies, and
   // one chunk's scales, biases and codes
-  constexpr int kCopyLoads = AI, kUnitSetLoads = BI * (2 + kUnitLoads<BITS>);
+  constexpr int kCopyLoads = AI, kUnitSetLoads = BI * (1 + kUnitLoads<BITS>);
   // A chunk's activations were issued one chunk before its barrier, ahead of
   // that chunk's weight loads (in the program, and sched_barriers keep them
   // there); at most the weight loads of that chunk plus everything the next
@@ -530,7 +540,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
     // dequantisation they would turn its wait into a wait for every load)
     __builtin_amdgcn_sched_barrier(0);
     h2_t s2[BI], b2[BI];
-    sb_pairs(nb, s2, b2);
+    sb_pairs(nb, c + 1, s2, b2);
     read_frags(st, buf, 1, f1);
     mma_step(mv, f0);
     store_b(nb, s2, b2, 0, buf ^ 1);
@@ -569,7 +579,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const GemmLds L, ui
   __builtin_amdgcn_sched_barrier(0);
   {
     h2_t s2[BI], b2[BI];
-    sb_pairs(u0, s2, b2);
+    sb_pairs(u0, 0, s2, b2);
 #pragma unroll
     for (int s = 0; s < 4; s++) store_b(u0, s2, b2, s, 0);
   }
