@@ -739,10 +739,13 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
     token rows) after `warmup` untimed eager calls. Calls rotate through L
     resident layers: call c (warm-up calls first) runs layer c % L, so the
     timed calls continue the rotation where the warm-up stopped and every
-    layer is used again only after the L - 1 others. The timed steps run as
-    min(5, steps // L) repeats, at least one (steps // repeats calls each, the
-    remainder spread over the first repeats), each one HIP-graph replay of its
-    own stretch of the rotation,
+    layer is used again only after the L - 1 others; before them, each
+    layer is called once as set-up (starting at the first timed layer). The graphs of the timed
+    calls are captured and uploaded first and the warm-up calls run right
+    before the timed ones, so that the timed calls start on the clocks of a
+    running loop. The timed steps run as min(5, steps // L) repeats, at least
+    one (steps // repeats calls each, the remainder spread over the first
+    repeats), each one HIP-graph replay of its own stretch of the rotation,
     bracketed by events on the launch stream; ms_per_step is the median over
     the repeats of (repeat time / its calls)."""
     T = cfg["T"]
@@ -754,15 +757,22 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
     ys = [torch.empty_like(x) for x in xs]
     for l in range(L):
         layers[l].workspace(T)
+    # set-up: every resident layer is called once, as a decode loop has used
+    # every layer before any given step (a layer's first call after a long
+    # idle stretch reads 1.5-2 us slower on GPT-OSS). The pass starts at the
+    # first timed layer, so between a timed layer's set-up call and its timed
+    # call come at least L + warmup other calls (GPT-OSS: 24 x 56 MB), far
+    # more than the 256 MB memory-side cache holds.
+    for i in range(L):
+        l = (warmup + i) % L
+        layers[l].forward(xs[l], out=ys[l])
     torch.cuda.synchronize()
     paths = layers[0].paths(T)
 
-    # warm-up: exactly `warmup` eager calls
+    # the warm-up calls (they run after the graphs are captured, below)
     last_use = {}
     for c in range(warmup):
-        layers[c % L].forward(xs[c % L], out=ys[c % L])
         last_use[c % L] = c
-    torch.cuda.synchronize()
 
     # the timed steps: up to 5 repeats, each one HIP-graph replay of the next
     # stretch of the rotation and each at least one full rotation long (a
@@ -789,13 +799,12 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(nrep)]
-    # a short spin on the device first, so that all the repeats (events and
-    # graph launches) are enqueued before the first one starts: the repeats
-    # then run back to back, without the host's launch time between them
-    # (a repeat of a few short calls would otherwise mostly time the host)
-    spun = hasattr(torch.cuda, "_sleep")
-    if spun:
-        torch.cuda._sleep(2_000_000)
+    # warm-up: exactly `warmup` eager calls, right before the timed replays
+    # (capture and upload leave the device idle for milliseconds; run before
+    # them, the warm-up left the first timed calls on idle clocks)
+    for c in range(warmup):
+        layers[c % L].forward(xs[c % L], out=ys[c % L])
+    torch.cuda.synchronize()
     w0 = time.perf_counter()
     for r in range(nrep):
         evs[r][0].record()
@@ -918,7 +927,8 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
     config = {"workload": cfg["workload"], "hidden": H, "experts": cfg["E"], "top_k": k,
               "intermediate": I, "tokens_per_step": T, "bits": [cfg["bits_gu"], cfg["bits_d"]],
               "group_size": 64, "resident_layers": L, "timed_layers": len(timed_layers),
-              "min_reuse_distance_calls": min_reuse, "parallelism": "single-gpu",
+              "min_reuse_distance_calls": min_reuse, "setup_calls": L,
+              "parallelism": "single-gpu",
               "paths": paths}
     if cfg["SI"]:
         config["shared_intermediate"] = cfg["SI"]
@@ -932,9 +942,10 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
         "timing": {"repeats": nrep, "calls_per_repeat": sizes,
                    "ms_per_step_each": [round(v, 6) for v in each],
                    "ms_per_step_all": round(span, 6), "graphs_uploaded": uploaded,
-                   "enqueued_ahead": spun,
-                   "method": "one HIP-graph replay per repeat (each its own stretch of the "
-                             "layer rotation), events on the launch stream, median"},
+                   "warmup_after_capture": True,
+                   "method": "graphs captured and uploaded, then the warm-up calls, then one "
+                             "HIP-graph replay per repeat (each its own stretch of the layer "
+                             "rotation), events on the launch stream, median"},
         "config": config,
         "roofline": roof,
         "layer_roofline": layer_roof,
