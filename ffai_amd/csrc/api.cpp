@@ -1269,17 +1269,37 @@ int pick_lg_dec1(int CU, int gsh) {
   return best < 0 ? 6 : best;
 }
 
-Dec1Geom dec1_geom(int N, int K, int gsh, int k, bool down) {
+Dec1Geom dec1_geom(int N, int K, int gsh, int k, bool down, int T = 1) {
   Dec1Geom g{};
   g.lg = pick_lg_dec1(K / 32, gsh);
   const int SG = 64 >> g.lg;
   const int rows_per_wave = down ? SG : 4 * SG;  // rows one rm step covers per block
-  const double waves1 = (double)k * N / SG;
+  const double waves1 = (double)T * k * N / SG;
   g.rm = std::max(1, std::min(kDec1MaxRows, (int)(waves1 / kDec1TargetWaves + 0.5)));
   g.rows_per_block = g.rm * rows_per_wave;
   const int row_blocks = (N + g.rows_per_block - 1) / g.rows_per_block;
   g.grid = down ? row_blocks : k * row_blocks;
   return g;
+}
+
+// Calls of a few tokens take the one-token kernels, each token routed and
+// streamed by its own blocks (grid.y): T tokens read T k expert slices where
+// the dispatch plan and the grouped GEMVs read each used expert once, about
+// E (1 - (1 - k / E)^T) of them under uniform routing. Measured, us per
+// layer step, one-token kernels against plan + grouped GEMVs: Qwen3 T = 2
+// 19.1 / 32.7, 4 29.5 / 42.2, 8 47.8 / 62.8; GPT-OSS 2 35.3 / 50.4, 4 60.5 /
+// 71.9, 8 109.0 / 107.1; mixed-bit 2 36.0 / 46.1, 4 45.6 / 58.4, 8 68.6 /
+// 74.4. The one-token kernels win up to about 1.35 slices per distinct
+// expert (GPT-OSS at 8 tokens: 1.52).
+constexpr int kDec1MaxT = 8;
+constexpr double kDec1MaxSlicesPerExpert = 1.35;
+
+bool dec1_tokens(const moe_layer_desc* d, int T) {
+  if (T == 1) return true;
+  if (T < 1 || T > kDec1MaxT) return false;
+  const double E = d->n_experts, k = d->top_k;
+  const double distinct = E * (1.0 - std::pow(1.0 - k / E, (double)T));
+  return (double)T * k <= kDec1MaxSlicesPerExpert * distinct;
 }
 
 bool dec1_supported(const moe_layer_desc* d) {
@@ -1335,13 +1355,14 @@ Dec1Shared dec1_shared(const moe_layer_desc* d) {
 
 // down projection + weighted combine of one token (down1_kernel), with the
 // shared expert's down rows and gated add when fs.on.
-moe_status run_down1(const moe_layer_desc* d, void* y, const uint32_t* idx, const float* w,
+moe_status run_down1(const moe_layer_desc* d, int T, void* y, const uint32_t* idx, const float* w,
                      const void* act, hipStream_t st, KEvents ev, const void* res = nullptr,
                      const Dec1Shared& fs = Dec1Shared{}, const void* s_act = nullptr,
                      const void* s_logit = nullptr) {
   const int k = d->top_k, H = d->hidden, I = d->intermediate;
-  const Dec1Geom dg = dec1_geom(H, I, group_shift(d->down.group_size), k, true);
+  const Dec1Geom dg = dec1_geom(H, I, group_shift(d->down.group_size), k, true, T);
   Down1Args dn{};
+  dn.T = T;
   if (fs.on) {
     dn.sp = to_proj(d->shared_down);
     dn.s_act = s_act;
@@ -1466,7 +1487,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     x16 = at<void>(ws, w.x16);
   }
 
-  const bool dec1 = (T == 1 && dec1_supported(d));
+  const bool dec1 = (dec1_tokens(d, T) && dec1_supported(d));
   int smode = 0;
   // a shared expert of kSideMinRows or more rows overlaps the routed experts
   // (MoELayer.swift:620-624: it only joins at the combine); a smaller one
@@ -1476,7 +1497,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
   MOE_TRY(side.status());
   // one token: the shared expert inside the two one-token launches when its
   // formats allow (its gate logit from its own launch unless dense)
-  const Dec1Shared fs = dec1 ? dec1_shared(d) : Dec1Shared{};
+  const Dec1Shared fs = (dec1 && T == 1) ? dec1_shared(d) : Dec1Shared{};
   if (fs.on) {
     if (!fs.in_kernel_gate) MOE_TRY(shared_gate_logits(d, x, T, ws, w, st));
   } else if (dec1) {
@@ -1489,16 +1510,19 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     // gate/up rows (the up projection alone for squared-ReLU experts: the
     // kernel reads zeros for the missing gate)
     const moe_qproj& gu = d->activation == MOE_ACT_RELU2 ? d->up : d->gate;
-    const Dec1Geom gg = dec1_geom(I, H, group_shift(gu.group_size), k, false);
+    const Dec1Geom gg = dec1_geom(I, H, group_shift(gu.group_size), k, false, T);
     Decode1Args g{};
     g.logits = at<void>(ws, w.logits);
     g.E = E;
     g.k = k;
+    g.T = T;
     g.ro = route_opts(d);
     g.idx = at<uint32_t>(ws, w.idx);
     g.w = at<float>(ws, w.w);
-    g.perm = at<uint32_t>(ws, w.perm);
-    g.offsets = at<uint32_t>(ws, w.offsets);
+    // the plan over several tokens comes from its own launch (below), when a
+    // trace asks for it
+    g.perm = T == 1 ? at<uint32_t>(ws, w.perm) : nullptr;
+    g.offsets = T == 1 ? at<uint32_t>(ws, w.offsets) : nullptr;
     g.x = x;
     g.g = to_proj(d->gate);
     g.u = to_proj(d->up);
@@ -1528,8 +1552,17 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
             "gate/up decode launch");
     // the residual goes into the last store: down1's without a separate
     // shared expert
-    MOE_TRY(run_down1(d, y, g.idx, g.w, g.act, st, kev(1), smode ? nullptr : res, fs,
+    MOE_TRY(run_down1(d, T, y, g.idx, g.w, g.act, st, kev(1), smode ? nullptr : res, fs,
                       at<void>(ws, w.s_act), sgate ? at<void>(ws, w.s_logit) : nullptr));
+    // several tokens: the dispatch plan only for a trace that asks for it
+    // (the kernels above route each token themselves)
+    if (T > 1 && tr && (tr->perm || tr->offsets))
+      MOE_HIP(launch_dispatch_plan(at<uint32_t>(ws, w.idx), T, k, E, at<uint32_t>(ws, w.counts),
+                                   at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.perm),
+                                   at<uint32_t>(ws, w.inv), at<uint32_t>(ws, w.used),
+                                   at<void>(ws, w.plan_scratch), dispatch_scratch_bytes(T, k, E),
+                                   st, nullptr, nullptr),
+              "dispatch plan launch");
     MOE_TRY(side.join());
     if (smode)
       MOE_HIP(launch_add_shared(y, at<void>(ws, w.s_out), at<void>(ws, w.s_logit), smode, T, H, xdt,
@@ -1615,7 +1648,7 @@ moe_layer_paths layer_paths(const moe_layer_desc* d, int T, bool x_aligned) {
   auto gk = [](GemvKind kd) { return (int32_t)(kd == kGemvMma ? MOE_PATH_GEMV_MMA : MOE_PATH_GEMV); };
   const moe_qproj& p0 = gated ? d->gate : d->up;
   const moe_qproj* p1 = gated ? &d->up : nullptr;
-  const bool dec1 = T == 1 && dec1_supported(d);
+  const bool dec1 = dec1_tokens(d, T) && dec1_supported(d);
   if (dec1) {
     p.gate_up = p.down = MOE_PATH_DECODE1;
   } else if (routed_gemm(d, T)) {
@@ -1628,7 +1661,7 @@ moe_layer_paths layer_paths(const moe_layer_desc* d, int T, bool x_aligned) {
   if (d->has_shared) {
     const moe_qproj& s0 = gated ? d->shared_gate : d->shared_up;
     const moe_qproj* s1 = gated ? &d->shared_up : nullptr;
-    if (dec1 && dec1_shared(d).on) {
+    if (dec1 && T == 1 && dec1_shared(d).on) {
       p.shared_gate_up = p.shared_down = MOE_PATH_DECODE1;
     } else if (shared_gemm(d, T)) {
       p.shared_gate_up = p.shared_down = MOE_PATH_GEMM;

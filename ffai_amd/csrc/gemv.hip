@@ -781,6 +781,7 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
   }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar branches below
+  const int t = blockIdx.y;  // the token (a shared expert in the launch: T = 1)
   // blocks from routed_blocks on hold rows of the shared expert (expert 0 of
   // its one-expert projections); the rest a slot of the routed experts
   const bool shb = SH && (int)blockIdx.x >= routed_blocks;
@@ -802,8 +803,8 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
   // the activation row in LDS in pair order with its unit sums, so that the
   // lanes' dot products after the weight stream read their units as they are.
   if (wave != 0)
-    stage_x_pairs<BITS, XT, 2>([&](int) { return reinterpret_cast<const XT*>(a.x); }, 1, K, xl, xsm,
-                               threadIdx.x - 64, blockDim.x - 64);
+    stage_x_pairs<BITS, XT, 2>([&](int) { return reinterpret_cast<const XT*>(a.x) + (size_t)t * K; },
+                               1, K, xl, xsm, threadIdx.x - 64, blockDim.x - 64);
   if (wave == 0 && shb) {
     if (lane == 0) {
       route[0] = 0;
@@ -814,8 +815,8 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
     int sel;
     float wgt = 0.f;
     uint64_t masks[kTopkEPL];
-    wave_topk<XT, EPL>(reinterpret_cast<const XT*>(a.logits), a.E, a.k, a.ro, sc, writer, &sel,
-                       &wgt, masks);
+    wave_topk<XT, EPL>(reinterpret_cast<const XT*>(a.logits) + (size_t)t * a.E, a.E, a.k, a.ro, sc,
+                       writer, &sel, &wgt, masks);
     const int e = __builtin_amdgcn_readfirstlane(selected_nth(masks, slot));
     const uint64_t hit = __ballot(lane < a.k && sel == e);
     if (lane == 0) {
@@ -824,9 +825,9 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
     }
     if (writer) {
       if (lane < a.k) {
-        a.idx[lane] = (uint32_t)sel;
-        a.w[lane] = wgt;
-        a.perm[selected_below(masks, sel)] = (uint32_t)lane;
+        a.idx[t * a.k + lane] = (uint32_t)sel;
+        a.w[t * a.k + lane] = wgt;
+        if (a.perm) a.perm[selected_below(masks, sel)] = (uint32_t)lane;
       }
       if (a.offsets)
         for (int ee = lane; ee <= a.E; ee += 64) a.offsets[ee] = (uint32_t)selected_below(masks, ee);
@@ -867,7 +868,8 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
   float xs[UR];
   lds_x_units_pairs<XT, UR>(xl, xsm, 0, li, L, CU, xu, xs);
 
-  XT* act = shb ? reinterpret_cast<XT*>(a.s_act) : reinterpret_cast<XT*>(a.act) + (size_t)rank * N;
+  XT* act = shb ? reinterpret_cast<XT*>(a.s_act)
+                : reinterpret_cast<XT*>(a.act) + ((size_t)t * a.k + rank) * N;
 #pragma unroll
   for (int it = 0; it < RM; it++) {
     float g = group_sum(dot_units<BITS, XT, ST, UR>(gw[it], xu, xs, li, L, CU), a.lg);
@@ -908,13 +910,14 @@ __global__ __launch_bounds__(SH ? 64 * kDec1MaxWaves : 64 * kDec1MaxK) void down
   const int r_begin = blockIdx.x * rpb;
   const bool shw = SH && q >= a.k;  // a shared-expert wave
   const int j = q - a.k;            // its column slice
+  const int t = blockIdx.y;         // the token (a shared expert in the launch: T = 1)
   const XT* ob = reinterpret_cast<const XT*>(a.p.ob);
 
   // The activation units go out first: they need no routing, and their
   // conversion to pair order then runs while the weights stream instead of
   // after them (loads complete in issue order).
   const XT* act = shw ? reinterpret_cast<const XT*>(a.s_act) + (size_t)j * K
-                      : reinterpret_cast<const XT*>(a.act) + (size_t)q * K;
+                      : reinterpret_cast<const XT*>(a.act) + ((size_t)t * a.k + q) * K;
   u32x4_t xraw[UR][4];
   {
     const rsrc_t xr = make_rsrc(act, (uint32_t)(K * sizeof(XT)));
@@ -939,8 +942,8 @@ __global__ __launch_bounds__(SH ? 64 * kDec1MaxWaves : 64 * kDec1MaxK) void down
 #pragma unroll
     for (int it = 0; it < RM; it++) obv[it] = 0.f;
   } else {
-    e = __builtin_amdgcn_readfirstlane(a.idx[q]);
-    if (lane == 0) wr[q] = round_to<XT>(a.w[q]);
+    e = __builtin_amdgcn_readfirstlane(a.idx[t * a.k + q]);
+    if (lane == 0) wr[q] = round_to<XT>(a.w[t * a.k + q]);
 #pragma unroll
     for (int it = 0; it < RM; it++)
       obv[it] = ob ? to_f<XT>(ob[(size_t)e * N + min(r_begin + sg + it * SG, N - 1)]) : 0.f;
@@ -981,7 +984,8 @@ __global__ __launch_bounds__(SH ? 64 * kDec1MaxWaves : 64 * kDec1MaxK) void down
     if (li == L - 1) ys[q * rpb + sg + it * SG] = y;
   }
   __syncthreads();
-  XT* out = reinterpret_cast<XT*>(a.out);
+  XT* out = reinterpret_cast<XT*>(a.out) + (size_t)t * N;
+  const XT* res = a.res ? reinterpret_cast<const XT*>(a.res) + (size_t)t * N : nullptr;
   const XT* sob = reinterpret_cast<const XT*>(a.sp.ob);
   const float gate = (SH && a.s_logit)
                          ? 1.0f / (1.0f + __expf(-to_f<XT>(reinterpret_cast<const XT*>(a.s_logit)[0])))
@@ -997,10 +1001,10 @@ __global__ __launch_bounds__(SH ? 64 * kDec1MaxWaves : 64 * kDec1MaxK) void down
       sv = round_to<XT>(sv);
       if (sob) sv = round_to<XT>(sv + to_f<XT>(sob[row]));
       acc = round_to<XT>(acc);
-      if (a.res) acc = to_f<XT>(reinterpret_cast<const XT*>(a.res)[row]) + acc;
+      if (res) acc = to_f<XT>(res[row]) + acc;
       acc = acc + gate * sv;
     } else {
-      if (a.res) acc = to_f<XT>(reinterpret_cast<const XT*>(a.res)[row]) + round_to<XT>(acc);
+      if (res) acc = to_f<XT>(res[row]) + round_to<XT>(acc);
     }
     out[row] = from_f<XT>(acc);
   }
@@ -1010,13 +1014,13 @@ template <int BITS, typename XT, typename ST, int UR, int RM, bool SH>
 static hipError_t launch_gateup1_e(int E, const Decode1Args& a, int grid, hipStream_t st,
                                    KEvents ev) {
   if (E <= 64)
-    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, 1, SH>), dim3(grid), dim3(256), 0,
+    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, 1, SH>), dim3(grid, a.T), dim3(256), 0,
                           st, ev.start, ev.stop, 0, a);
   else if (E <= 128)
-    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, 2, SH>), dim3(grid), dim3(256), 0,
+    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, 2, SH>), dim3(grid, a.T), dim3(256), 0,
                           st, ev.start, ev.stop, 0, a);
   else
-    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, kTopkEPL, SH>), dim3(grid),
+    hipExtLaunchKernelGGL((gateup1_kernel<BITS, XT, ST, UR, RM, kTopkEPL, SH>), dim3(grid, a.T),
                           dim3(256), 0, st, ev.start, ev.stop, 0, a);
   return hipGetLastError();
 }
@@ -1041,10 +1045,10 @@ static hipError_t launch_dec1_u(bool down, int var, const void* args, int grid, 
   const dim3 block(64 * (a.k + a.m));
 #define MOE_DN(RM)                                                                           \
   if (sh)                                                                                    \
-    hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, RM, true>), dim3(grid), block, 0,  \
+    hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, RM, true>), dim3(grid, a.T), block, 0, \
                           st, ev.start, ev.stop, 0, a);                                      \
   else                                                                                       \
-    hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, RM, false>), dim3(grid), block, 0, \
+    hipExtLaunchKernelGGL((down1_kernel<BITS, XT, ST, UR, RM, false>), dim3(grid, a.T), block, 0, \
                           st, ev.start, ev.stop, 0, a);
   switch (var) {
     case 1: MOE_DN(1) break;

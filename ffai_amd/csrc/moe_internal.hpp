@@ -71,21 +71,24 @@ struct GemvArgs {
 // Decode of one token (T = 1). gate/up kernel: every wave selects the top-k
 // from the router logits itself; block 0 publishes the routing. down kernel:
 // fused weighted combine over the k experts.
+// The one-token kernels over T tokens (grid.y = T): block row t routes and
+// computes token t on its own (its slots' weights are read once per token,
+// so a few tokens at most).
 struct Decode1Args {
-  const void* logits;        // [E] activation dtype
-  int E, k;
+  const void* logits;        // [T, E] activation dtype
+  int E, k, T;
   RouteOpts ro;
-  uint32_t* idx;             // [k] out: experts in rank order
-  float* w;                  // [k] out: combine weights
-  uint32_t* perm;            // [k] out: sorted position -> rank
-  uint32_t* offsets;         // nullable [E+1] out: CSR offsets of the plan
-  const void* x;             // [K]
+  uint32_t* idx;             // [T, k] out: experts in rank order
+  float* w;                  // [T, k] out: combine weights
+  uint32_t* perm;            // nullable [k] out (T = 1): sorted position -> rank
+  uint32_t* offsets;         // nullable [E+1] out (T = 1): CSR offsets of the plan
+  const void* x;             // [T, K]
   GemvProj g, u;             // gate / up
-  void* act;                 // [k, N] in rank order
+  void* act;                 // [T, k, N] in rank order
   int N, K, gsh, row_blocks, rows_per_block, lg;
   int act_kind;
   float alpha, limit;
-  // A shared expert in the same launch (s_blocks > 0): blocks k * row_blocks
+  // A shared expert in the same launch (s_blocks > 0, T = 1 only): blocks k * row_blocks
   // onwards compute its SN gate/up rows (one-expert projections sg / su,
   // same bits, group size and scale dtype as g / u) into s_act; with sgw (a
   // dense gate row [K] in the activation dtype) one more block computes the
@@ -98,14 +101,14 @@ struct Decode1Args {
 };
 
 struct Down1Args {
-  const uint32_t* idx;       // [k] experts in rank order
-  const float* w;            // [k] combine weights in rank order
-  const void* act;           // [k, K] in rank order
+  const uint32_t* idx;       // [T, k] experts in rank order
+  const float* w;            // [T, k] combine weights in rank order
+  const void* act;           // [T, k, K] in rank order
   GemvProj p;
-  void* out;                 // [N]
-  const void* res;           // nullable [N]: residual added before the final rounding
-  int k, N, K, gsh, rows_per_block, lg;
-  // A shared expert as m more waves (m > 0): wave k + j reads columns
+  void* out;                 // [T, N]
+  const void* res;           // nullable [T, N]: residual added before the final rounding
+  int k, N, K, gsh, rows_per_block, lg, T;
+  // A shared expert as m more waves (m > 0, T = 1 only): wave k + j reads columns
   // [j K, (j + 1) K) of the rows of sp (one expert, m K columns, same bits,
   // group size and scale dtype as p) against s_act[j K, ...); the waves'
   // sum is rounded (then its output bias added and rounded) and added to

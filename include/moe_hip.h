@@ -347,9 +347,13 @@ moe_status moe_layer_forward_residual(const moe_layer_desc* d, const void* h,
  * to know which kernel a configuration exercises. 0 = stage absent. */
 typedef enum moe_path {
     MOE_PATH_NONE = 0,
-    MOE_PATH_DECODE1 = 1,   /* one token: gate/up with in-kernel routing,
-                               fused down + combine (for the shared stages:
-                               the shared expert runs inside those two
+    MOE_PATH_DECODE1 = 1,   /* one token, or a few (up to 8, while the
+                               T * top_k expert slices stay within 1.35 per
+                               distinct expert expected under uniform
+                               routing): gate/up with in-kernel routing per
+                               token, fused down + combine, no dispatch plan
+                               (for the shared stages, one token only: the
+                               shared expert runs inside those two
                                launches) */
     MOE_PATH_GEMV = 2,      /* HBM-streaming grouped GEMV (VALU dot2) */
     MOE_PATH_GEMV_MMA = 3,  /* batched grouped GEMV on the matrix cores */

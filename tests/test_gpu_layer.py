@@ -641,6 +641,35 @@ def test_one_token_shared_expert(kind, fused):
     run_layer(spec, 1, seed=3)
 
 
+@pytest.mark.parametrize("cfg,T,dec1", [("qwen3", 2, True), ("qwen3", 8, True), ("gptoss", 5, True),
+                                        ("gptoss", 6, False), ("mixed", 3, True),
+                                        ("nemotron", 4, True)])
+def test_few_token_decode(cfg, T, dec1):
+    """Calls of a few tokens run the one-token kernels with one block row per
+    token (each block routes its token itself; a shared expert and the
+    trace's dispatch plan take their own launches) while the T k expert
+    slices they stream stay within 1.35 per distinct expert expected under
+    uniform routing: Qwen3 (128 experts, top-8) up to 8 tokens, GPT-OSS (32,
+    top-4) up to 5 (6 tokens: 24 slices over 19.7 expected experts), the
+    mixed-bit and NemotronH shapes. Both paths match the oracle, residual
+    included."""
+    spec = {"qwen3": lambda: cfg_qwen3(),
+            "gptoss": lambda: cfg_gptoss(),
+            "mixed": lambda: cfg_mixed(n_experts=64),
+            "nemotron": lambda: cfg_nemotron()}[cfg]()
+    p = _lib.LayerPaths()
+    check(_lib.load().moe_layer_path(C.byref(spec.device().desc), T, C.byref(p)))
+    names = p.names()
+    if dec1:
+        assert names["gate_up"] == names["down"] == "decode1", names
+    else:
+        assert names["gate_up"] != "decode1" and names["down"] != "decode1", names
+    if spec.shared is not None:
+        assert names["shared_gate_up"] != "decode1", names
+    run_layer(spec, T, seed=T)
+    run_layer_residual(spec, T, seed=T + 1)
+
+
 BITS_CASES = [(2, 8, 64, F16, BF16), (5, 2, 32, BF16, F16), (8, 5, 128, F16, F16),
               (6, 3, 64, BF16, BF16), (3, 4, 128, BF16, BF16), (8, 8, 64, BF16, BF16)]
 
