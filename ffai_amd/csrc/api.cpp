@@ -1578,8 +1578,10 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
                             H,    false,         at<uint32_t>(ws, w.items_dn)};
     bool items_done = false;
     // 2. selection + dispatch plan (MoELayer.swift:706-792): one launch for a
-    //    small batch, else the top-k and plan kernels
-    if (launch_route_plan(at<void>(ws, w.logits), xdt, T, E, k, route_opts(d),
+    //    small batch, else the top-k and plan kernels (past 8 tokens the GEMM
+    //    path keeps the plan kernel, whose last launch writes the work lists)
+    if ((T > 8 && gemm) ||
+        launch_route_plan(at<void>(ws, w.logits), xdt, T, E, k, route_opts(d),
                           at<uint32_t>(ws, w.idx), at<float>(ws, w.w), at<uint32_t>(ws, w.counts),
                           at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.perm),
                           at<uint32_t>(ws, w.inv), at<uint32_t>(ws, w.used), st) != hipSuccess) {

@@ -24,11 +24,12 @@ constexpr int kPlanMaxE = 1024;
 constexpr int kChunk = 1024;             // entries per chunk in the multi-block plan
 constexpr int kSingleBlockMax = 4096;    // M at or below which one workgroup plans
 
-// Exclusive scan of cnt[0..E) over 256 threads (4 experts per thread).
+// Exclusive scan of cnt[0..E) over NT threads (4 experts per thread).
 // Writes offsets[0..E], counts, the used list, and base[e] = offsets[e].
+template <int NT = kPlanThreads>
 __device__ void scan_experts(const uint32_t* cnt, int E, uint32_t* counts, uint32_t* offsets,
                              uint32_t* used, uint32_t* base) {
-  __shared__ uint32_t wsum[kPlanThreads / 64], wused[kPlanThreads / 64];
+  __shared__ uint32_t wsum[NT / 64], wused[NT / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint32_t c[4], f[4], tot = 0, ftot = 0;
 #pragma unroll
@@ -71,7 +72,7 @@ __device__ void scan_experts(const uint32_t* cnt, int E, uint32_t* counts, uint3
     run += c[j];
     frun += f[j];
   }
-  if (tid == kPlanThreads - 1) {
+  if (tid == NT - 1) {
     offsets[E] = run;
     used[0] = frun;
   }
@@ -97,18 +98,21 @@ __device__ __forceinline__ void wave_peers(uint32_t e, bool valid, int nbits, ui
 
 // Ranks the entries [begin, end) in order and scatters them starting from
 // cursor[e]; cursor ends advanced by the number of entries of each expert.
+// NT threads; the waves take turns at the cursors, only those with entries.
+template <int NT = kPlanThreads>
 __device__ void stable_scatter(const uint32_t* __restrict__ idx, int begin, int end, int E,
                                int nbits, uint32_t* cursor, uint32_t* __restrict__ perm,
                                uint32_t* __restrict__ inv) {
   const int tid = threadIdx.x, wave = tid >> 6;
-  for (int base = begin; base < end; base += kPlanThreads) {
+  for (int base = begin; base < end; base += NT) {
     const int m = base + tid;
     uint32_t e = m < end ? idx[m] : 0xffffffffu;
     const bool valid = m < end && e < (uint32_t)E;
     uint32_t rank, count;
     bool last;
     wave_peers(e, valid, nbits, &rank, &count, &last);
-    for (int w = 0; w < kPlanThreads / 64; w++) {
+    const int nw = min(NT, end - base + 63) / 64;  // block-uniform
+    for (int w = 0; w < nw; w++) {
       if (wave == w && valid) {
         const uint32_t pos = cursor[e] + rank;
         perm[pos] = (uint32_t)m;
@@ -142,26 +146,29 @@ __global__ __launch_bounds__(kPlanThreads) void plan_single_kernel(
   stable_scatter(idx, 0, M, E, id_bits(E), cursor, perm, inv);
 }
 
-// Routing and dispatch plan of a small batch in one launch: the four waves
-// route tokens t = wave, wave + 4, ... exactly as router_topk_kernel does
-// (wave_topk, same results bit for bit), then the block plans the T * k
-// entries as plan_single_kernel does, reading the ids from LDS. At most two
-// tokens per wave: at 16 tokens (four per wave) the routing chain outlasts
-// the launch it saves (Qwen3 shape: 90.7 -> 96.5 us per layer step).
-constexpr int kRoutePlanMaxT = 8;
+// Routing and dispatch plan of a small batch in one launch: the NT / 64
+// waves route tokens t = wave, wave + NT / 64, ... exactly as
+// router_topk_kernel does (wave_topk, same results bit for bit), then the
+// block plans the T * k entries as plan_single_kernel does, reading the ids
+// from LDS. One wave per token past four tokens: the routing chain of a
+// wave outlasts the launch it saves once a wave routes two tokens or more of
+// a larger batch (Qwen3 shape, per layer step: 16 tokens on 4 waves 96.5 us
+// against 90.7 us for the top-k and plan launches; 64 tokens on 16 waves
+// 142.9 us against 133.6 us; 16 tokens on 16 waves 83.6 us against 84.4 us).
+constexpr int kRoutePlanMaxT = 16;
 constexpr int kRoutePlanMaxM = 1024;
 
-template <typename XT, int EPL>
-__global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(
+template <typename XT, int EPL, int NT>
+__global__ __launch_bounds__(NT) void route_plan_kernel(
     const XT* __restrict__ logits, int T, int E, int k, const RouteOpts ro, uint32_t* idx, float* w,
     uint32_t* counts, uint32_t* offsets, uint32_t* perm, uint32_t* inv, uint32_t* used) {
-  __shared__ float sc[kPlanThreads / 64][kTopkMaxE];
+  __shared__ float sc[NT / 64][kTopkMaxE];
   __shared__ uint32_t sidx[kRoutePlanMaxM];
   __shared__ uint32_t cnt[kPlanMaxE], cursor[kPlanMaxE];
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
   const int M = T * k;
-  for (int e = tid; e < E; e += kPlanThreads) cnt[e] = 0;
-  for (int t = wv; t < T; t += kPlanThreads / 64) {  // wave-uniform
+  for (int e = tid; e < E; e += NT) cnt[e] = 0;
+  for (int t = wv; t < T; t += NT / 64) {  // wave-uniform
     int sel;
     float wt;
     wave_topk<XT, EPL>(logits + (size_t)t * E, E, k, ro, sc[wv], true, &sel, &wt);
@@ -172,13 +179,13 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(
     }
   }
   __syncthreads();
-  for (int m = tid; m < M; m += kPlanThreads) {
+  for (int m = tid; m < M; m += NT) {
     const uint32_t e = sidx[m];
     if (e < (uint32_t)E) atomicAdd(&cnt[e], 1u);
   }
   __syncthreads();
-  scan_experts(cnt, E, counts, offsets, used, cursor);
-  stable_scatter(sidx, 0, M, E, id_bits(E), cursor, perm, inv);
+  scan_experts<NT>(cnt, E, counts, offsets, used, cursor);
+  stable_scatter<NT>(sidx, 0, M, E, id_bits(E), cursor, perm, inv);
 }
 
 hipError_t launch_route_plan(const void* logits, int dt, int T, int E, int k, const RouteOpts& ro,
@@ -186,9 +193,17 @@ hipError_t launch_route_plan(const void* logits, int dt, int T, int E, int k, co
                              uint32_t* perm, uint32_t* inv, uint32_t* used, hipStream_t st) {
   if (T > kRoutePlanMaxT || T * k > kRoutePlanMaxM || E > kTopkMaxE || k > 64)
     return hipErrorInvalidValue;
-#define MOE_RP(XT, EPL)                                                                         \
-  hipLaunchKernelGGL((route_plan_kernel<XT, EPL>), dim3(1), dim3(kPlanThreads), 0, st,          \
-                     (const XT*)logits, T, E, k, ro, idx, w, counts, offsets, perm, inv, used); \
+#define MOE_RP(XT, EPL)                                                                          \
+  if (T <= 4)                                                                                    \
+    hipLaunchKernelGGL((route_plan_kernel<XT, EPL, kPlanThreads>), dim3(1), dim3(kPlanThreads),  \
+                       0, st, (const XT*)logits, T, E, k, ro, idx, w, counts, offsets, perm, inv, \
+                       used);                                                                    \
+  else if (T <= 8)                                                                               \
+    hipLaunchKernelGGL((route_plan_kernel<XT, EPL, 512>), dim3(1), dim3(512), 0, st,             \
+                       (const XT*)logits, T, E, k, ro, idx, w, counts, offsets, perm, inv, used); \
+  else                                                                                           \
+    hipLaunchKernelGGL((route_plan_kernel<XT, EPL, 1024>), dim3(1), dim3(1024), 0, st,           \
+                       (const XT*)logits, T, E, k, ro, idx, w, counts, offsets, perm, inv, used); \
   return hipGetLastError();
 #define MOE_RP_E(XT)                  \
   if (E <= 64) { MOE_RP(XT, 1) }      \
