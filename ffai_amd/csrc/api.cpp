@@ -873,7 +873,9 @@ extern "C" moe_status moe_router_topk_scaled(const void* logits, int32_t dtype, 
   if (k > 64) return fail(MOE_ERR_UNSUPPORTED, "router_topk: k=%d above 64", k);
   const RouteOpts ro = route_opts(gating, norm_topk_prob, expert_bias, logit_scale, routed_scale,
                                   expert_scale);
-  MOE_HIP(launch_router_topk(logits, dtype, T, n_experts, k, ro, topk_idx, topk_weight, stream),
+  // no partials: the logits are only read
+  MOE_HIP(launch_router_topk(const_cast<void*>(logits), dtype, T, n_experts, k, ro, topk_idx,
+                             topk_weight, stream),
           "router top-k launch");
   return ok();
 }
@@ -1459,6 +1461,7 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
   const bool gemm = !(T == 1 && dec1_supported(d)) && routed_gemm(d, T);
   const bool want_x16 = (gemm || shared_gemm(d, T)) && xdt == MOE_BF16;
   bool x16_done = false, sgate_done = false;
+  int rsplits = 1;  // > 1: the router left partial sums for the top-k launch
 
   // 1. router projection (MoELayer.swift:540 / 689-690)
   if (logits_done) {
@@ -1472,11 +1475,15 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     // a dense shared gate of the router's type, applied to the same rows, is
     // computed by the router launch when that runs on the matrix cores
     const bool gate2 = d->has_shared && d->shared_gate_weight && !d->shared_gate_q.weight && rx == x;
+    // a split-K router writes fp32 partials into the down projection's
+    // output rows (Y, unused until the down projection), which the top-k
+    // launch below reduces
     MOE_HIP(launch_router_logits(rx, xdt, T, H, d->router_weight, d->router_dtype, d->router_bias,
                                  E, at<void>(ws, w.logits), st,
                                  want_x16 && rx == x ? at<void>(ws, w.x16) : nullptr, &x16_done,
                                  gate2 ? d->shared_gate_weight : nullptr, 1,
-                                 gate2 ? at<void>(ws, w.s_logit) : nullptr, &sgate_done),
+                                 gate2 ? at<void>(ws, w.s_logit) : nullptr, &sgate_done,
+                                 at<float>(ws, w.Y), (size_t)T * k * H * dt_size(xdt), &rsplits),
             "router logits launch");
   }
 
@@ -1580,14 +1587,16 @@ moe_status layer_forward(const moe_layer_desc* d, const void* x, const void* rx,
     // 2. selection + dispatch plan (MoELayer.swift:706-792): one launch for a
     //    small batch, else the top-k and plan kernels (past 8 tokens the GEMM
     //    path keeps the plan kernel, whose last launch writes the work lists)
-    if ((T > 8 && gemm) ||
+    if ((T > 8 && gemm) || rsplits > 1 ||
         launch_route_plan(at<void>(ws, w.logits), xdt, T, E, k, route_opts(d),
                           at<uint32_t>(ws, w.idx), at<float>(ws, w.w), at<uint32_t>(ws, w.counts),
                           at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.perm),
                           at<uint32_t>(ws, w.inv), at<uint32_t>(ws, w.used), st) != hipSuccess) {
       (void)hipGetLastError();  // a refused fused launch leaves no error behind
       MOE_HIP(launch_router_topk(at<void>(ws, w.logits), xdt, T, E, k, route_opts(d),
-                                 at<uint32_t>(ws, w.idx), at<float>(ws, w.w), st),
+                                 at<uint32_t>(ws, w.idx), at<float>(ws, w.w), st,
+                                 at<float>(ws, w.Y), rsplits, d->router_bias,
+                                 sgate_done ? at<void>(ws, w.s_logit) : nullptr, 1),
               "router top-k launch");
       MOE_HIP(launch_dispatch_plan(at<uint32_t>(ws, w.idx), T, k, E, at<uint32_t>(ws, w.counts),
                                    at<uint32_t>(ws, w.offsets), at<uint32_t>(ws, w.perm),

@@ -153,13 +153,20 @@ size_t gemv_smem_bytes(int xdt, int K, int tok_chunk);
 // second projection of the same rows with weights of W's type and no bias
 // (a shared expert's gate), which that kernel computes in the same launch;
 // *second_done tells whether it did (else the caller launches it).
+// part / part_bytes / splits: fp32 scratch that a batch of few token tiles on
+// the matrix cores may split K over; *splits > 1 then means that neither
+// logits nor logits2 is written yet: launch_router_topk with the same part,
+// splits, bias and logits2 adds the partials, rounds and writes both.
 hipError_t launch_router_logits(const void* x, int xdt, int T, int H, const void* W, int wdt,
                                 const void* bias, int E, void* logits, hipStream_t st,
                                 void* x16 = nullptr, bool* x16_done = nullptr,
                                 const void* W2 = nullptr, int E2 = 0, void* logits2 = nullptr,
-                                bool* second_done = nullptr);
-hipError_t launch_router_topk(const void* logits, int dt, int T, int E, int k,
-                              const RouteOpts& ro, uint32_t* idx, float* w, hipStream_t st);
+                                bool* second_done = nullptr, float* part = nullptr,
+                                size_t part_bytes = 0, int* splits = nullptr);
+hipError_t launch_router_topk(void* logits, int dt, int T, int E, int k, const RouteOpts& ro,
+                              uint32_t* idx, float* w, hipStream_t st, const float* part = nullptr,
+                              int KS = 1, const void* bias = nullptr, void* logits2 = nullptr,
+                              int E2 = 0);
 // One token: res = round(h + m), xn = round(rmsnorm(res) * nw), then the
 // router logits of xn, in one launch. 16-bit x and W of one type, H <= 8192;
 // hipErrorInvalidValue otherwise (launch_add_rmsnorm + launch_router_logits).

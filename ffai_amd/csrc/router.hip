@@ -7,6 +7,8 @@
 // 140-205) and to GPT-OSS's biased router (Models/Text/GPTOSSText.swift:
 // 345-366,1349-1361). Selection order is (value desc, index asc): the
 // reference heap's tie rule (MoELayer.swift:223-296).
+#include <algorithm>
+
 #include "moe_common.hpp"
 #include "moe_internal.hpp"
 
@@ -238,6 +240,13 @@ __global__ __launch_bounds__(256) void router_logits_row_kernel(const XT* __rest
 // rounds (product, then + bias). Needs H % 64 == 0 and T * H, E * H below
 // 2^31 elements (32-bit byte offsets); the last expert tile repeats expert
 // E - 1 past E and stores nothing there.
+// Split K (KS > 1, `psum` non-null): the grid holds KS copies of the tiles,
+// copy s over chunks [s * cps, (s + 1) * cps) of the hidden dimension, and
+// each writes its unrounded fp32 tile to psum[s][T][E] (the second
+// projection's after them, psum[KS * T * E + (s * T + t) * E2 + e]);
+// router_topk_kernel adds the KS partials in split order, rounds and routes.
+// A batch of 32-255 tokens has only 1-8 token tiles, too few blocks to hide
+// the chunk loop's latency.
 //
 // Both tiles pass through LDS in chunks of 256 values: a wave's load
 // instruction covers two rows x 512 contiguous bytes (whole cache lines),
@@ -279,7 +288,8 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
                                                                     int H, int E,
                                                                     uint4* __restrict__ x16,
                                                                     const XT* __restrict__ W2,
-                                                                    XT* __restrict__ logits2, int E2) {
+                                                                    XT* __restrict__ logits2, int E2,
+                                                                    float* __restrict__ psum, int KS) {
   // token tile and expert tile of one chunk; the partial tiles of the
   // epilogue (rows padded to 33 floats) reuse the same bytes
   __shared__ u32x4_t stage[2][32 * kRgPieces];
@@ -292,7 +302,8 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
   // of the same rows (W2: E2 rows, no bias, into logits2), such as a shared
   // expert's gate, so that it costs no launch of its own.
   const int nE1 = (E + 31) >> 5, nE = nE1 + ((E2 + 31) >> 5);
-  const int b = (int)blockIdx.x, win = b / (8 * nE), slot = b - win * 8 * nE;
+  const int nB = (int)gridDim.x / KS, ks = (int)blockIdx.x / nB;  // K split of this block
+  const int b = (int)blockIdx.x - ks * nB, win = b / (8 * nE), slot = b - win * 8 * nE;
   const int tt = win * 8 + (slot & 7), et = slot >> 3;
   if (tt * 32 >= T) return;  // padding of the last window; uniform over the block
   const bool second = et >= nE1;
@@ -305,6 +316,7 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, h = lane >> 5;
   const int G = H >> 6, nC = (H + kRgChunk - 1) / kRgChunk;
+  const int cps = (nC + KS - 1) / KS, c0 = ks * cps, c1 = min(nC, c0 + cps);  // this split's chunks
   const rsrc_t xr = make_rsrc(x, (uint32_t)((size_t)T * H * sizeof(XT)));
   const rsrc_t wr = make_rsrc(Wt, (uint32_t)((size_t)Et * H * sizeof(XT)));
   // thread piece j: row (j * 64 * kRgWaves + tid) / kRgPieces of the tile,
@@ -326,7 +338,7 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
     u32x4_t a[kRgLoads], b[kRgLoads];
   };
   auto load = [&](int c, Tile& s) __attribute__((always_inline)) {
-    const uint32_t kb = (uint32_t)min(c, nC - 1) * (uint32_t)(kRgChunk * 2);
+    const uint32_t kb = (uint32_t)min(c, c1 - 1) * (uint32_t)(kRgChunk * 2);
 #pragma unroll
     for (int j = 0; j < kRgLoads; j++) {
       s.a[j] = bload128(xr, xo[j] + kb);
@@ -351,7 +363,7 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
 #pragma unroll
     for (int j = 0; j < kRgLoads; j++) {
       const int k8 = c * kRgPieces + ppc[j];  // piece of the whole row
-      const bool mine = prow[j] >= cv0 && prow[j] < cv1 && 8 * k8 < H;
+      const bool mine = prow[j] >= cv0 && prow[j] < cv1 && 8 * k8 < H && c < c1;
       const uint32_t off = mine ? ((uint32_t)(t0 + prow[j]) * (uint32_t)(H / 8) + (uint32_t)k8) * 16u : x16_bytes;
       const uint4 v = bf16x8_to_a16<kA16Shift>(make_uint4(s.a[j].x, s.a[j].y, s.a[j].z, s.a[j].w));
       bstore128(cr, off, u32x4_t{v.x, v.y, v.z, v.w});
@@ -359,7 +371,7 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
   };
   f32x16_t acc = {};
   auto mma = [&](int c) __attribute__((always_inline)) {
-    if (4 * c + wv < G) {  // wave-uniform: the wave's group of chunk c
+    if (c < c1 && 4 * c + wv < G) {  // wave-uniform: the wave's group of chunk c
       u32x4_t fa[4], fb[4];
 #pragma unroll
       for (int q = 0; q < 4; q++) {
@@ -375,15 +387,16 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
   // (the scheduling barrier keeps chunk 0's loads ahead of chunk 1's, so the
   // first stores to LDS wait for chunk 0 only)
   Tile s0, s1;
-  load(0, s0);
+  load(c0, s0);
   __builtin_amdgcn_sched_barrier(0);
-  load(1, s1);
+  load(c0 + 1, s1);
   __builtin_amdgcn_sched_barrier(0);
   // Chunk c from s0, chunk c + 1 from s1; each set reloads two chunks on.
-  // With nC odd the last trip's second chunk is past H: its loads repeat the
-  // last chunk, its x16 stores are dropped and no wave has a group in it (no
-  // break in the loop, which would cost the wait counts their exactness).
-  for (int c = 0; c < nC; c += 2) {  // nC is uniform: a scalar loop
+  // With an odd chunk count the last trip's second chunk is past the split:
+  // its loads repeat the last chunk, its x16 stores are dropped and no wave
+  // has a group in it (no break in the loop, which would cost the wait counts
+  // their exactness).
+  for (int c = c0; c < c1; c += 2) {  // c0 and c1 are uniform: a scalar loop
     put(c, s0);
     lds_barrier();
     load(c + 2, s0);
@@ -409,6 +422,11 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
 #pragma unroll
     for (int w = 1; w < kRgWaves; w++) s += part[w * 32 * 33 + r * 33 + c];
     if (t0 + r < T && e0 + c < Et) {
+      if (psum) {  // block-uniform
+        float* pp = second ? psum + (size_t)KS * T * E + (size_t)ks * T * E2 : psum + (size_t)ks * T * E;
+        pp[(size_t)(t0 + r) * Et + e0 + c] = s;
+        continue;
+      }
       float l = round_to<XT>(s);
       if (bt) l = round_to<XT>(l + to_f<XT>(bt[e0 + c]));
       out[(size_t)(t0 + r) * Et + e0 + c] = from_f<XT>(l);
@@ -417,40 +435,107 @@ __global__ __launch_bounds__(64 * kRgWaves) void router_gemm_kernel(const XT* __
 }
 
 // One wave per token row (wave_topk); weights are reproducible bit for bit.
-template <typename XT>
-__global__ __launch_bounds__(256) void router_topk_kernel(const XT* __restrict__ logits, int T,
+// With the partial tiles of a split-K router_gemm_kernel (rp.part), the wave
+// first adds the token's KS partials in split order, rounds as the router
+// kernels round (sum, then + bias), and writes the logits row (and the
+// second projection's row) before routing it from LDS.
+struct RouterPartials {
+  const float* part;  // [KS][T][E], then [KS][T][E2]
+  int KS;
+  const void* bias;   // router bias (XT), nullable
+  void* logits2;      // second projection's logits (XT), when E2 > 0
+  int E2;
+};
+
+// The sum over KS <= MAXKS partials at p[q * stride], in split order: all
+// loads first (splits past KS repeat the last one), then the adds.
+template <int MAXKS>
+__device__ __forceinline__ float split_sum(const float* __restrict__ p, size_t stride, int KS) {
+  float v[MAXKS];
+#pragma unroll
+  for (int q = 0; q < MAXKS; q++) v[q] = p[(size_t)min(q, KS - 1) * stride];
+  float s = v[0];
+#pragma unroll
+  for (int q = 1; q < MAXKS; q++) s = q < KS ? s + v[q] : s;
+  return s;
+}
+
+// MAXKS: 1 without partials, else a bound on rp.KS
+template <typename XT, int MAXKS>
+__global__ __launch_bounds__(256) void router_topk_kernel(XT* __restrict__ logits, int T,
                                                           int E, int k, const RouteOpts ro,
                                                           uint32_t* __restrict__ idx_out,
-                                                          float* __restrict__ w_out) {
+                                                          float* __restrict__ w_out,
+                                                          const RouterPartials rp) {
   __shared__ float sc[4][kTopkMaxE];
+  __shared__ XT lrow[MAXKS > 1 ? 4 : 1][MAXKS > 1 ? kTopkMaxE : 1];
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + wv;
   if (t >= T) return;  // wave-uniform; the kernel has no block barrier
+  const XT* row = logits + (size_t)t * E;
+  if constexpr (MAXKS > 1) {
+    const XT* bias = reinterpret_cast<const XT*>(rp.bias);
+    const size_t stride = (size_t)T * E;
+#pragma unroll
+    for (int j = 0; j < kTopkEPL; j++) {
+      if (64 * j >= E) break;  // wave-uniform
+      const int e = lane + 64 * j, ec = min(e, E - 1);
+      float l = round_to<XT>(split_sum<MAXKS>(rp.part + (size_t)t * E + ec, stride, rp.KS));
+      if (bias) l = round_to<XT>(l + to_f<XT>(bias[ec]));
+      if (e < E) {
+        logits[(size_t)t * E + e] = from_f<XT>(l);
+        lrow[wv][e] = from_f<XT>(l);
+      }
+    }
+    if (lane < rp.E2) {
+      const float* p2 = rp.part + (size_t)rp.KS * stride + (size_t)t * rp.E2 + lane;
+      const float s = split_sum<MAXKS>(p2, (size_t)T * rp.E2, rp.KS);
+      reinterpret_cast<XT*>(rp.logits2)[(size_t)t * rp.E2 + lane] = from_f<XT>(s);
+    }
+    wave_sync();
+    row = lrow[wv];
+  }
   int sel;
   float w;
-  wave_topk<XT>(logits + (size_t)t * E, E, k, ro, sc[wv], true, &sel, &w);
+  wave_topk<XT>(row, E, k, ro, sc[wv], true, &sel, &w);
   if (lane < k) {
     idx_out[(size_t)t * k + lane] = (uint32_t)sel;
     w_out[(size_t)t * k + lane] = w;
   }
 }
 
+// Token x expert tiles below which router_gemm_kernel splits K: splits
+// until about this many blocks run (at most one per 256-value chunk).
+constexpr int kRgSplitBlocks = 256;
+constexpr int kRgMaxSplits = 16;
+
 template <typename XT, typename WT>
 static hipError_t launch_rl(const void* x, int T, int H, const void* W, const void* bias, int E,
                             void* logits, hipStream_t st, void* x16, bool* x16_done,
-                            const void* W2, int E2, void* logits2, bool* second_done) {
+                            const void* W2, int E2, void* logits2, bool* second_done,
+                            float* part, size_t part_bytes, int* splits) {
   if constexpr (__is_same(XT, WT) && !__is_same(XT, float)) {
     if (T >= 32 && H % 64 == 0 && (size_t)T * H < (1ull << 31) && (size_t)E * H < (1ull << 31)) {
       const bool conv = x16 && __is_same(XT, bf16_t);
       const bool two = W2 && logits2 && E2 > 0 && (size_t)E2 * H < (1ull << 31);
       const int windows = (T + 255) / 256;  // eight token tiles each
       const int tiles = (E + 31) / 32 + (two ? (E2 + 31) / 32 : 0);
-      hipLaunchKernelGGL((router_gemm_kernel<XT>), dim3(windows * 8 * tiles), dim3(64 * kRgWaves),
-                         0, st, (const XT*)x, (const XT*)W, (const XT*)bias, (XT*)logits, T, H, E,
-                         conv ? (uint4*)x16 : nullptr, two ? (const XT*)W2 : nullptr,
-                         two ? (XT*)logits2 : nullptr, two ? E2 : 0);
+      const int nC = (H + kRgChunk - 1) / kRgChunk, active = (T + 31) / 32 * tiles;
+      int KS = 1;
+      if (part && splits && active < kRgSplitBlocks) {
+        KS = std::min(std::min(nC, kRgMaxSplits), (kRgSplitBlocks + active - 1) / active);
+        const int cps = (nC + KS - 1) / KS;  // chunks per split
+        KS = (nC + cps - 1) / cps;           // no split without chunks
+        if ((size_t)KS * T * (E + (two ? E2 : 0)) * sizeof(float) > part_bytes) KS = 1;
+      }
+      hipLaunchKernelGGL((router_gemm_kernel<XT>), dim3(KS * windows * 8 * tiles),
+                         dim3(64 * kRgWaves), 0, st, (const XT*)x, (const XT*)W, (const XT*)bias,
+                         (XT*)logits, T, H, E, conv ? (uint4*)x16 : nullptr,
+                         two ? (const XT*)W2 : nullptr, two ? (XT*)logits2 : nullptr,
+                         two ? E2 : 0, KS > 1 ? part : nullptr, KS);
       if (x16_done) *x16_done = conv;
       if (second_done) *second_done = two;
+      if (splits) *splits = KS;
       return hipGetLastError();
     }
     if (T == 1 && H <= 4 * 2048) {
@@ -488,11 +573,13 @@ static hipError_t launch_rl(const void* x, int T, int H, const void* W, const vo
 hipError_t launch_router_logits(const void* x, int xdt, int T, int H, const void* W, int wdt,
                                 const void* bias, int E, void* logits, hipStream_t st, void* x16,
                                 bool* x16_done, const void* W2, int E2, void* logits2,
-                                bool* second_done) {
+                                bool* second_done, float* part, size_t part_bytes, int* splits) {
   if (x16_done) *x16_done = false;
   if (second_done) *second_done = false;
-#define MOE_RL2(XT, WT) \
-  return launch_rl<XT, WT>(x, T, H, W, bias, E, logits, st, x16, x16_done, W2, E2, logits2, second_done);
+  if (splits) *splits = 1;
+#define MOE_RL2(XT, WT)                                                                        \
+  return launch_rl<XT, WT>(x, T, H, W, bias, E, logits, st, x16, x16_done, W2, E2, logits2, \
+                           second_done, part, part_bytes, splits);
   if (xdt == DT_BF16) {
     if (wdt == DT_BF16) { MOE_RL2(bf16_t, bf16_t) }
     if (wdt == DT_F16) { MOE_RL2(bf16_t, f16_t) }
@@ -531,17 +618,29 @@ hipError_t launch_router_logits_norm(const void* h, const void* m, const void* n
 #undef MOE_RLN
 }
 
-hipError_t launch_router_topk(const void* logits, int dt, int T, int E, int k,
-                              const RouteOpts& ro, uint32_t* idx, float* w, hipStream_t st) {
+hipError_t launch_router_topk(void* logits, int dt, int T, int E, int k, const RouteOpts& ro,
+                              uint32_t* idx, float* w, hipStream_t st, const float* part, int KS,
+                              const void* bias, void* logits2, int E2) {
   const int grid = (T + 3) / 4;
-#define MOE_TK(XT)                                                                          \
-  hipLaunchKernelGGL((router_topk_kernel<XT>), dim3(grid), dim3(256), 0, st,               \
-                     (const XT*)logits, T, E, k, ro, idx, w);                              \
+  const RouterPartials rp{KS > 1 ? part : nullptr, KS, bias, logits2, KS > 1 && logits2 ? E2 : 0};
+  if (rp.part && (E > kTopkMaxE || E2 > 64 || KS > kRgMaxSplits || dt == DT_F32))
+    return hipErrorInvalidValue;
+#define MOE_TK2(XT, MK)                                                                     \
+  hipLaunchKernelGGL((router_topk_kernel<XT, MK>), dim3(grid), dim3(256), 0, st,           \
+                     (XT*)logits, T, E, k, ro, idx, w, rp);                                \
   return hipGetLastError();
+#define MOE_TK(XT)                                 \
+  if (!rp.part) { MOE_TK2(XT, 1) }                 \
+  if constexpr (!__is_same(XT, float)) {           \
+    if (KS <= 4) { MOE_TK2(XT, 4) }                \
+    if (KS <= 8) { MOE_TK2(XT, 8) }                \
+    MOE_TK2(XT, kRgMaxSplits)                      \
+  }
   if (dt == DT_BF16) { MOE_TK(bf16_t) }
   if (dt == DT_F16) { MOE_TK(f16_t) }
   if (dt == DT_F32) { MOE_TK(float) }
 #undef MOE_TK
+#undef MOE_TK2
   return hipErrorInvalidValue;
 }
 
