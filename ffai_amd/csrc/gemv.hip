@@ -341,6 +341,9 @@ __global__ __launch_bounds__(256, 2) void gemv_multi_kernel(const GemvArgs a) {
   };
 
   WSet wa, wb;
+  // (reading iteration 0's weights before the rows' range and positions, as
+  // gemv_mma_kernel does, measured slower here: Qwen3 16 tokens gate/up 43.2
+  // -> 51.2 us)
   for (uint32_t pc = pbeg; pc < pend;) {
     const int nt = min((int)(pend - pc), TM);
     // this pass's first activation loads, then iteration 0's weights, then
@@ -457,8 +460,6 @@ void gemv_mma_kernel(const GemvArgs a) {
   const int slot = blockIdx.x / a.row_blocks, rb = blockIdx.x - slot * a.row_blocks;
   if ((uint32_t)slot >= a.used[0]) return;  // block-uniform, before any barrier
   const uint32_t e = __builtin_amdgcn_readfirstlane(a.used[1 + slot]);
-  const uint32_t pbeg = __builtin_amdgcn_readfirstlane(a.offsets[e]);
-  const uint32_t pend = __builtin_amdgcn_readfirstlane(a.offsets[e + 1]);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
@@ -486,7 +487,7 @@ void gemv_mma_kernel(const GemvArgs a) {
   struct Stage {
     uint32_t w[2][BITS];
     u32x4_t x[2];
-    uint32_t sb[2];
+    uint32_t s[2], b[2];  // 16-bit scale and bias, merged only when stored (no early wait)
   };
   auto gw_row = [&](int slr) -> uint32_t {
     const int g = GATEUP ? r_begin + (slr & 31) : r_begin + slr;
@@ -496,7 +497,7 @@ void gemv_mma_kernel(const GemvArgs a) {
   // (2^31 and more: the views of one expert are far smaller), which read zero
   // without touching memory, so the loop below issues the same loads on every
   // trip. (Selecting views of zero bytes instead cost eight VGPRs.)
-  auto load_stage = [&](int c, uint32_t xrow, Stage& st) __attribute__((always_inline)) {
+  auto load_w_stage = [&](int c, Stage& st) __attribute__((always_inline)) {
     const int cc = min(c, nchunks - 1);
     const uint32_t dead = c < nchunks ? 0u : 0x80000000u;  // block-uniform
 #pragma unroll
@@ -507,10 +508,21 @@ void gemv_mma_kernel(const GemvArgs a) {
       const uint32_t u = (uint32_t)min(kMmaU * cc + s_us, CU - 1);
       bload_unit<BITS>(pv.w, (grow * (uint32_t)row_words + u * (uint32_t)BITS) * 4u + dead, st.w[j]);
       const uint32_t gi = (grow * (uint32_t)groups + (u >> a.gsh)) * (uint32_t)sizeof(ST) + dead;
-      st.sb[j] = (uint32_t)bload16(pv.s, gi) | ((uint32_t)bload16(pv.b, gi) << 16);
+      st.s[j] = (uint32_t)bload16(pv.s, gi);
+      st.b[j] = (uint32_t)bload16(pv.b, gi);
+    }
+  };
+  auto load_x_stage = [&](int c, uint32_t xrow, Stage& st) __attribute__((always_inline)) {
+    const int cc = min(c, nchunks - 1);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
       const int ux = min(kMmaU * cc + x_us0 + 4 * j, CU - 1);
       st.x[j] = *reinterpret_cast<const u32x4_t*>(x + (size_t)xrow * K + (size_t)ux * 32 + x_kb * 8);
     }
+  };
+  auto load_stage = [&](int c, uint32_t xrow, Stage& st) __attribute__((always_inline)) {
+    load_w_stage(c, st);
+    load_x_stage(c, xrow, st);
   };
   auto store_stage = [&](const Stage& st, int buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -523,7 +535,7 @@ void gemv_mma_kernel(const GemvArgs a) {
 #pragma unroll
         for (int q = 0; q < BITS; q++) wd[q] = st.w[j][q];
       }
-      sl[buf][slr * kMmaU + s_us] = st.sb[j];
+      sl[buf][slr * kMmaU + s_us] = st.s[j] | (st.b[j] << 16);
       // natural values x0..x7 -> pairs (x0, x4), (x1, x5), (x2, x6), (x3, x7)
       const u32x4_t n = st.x[j];
       const u32x4_t pw = {(n[0] & 0xFFFFu) | (n[2] << 16), (n[0] >> 16) | (n[2] & 0xFFFF0000u),
@@ -559,13 +571,21 @@ void gemv_mma_kernel(const GemvArgs a) {
   };
 
   XT* out = reinterpret_cast<XT*>(a.out);
+  Stage s0, s1;
+  // chunk 0 and 1 weights need only the expert: the first pass's go out
+  // before its rows' range and positions are read (two dependent loads),
+  // each later pass's at the end of the pass before
+  load_w_stage(0, s0);
+  load_w_stage(1, s1);
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t pbeg = __builtin_amdgcn_readfirstlane(a.offsets[e]);
+  const uint32_t pend = __builtin_amdgcn_readfirstlane(a.offsets[e + 1]);
   for (uint32_t pc = pbeg; pc < pend; pc += kMmaTok) {
     const int nt = min((int)(pend - pc), kMmaTok);
     const uint32_t p = pc + (uint32_t)min(x_t, nt - 1);
     const uint32_t xrow = a.perm ? a.perm[p] / (uint32_t)a.topk : p;
-    Stage s0, s1;
-    load_stage(0, xrow, s0);
-    load_stage(1, xrow, s1);
+    load_x_stage(0, xrow, s0);
+    load_x_stage(1, xrow, s1);
     lds_barrier();  // the last pass's LDS reads (and gl) are done; loads stay in flight
     store_stage(s0, 0);
     load_stage(2, xrow, s0);
@@ -623,6 +643,10 @@ void gemv_mma_kernel(const GemvArgs a) {
         const float v = a.act == ACT_RELU2 ? apply_act<XT>(0.f, g, ACT_RELU2, 0.f, 0.f) : g;
         if (t < nt && orow < N) out[(size_t)(pc + t) * N + orow] = from_f<XT>(v);
       }
+    }
+    if (pc + kMmaTok < pend) {  // the next pass's chunk 0 and 1 weights (block-uniform)
+      load_w_stage(0, s0);
+      load_w_stage(1, s1);
     }
   }
 }
