@@ -861,13 +861,20 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
   const int e = __builtin_amdgcn_readfirstlane(route[0]);
   const int rank = __builtin_amdgcn_readfirstlane(route[1]);
 
-  // output biases first: waiting for them never waits for weight loads
-  float obg[RM], obu[RM];
+  // output biases first (a missing one through an empty view, which reads
+  // zero), kept raw until every weight load is out: converting them here
+  // would wait for them, and for every load issued before them, ahead of the
+  // weight stream
+  uint16_t obg_raw[RM], obu_raw[RM];
+  {
+    const rsrc_t gr = make_rsrc(ob_g ? ob_g + (size_t)e * N : nullptr, ob_g ? (uint32_t)(N * sizeof(XT)) : 0u);
+    const rsrc_t ur = make_rsrc(ob_u ? ob_u + (size_t)e * N : nullptr, ob_u ? (uint32_t)(N * sizeof(XT)) : 0u);
 #pragma unroll
-  for (int it = 0; it < RM; it++) {
-    const int row = min(r0 + it * stride, N - 1);
-    obg[it] = ob_g ? to_f<XT>(ob_g[(size_t)e * N + row]) : 0.f;
-    obu[it] = ob_u ? to_f<XT>(ob_u[(size_t)e * N + row]) : 0.f;
+    for (int it = 0; it < RM; it++) {
+      const uint32_t off = (uint32_t)min(r0 + it * stride, N - 1) * (uint32_t)sizeof(XT);
+      obg_raw[it] = bload16(gr, off);
+      obu_raw[it] = bload16(ur, off);
+    }
   }
   // squared-ReLU experts have no gate projection (g.w null): the gate reads
   // go to empty buffer views, which return zeros without touching memory
@@ -902,8 +909,8 @@ __global__ __launch_bounds__(256) void gateup1_kernel(const Decode1Args a) {
     if (li == L - 1 && row < r_end) {
       g = round_to<XT>(g);
       u = round_to<XT>(u);
-      if (ob_g) g = round_to<XT>(g + obg[it]);
-      if (ob_u) u = round_to<XT>(u + obu[it]);
+      if (ob_g) g = round_to<XT>(g + to_f<XT>(__builtin_bit_cast(XT, obg_raw[it])));
+      if (ob_u) u = round_to<XT>(u + to_f<XT>(__builtin_bit_cast(XT, obu_raw[it])));
       act[row] = from_f<XT>(apply_act<XT>(g, u, a.act_kind, a.alpha, a.limit));
     }
   }
@@ -956,7 +963,11 @@ __global__ __launch_bounds__(SH ? 64 * kDec1MaxWaves : 64 * kDec1MaxK) void down
   ProjView P;
   UnitAddr base{0u, 0u};
   int rw = row_words, grp = groups;
-  float obv[RM];
+  // output biases kept raw until the weight loads are out (converting them
+  // here would wait for them, and for the activation loads before them,
+  // ahead of the weight stream); shared waves and a missing bias read zero
+  // through an empty view
+  uint16_t obraw[RM];
   if (shw) {
     rw = a.m * row_words;
     grp = a.m * groups;
@@ -964,13 +975,14 @@ __global__ __launch_bounds__(SH ? 64 * kDec1MaxWaves : 64 * kDec1MaxK) void down
     base.w0 = (uint32_t)(j * row_words * 4);
     base.s0 = (uint32_t)(j * groups * (int)sizeof(ST));
 #pragma unroll
-    for (int it = 0; it < RM; it++) obv[it] = 0.f;
+    for (int it = 0; it < RM; it++) obraw[it] = 0;
   } else {
     e = __builtin_amdgcn_readfirstlane(a.idx[t * a.k + q]);
     if (lane == 0) wr[q] = round_to<XT>(a.w[t * a.k + q]);
+    const rsrc_t obr = make_rsrc(ob ? ob + (size_t)e * N : nullptr, ob ? (uint32_t)(N * sizeof(XT)) : 0u);
 #pragma unroll
     for (int it = 0; it < RM; it++)
-      obv[it] = ob ? to_f<XT>(ob[(size_t)e * N + min(r_begin + sg + it * SG, N - 1)]) : 0.f;
+      obraw[it] = bload16(obr, (uint32_t)min(r_begin + sg + it * SG, N - 1) * (uint32_t)sizeof(XT));
     P = proj_view<BITS, ST>(a.p, e, N, row_words, groups);
   }
   const uint32_t wstep = (uint32_t)(L * BITS * 4), sstep = (uint32_t)((L >> a.gsh) * sizeof(ST));
@@ -1003,7 +1015,7 @@ __global__ __launch_bounds__(SH ? 64 * kDec1MaxWaves : 64 * kDec1MaxK) void down
     float y = group_sum(dot_units<BITS, XT, ST, UR>(w[it], xu, xs, li, L, CU), a.lg);
     if (!shw) {
       y = round_to<XT>(y);
-      if (ob) y = round_to<XT>(y + obv[it]);
+      if (ob) y = round_to<XT>(y + to_f<XT>(__builtin_bit_cast(XT, obraw[it])));
     }
     if (li == L - 1) ys[q * rpb + sg + it * SG] = y;
   }
