@@ -184,8 +184,9 @@ hipError_t launch_router_q(int bits, const void* x, int xdt, int T, int H, const
 
 // ------------------------------------------------------------- dispatch --
 // Writes counts, offsets, perm, inv_perm and the used-expert list.
-// launch_router_topk + launch_dispatch_plan in one workgroup for T <= 8
-// and T * k <= 1024 (hipErrorInvalidValue otherwise, nothing launched).
+// launch_router_topk + launch_dispatch_plan in one workgroup for T <= 16,
+// T * k <= 1024, E <= 512 and k <= 64 (hipErrorInvalidValue otherwise,
+// nothing launched).
 hipError_t launch_route_plan(const void* logits, int dt, int T, int E, int k, const RouteOpts& ro,
                              uint32_t* idx, float* w, uint32_t* counts, uint32_t* offsets,
                              uint32_t* perm, uint32_t* inv, uint32_t* used, hipStream_t st);
