@@ -460,8 +460,9 @@ __device__ __forceinline__ float split_sum(const float* __restrict__ p, size_t s
   return s;
 }
 
-// MAXKS: 1 without partials, else a bound on rp.KS
-template <typename XT, int MAXKS>
+// MAXKS: 1 without partials, else a bound on rp.KS; EPL: logits per lane
+// (E <= 64 EPL)
+template <typename XT, int MAXKS, int EPL>
 __global__ __launch_bounds__(256) void router_topk_kernel(XT* __restrict__ logits, int T,
                                                           int E, int k, const RouteOpts ro,
                                                           uint32_t* __restrict__ idx_out,
@@ -477,7 +478,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(XT* __restrict__ logit
     const XT* bias = reinterpret_cast<const XT*>(rp.bias);
     const size_t stride = (size_t)T * E;
 #pragma unroll
-    for (int j = 0; j < kTopkEPL; j++) {
+    for (int j = 0; j < EPL; j++) {
       if (64 * j >= E) break;  // wave-uniform
       const int e = lane + 64 * j, ec = min(e, E - 1);
       float l = round_to<XT>(split_sum<MAXKS>(rp.part + (size_t)t * E + ec, stride, rp.KS));
@@ -497,7 +498,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(XT* __restrict__ logit
   }
   int sel;
   float w;
-  wave_topk<XT>(row, E, k, ro, sc[wv], true, &sel, &w);
+  wave_topk<XT, EPL>(row, E, k, ro, sc[wv], true, &sel, &w);
   if (lane < k) {
     idx_out[(size_t)t * k + lane] = (uint32_t)sel;
     w_out[(size_t)t * k + lane] = w;
@@ -625,10 +626,15 @@ hipError_t launch_router_topk(void* logits, int dt, int T, int E, int k, const R
   const RouterPartials rp{KS > 1 ? part : nullptr, KS, bias, logits2, KS > 1 && logits2 ? E2 : 0};
   if (rp.part && (E > kTopkMaxE || E2 > 64 || KS > kRgMaxSplits || dt == DT_F32))
     return hipErrorInvalidValue;
-#define MOE_TK2(XT, MK)                                                                     \
-  hipLaunchKernelGGL((router_topk_kernel<XT, MK>), dim3(grid), dim3(256), 0, st,           \
+#define MOE_TK3(XT, MK, EPL)                                                                \
+  hipLaunchKernelGGL((router_topk_kernel<XT, MK, EPL>), dim3(grid), dim3(256), 0, st,      \
                      (XT*)logits, T, E, k, ro, idx, w, rp);                                \
   return hipGetLastError();
+#define MOE_TK2(XT, MK)                   \
+  if (E <= 64) { MOE_TK3(XT, MK, 1) }     \
+  if (E <= 128) { MOE_TK3(XT, MK, 2) }    \
+  if (E <= 256) { MOE_TK3(XT, MK, 4) }    \
+  MOE_TK3(XT, MK, kTopkEPL)
 #define MOE_TK(XT)                                 \
   if (!rp.part) { MOE_TK2(XT, 1) }                 \
   if constexpr (!__is_same(XT, float)) {           \
@@ -641,6 +647,7 @@ hipError_t launch_router_topk(void* logits, int dt, int T, int E, int k, const R
   if (dt == DT_F32) { MOE_TK(float) }
 #undef MOE_TK
 #undef MOE_TK2
+#undef MOE_TK3
   return hipErrorInvalidValue;
 }
 
