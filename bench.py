@@ -741,13 +741,16 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
     timed calls continue the rotation where the warm-up stopped and every
     layer is used again only after the L - 1 others; before them, each
     layer is called once as set-up (starting at the first timed layer). The graphs of the timed
-    calls are captured and uploaded first and the warm-up calls run right
+    calls are captured, uploaded and launched once (untimed: a graph's first
+    launch carries a one-time runtime cost), and the warm-up calls run right
     before the timed ones, so that the timed calls start on the clocks of a
     running loop. The timed steps run as min(5, steps // L) repeats, at least
     one (steps // repeats calls each, the remainder spread over the first
     repeats), each one HIP-graph replay of its own stretch of the rotation,
     bracketed by events on the launch stream; ms_per_step is the median over
-    the repeats of (repeat time / its calls)."""
+    the repeats of (repeat time / its calls). Every call, untimed ones
+    included, advances one clock; a timed call's reuse distance is the
+    number of calls since its layer's previous call."""
     T = cfg["T"]
     if layers is None:
         layers = build_layers(cfg, L, torch, fl, lib)
@@ -763,16 +766,15 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
     # first timed layer, so between a timed layer's set-up call and its timed
     # call come at least L + warmup other calls (GPT-OSS: 24 x 56 MB), far
     # more than the 256 MB memory-side cache holds.
+    clock = 0          # calls so far, in the order the device runs them
+    last_use = {}      # layer -> clock of its latest call
     for i in range(L):
         l = (warmup + i) % L
         layers[l].forward(xs[l], out=ys[l])
+        last_use[l] = clock
+        clock += 1
     torch.cuda.synchronize()
     paths = layers[0].paths(T)
-
-    # the warm-up calls (they run after the graphs are captured, below)
-    last_use = {}
-    for c in range(warmup):
-        last_use[c % L] = c
 
     # the timed steps: up to 5 repeats, each one HIP-graph replay of the next
     # stretch of the rotation and each at least one full rotation long (a
@@ -780,22 +782,28 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
     nrep = max(1, min(5, steps // L))
     sizes = [steps // nrep + (1 if r < steps % nrep else 0) for r in range(nrep)]
     graphs = []
+    timed_seq = []     # layer of each timed call, in order
     c = warmup
-    reuse = []
-    timed_layers = set()
     for n in sizes:
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for _ in range(n):
                 l = c % L
                 layers[l].forward(xs[l], out=ys[l])
-                if l in last_use:
-                    reuse.append(c - last_use[l])
-                last_use[l] = c
-                timed_layers.add(l)
+                timed_seq.append(l)
                 c += 1
         graphs.append(g)
     uploaded = all([graph_upload(g, torch) for g in graphs])
+    torch.cuda.synchronize()
+    # each graph launched once, untimed: after hipGraphUpload the first
+    # launch of an executable graph still stalls once for about 30 us on
+    # this runtime (one gap inside the replay, none in later replays:
+    # GPT-OSS 20-call replay 22.6-23.0 us per call first, 21.5-21.6 after)
+    for g in graphs:
+        g.replay()
+    for l in timed_seq:
+        last_use[l] = clock
+        clock += 1
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(nrep)]
@@ -804,7 +812,15 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
     # them, the warm-up left the first timed calls on idle clocks)
     for c in range(warmup):
         layers[c % L].forward(xs[c % L], out=ys[c % L])
+        last_use[c % L] = clock
+        clock += 1
     torch.cuda.synchronize()
+    reuse = []
+    for l in timed_seq:
+        reuse.append(clock - last_use[l])
+        last_use[l] = clock
+        clock += 1
+    timed_layers = set(timed_seq)
     w0 = time.perf_counter()
     for r in range(nrep):
         evs[r][0].record()
@@ -942,10 +958,10 @@ def run_config(cfg, torch, fl, lib, steps, warmup, L, layers=None):
         "timing": {"repeats": nrep, "calls_per_repeat": sizes,
                    "ms_per_step_each": [round(v, 6) for v in each],
                    "ms_per_step_all": round(span, 6), "graphs_uploaded": uploaded,
-                   "warmup_after_capture": True,
-                   "method": "graphs captured and uploaded, then the warm-up calls, then one "
-                             "HIP-graph replay per repeat (each its own stretch of the layer "
-                             "rotation), events on the launch stream, median"},
+                   "warmup_after_capture": True, "graphs_launched_before_timing": True,
+                   "method": "graphs captured, uploaded and launched once (untimed), then the "
+                             "warm-up calls, then one HIP-graph replay per repeat (each its own "
+                             "stretch of the layer rotation), events on the launch stream, median"},
         "config": config,
         "roofline": roof,
         "layer_roofline": layer_roof,
