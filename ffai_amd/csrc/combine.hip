@@ -61,6 +61,8 @@ __device__ __forceinline__ float shared_gate(int mode, const XT* logit, int t) {
   return 1.0f;
 }
 
+constexpr int kCombineBatch = 8;  // expert ranks whose rows load together
+
 // One block per token; threads stride over hidden 8 values at a time.
 // res (nullable): the decoder residual added before the final rounding.
 template <typename XT>
@@ -76,14 +78,29 @@ __global__ __launch_bounds__(256) void unpermute_kernel(const XT* __restrict__ Y
   const float g = smode ? shared_gate<XT>(smode, slogit, t) : 0.f;
   for (int h = threadIdx.x * 8; h < H; h += blockDim.x * 8) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < k; s++) {
-      const uint32_t p = inv[(size_t)t * k + s];
-      if (p >= M) continue;
-      const float ws = round_to<XT>(w[(size_t)t * k + s]);
-      float y[8];
-      Vec8<XT>::load(Y + (size_t)p * H + h, y);
+    // ranks in batches of kCombineBatch: every position, then every row of a
+    // batch in flight before its fused multiply-adds (in rank order, as the
+    // loop over the ranks one at a time contracted them); a position past M
+    // reads row 0 and leaves the sum unchanged
+    for (int s0 = 0; s0 < k; s0 += kCombineBatch) {
+      uint32_t p[kCombineBatch];
+      float ws[kCombineBatch];
 #pragma unroll
-      for (int j = 0; j < 8; j++) acc[j] = acc[j] + ws * y[j];
+      for (int q = 0; q < kCombineBatch; q++) {
+        const int s = min(s0 + q, k - 1);
+        p[q] = inv[(size_t)t * k + s];
+        ws[q] = round_to<XT>(w[(size_t)t * k + s]);
+      }
+      float y[kCombineBatch][8];
+#pragma unroll
+      for (int q = 0; q < kCombineBatch; q++)
+        Vec8<XT>::load(Y + (size_t)(p[q] < M ? p[q] : 0u) * H + h, y[q]);
+#pragma unroll
+      for (int q = 0; q < kCombineBatch; q++) {
+        const bool valid = s0 + q < k && p[q] < M;
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[j] = valid ? __builtin_fmaf(ws[q], y[q][j], acc[j]) : acc[j];
+      }
     }
 #pragma unroll
     for (int j = 0; j < 8; j++) acc[j] = round_to<XT>(acc[j]);
