@@ -60,18 +60,35 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT* __restrict
     u32x4_t wv[NL];
 #pragma unroll
     for (int j = 0; j < NL; j++) wv[j] = bload128(wr, (uint32_t)((lane + 64 * j) * 16));
+    // tokens in batches of TB: every activation load of a batch goes out
+    // before its dot products (a branch per token made each token's loads
+    // wait for the token before); tokens past nt repeat the last one and
+    // are not stored
+    constexpr int TB = NL <= 4 ? 8 : (NL <= 8 ? 4 : 2);
 #pragma unroll
-    for (int t = 0; t < 8; t++) {
-      acc[t] = 0.f;
-      if (t < nt) {  // wave-uniform
-        const rsrc_t xr = make_rsrc(x + (size_t)(t0 + t) * H, (uint32_t)(H * sizeof(XT)));
+    for (int tb = 0; tb < 8; tb += TB) {
+      if (tb < nt) {  // wave-uniform
+        u32x4_t xv[TB][NL];
 #pragma unroll
-        for (int j = 0; j < NL; j++) {
-          const u32x4_t xv = bload128(xr, (uint32_t)((lane + 64 * j) * 16));
+        for (int q = 0; q < TB; q++) {
+          const int t = min(tb + q, nt - 1);
+          const rsrc_t xr = make_rsrc(x + (size_t)(t0 + t) * H, (uint32_t)(H * sizeof(XT)));
 #pragma unroll
-          for (int i = 0; i < 4; i++) acc[t] = dot2_16<XT>(wv[j][i], xv[i], acc[t]);
+          for (int j = 0; j < NL; j++) xv[q][j] = bload128(xr, (uint32_t)((lane + 64 * j) * 16));
         }
-        acc[t] = group_sum(acc[t], 6);
+        __builtin_amdgcn_sched_barrier(0);  // the batch's loads stay ahead of its math
+#pragma unroll
+        for (int q = 0; q < TB; q++) {
+          float a = 0.f;
+#pragma unroll
+          for (int j = 0; j < NL; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) a = dot2_16<XT>(wv[j][i], xv[q][j][i], a);
+          acc[tb + q] = group_sum(a, 6);
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < TB; q++) acc[tb + q] = 0.f;
       }
     }
   } else {
