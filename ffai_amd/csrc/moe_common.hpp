@@ -191,6 +191,24 @@ __device__ __forceinline__ float det_expf(float x) {
   return __builtin_ldexpf(y, (int)n);
 }
 
+// ------------------------------------------------------------ bias words --
+// A per-expert bias element's raw bits through a buffer view (no bias: an
+// empty view, which reads 0 without touching memory), converted only where
+// the bias is added (bias_f). Converting it where it is loaded makes the wave
+// wait for it, and for every load issued before it, ahead of the loads that
+// follow (vector loads complete in issue order).
+template <typename XT>
+__device__ __forceinline__ uint32_t bias_raw(const XT* bias, int e) {
+  const rsrc_t r = make_rsrc(bias ? bias + e : nullptr, bias ? (uint32_t)sizeof(XT) : 0u);
+  if constexpr (sizeof(XT) == 2) return (uint32_t)bload16(r, 0u);
+  else return bload32(r, 0u);
+}
+template <typename XT>
+__device__ __forceinline__ float bias_f(uint32_t raw) {
+  if constexpr (sizeof(XT) == 2) return to_f<XT>(__builtin_bit_cast(XT, (uint16_t)raw));
+  else return __uint_as_float(raw);
+}
+
 // ------------------------------------------------------------ wave top-k --
 // Makes LDS writes of this wave visible to its other lanes.
 __device__ __forceinline__ void wave_sync() {

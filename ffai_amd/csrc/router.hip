@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT* __restrict
   if (e >= E) return;  // the kernel has no block barrier
   const int lane = threadIdx.x & 63;
   const int t0 = tc * 8, nt = min(8, T - t0);
-  const float bv = bias ? to_f<XT>(bias[e]) : 0.f;  // issued before the row loads
+  const uint32_t bv = bias_raw<XT>(bias, e);  // issued before the row loads, converted at the end
   const rsrc_t wr = make_rsrc(W + (size_t)e * H, (uint32_t)(H * sizeof(WT)));
   float acc[8];
   if constexpr (__is_same(XT, WT) && !__is_same(XT, float)) {
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT* __restrict
   if (lane == 63) {
     for (int t = 0; t < nt; t++) {
       float l = round_to<XT>(acc[t]);
-      if (bias) l = round_to<XT>(l + bv);
+      if (bias) l = round_to<XT>(l + bias_f<XT>(bv));
       logits[(size_t)(t0 + t) * E + e] = from_f<XT>(l);
     }
   }
@@ -138,7 +138,7 @@ __global__ __launch_bounds__(256) void router_logits_norm_kernel(
   __shared__ float part[2][4];
   const int e = blockIdx.x;  // grid == E
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const float bv = bias ? to_f<XT>(bias[e]) : 0.f;
+  const uint32_t bv = bias_raw<XT>(bias, e);  // converted where it is added
   const uint32_t rb = (uint32_t)(H * sizeof(XT));
   const rsrc_t wr = make_rsrc(W + (size_t)e * H, rb);
   const rsrc_t hr = make_rsrc(h, rb), mr = make_rsrc(m, rb), nr = make_rsrc(nw, rb);
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(256) void router_logits_norm_kernel(
   __syncthreads();
   if (tid == 0) {
     float l = round_to<XT>((part[1][0] + part[1][1]) + (part[1][2] + part[1][3]));
-    if (bias) l = round_to<XT>(l + bv);
+    if (bias) l = round_to<XT>(l + bias_f<XT>(bv));
     logits[e] = from_f<XT>(l);
   }
 }
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(256) void router_logits_row_kernel(const XT* __rest
   __shared__ float part[4];
   const int e = blockIdx.x;  // grid == E
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const float bv = bias ? to_f<XT>(bias[e]) : 0.f;
+  const uint32_t bv = bias_raw<XT>(bias, e);  // converted where it is added
   const uint32_t rb = (uint32_t)(H * sizeof(XT));
   const rsrc_t wr = make_rsrc(W + (size_t)e * H, rb), xr = make_rsrc(x, rb);
   u32x4_t wq[NL], xq[NL];
@@ -243,7 +243,7 @@ __global__ __launch_bounds__(256) void router_logits_row_kernel(const XT* __rest
   __syncthreads();
   if (tid == 0) {
     float l = round_to<XT>((part[0] + part[1]) + (part[2] + part[3]));
-    if (bias) l = round_to<XT>(l + bv);
+    if (bias) l = round_to<XT>(l + bias_f<XT>(bv));
     logits[e] = from_f<XT>(l);
   }
 }

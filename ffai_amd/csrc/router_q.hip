@@ -45,7 +45,7 @@ __global__ __launch_bounds__(256) void router_qrow_kernel(const XT* __restrict__
   const int lane = threadIdx.x & 63;
   const int t0 = tc * 8, nt = min(8, T - t0);
   const int CU = H >> 5, groups = CU >> gsh, row_words = CU * BITS;
-  const float bv = bias ? to_f<XT>(bias[e]) : 0.f;
+  const uint32_t bv = bias_raw<XT>(bias, e);  // converted where it is added
   const ProjView V = proj_view<BITS, ST>(W, 0u, E, row_words, groups);
   const uint32_t wstep = (uint32_t)(64 * BITS * 4), sstep = (uint32_t)((64 >> gsh) * sizeof(ST));
   WUnit<BITS, ST> w[UR];
@@ -66,7 +66,7 @@ __global__ __launch_bounds__(256) void router_qrow_kernel(const XT* __restrict__
   if (lane == 63) {
     for (int t = 0; t < nt; t++) {
       float l = round_to<XT>(acc[t]);
-      if (bias) l = round_to<XT>(l + bv);
+      if (bias) l = round_to<XT>(l + bias_f<XT>(bv));
       logits[(size_t)(t0 + t) * E + e] = from_f<XT>(l);
     }
   }
