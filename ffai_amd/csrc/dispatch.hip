@@ -124,6 +124,39 @@ __device__ void stable_scatter(const uint32_t* __restrict__ idx, int begin, int 
   }
 }
 
+// stable_scatter over entries [begin, begin + n) whose ids thread t already
+// holds: ev[i] = the id of entry begin + t + NT i (n <= NT * PER), loaded
+// all at once up front. Loading them tile by tile, after each tile's
+// barriers, put one memory round trip per NT entries on the plan's
+// critical path.
+template <int NT, int PER>
+__device__ void stable_scatter_held(const uint32_t (&ev)[PER], int begin, int n, int E, int nbits,
+                                    uint32_t* cursor, uint32_t* __restrict__ perm,
+                                    uint32_t* __restrict__ inv) {
+  const int tid = threadIdx.x, wave = tid >> 6;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int base = i * NT;
+    if (base >= n) break;  // block-uniform
+    const int o = base + tid, m = begin + o;
+    const uint32_t e = o < n ? ev[i] : 0xffffffffu;
+    const bool valid = o < n && e < (uint32_t)E;
+    uint32_t rank, count;
+    bool last;
+    wave_peers(e, valid, nbits, &rank, &count, &last);
+    const int nw = min(NT, n - base + 63) / 64;  // block-uniform
+    for (int w = 0; w < nw; w++) {
+      if (wave == w && valid) {
+        const uint32_t pos = cursor[e] + rank;
+        perm[pos] = (uint32_t)m;
+        inv[m] = pos;
+        if (last) cursor[e] += count;
+      }
+      __syncthreads();
+    }
+  }
+}
+
 __device__ __forceinline__ int id_bits(int E) {
   int nb = 0;
   while ((1 << nb) < E) nb++;
@@ -134,16 +167,23 @@ __global__ __launch_bounds__(kPlanThreads) void plan_single_kernel(
     const uint32_t* __restrict__ idx, int M, int E, uint32_t* counts, uint32_t* offsets,
     uint32_t* perm, uint32_t* inv, uint32_t* used) {
   __shared__ uint32_t cnt[kPlanMaxE], cursor[kPlanMaxE];
+  constexpr int PER = kSingleBlockMax / kPlanThreads;
   const int tid = threadIdx.x;
+  // every id of this thread's entries in flight at once, kept for the scatter
+  uint32_t ev[PER];
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int m = tid + i * kPlanThreads;
+    ev[i] = m < M ? idx[m] : 0xffffffffu;
+  }
   for (int e = tid; e < E; e += kPlanThreads) cnt[e] = 0;
   __syncthreads();
-  for (int m = tid; m < M; m += kPlanThreads) {
-    const uint32_t e = idx[m];
-    if (e < (uint32_t)E) atomicAdd(&cnt[e], 1u);
-  }
+#pragma unroll
+  for (int i = 0; i < PER; i++)
+    if (ev[i] < (uint32_t)E) atomicAdd(&cnt[ev[i]], 1u);
   __syncthreads();
   scan_experts(cnt, E, counts, offsets, used, cursor);
-  stable_scatter(idx, 0, M, E, id_bits(E), cursor, perm, inv);
+  stable_scatter_held<kPlanThreads, PER>(ev, 0, M, E, id_bits(E), cursor, perm, inv);
 }
 
 // Routing and dispatch plan of a small batch in one launch: the NT / 64
@@ -281,11 +321,18 @@ __global__ __launch_bounds__(kPlanThreads) void plan_scatter_kernel(
     const uint32_t* __restrict__ idx, int M, int E, const uint32_t* __restrict__ hist,
     uint32_t* perm, uint32_t* inv) {
   __shared__ uint32_t cursor[kPlanMaxE];
+  constexpr int PER = kChunk / kPlanThreads;
   const int tid = threadIdx.x, c = blockIdx.x;
+  const int begin = c * kChunk, end = min(M, begin + kChunk);
+  uint32_t ev[PER];  // the chunk's ids, all loads in flight at once
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int m = begin + tid + i * kPlanThreads;
+    ev[i] = m < end ? idx[m] : 0xffffffffu;
+  }
   for (int e = tid; e < E; e += kPlanThreads) cursor[e] = hist[(size_t)c * E + e];
   __syncthreads();
-  const int begin = c * kChunk, end = min(M, begin + kChunk);
-  stable_scatter(idx, begin, end, E, id_bits(E), cursor, perm, inv);
+  stable_scatter_held<kPlanThreads, PER>(ev, begin, end - begin, E, id_bits(E), cursor, perm, inv);
 }
 
 __global__ void identity_plan_kernel(uint32_t* offsets, uint32_t* used, int M) {
@@ -435,11 +482,18 @@ __global__ __launch_bounds__(kPlanThreads) void plan_scatter_items_kernel(
     uint32_t* perm, uint32_t* inv, const uint32_t* __restrict__ offsets, const ItemCols ic,
     uint32_t* __restrict__ items0, uint32_t* __restrict__ items1) {
   __shared__ uint32_t cursor[kPlanMaxE];
+  constexpr int PER = kChunk / kPlanThreads;
   const int tid = threadIdx.x, c = blockIdx.x;
+  const int begin = c * kChunk, end = min(M, begin + kChunk);
+  uint32_t ev[PER];  // the chunk's ids, all loads in flight at once
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int m = begin + tid + i * kPlanThreads;
+    ev[i] = m < end ? idx[m] : 0xffffffffu;
+  }
   for (int e = tid; e < E; e += kPlanThreads) cursor[e] = hist[(size_t)c * E + e];
   __syncthreads();
-  const int begin = c * kChunk, end = min(M, begin + kChunk);
-  stable_scatter(idx, begin, end, E, id_bits(E), cursor, perm, inv);
+  stable_scatter_held<kPlanThreads, PER>(ev, begin, end - begin, E, id_bits(E), cursor, perm, inv);
   gemm_items_body(offsets, E, ic, items0, items1, c, (int)gridDim.x);
 }
 
