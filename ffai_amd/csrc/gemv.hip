@@ -424,12 +424,15 @@ constexpr int kMmaRows = 64;  // LDS weight rows per block
 constexpr int kMmaTok = 16;   // activation rows per pass
 
 // Codes of 8-value block kb of a unit as four magic-offset pairs (j, j + 4).
+// m4 (4-bit codes): the nibble-pair mask 0x000F000F, held by the caller in a
+// scalar register, with MB in a vector register: gfx9's three-operand
+// v_and_or_b32 takes no literal, so with both as compile-time constants each
+// pair cost a v_and_b32 and a v_or_b32.
 template <int BITS>
-__device__ __forceinline__ u32x4_t mma_codes(const uint32_t* unit, int kb, uint32_t MB) {
+__device__ __forceinline__ u32x4_t mma_codes(const uint32_t* unit, int kb, uint32_t MB, uint32_t m4) {
   if constexpr (BITS == 4) {
     const uint32_t w = unit[kb];
-    return u32x4_t{(w & 0x000F000Fu) | MB, ((w >> 4) & 0x000F000Fu) | MB,
-                   ((w >> 8) & 0x000F000Fu) | MB, ((w >> 12) & 0x000F000Fu) | MB};
+    return u32x4_t{(w & m4) | MB, ((w >> 4) & m4) | MB, ((w >> 8) & m4) | MB, ((w >> 12) & m4) | MB};
   } else {
     // 8 BITS <= 48 bits from bit 8 kb BITS: two consecutive words of the
     // unit hold them after the in-word shift (at most 24)
@@ -450,7 +453,8 @@ __device__ __forceinline__ u32x4_t mma_codes(const uint32_t* unit, int kb, uint3
 template <int BITS, bool GATEUP>
 constexpr int kMmaWavesPerEu = (BITS == 2 || BITS == 4 || (BITS == 3 && GATEUP)) ? 4 : 1;
 
-template <int BITS, typename XT, typename ST, bool GATEUP>
+// GSH: log2(group size / 32), the launch's a.gsh (group sizes 32, 64, 128).
+template <int BITS, typename XT, typename ST, bool GATEUP, int GSH>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kMmaWavesPerEu<BITS, GATEUP>)))
 void gemv_mma_kernel(const GemvArgs a) {
   __shared__ __align__(16) uint32_t wl[2][kMmaRows * kMmaU * BITS];  // [row][unit slot][BITS words]
@@ -462,8 +466,8 @@ void gemv_mma_kernel(const GemvArgs a) {
   const uint32_t e = __builtin_amdgcn_readfirstlane(a.used[1 + slot]);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> a.gsh, row_words = CU * BITS;
-  const int upg = 1 << a.gsh;
+  const int N = a.N, K = a.K, CU = K >> 5, groups = CU >> GSH, row_words = CU * BITS;
+  constexpr int UPG = 1 << GSH;  // units per scale group
   const int nchunks = (CU + kMmaU - 1) / kMmaU;
   constexpr int RPB = GATEUP ? 32 : 64;  // output rows per block
   const int r_begin = rb * RPB;
@@ -505,9 +509,13 @@ void gemv_mma_kernel(const GemvArgs a) {
       const int slr = s_lr0 + 32 * j;
       const ProjView& pv = (GATEUP && j == 1) ? P1 : P0;
       const uint32_t grow = gw_row(slr);
-      const uint32_t u = (uint32_t)min(kMmaU * cc + s_us, CU - 1);
+      const int uu = kMmaU * cc + s_us;
+      const uint32_t u = (uint32_t)min(uu, CU - 1);
       bload_unit<BITS>(pv.w, (grow * (uint32_t)row_words + u * (uint32_t)BITS) * 4u + dead, st.w[j]);
-      const uint32_t gi = (grow * (uint32_t)groups + (u >> a.gsh)) * (uint32_t)sizeof(ST) + dead;
+      // units past K (the last chunk's tail) read a zero scale and bias, so
+      // their products with the clamped unit's codes add zero
+      const uint32_t sdead = uu < CU ? dead : 0x80000000u;
+      const uint32_t gi = (grow * (uint32_t)groups + (u >> GSH)) * (uint32_t)sizeof(ST) + sdead;
       st.s[j] = (uint32_t)bload16(pv.s, gi);
       st.b[j] = (uint32_t)bload16(pv.b, gi);
     }
@@ -545,27 +553,32 @@ void gemv_mma_kernel(const GemvArgs a) {
     }
   };
   const u32x4_t ones = {Mma16<XT>::ones, Mma16<XT>::ones, Mma16<XT>::ones, Mma16<XT>::ones};
+  // opaque copies of the 4-bit unpack's two constants (see mma_codes)
+  uint32_t m4, mbv;
+  asm("s_mov_b32 %0, 0xf000f" : "=s"(m4));
+  asm("v_mov_b32 %0, %1" : "=v"(mbv) : "i"(MB));
   f32x4_t acc;
-  auto compute = [&](int c, int buf) __attribute__((always_inline)) {
-    const int nu = min(kMmaU, CU - kMmaU * c);  // block-uniform
+  // Every chunk runs the same straight-line code: K is a multiple of the
+  // group size, so groups never straddle the end of K, and the units past it
+  // carry zero scales and biases. A group's first unit starts P and Q from a
+  // zero accumulator (no register clears), its last applies the group's
+  // scale and bias; with the group size a runtime value the compiler kept
+  // both per unit behind branches, with eight register clears per group.
+  auto compute = [&](int buf) __attribute__((always_inline)) {
     f32x4_t P = {}, Q = {};
 #pragma unroll
     for (int us = 0; us < kMmaU; us++) {
-      if (us < nu) {
-        const u32x4_t bop = mma_codes<BITS>(&wl[buf][(lr * kMmaU + ((us + lr) & 7)) * BITS], kb, MB);
-        const u32x4_t aop =
-            *reinterpret_cast<const u32x4_t*>(&xl[buf][((us * kMmaTok + r) * 4 + (kb ^ ((r >> 2) & 3))) * 4]);
-        P = Mma16<XT>::mma(aop, bop, P);
-        Q = Mma16<XT>::mma(aop, ones, Q);
-        if (((kMmaU * c + us + 1) & (upg - 1)) == 0 || us == nu - 1) {
-          const uint32_t sb = sl[buf][lr * kMmaU + us];
-          const float sc = to_f<ST>(__builtin_bit_cast(ST, (uint16_t)(sb & 0xFFFFu)));
-          const float bi = to_f<ST>(__builtin_bit_cast(ST, (uint16_t)(sb >> 16))) - MAGIC * sc;
+      const u32x4_t bop = mma_codes<BITS>(&wl[buf][(lr * kMmaU + ((us + lr) & 7)) * BITS], kb, mbv, m4);
+      const u32x4_t aop =
+          *reinterpret_cast<const u32x4_t*>(&xl[buf][((us * kMmaTok + r) * 4 + (kb ^ ((r >> 2) & 3))) * 4]);
+      P = Mma16<XT>::mma(aop, bop, us % UPG == 0 ? f32x4_t{} : P);
+      Q = Mma16<XT>::mma(aop, ones, us % UPG == 0 ? f32x4_t{} : Q);
+      if ((us + 1) % UPG == 0) {
+        const uint32_t sb = sl[buf][lr * kMmaU + us];
+        const float sc = to_f<ST>(__builtin_bit_cast(ST, (uint16_t)(sb & 0xFFFFu)));
+        const float bi = to_f<ST>(__builtin_bit_cast(ST, (uint16_t)(sb >> 16))) - MAGIC * sc;
 #pragma unroll
-          for (int i = 0; i < 4; i++) acc[i] += sc * P[i] + bi * Q[i];
-          P = f32x4_t{};
-          Q = f32x4_t{};
-        }
+        for (int i = 0; i < 4; i++) acc[i] += sc * P[i] + bi * Q[i];
       }
     }
   };
@@ -598,11 +611,11 @@ void gemv_mma_kernel(const GemvArgs a) {
     // loads read nothing, its stores land in a buffer nothing reads). Peeling
     // that chunk off the loop instead cost eight VGPRs and one wave per SIMD.
     for (int c = 0; c < nchunks; c += 2) {
-      compute(c, 0);
+      compute(0);
       store_stage(s1, 1);  // chunk c + 1
       load_stage(c + 3, xrow, s1);
       lds_barrier();
-      if (c + 1 < nchunks) compute(c + 1, 1);
+      if (c + 1 < nchunks) compute(1);
       store_stage(s0, 0);  // chunk c + 2
       load_stage(c + 4, xrow, s0);
       lds_barrier();
@@ -651,16 +664,26 @@ void gemv_mma_kernel(const GemvArgs a) {
   }
 }
 
+template <typename XT, typename ST, int GSH>
+static hipError_t launch_mma_g(bool gateup, const GemvArgs& a, int grid, hipStream_t st, KEvents ev) {
+  if (gateup)
+    hipExtLaunchKernelGGL((gemv_mma_kernel<MOE_BITS, XT, ST, true, GSH>), dim3(grid), dim3(256), 0, st,
+                          ev.start, ev.stop, 0, a);
+  else
+    hipExtLaunchKernelGGL((gemv_mma_kernel<MOE_BITS, XT, ST, false, GSH>), dim3(grid), dim3(256), 0, st,
+                          ev.start, ev.stop, 0, a);
+  return hipGetLastError();
+}
+
 hipError_t MOE_CAT(launch_mma_b, MOE_BITS)(int xdt, int sbdt, bool gateup, const GemvArgs& a,
                                             int grid, hipStream_t st, KEvents ev) {
-#define MOE_MMA(XT, ST)                                                                          \
-  if (gateup)                                                                                    \
-    hipExtLaunchKernelGGL((gemv_mma_kernel<MOE_BITS, XT, ST, true>), dim3(grid), dim3(256), 0,   \
-                          st, ev.start, ev.stop, 0, a);                                          \
-  else                                                                                           \
-    hipExtLaunchKernelGGL((gemv_mma_kernel<MOE_BITS, XT, ST, false>), dim3(grid), dim3(256), 0,  \
-                          st, ev.start, ev.stop, 0, a);                                          \
-  return hipGetLastError();
+#define MOE_MMA(XT, ST)                                                \
+  switch (a.gsh) {                                                     \
+    case 0: return launch_mma_g<XT, ST, 0>(gateup, a, grid, st, ev);   \
+    case 1: return launch_mma_g<XT, ST, 1>(gateup, a, grid, st, ev);   \
+    case 2: return launch_mma_g<XT, ST, 2>(gateup, a, grid, st, ev);   \
+    default: return hipErrorInvalidValue;                              \
+  }
   if (xdt == DT_BF16 && sbdt == DT_BF16) { MOE_MMA(bf16_t, bf16_t) }
   if (xdt == DT_BF16 && sbdt == DT_F16) { MOE_MMA(bf16_t, f16_t) }
   if (xdt == DT_F16 && sbdt == DT_F16) { MOE_MMA(f16_t, f16_t) }
