@@ -487,7 +487,7 @@ void gemv_mma_kernel(const GemvArgs a) {
   // (tid >> 3) + 32 j, unit slot tid & 7; activation quad q = tid + 256 j:
   // unit q >> 6, row (q >> 2) & 15 (the same for both j), quad q & 3
   const int s_lr0 = tid >> 3, s_us = tid & 7;
-  const int x_t = (tid >> 2) & 15, x_kb = tid & 3, x_us0 = tid >> 6;
+  const int x_t = (tid >> 2) & 15, x_kb = tid & 3, x_us0 = wave;  // x_us0 scalar
   struct Stage {
     uint32_t w[2][BITS];
     u32x4_t x[2];
@@ -577,8 +577,10 @@ void gemv_mma_kernel(const GemvArgs a) {
         const uint32_t sb = sl[buf][lr * kMmaU + us];
         const float sc = to_f<ST>(__builtin_bit_cast(ST, (uint16_t)(sb & 0xFFFFu)));
         const float bi = to_f<ST>(__builtin_bit_cast(ST, (uint16_t)(sb >> 16))) - MAGIC * sc;
+        // two chained fmas per output (the sum s P + bi Q as written cost a
+        // multiply, an fma and an add)
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[i] += sc * P[i] + bi * Q[i];
+        for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(bi, Q[i], __builtin_fmaf(sc, P[i], acc[i]));
       }
     }
   };
