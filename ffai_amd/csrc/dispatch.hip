@@ -40,24 +40,21 @@ __device__ void scan_experts(const uint32_t* cnt, int E, uint32_t* counts, uint3
     tot += c[j];
     ftot += f[j];
   }
-  // inclusive wave scan of (tot, ftot)
-  uint32_t s = tot, fs = ftot;
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t o = __shfl_up(s, off, 64), fo = __shfl_up(fs, off, 64);
-    if (lane >= off) {
-      s += o;
-      fs += fo;
-    }
-  }
+  // inclusive wave scan of (tot, ftot) by DPP (shuffles put an LDS round
+  // trip per step on the plan's chain)
+  const uint32_t s = wave_scan_u32(tot), fs = wave_scan_u32(ftot);
   if (lane == 63) {
     wsum[wave] = s;
     wused[wave] = fs;
   }
   __syncthreads();
+  // the earlier waves' totals, all read at once
   uint32_t wb = 0, fb = 0;
-  for (int w = 0; w < wave; w++) {
-    wb += wsum[w];
-    fb += wused[w];
+#pragma unroll
+  for (int w = 0; w < NT / 64; w++) {
+    const uint32_t a = wsum[w], b = wused[w];
+    wb += w < wave ? a : 0u;
+    fb += w < wave ? b : 0u;
   }
   uint32_t run = wb + s - tot, frun = fb + fs - ftot;
 #pragma unroll

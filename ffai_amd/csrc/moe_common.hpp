@@ -44,7 +44,8 @@ __device__ __forceinline__ float dpp_f32(float old, float x) {
                                                     ROW_MASK, 0xF, false));
 }
 
-// Maximum over the wave (NaN-free input), returned wave-uniform.
+// Maximum over the wave, returned wave-uniform; as with fmaxf (v_max_f32 in
+// IEEE mode), NaN lanes are ignored unless every lane is NaN.
 __device__ __forceinline__ float wave_max_f32(float x) {
   x = fmaxf(x, dpp_f32<0xB1, 0xF>(x, x));
   x = fmaxf(x, dpp_f32<0x4E, 0xF>(x, x));
@@ -69,6 +70,26 @@ __device__ __forceinline__ int wave_max_i32(int x) {
   x = max(x, dpp_i32<0x142, 0xA>(x, x));
   x = max(x, dpp_i32<0x143, 0xC>(x, x));
   return __builtin_amdgcn_readlane(x, 63);
+}
+
+// Lane r's value (r wave-uniform), through a scalar register.
+__device__ __forceinline__ float lane_f32(float x, int r) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), r));
+}
+
+// Inclusive prefix sum over the wave by DPP: row_shr 1, 2, 4, 8 within each
+// row of 16 lanes (lanes without a source add 0), then row 0's total into
+// row 1 and row 2's into row 3 (row_bcast:15), then rows 0-1's into rows
+// 2-3 (row_bcast:31).
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x) {
+  int v = (int)x;
+  v += dpp_i32<0x111, 0xF>(0, v);
+  v += dpp_i32<0x112, 0xF>(0, v);
+  v += dpp_i32<0x114, 0xF>(0, v);
+  v += dpp_i32<0x118, 0xF>(0, v);
+  v += dpp_i32<0x142, 0xA>(0, v);
+  v += dpp_i32<0x143, 0xC>(0, v);
+  return (uint32_t)v;
 }
 
 // Order-preserving map of non-NaN floats onto signed ints (an involution):
@@ -263,7 +284,7 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, const RouteO
   }
   if (!on_logits && !sigmoid) {
     // full softmax (+ expert bias): MoELayer.swift:174-195
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    m = wave_max_f32(m);
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
       const int i = lane + 64 * j;
@@ -276,7 +297,7 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, const RouteO
     float s = 0.f;
     if (lane == 0)
       for (int i = 0; i < E; i++) s += sc[i];
-    s = __shfl(s, 0, 64);
+    s = lane_f32(s, 0);
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
       const int i = lane + 64 * j;
@@ -349,26 +370,27 @@ __device__ void wave_topk(const XT* __restrict__ row, int E, int k, const RouteO
   if (on_logits) {
     // softmax over the k picked raw logits — MoELayer.swift:166-172,197-203
     // (the values travelled with the selection: no second read of the row)
+    // (the max by DPP and the rank-order sum by readlane: shuffles would put
+    // an LDS round trip per step on the routing chain)
     const float lv = (lane < k) ? my_raw : NEG;
-    float mx = lv;
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    const float mx = wave_max_f32(lv);
     const float ex = (lane < k) ? det_expf(lv - mx) : 0.f;
     float s = 0.f;
-    for (int r = 0; r < k; r++) s += __shfl(ex, r, 64);
+    for (int r = 0; r < k; r++) s += lane_f32(ex, r);
     wv = (s > 0.f) ? ex / s : 1.0f / (float)k;
   } else if (sigmoid) {
     // raw sigmoid of the pick, / (sum in rank order + 1e-20) when norm, k > 1
     wv = my_raw;
     if (norm && k > 1) {
       float s = 0.f;
-      for (int r = 0; r < k; r++) s += __shfl(my_raw, r, 64);
+      for (int r = 0; r < k; r++) s += lane_f32(my_raw, r);
       wv = wv / (s + 1e-20f);
     }
   } else {
     wv = my_val;
     if (norm) {
       float s = 0.f;
-      for (int r = 0; r < k; r++) s += __shfl(my_val, r, 64);
+      for (int r = 0; r < k; r++) s += lane_f32(my_val, r);
       if (s > 0.f) wv = wv / s;
     }
   }
