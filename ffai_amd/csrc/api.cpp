@@ -541,10 +541,22 @@ constexpr int kMultiBlocks = 512;
 // tokens 124.3 -> 117.6 us, GPT-OSS 16 tokens gate/up 96.8 -> 85.1 us), a
 // single projection from 3 (GPT-OSS 16 tokens, 2 per expert: down 45.5 on
 // gemv_multi_kernel against 50.0; at 24 tokens 58.8 against 52.5).
-constexpr int kMmaMinRowsPair = 2;
-constexpr int kMmaMinRowsSingle = 3;
-constexpr int kMmaMinRowsOther = 2;
-constexpr int kMmaMinRowsSingleExpert = 16;
+// Thresholds in tenths of a row per used expert. With the matrix-core GEMV's
+// straight-line chunks the 4-bit crossovers moved down again (µs per launch,
+// gemv_multi_kernel against gemv_mma_kernel): a gate/up pair is as fast or
+// faster on the matrix cores at every measured count (Qwen3 12 tokens, 1.2
+// rows per used expert: 36.2 / 34.6; 16 tokens, 1.56 rows: 42.7 / 39.4; 24
+// tokens, 1.94 rows: 56.3 / 46.1; GPT-OSS 8 tokens, 1.45 rows: 62.1 / 60.1;
+// 12 tokens: 79.6 / 68.9), a single projection from 1.8 rows (Qwen3 16
+// tokens: 23.1 / 24.5; 20 tokens, 1.72 rows: 26.3 / 26.9; 24 tokens: 30.6 /
+// 28.8; GPT-OSS 8 tokens: 29.6 / 33.4; 16 tokens, 2.2 rows: 45.9 / 43.3).
+// Layer steps, old thresholds / these: Qwen3 16 tokens 80.0 / 77.7, 24
+// tokens 99.7 / 90.3, GPT-OSS 12 tokens 129.0 / 120.7. Other widths stay at
+// 2 (mixed-bit 16 tokens: gate/up 37.3 / 41.6).
+constexpr int kMmaMinRowsPair10 = 10;
+constexpr int kMmaMinRowsSingle10 = 18;
+constexpr int kMmaMinRowsOther10 = 20;
+constexpr int kMmaMinRowsSingleExpert10 = 160;
 
 // gemv_mma_kernel applies: 2- to 6-bit codes (exact with the magic offset in
 // either 16-bit type), 16-bit activations at 16-byte aligned rows, and
@@ -581,10 +593,10 @@ GemvKind gemv_kind(const moe_qproj& p0, const moe_qproj* p1, bool x_aligned, int
   if (single) return kGemvGrouped;
   // the matrix cores once the used experts average enough rows: below that
   // the K-chunk pipeline's latency outweighs the VALU it saves
-  const int min_rows = slots <= 1 ? kMmaMinRowsSingleExpert
-                      : p0.bits != 4 ? kMmaMinRowsOther
-                                     : (p1 ? kMmaMinRowsPair : kMmaMinRowsSingle);
-  if ((long)M >= (long)min_rows * std::max(1, slots) && mma_ok(p0, p1, x_aligned, xdt))
+  const int min_rows10 = slots <= 1 ? kMmaMinRowsSingleExpert10
+                        : p0.bits != 4 ? kMmaMinRowsOther10
+                                       : (p1 ? kMmaMinRowsPair10 : kMmaMinRowsSingle10);
+  if (10L * M >= (long)min_rows10 * std::max(1, slots) && mma_ok(p0, p1, x_aligned, xdt))
     return kGemvMma;
   const int tm = multi_rows_per_pass(std::min(max_rows, M), M, slots);
   if (multi_ok(p0, x_aligned, xdt, tm)) return kGemvMulti;
