@@ -158,6 +158,33 @@ def test_unsupported_dtype_pair():
     assert lib.moe_validate_layer(C.byref(d)) == _lib.MOE_ERR_UNSUPPORTED
 
 
+@pytest.mark.parametrize("E,k,H,I,bits_gu,bits_d,gs,T,gate_up,down", [
+    # Qwen3-shaped; the path query counts min(E, T k) used experts
+    (128, 8, 2048, 768, 4, 4, 64, 1, "decode1", "decode1"),
+    (128, 8, 2048, 768, 4, 4, 64, 16, "gemv_mma", "gemv"),      # 1 row per expert
+    (128, 8, 2048, 768, 4, 4, 64, 24, "gemv_mma", "gemv"),      # 1.5 rows
+    (128, 8, 2048, 768, 4, 4, 64, 32, "gemv_mma", "gemv_mma"),  # 2 rows
+    (128, 8, 2048, 768, 4, 4, 64, 256, "gemm", "gemm"),         # 16 rows
+    # GPT-OSS-shaped: 2 rows per expert at 16 tokens
+    (32, 4, 2880, 2880, 4, 4, 32, 16, "gemv_mma", "gemv_mma"),
+    # 3-bit gate/up, 6-bit down: the matrix cores from 2 rows
+    (128, 8, 2048, 768, 3, 6, 64, 16, "gemv", "gemv"),
+    (128, 8, 2048, 768, 3, 6, 64, 32, "gemv_mma", "gemv_mma"),
+])
+def test_gemv_selection(E, k, H, I, bits_gu, bits_d, gs, T, gate_up, down):
+    """The grouped kernel each projection takes (moe_layer_path, host only): a
+    4-bit gate/up pair on the matrix-core GEMV at any row count, a 4-bit single
+    projection from 1.8 rows per used expert, other widths from 2, the GEMM
+    from 16 rows (64+ experts)."""
+    d = layer(E=E, k=k, H=H, I=I)
+    d.gate, d.up = qproj(E, I, H, bits_gu, gs), qproj(E, I, H, bits_gu, gs)
+    d.down = qproj(E, H, I, bits_d, gs)
+    p = _lib.LayerPaths()
+    assert _lib.load().moe_layer_path(C.byref(d), T, C.byref(p)) == _lib.MOE_OK
+    got = p.names()
+    assert (got["gate_up"], got["down"]) == (gate_up, down), got
+
+
 def test_derive_bits_cases():
     lib = _lib.load()
     out = C.c_int32()
