@@ -389,8 +389,8 @@ __global__ __launch_bounds__(256, 2) void gemv_multi_kernel(const GemvArgs a) {
 // v_mfma_f32_16x16x32: A = 16 activation rows, B = the 16 weight rows' codes
 // with the magic offset (MAGIC + q exact in the 16-bit type), per 32-value
 // unit. A second MFMA against all-ones gives the unit's activation sums Q, so
-// the affine scale and bias apply per group in fp32 exactly as the one-token
-// kernels apply them: acc += s P + (b - MAGIC s) Q. Lane (r, kb) = (lane % 16,
+// the affine scale and bias apply per group in fp32 on the accumulators:
+// acc = fma(b - MAGIC s, Q, fma(s, P, acc)). Lane (r, kb) = (lane % 16,
 // lane / 16) supplies the codes of 8-value block kb of weight row r (bits
 // [8 kb BITS, +8 BITS) of the unit's BITS words; for 4 bits, word kb), whose
 // pairs (j, j + 4) match the activations' pair order, and
@@ -533,7 +533,9 @@ void gemv_mma_kernel(const GemvArgs a) {
       const uint32_t u = (uint32_t)min(uu, CU - 1);
       bload_unit<BITS>(pv.w, (grow * (uint32_t)row_words + u * (uint32_t)BITS) * 4u + dead, st.w[j]);
       // units past K (the last chunk's tail) read a zero scale and bias, so
-      // their products with the clamped unit's codes add zero
+      // their products with the clamped unit's codes and activations add
+      // zero (for finite activations; a non-finite one in a row's last unit
+      // makes its outputs non-finite either way)
       const uint32_t sdead = uu < CU ? dead : 0x80000000u;
       const uint32_t gi = (grow * (uint32_t)groups + (u >> GSH)) * (uint32_t)sizeof(ST) + sdead;
       st.s[j] = (uint32_t)bload16(pv.s, gi);
