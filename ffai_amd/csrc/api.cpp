@@ -596,7 +596,9 @@ GemvKind gemv_kind(const moe_qproj& p0, const moe_qproj* p1, bool x_aligned, int
   const int min_rows10 = slots <= 1 ? kMmaMinRowsSingleExpert10
                         : p0.bits != 4 ? kMmaMinRowsOther10
                                        : (p1 ? kMmaMinRowsPair10 : kMmaMinRowsSingle10);
-  if (10L * M >= (long)min_rows10 * std::max(1, slots) && mma_ok(p0, p1, x_aligned, xdt))
+  // (its activation view holds at most M rows of K 16-bit values in 32-bit offsets)
+  if (10L * M >= (long)min_rows10 * std::max(1, slots) && mma_ok(p0, p1, x_aligned, xdt) &&
+      (size_t)M * (size_t)p0.k * 2 < (1ull << 31))
     return kGemvMma;
   const int tm = multi_rows_per_pass(std::min(max_rows, M), M, slots);
   if (multi_ok(p0, x_aligned, xdt, tm)) return kGemvMulti;
@@ -656,7 +658,7 @@ void run_multi(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
 // block, 16 activation rows per pass. The caller has checked mma_ok.
 void run_mma(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
              const uint32_t* perm, int topk, const uint32_t* offsets, const uint32_t* used, int slots,
-             void* out, int act, float alpha, float limit, hipStream_t st, KEvents ev,
+             int x_rows, void* out, int act, float alpha, float limit, hipStream_t st, KEvents ev,
              moe_status* status) {
   const int rows_per_block = p1 ? 32 : 64;
   const int row_blocks = (p0.n + rows_per_block - 1) / rows_per_block;
@@ -677,6 +679,7 @@ void run_mma(const moe_qproj& p0, const moe_qproj* p1, const void* x, int xdt,
   a.act = act;
   a.alpha = alpha;
   a.limit = limit;
+  a.x_rows = x_rows;
   *status = hip_check(launch_mma(p0.bits, xdt, p0.sb_dtype, p1 != nullptr, a, slots * row_blocks, st, ev),
                       "grouped GEMV launch");
 }
@@ -691,8 +694,10 @@ moe_status run_gemv(const moe_qproj& p0, const moe_qproj* p1, const void* x, int
   const GemvKind kind = gemv_kind(p0, p1, aligned16(x), xdt, slots, M, single, max_rows);
   if (kind == kGemvMma) {
     moe_status status = MOE_OK;
-    run_mma(p0, p1, x, xdt, perm, topk, offsets, used, slots, out, act, alpha, limit, st, ev,
-            &status);
+    // the activation rows: one per token on the gather path (M = T topk)
+    const int x_rows = perm ? (M + topk - 1) / topk : M;
+    run_mma(p0, p1, x, xdt, perm, topk, offsets, used, slots, x_rows, out, act, alpha, limit, st,
+            ev, &status);
     return status;
   }
   if (kind == kGemvMulti) {

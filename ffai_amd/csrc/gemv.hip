@@ -493,7 +493,10 @@ void gemv_mma_kernel(const GemvArgs a) {
   const int r_begin = rb * RPB;
   const ProjView P0 = proj_view<BITS, ST>(a.p0, e, N, row_words, groups);
   const ProjView P1 = GATEUP ? proj_view<BITS, ST>(a.p1, e, N, row_words, groups) : P0;
-  const XT* x = reinterpret_cast<const XT*>(a.x);
+  // activation rows through a buffer view (the host keeps x_rows K 16-bit
+  // values below 2^31 bytes): the rows of a pass past its end read zero at a
+  // dead offset instead of repeating its last row, and offsets stay 32-bit
+  const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.x_rows * (size_t)K * sizeof(XT)));
   // MAGIC + q is exact in the 16-bit type for q < 128 (bf16) / 1024 (f16)
   constexpr float MAGIC = Magic<BITS, XT>::value;
   constexpr uint32_t MB = Magic<BITS, XT>::bits;
@@ -542,17 +545,17 @@ void gemv_mma_kernel(const GemvArgs a) {
       st.b[j] = (uint32_t)bload16(pv.b, gi);
     }
   };
-  auto load_x_stage = [&](int c, uint32_t xrow, Stage& st) __attribute__((always_inline)) {
+  auto load_x_stage = [&](int c, uint32_t xbase, Stage& st) __attribute__((always_inline)) {
     const int cc = min(c, nchunks - 1);
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int ux = min(kMmaU * cc + x_us0 + 4 * j, CU - 1);
-      st.x[j] = *reinterpret_cast<const u32x4_t*>(x + (size_t)xrow * K + (size_t)ux * 32 + x_kb * 8);
+      st.x[j] = bload128(xr, xbase + (uint32_t)ux * 64u + (uint32_t)x_kb * 16u);
     }
   };
-  auto load_stage = [&](int c, uint32_t xrow, Stage& st) __attribute__((always_inline)) {
+  auto load_stage = [&](int c, uint32_t xbase, Stage& st) __attribute__((always_inline)) {
     load_w_stage(c, st);
-    load_x_stage(c, xrow, st);
+    load_x_stage(c, xbase, st);
   };
   auto store_stage = [&](const Stage& st, int buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -622,11 +625,12 @@ void gemv_mma_kernel(const GemvArgs a) {
     const int nt = min((int)(pend - pc), kMmaTok);
     const uint32_t p = pc + (uint32_t)min(x_t, nt - 1);
     const uint32_t xrow = a.perm ? a.perm[p] / (uint32_t)a.topk : p;
-    load_x_stage(0, xrow, s0);
-    load_x_stage(1, xrow, s1);
+    const uint32_t xbase = x_t < nt ? xrow * (uint32_t)K * (uint32_t)sizeof(XT) : 0x80000000u;
+    load_x_stage(0, xbase, s0);
+    load_x_stage(1, xbase, s1);
     lds_barrier();  // the last pass's LDS reads (and gl) are done; loads stay in flight
     store_stage(s0, 0);
-    load_stage(2, xrow, s0);
+    load_stage(2, xbase, s0);
     lds_barrier();
     acc = f32x4_t{};
     // No break in this loop: with one, the compiler's wait counts at the loop
@@ -638,11 +642,11 @@ void gemv_mma_kernel(const GemvArgs a) {
     for (int c = 0; c < nchunks; c += 2) {
       compute(0);
       store_stage(s1, 1);  // chunk c + 1
-      load_stage(c + 3, xrow, s1);
+      load_stage(c + 3, xbase, s1);
       lds_barrier();
       if (c + 1 < nchunks) compute(1);
       store_stage(s0, 0);  // chunk c + 2
-      load_stage(c + 4, xrow, s0);
+      load_stage(c + 4, xbase, s0);
       lds_barrier();
     }
     // lane (r, kb): output column orow, activation rows 4 kb + i of the pass

@@ -66,6 +66,7 @@ struct GemvArgs {
   int tok_chunk;             // activation rows staged per pass (<= TOKMAX)
   int act;                   // activation (gate/up pair only)
   float alpha, limit;
+  int x_rows;                // rows of x (gemv_mma_kernel reads them through a buffer view)
 };
 
 // Decode of one token (T = 1). gate/up kernel: every wave selects the top-k
